@@ -1,0 +1,213 @@
+/*
+ * rembed_hip.h — C ABI of the MI355X (gfx950) GEMM backend for rembed.
+ *
+ * Drop-in boundary for rembed's internal/tensor matmul family and the
+ * encoder forward that calls it. Every entry point is plain C: opaque
+ * handles, plain pointers and sizes, an int status (RH_OK == 0) and a
+ * thread-local message from rh_last_error(). No entry point aborts the host.
+ *
+ * Pointer conventions
+ *   "host"  — ordinary CPU memory, borrowed for the duration of the call.
+ *   "dev"   — device memory from rh_malloc (or any HIP allocation on the
+ *             context's device). Calls taking dev pointers are enqueued on
+ *             the context's stream and return without waiting; call
+ *             rh_context_sync before reading results back.
+ *
+ * Each declaration names the reference interface it replaces (file:line,
+ * relative to the rembed source tree).
+ */
+#ifndef REMBED_HIP_H
+#define REMBED_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define RH_OK 0
+#define RH_ERR_NO_DEVICE 1 /* no usable GPU: the host falls back to its CPU path */
+#define RH_ERR_INVALID 2   /* contract violation (the reference panics on these) */
+#define RH_ERR_SHAPE 3     /* PackB*: n%16 != 0, n < 16, k < 1 (pack.go:29-37) */
+#define RH_ERR_NONFINITE 4 /* PackB8/PackB8VNNI: NaN/Inf weight (pack8.go:43-48) */
+#define RH_ERR_HIP 5       /* HIP runtime failure */
+#define RH_ERR_OOM 6       /* device allocation failed */
+#define RH_ERR_VOCAB 7     /* token id out of vocab range (bert.go:797-800) */
+#define RH_ERR_SEQ 8       /* empty or over-long sequence (bert.go:741-747) */
+#define RH_ERR_MISSING 9   /* model tensor missing or misshapen (bert.go:345-360) */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *rh_last_error(void);
+/* ABI version: major*10000 + minor*100 + patch. */
+int rh_version(void);
+
+/* ---- context ---------------------------------------------------------------
+ * One context = one device + one HIP stream (default priority). A context
+ * serializes the calls made on it; use one context per concurrent caller
+ * (the reference's Model is safe for concurrent use, bert.go:54-56). */
+typedef struct rh_context rh_context;
+
+int rh_device_count(int *count);
+int rh_context_create(int device, rh_context **out);
+void rh_context_destroy(rh_context *ctx);
+int rh_context_sync(rh_context *ctx);
+/* The context's hipStream_t, for callers that time or order work around it. */
+void *rh_context_stream(rh_context *ctx);
+/* fp32 GEMM strategy: 0 = three bf16 MFMA products (default), 1 = native
+ * f32 MFMA. Both meet the fp32 contract; this exists to re-measure. */
+int rh_context_set_f32_algo(rh_context *ctx, int algo);
+
+/* Device memory helpers (the Go host has no other allocator for HBM). */
+int rh_malloc(rh_context *ctx, size_t bytes, void **dev);
+int rh_free(rh_context *ctx, void *dev);
+int rh_memcpy_h2d(rh_context *ctx, void *dev_dst, const void *host_src, size_t bytes);
+int rh_memcpy_d2h(rh_context *ctx, void *host_dst, const void *dev_src, size_t bytes);
+
+/* Per-launch GEMM timing with HIP events on the context's stream.
+ * kind: 0 = full-int8 GEMM, 1 = weight-only int8 GEMM, 2 = fp32 GEMM,
+ * 3 = attention. Reading syncs the stream. */
+typedef struct {
+  int64_t launches;
+  double total_ms;    /* sum of per-launch event durations */
+  double total_ops;   /* algorithmic 2*M*K*N summed over launches */
+  double total_bytes; /* algorithmic minimal HBM bytes summed over launches */
+} rh_profile_stat;
+int rh_profile_enable(rh_context *ctx, int on); /* also clears the tallies */
+int rh_profile_read(rh_context *ctx, int kind, rh_profile_stat *out);
+
+/* ---- weights (tensor level) --------------------------------------------------
+ * Quantize/pack on the host exactly as the reference does, then upload once
+ * to HBM; the handle owns the device copy until rh_weight_destroy.
+ *   mode RH_MODE_F32  replaces PackB       (internal/tensor/pack.go:25-50)
+ *   mode RH_MODE_W8   replaces PackB8      (internal/tensor/pack8.go:25-76)
+ *   mode RH_MODE_A8W8 replaces PackB8VNNI  (internal/tensor/pack_vnni.go:28-77)
+ * bT is the HF [out=n][in=k] row-major matrix; bias (length n) may be NULL
+ * and is applied by rh_linear only (newDense's bias, bert.go:263-278). */
+#define RH_MODE_F32 0
+#define RH_MODE_W8 1
+#define RH_MODE_A8W8 2
+typedef struct rh_weight rh_weight;
+
+int rh_pack_weight(rh_context *ctx, int mode, const float *bT, const float *bias,
+                   int k, int n, rh_weight **out);
+void rh_weight_destroy(rh_weight *w);
+/* Shape and mode of a packed weight. */
+int rh_weight_info(const rh_weight *w, int *mode, int *k, int *n);
+/* Host copies of the quantization results, for parity checks: q is
+ * [n][k] row-major (RH_MODE_W8 / RH_MODE_A8W8), scales [n], colsum [n]
+ * (RH_MODE_A8W8 only). Any output may be NULL. */
+int rh_weight_export(const rh_weight *w, int8_t *q, float *scales, int32_t *colsum);
+
+/* ---- activations and GEMMs (tensor level, dev pointers) ---------------------
+ * QuantizeRowU8 over m rows (internal/tensor/pack_vnni.go:85-117, the row
+ * loop of pack_vnni.go:129-140): qa is [m][ldq] bytes, ldq >= k and a
+ * multiple of 16; bytes k..ldq-1 of each row are zeroed. a is [m][k]. */
+int rh_quantize_rows_u8(rh_context *ctx, const float *a, int m, int k,
+                        uint8_t *qa, int ldq, float *row_scales);
+
+/* MatMulPacked (internal/tensor/pack.go:123-176): dst[m][n] = a[m][k]·Wᵀ. */
+int rh_matmul_packed(rh_context *ctx, float *dst, const float *a,
+                     const rh_weight *w, int m);
+/* MatMulPacked8 (internal/tensor/pack8.go:80-111). */
+int rh_matmul_packed8(rh_context *ctx, float *dst, const float *a,
+                      const rh_weight *w, int m);
+/* MatMulPackedVNNI (internal/tensor/pack_vnni.go:124-176): quantizes a into
+ * qa/row_scales (caller scratch, [m][ldq] and [m]) and writes
+ * dst = float32(acc - 128·colSum)·rowScale·colScale. */
+int rh_matmul_packed_vnni(rh_context *ctx, float *dst, const float *a,
+                          const rh_weight *w, int m, uint8_t *qa, int ldq,
+                          float *row_scales);
+/* The int32 accumulators of gemm4x16vnni (internal/tensor/vnni_amd64.s:22-82)
+ * over already-quantized rows: acc[m][n] = Σ_p u8(qa[i][p])·s8(q[j][p]),
+ * wrapping. For bit-exact parity checks. */
+int rh_gemm_u8s8_i32(rh_context *ctx, int32_t *acc, const uint8_t *qa, int ldq,
+                     const rh_weight *w, int m);
+
+/* applyDense (internal/model/bert.go:282-301) with the bias and activation
+ * fused into the GEMM epilogue: dst = act(a·Wᵀ + bias). act: 0 none,
+ * 1 erf-GELU (geluScalar, internal/tensor/tensor.go:508-538). For
+ * RH_MODE_A8W8 the quantization scratch comes from qa/row_scales as in
+ * rh_matmul_packed_vnni (both may be NULL for the other modes). */
+#define RH_ACT_NONE 0
+#define RH_ACT_GELU 1
+int rh_linear(rh_context *ctx, float *dst, const float *a, const rh_weight *w,
+              int m, int act, uint8_t *qa, int ldq, float *row_scales);
+
+/* Elementwise entry points used by parity tests (dev pointers). */
+int rh_gelu(rh_context *ctx, float *x, size_t n);          /* tensor.go:508-538 */
+int rh_layernorm(rh_context *ctx, float *x, const float *gamma,
+                 const float *beta, int m, int n, float eps); /* tensor.go:433-452 */
+
+/* ---- encoder model ------------------------------------------------------------
+ * Replaces model.Load + Model.Forward/ForwardTokens + the Embed batch loop
+ * (internal/model/bert.go:307-524,649-731; rembed.go:287-411) with one
+ * device-resident forward over a packed variable-length batch. */
+#define RH_ARCH_BERT 0 /* BERT / RoBERTa / DistilBERT-style post-LN encoder */
+#define RH_POOL_MEAN 0
+#define RH_POOL_CLS 1
+#define RH_POOL_LAST 2
+/* Quantization requests, WithInt8 / WithInt8Activations (rembed.go:60-81,
+ * 241-247). Per-matrix fallback as newDense (bert.go:263-278). */
+#define RH_QUANT_NONE 0
+#define RH_QUANT_WEIGHTS 1
+#define RH_QUANT_FULL 2
+
+typedef struct {
+  int arch;
+  int hidden;           /* H */
+  int layers;
+  int heads;
+  int intermediate;     /* I */
+  int vocab;
+  int max_position;     /* rows of the position table */
+  int position_offset;  /* Config.PositionOffset (config.go:84-89) */
+  int type_vocab;       /* rows of token_type_embeddings (only row 0 used) */
+  float layer_norm_eps; /* 0 means 1e-12 (config.go:228-230) */
+  int pooling;          /* RH_POOL_* */
+  int normalize;        /* L2-normalize pooled vectors */
+  int reserved[8];      /* zero */
+} rh_model_config;
+
+typedef struct rh_model rh_model;
+
+int rh_model_create(rh_context *ctx, const rh_model_config *cfg, int quant,
+                    rh_model **out);
+/* Hand one HF tensor (by its safetensors name, with or without the
+ * "bert."/"roberta."/"distilbert." prefix) to the model; data is copied. */
+int rh_model_set_tensor(rh_model *m, const char *name, const float *host,
+                        const int64_t *shape, int ndim);
+/* Check every tensor is present, fuse Q|K|V, quantize/pack and upload. */
+int rh_model_finalize(rh_model *m);
+void rh_model_destroy(rh_model *m);
+/* Per-model switches. RH_OPT_ATTN_PRECISION: 1 = bf16 attention operands,
+ * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE). */
+#define RH_OPT_ATTN_PRECISION 1
+int rh_model_set_option(rh_model *m, int option, int value);
+/* Model.Quantized / QuantizedActivations (bert.go:526-644). */
+int rh_model_quantized(const rh_model *m);
+int rh_model_quantized_activations(const rh_model *m);
+
+/* Embed (rembed.go:287-332 + Forward bert.go:649-689): ids is [batch][stride]
+ * host, text b is ids[b*stride .. b*stride+lens[b]); out is [batch][H] host. */
+int rh_model_embed(rh_model *m, const int32_t *ids, const int32_t *lens,
+                   int batch, int stride, float *out);
+/* EmbedTokens / ForwardTokens (rembed.go:370-411, bert.go:705-731): out is
+ * [sum(lens)][H] host, texts concatenated in order. */
+int rh_model_embed_tokens(rh_model *m, const int32_t *ids, const int32_t *lens,
+                          int batch, int stride, float *out);
+/* Device-resident variant: ids_dev [batch][stride] and out_dev [batch][H]
+ * in HBM, lens on the host; enqueued on the context stream (no sync). Ids
+ * out of range are clamped and reported by the next rh_model_check. */
+int rh_model_embed_device(rh_model *m, const int32_t *ids_dev,
+                          const int32_t *lens, int batch, int stride,
+                          float *out_dev);
+/* Sync and report a deferred device-side error (RH_ERR_VOCAB) of the
+ * previous rh_model_embed_device calls. */
+int rh_model_check(rh_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* REMBED_HIP_H */

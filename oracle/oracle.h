@@ -1,0 +1,150 @@
+/*
+ * oracle.h — CPU restatement of rembed's GEMM family and BERT forward pass.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library (rembed_amd/)
+ * links, loads or calls this code: it is the checker that the parity tests,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg compare the HIP
+ * path against. Each function cites the reference file:line it restates
+ * (paths relative to the rembed source tree).
+ *
+ * Arithmetic discipline: compiled with -ffp-contract=off so only explicit
+ * fmaf() fuses, matching Go on amd64 which never fuses scalar mul+add
+ * (internal/tensor/tensor_test.go:126-131) while the packed GEMM assembly
+ * uses explicit VFMADD231PS (internal/tensor/gemm_amd64.s:38-45).
+ *
+ * Pinning (what checks each function beyond retyping its formula):
+ *   or_quantize_row_u8   known answers of TestQuantizeRowU8Rails
+ *                        (internal/tensor/vnni_test.go:118-134) + rail inputs
+ *   or_pack_b8_vnni /    vnniReference closed form (vnni_test.go:11-59)
+ *   or_gemm_u8s8_i32     restated independently in tests, brute force int64
+ *   or_pack_b8           |deq-w| <= maxAbs/254 (pack8_test.go:114-144),
+ *                        zero-channel scale 1, NaN/Inf refusal
+ *   or_matmul_f32/_w8    float64 reference within max(1e-5,1e-6*sqrt k)(1+|w|)
+ *                        (pack_test.go:55-67), KAT {58,64,139,154}
+ *   elementwise          KATs of tensor_test.go:154-268, float64 erf/tanh
+ *   or_bert_*            composition pinned by source reading; invariants
+ *                        (unit L2 norm, batch == single, mode agreement)
+ */
+#ifndef REMBED_ORACLE_H
+#define REMBED_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes (mirror the reference's error returns) */
+#define OR_OK 0
+#define OR_ERR_SHAPE 1
+#define OR_ERR_NONFINITE 2
+#define OR_ERR_VOCAB 3
+#define OR_ERR_SEQ 4
+
+/* ---- weight quantizers ------------------------------------------------ */
+/* PackB8 (internal/tensor/pack8.go:25-76). q is [n][k] row-major. */
+int or_pack_b8(const float *bT, int k, int n, int8_t *q, float *scales);
+/* PackB8VNNI (internal/tensor/pack_vnni.go:28-77). q is [n][k] row-major. */
+int or_pack_b8_vnni(const float *bT, int k, int n, int8_t *q, int32_t *colsum,
+                    float *scales);
+
+/* QuantizeRowU8 (internal/tensor/pack_vnni.go:85-117): dst holds dstlen >= k
+ * bytes, bytes k..dstlen-1 are zeroed; returns the row scale. */
+float or_quantize_row_u8(uint8_t *dst, int dstlen, const float *a, int k);
+
+/* ---- the three GEMMs (dst[m][n] = a[m][k] . bT^T) ---------------------- */
+/* MatMulPacked: one sequential fmaf chain per element, ascending k
+ * (internal/tensor/pack.go:123-210, gemm_amd64.s:31-49). */
+void or_matmul_f32(float *dst, const float *a, const float *bT, int m, int k,
+                   int n);
+/* MatMulPacked8: fmaf chain over float(q), then *scale
+ * (internal/tensor/pack8.go:80-126, gemm8_amd64.s:32-64). */
+void or_matmul_w8(float *dst, const float *a, const int8_t *q,
+                  const float *scales, int m, int k, int n);
+/* VPDPBUSD accumulators: acc[i][j] = sum_p u8(qa[i][p]) * s8(q[j][p]),
+ * int32 wrapping (internal/tensor/vnni_amd64.s:22-82). qa row stride lda. */
+void or_gemm_u8s8_i32(int32_t *acc, const uint8_t *qa, int lda,
+                      const int8_t *q, int m, int k, int n);
+/* MatMulPackedVNNI (internal/tensor/pack_vnni.go:124-176): quantize rows,
+ * accumulate, epilogue (acc - 128*colSum)*rs*scale. qa_out ([m][k]),
+ * rs_out ([m]) and acc_out ([m][n]) may be NULL. */
+void or_matmul_vnni(float *dst, const float *a, const int8_t *q,
+                    const int32_t *colsum, const float *scales, int m, int k,
+                    int n, uint8_t *qa_out, float *rs_out, int32_t *acc_out);
+
+/* ---- elementwise (internal/tensor/tensor.go:372-554, fastmath.go) ------ */
+float or_expf32(float x);  /* fastmath.go:26-55 */
+float or_erff32(float x);  /* fastmath.go:69-82 */
+void or_add_bias(float *x, const float *bias, int m, int n);
+void or_add(float *dst, const float *src, int n);
+void or_softmax(float *x, int m, int n);
+void or_layernorm(float *x, const float *g, const float *b, int m, int n,
+                  float eps);
+void or_rmsnorm(float *x, const float *g, int m, int n, float eps);
+void or_gelu(float *x, int n);      /* geluScalar, tensor.go:508-538 */
+void or_gelu_tanh(float *x, int n); /* tensor.go:490-497 */
+void or_silu(float *x, int n);      /* tensor.go:477-481 */
+void or_l2normalize(float *x, int n);
+/* dot4 (internal/tensor/dot_amd64.s:13-94): 8-lane FMA body, fold, FMA
+ * tail into lane 0, two horizontal adds. */
+void or_dot4(float *dst, const float *a, const float *b0, const float *b1,
+             const float *b2, const float *b3, int k);
+/* MatMulSerial with the SIMD body (tensor.go:284-330). */
+void or_matmul_serial(float *dst, const float *a, const float *bT, int m,
+                      int k, int n);
+
+/* ---- BERT-family encoder (internal/model/bert.go) ----------------------- */
+#define OR_QUANT_NONE 0
+#define OR_QUANT_WEIGHTS 1
+#define OR_QUANT_FULL 2
+#define OR_POOL_MEAN 0
+#define OR_POOL_CLS 1
+#define OR_POOL_LAST 2
+
+typedef struct {
+  int vocab, hidden, layers, heads, inter, max_pos, type_vocab;
+  float eps;
+  int pooling;   /* OR_POOL_* */
+  int normalize; /* L2-normalize the pooled vector */
+} or_bert_config;
+
+/* Per-layer tensor order inside `layer_tensors` (16 per layer, HF layouts):
+ * q_w[H][H] q_b k_w k_b v_w v_b o_w[H][H] o_b ln1_g ln1_b
+ * f1_w[I][H] f1_b f2_w[H][I] f2_b ln2_g ln2_b */
+#define OR_BERT_TENSORS_PER_LAYER 16
+
+typedef struct or_bert_model or_bert_model;
+
+/* Load: fuse Q|K|V and pack/quantize every dense once (bert.go:307-524,
+ * newDense bert.go:263-278). Weight pointers are borrowed for the model's
+ * lifetime (embedding tables, norms and biases are not copied). */
+or_bert_model *or_bert_create(const or_bert_config *cfg, int quant,
+                              const float *word_emb, const float *pos_emb,
+                              const float *type_emb, const float *emb_ln_g,
+                              const float *emb_ln_b,
+                              const float *const *layer_tensors);
+void or_bert_free(or_bert_model *m);
+
+/* encodeWorkers (bert.go:740-923): one unpadded forward over seq ids,
+ * writing the final hidden states [seq][H]. */
+int or_bert_encode(const or_bert_model *m, const int32_t *ids, int seq,
+                   float *hidden);
+/* Forward (bert.go:649-703): encode, pool, optional L2. out is [H]. */
+int or_bert_forward(const or_bert_model *m, const int32_t *ids, int seq,
+                    float *out);
+/* Embed batch policy (rembed.go:309-330): one serial forward per text,
+ * fanned out across texts on `threads` OS threads. ids is [batch][stride],
+ * text b uses ids[b*stride .. b*stride+lens[b]). out is [batch][H]. */
+int or_bert_embed_batch(const or_bert_model *m, const int32_t *ids,
+                        const int32_t *lens, int batch, int stride,
+                        float *out, int threads);
+
+/* Which int8 dot-product body the oracle picked at run time (for reports):
+ * 2 = AVX-512-VNNI intrinsics, 0 = portable C. Both produce identical
+ * integers. */
+int or_vnni_kind(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

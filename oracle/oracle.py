@@ -1,0 +1,243 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker. The product never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = ctypes.CDLL(LIB_PATH)
+    P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    sig = {
+        "or_pack_b8": (I, [P, I, I, P, P]),
+        "or_pack_b8_vnni": (I, [P, I, I, P, P, P]),
+        "or_quantize_row_u8": (F, [P, I, P, I]),
+        "or_matmul_f32": (None, [P, P, P, I, I, I]),
+        "or_matmul_w8": (None, [P, P, P, P, I, I, I]),
+        "or_gemm_u8s8_i32": (None, [P, P, I, P, I, I, I]),
+        "or_matmul_vnni": (None, [P, P, P, P, P, I, I, I, P, P, P]),
+        "or_expf32": (F, [F]),
+        "or_erff32": (F, [F]),
+        "or_add_bias": (None, [P, P, I, I]),
+        "or_add": (None, [P, P, I]),
+        "or_softmax": (None, [P, I, I]),
+        "or_layernorm": (None, [P, P, P, I, I, F]),
+        "or_rmsnorm": (None, [P, P, I, I, F]),
+        "or_gelu": (None, [P, I]),
+        "or_gelu_tanh": (None, [P, I]),
+        "or_silu": (None, [P, I]),
+        "or_l2normalize": (None, [P, I]),
+        "or_dot4": (None, [P, P, P, P, P, P, I]),
+        "or_matmul_serial": (None, [P, P, P, I, I, I]),
+        "or_bert_create": (P, [P, I, P, P, P, P, P, P]),
+        "or_bert_free": (None, [P]),
+        "or_bert_encode": (I, [P, P, I, P]),
+        "or_bert_forward": (I, [P, P, I, P]),
+        "or_bert_embed_batch": (I, [P, P, P, I, I, P, I]),
+        "or_vnni_kind": (I, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- tensor-level wrappers ------------------------------------------------------
+
+def pack_b8(bT, k, n):
+    q = np.empty((n, k), np.int8)
+    sc = np.empty(n, np.float32)
+    bT = f32(bT)
+    st = lib.or_pack_b8(_p(bT), k, n, _p(q), _p(sc))
+    return st, q, sc
+
+
+def pack_b8_vnni(bT, k, n):
+    q = np.empty((n, k), np.int8)
+    sc = np.empty(n, np.float32)
+    cs = np.empty(n, np.int32)
+    bT = f32(bT)
+    st = lib.or_pack_b8_vnni(_p(bT), k, n, _p(q), _p(cs), _p(sc))
+    return st, q, sc, cs
+
+
+def quantize_row_u8(a, dstlen=None):
+    a = f32(a)
+    k = a.shape[0]
+    dst = np.empty(dstlen or k, np.uint8)
+    s = lib.or_quantize_row_u8(_p(dst), dst.shape[0], _p(a), k)
+    return dst, np.float32(s)
+
+
+def matmul_f32(a, bT):
+    a, bT = f32(a), f32(bT)
+    m, k = a.shape
+    n = bT.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib.or_matmul_f32(_p(out), _p(a), _p(bT), m, k, n)
+    return out
+
+
+def matmul_w8(a, q, scales):
+    a = f32(a)
+    m, k = a.shape
+    n = q.shape[0]
+    out = np.empty((m, n), np.float32)
+    q = np.ascontiguousarray(q, np.int8)
+    scales = f32(scales)
+    lib.or_matmul_w8(_p(out), _p(a), _p(q), _p(scales), m, k, n)
+    return out
+
+
+def gemm_u8s8_i32(qa, q):
+    qa = np.ascontiguousarray(qa, np.uint8)
+    q = np.ascontiguousarray(q, np.int8)
+    m, lda = qa.shape
+    n, k = q.shape
+    acc = np.empty((m, n), np.int32)
+    lib.or_gemm_u8s8_i32(_p(acc), _p(qa), lda, _p(q), m, k, n)
+    return acc
+
+
+def matmul_vnni(a, q, colsum, scales):
+    """Returns (dst, qa, row_scales, acc)."""
+    a = f32(a)
+    m, k = a.shape
+    n = q.shape[0]
+    out = np.empty((m, n), np.float32)
+    qa = np.empty((m, k), np.uint8)
+    rs = np.empty(m, np.float32)
+    acc = np.empty((m, n), np.int32)
+    q = np.ascontiguousarray(q, np.int8)
+    colsum = np.ascontiguousarray(colsum, np.int32)
+    scales = f32(scales)
+    lib.or_matmul_vnni(_p(out), _p(a), _p(q), _p(colsum), _p(scales),
+                       m, k, n, _p(qa), _p(rs), _p(acc))
+    return out, qa, rs, acc
+
+
+def rowwise(fn, x, *args):
+    x = f32(x).copy()
+    fn(_p(x), *args)
+    return x
+
+
+def gelu(x):
+    x = f32(x).copy()
+    lib.or_gelu(_p(x), x.size)
+    return x
+
+
+def layernorm(x, g, b, eps):
+    x = f32(x).copy()
+    m, n = x.shape
+    g, b = f32(g), f32(b)
+    lib.or_layernorm(_p(x), _p(g), _p(b), m, n, eps)
+    return x
+
+
+# ---- BERT model ------------------------------------------------------------------
+
+class BertConfig(ctypes.Structure):
+    _fields_ = [("vocab", ctypes.c_int), ("hidden", ctypes.c_int),
+                ("layers", ctypes.c_int), ("heads", ctypes.c_int),
+                ("inter", ctypes.c_int), ("max_pos", ctypes.c_int),
+                ("type_vocab", ctypes.c_int), ("eps", ctypes.c_float),
+                ("pooling", ctypes.c_int), ("normalize", ctypes.c_int)]
+
+
+LAYER_ORDER = [
+    "attention.self.query.weight", "attention.self.query.bias",
+    "attention.self.key.weight", "attention.self.key.bias",
+    "attention.self.value.weight", "attention.self.value.bias",
+    "attention.output.dense.weight", "attention.output.dense.bias",
+    "attention.output.LayerNorm.weight", "attention.output.LayerNorm.bias",
+    "intermediate.dense.weight", "intermediate.dense.bias",
+    "output.dense.weight", "output.dense.bias",
+    "output.LayerNorm.weight", "output.LayerNorm.bias",
+]
+
+
+class BertOracle:
+    """The reference's per-text unpadded BERT forward on the CPU."""
+
+    def __init__(self, shape, tensors, quant):
+        self._keep = {k: f32(v) for k, v in tensors.items()}
+        t = self._keep
+        cfg = BertConfig(shape.vocab, shape.hidden, shape.layers, shape.heads,
+                         shape.intermediate, shape.max_position, shape.type_vocab,
+                         shape.eps, shape.pooling, shape.normalize)
+        self.shape = shape
+        layer_ptrs = [t[f"encoder.layer.{l}.{n}"].ctypes.data
+                      for l in range(shape.layers) for n in LAYER_ORDER]
+        self._arr = (ctypes.c_void_p * len(layer_ptrs))(*layer_ptrs)
+        self.h = lib.or_bert_create(
+            ctypes.byref(cfg), quant,
+            _p(t["embeddings.word_embeddings.weight"]),
+            _p(t["embeddings.position_embeddings.weight"]),
+            _p(t["embeddings.token_type_embeddings.weight"]),
+            _p(t["embeddings.LayerNorm.weight"]), _p(t["embeddings.LayerNorm.bias"]),
+            ctypes.cast(self._arr, ctypes.c_void_p))
+        if not self.h:
+            raise RuntimeError("oracle: bad BERT config")
+
+    def close(self):
+        if self.h:
+            lib.or_bert_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def encode(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
+        st = lib.or_bert_encode(self.h, _p(ids), ids.shape[0], _p(out))
+        if st:
+            raise RuntimeError(f"oracle encode status {st}")
+        return out
+
+    def forward(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty(self.shape.hidden, np.float32)
+        st = lib.or_bert_forward(self.h, _p(ids), ids.shape[0], _p(out))
+        if st:
+            raise RuntimeError(f"oracle forward status {st}")
+        return out
+
+    def embed_batch(self, ids, lens, threads=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        lens = np.ascontiguousarray(lens, np.int32)
+        out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
+        st = lib.or_bert_embed_batch(self.h, _p(ids), _p(lens), ids.shape[0],
+                                     ids.shape[1], _p(out), threads)
+        if st:
+            raise RuntimeError(f"oracle embed status {st}")
+        return out

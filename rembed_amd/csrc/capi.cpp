@@ -1,0 +1,546 @@
+// capi.cpp — C ABI: contexts, device memory, weight packing/upload and the
+// tensor-level GEMM entry points (the internal/tensor mirror).
+//
+// Host-side quantization restates the reference exactly (it runs once at
+// load, as PackB8/PackB8VNNI do); the device kernels then consume the packed
+// bytes. Every entry point validates its arguments and returns an RH_*
+// status with a thread-local message instead of aborting.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "context.h"
+
+namespace rh {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string& msg) { g_err = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what, const char* file, int line) {
+  char buf[512];
+  snprintf(buf, sizeof buf, "%s failed: %s (%s:%d)", what, hipGetErrorString(e),
+           file, line);
+  g_err = buf;
+  return e == hipErrorOutOfMemory ? RH_ERR_OOM : RH_ERR_HIP;
+}
+
+}  // namespace rh
+
+// ---- profiling ---------------------------------------------------------------
+hipError_t rh_context::prof_begin(int kind, double ops, double bytes, int* slot) {
+  *slot = -1;
+  if (!profiling) return hipSuccess;
+  ProfRec r{};
+  hipError_t e = hipEventCreate(&r.a);
+  if (e != hipSuccess) return e;
+  e = hipEventCreate(&r.b);
+  if (e != hipSuccess) return e;
+  r.kind = kind;
+  r.ops = ops;
+  r.bytes = bytes;
+  e = hipEventRecord(r.a, stream);
+  if (e != hipSuccess) return e;
+  recs.push_back(r);
+  *slot = (int)recs.size() - 1;
+  return hipSuccess;
+}
+
+hipError_t rh_context::prof_end(int slot) {
+  if (slot < 0) return hipSuccess;
+  return hipEventRecord(recs[slot].b, stream);
+}
+
+void rh_context::prof_clear() {
+  for (auto& r : recs) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  recs.clear();
+}
+
+namespace rh {
+
+// ---- host quantizers (restated from the reference) ----------------------------
+
+// PackB8, internal/tensor/pack8.go:25-76.
+int quantize_b8(const float* bT, int k, int n, std::vector<int8_t>& q,
+                std::vector<float>& scales) {
+  q.assign((size_t)n * k, 0);
+  scales.assign(n, 0.0f);
+  for (int j = 0; j < n; j++) {
+    const float* row = bT + (size_t)j * k;
+    float maxAbs = 0.0f;
+    for (int p = 0; p < k; p++) {
+      const float v = row[p];
+      if (std::isnan(v) || std::isinf(v)) {
+        char buf[160];
+        snprintf(buf, sizeof buf, "PackB8 channel %d has a non-finite weight", j);
+        return fail(RH_ERR_NONFINITE, buf);
+      }
+      const float a = std::fabs(v);
+      if (a > maxAbs) maxAbs = a;
+    }
+    float scale = maxAbs / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    scales[j] = scale;
+    for (int p = 0; p < k; p++) {
+      double qd = std::rint((double)row[p] / (double)scale);
+      if (qd > 127.0) qd = 127.0;
+      if (qd < -127.0) qd = -127.0;
+      q[(size_t)j * k + p] = (int8_t)qd;
+    }
+  }
+  return RH_OK;
+}
+
+// PackB8VNNI, internal/tensor/pack_vnni.go:28-77.
+int quantize_b8_vnni(const float* bT, int k, int n, std::vector<int8_t>& q,
+                     std::vector<float>& scales, std::vector<int32_t>& colsum) {
+  q.assign((size_t)n * k, 0);
+  scales.assign(n, 0.0f);
+  colsum.assign(n, 0);
+  for (int c = 0; c < n; c++) {
+    const float* row = bT + (size_t)c * k;
+    double maxAbs = 0.0;
+    for (int p = 0; p < k; p++) {
+      const double v = (double)row[p];
+      if (std::isnan(v) || std::isinf(v)) {
+        char buf[160];
+        snprintf(buf, sizeof buf, "PackB8VNNI weight [%d,%d] is not finite", c, p);
+        return fail(RH_ERR_NONFINITE, buf);
+      }
+      const double a = std::fabs(v);
+      if (a > maxAbs) maxAbs = a;
+    }
+    double scale = maxAbs / 127.0;
+    if (scale == 0.0) scale = 1.0;
+    scales[c] = (float)scale;
+    uint32_t sum = 0;
+    for (int p = 0; p < k; p++) {
+      const int8_t qv = (int8_t)std::rint((double)row[p] / scale);
+      sum += (uint32_t)(int32_t)qv;
+      q[(size_t)c * k + p] = qv;
+    }
+    colsum[c] = (int32_t)sum;
+  }
+  return RH_OK;
+}
+
+static int check_pack_shape(const char* who, int k, int n) {
+  char buf[160];
+  if (n < 16 || n % 16 != 0) {
+    snprintf(buf, sizeof buf, "%s needs n%%16==0 and n>=16, got n=%d", who, n);
+    return fail(RH_ERR_SHAPE, buf);
+  }
+  if (k < 1) {
+    snprintf(buf, sizeof buf, "%s needs k>=1, got k=%d", who, k);
+    return fail(RH_ERR_SHAPE, buf);
+  }
+  return RH_OK;
+}
+
+int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
+                int n, rh_weight** out) {
+  static const char* names[] = {"PackB", "PackB8", "PackB8VNNI"};
+  int st = check_pack_shape(names[mode], k, n);
+  if (st != RH_OK) return st;
+  auto* w = new rh_weight();
+  w->ctx = ctx;
+  w->mode = mode;
+  w->k = k;
+  w->n = n;
+  w->kp = (int)round_up(k, kWeightKPad);
+  w->np = (int)round_up(n, kWeightRowPad);
+  std::vector<int8_t> q;
+  std::vector<float> scales;
+  std::vector<int32_t> colsum;
+  size_t elem = mode == RH_MODE_F32 ? 4 : 1;
+  if (mode == RH_MODE_W8) st = quantize_b8(bT, k, n, q, scales);
+  else if (mode == RH_MODE_A8W8) st = quantize_b8_vnni(bT, k, n, q, scales, colsum);
+  if (st != RH_OK) {
+    delete w;
+    return st;
+  }
+  // Padded [np][kp] image, zero outside [n][k].
+  std::vector<uint8_t> img((size_t)w->np * w->kp * elem, 0);
+  for (int j = 0; j < n; j++) {
+    uint8_t* dst = img.data() + (size_t)j * w->kp * elem;
+    if (mode == RH_MODE_F32) memcpy(dst, bT + (size_t)j * k, (size_t)k * 4);
+    else memcpy(dst, q.data() + (size_t)j * k, (size_t)k);
+  }
+  hipError_t e = hipMalloc(&w->d_data, img.size());
+  if (e == hipSuccess) e = hipMemcpy(w->d_data, img.data(), img.size(), hipMemcpyHostToDevice);
+  if (e == hipSuccess && !scales.empty()) {
+    e = hipMalloc(&w->d_scales, n * sizeof(float));
+    if (e == hipSuccess)
+      e = hipMemcpy(w->d_scales, scales.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess && !colsum.empty()) {
+    e = hipMalloc(&w->d_colsum, n * sizeof(int32_t));
+    if (e == hipSuccess)
+      e = hipMemcpy(w->d_colsum, colsum.data(), n * sizeof(int32_t), hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess && bias) {
+    e = hipMalloc(&w->d_bias, n * sizeof(float));
+    if (e == hipSuccess)
+      e = hipMemcpy(w->d_bias, bias, n * sizeof(float), hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) {
+    destroy_weight(w);
+    return hip_fail(e, "weight upload", __FILE__, __LINE__);
+  }
+  *out = w;
+  return RH_OK;
+}
+
+void destroy_weight(rh_weight* w) {
+  if (!w) return;
+  if (w->d_data) (void)hipFree(w->d_data);
+  if (w->d_scales) (void)hipFree(w->d_scales);
+  if (w->d_colsum) (void)hipFree(w->d_colsum);
+  if (w->d_bias) (void)hipFree(w->d_bias);
+  delete w;
+}
+
+// One linear: the GEMM family dispatch of applyDense (bert.go:282-301) with
+// bias/activation fused. For A8W8 the input must already be quantized into
+// qa/rs (row stride ldq) unless `a` is given, in which case it is quantized
+// here first.
+int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
+               float* dst, int ldc, int act, const float* bias, uint8_t* qa,
+               int ldq, float* rs, bool quantize_first, int32_t* acc_out) {
+  if (m <= 0) return RH_OK;
+  hipStream_t s = ctx->stream;
+  const double M = m, K = w->k, N = w->n;
+  const double ops = 2.0 * M * K * N;
+  int slot = -1;
+  hipError_t e = hipSuccess;
+  if (w->mode == RH_MODE_A8W8) {
+    if (quantize_first) {
+      e = launch_quantize_rows_u8(a, lda, m, w->k, qa, ldq, rs, s);
+      if (e != hipSuccess) return hip_fail(e, "quantize_rows_u8", __FILE__, __LINE__);
+    }
+    GemmI8Args g{};
+    g.A = qa;
+    g.lda = ldq;
+    g.B = static_cast<const int8_t*>(w->d_data);
+    g.ldb = w->kp;
+    g.M = m;
+    g.N = w->n;
+    g.K = w->k;
+    g.row_scales = rs;
+    g.col_scales = w->d_scales;
+    g.colsum = w->d_colsum;
+    g.bias = bias;
+    g.C = acc_out ? nullptr : dst;
+    g.Cacc = acc_out;
+    g.ldc = ldc;
+    g.act = act;
+    const double bytes = M * K + K * N + M * N * 4 + 4 * M + 8 * N + (bias ? 4 * N : 0);
+    e = ctx->prof_begin(0, ops, bytes, &slot);
+    if (e == hipSuccess) e = launch_gemm_i8(g, s);
+    if (e == hipSuccess) e = ctx->prof_end(slot);
+  } else {
+    GemmBfArgs g{};
+    g.A = a;
+    g.lda = lda;
+    g.B = w->d_data;
+    g.ldb = w->kp;
+    g.M = m;
+    g.N = w->n;
+    g.K = w->k;
+    g.col_scales = w->mode == RH_MODE_W8 ? w->d_scales : nullptr;
+    g.bias = bias;
+    g.C = dst;
+    g.ldc = ldc;
+    g.act = act;
+    if (w->mode == RH_MODE_W8) {
+      const double bytes = M * K * 4 + K * N + M * N * 4 + 4 * N + (bias ? 4 * N : 0);
+      e = ctx->prof_begin(1, ops, bytes, &slot);
+      if (e == hipSuccess) e = launch_gemm_w8(g, ctx->w8_terms, s);
+    } else {
+      const double bytes = M * K * 4 + K * N * 4 + M * N * 4 + (bias ? 4 * N : 0);
+      e = ctx->prof_begin(2, ops, bytes, &slot);
+      if (e == hipSuccess) e = launch_gemm_f32(g, ctx->f32_algo, s);
+    }
+    if (e == hipSuccess) e = ctx->prof_end(slot);
+  }
+  if (e != hipSuccess) return hip_fail(e, "gemm launch", __FILE__, __LINE__);
+  return RH_OK;
+}
+
+}  // namespace rh
+
+using namespace rh;
+
+// ---- C ABI ---------------------------------------------------------------------
+
+#define CTX_GUARD(ctx)                                               \
+  if (!(ctx)) return fail(RH_ERR_INVALID, "null context");           \
+  std::lock_guard<std::mutex> lk_((ctx)->mu);                         \
+  RH_HIP(hipSetDevice((ctx)->device))
+
+extern "C" {
+
+const char* rh_last_error(void) { return g_err.c_str(); }
+
+int rh_version(void) { return 100; }
+
+int rh_device_count(int* count) {
+  if (!count) return fail(RH_ERR_INVALID, "null count");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    *count = 0;
+    return fail(RH_ERR_NO_DEVICE, "no HIP device available");
+  }
+  *count = n;
+  return RH_OK;
+}
+
+int rh_context_create(int device, rh_context** out) {
+  if (!out) return fail(RH_ERR_INVALID, "null out");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+    return fail(RH_ERR_NO_DEVICE, "no HIP device available");
+  if (device < 0 || device >= n) return fail(RH_ERR_INVALID, "device index out of range");
+  RH_HIP(hipSetDevice(device));
+  auto* c = new rh_context();
+  c->device = device;
+  hipError_t e = hipStreamCreate(&c->stream);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipStreamCreate", __FILE__, __LINE__);
+  }
+  *out = c;
+  return RH_OK;
+}
+
+void rh_context_destroy(rh_context* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  ctx->prof_clear();
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+int rh_context_sync(rh_context* ctx) {
+  CTX_GUARD(ctx);
+  RH_HIP(hipStreamSynchronize(ctx->stream));
+  return RH_OK;
+}
+
+void* rh_context_stream(rh_context* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int rh_context_set_f32_algo(rh_context* ctx, int algo) {
+  if (!ctx) return fail(RH_ERR_INVALID, "null context");
+  if (algo != F32_SPLIT3 && algo != F32_NATIVE) return fail(RH_ERR_INVALID, "unknown fp32 algo");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->f32_algo = algo;
+  return RH_OK;
+}
+
+int rh_malloc(rh_context* ctx, size_t bytes, void** dev) {
+  if (!dev) return fail(RH_ERR_INVALID, "null out");
+  CTX_GUARD(ctx);
+  RH_HIP(hipMalloc(dev, bytes ? bytes : 1));
+  return RH_OK;
+}
+
+int rh_free(rh_context* ctx, void* dev) {
+  CTX_GUARD(ctx);
+  RH_HIP(hipStreamSynchronize(ctx->stream));
+  RH_HIP(hipFree(dev));
+  return RH_OK;
+}
+
+int rh_memcpy_h2d(rh_context* ctx, void* dst, const void* src, size_t bytes) {
+  CTX_GUARD(ctx);
+  RH_HIP(hipStreamSynchronize(ctx->stream));
+  RH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return RH_OK;
+}
+
+int rh_memcpy_d2h(rh_context* ctx, void* dst, const void* src, size_t bytes) {
+  CTX_GUARD(ctx);
+  RH_HIP(hipStreamSynchronize(ctx->stream));
+  RH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return RH_OK;
+}
+
+int rh_profile_enable(rh_context* ctx, int on) {
+  CTX_GUARD(ctx);
+  RH_HIP(hipStreamSynchronize(ctx->stream));
+  ctx->prof_clear();
+  ctx->profiling = on != 0;
+  return RH_OK;
+}
+
+int rh_profile_read(rh_context* ctx, int kind, rh_profile_stat* out) {
+  if (!out) return fail(RH_ERR_INVALID, "null out");
+  CTX_GUARD(ctx);
+  RH_HIP(hipStreamSynchronize(ctx->stream));
+  rh_profile_stat st{};
+  for (auto& r : ctx->recs) {
+    if (r.kind != kind) continue;
+    float ms = 0.0f;
+    RH_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+    st.launches++;
+    st.total_ms += ms;
+    st.total_ops += r.ops;
+    st.total_bytes += r.bytes;
+  }
+  *out = st;
+  return RH_OK;
+}
+
+int rh_pack_weight(rh_context* ctx, int mode, const float* bT, const float* bias,
+                   int k, int n, rh_weight** out) {
+  if (!out || !bT) return fail(RH_ERR_INVALID, "null argument");
+  if (mode < RH_MODE_F32 || mode > RH_MODE_A8W8) return fail(RH_ERR_INVALID, "unknown mode");
+  CTX_GUARD(ctx);
+  return pack_weight(ctx, mode, bT, bias, k, n, out);
+}
+
+void rh_weight_destroy(rh_weight* w) {
+  if (!w) return;
+  std::lock_guard<std::mutex> lk(w->ctx->mu);
+  (void)hipSetDevice(w->ctx->device);
+  (void)hipStreamSynchronize(w->ctx->stream);
+  destroy_weight(w);
+}
+
+int rh_weight_info(const rh_weight* w, int* mode, int* k, int* n) {
+  if (!w) return fail(RH_ERR_INVALID, "null weight");
+  if (mode) *mode = w->mode;
+  if (k) *k = w->k;
+  if (n) *n = w->n;
+  return RH_OK;
+}
+
+int rh_weight_export(const rh_weight* w, int8_t* q, float* scales, int32_t* colsum) {
+  if (!w) return fail(RH_ERR_INVALID, "null weight");
+  Context* ctx = w->ctx;
+  CTX_GUARD(ctx);
+  RH_HIP(hipStreamSynchronize(ctx->stream));
+  if (q) {
+    if (w->mode == RH_MODE_F32) return fail(RH_ERR_INVALID, "fp32 weight has no int8 image");
+    std::vector<int8_t> img((size_t)w->np * w->kp);
+    RH_HIP(hipMemcpy(img.data(), w->d_data, img.size(), hipMemcpyDeviceToHost));
+    for (int j = 0; j < w->n; j++)
+      memcpy(q + (size_t)j * w->k, img.data() + (size_t)j * w->kp, w->k);
+  }
+  if (scales) {
+    if (!w->d_scales) return fail(RH_ERR_INVALID, "weight has no scales");
+    RH_HIP(hipMemcpy(scales, w->d_scales, w->n * sizeof(float), hipMemcpyDeviceToHost));
+  }
+  if (colsum) {
+    if (!w->d_colsum) return fail(RH_ERR_INVALID, "weight has no colsum");
+    RH_HIP(hipMemcpy(colsum, w->d_colsum, w->n * sizeof(int32_t), hipMemcpyDeviceToHost));
+  }
+  return RH_OK;
+}
+
+int rh_quantize_rows_u8(rh_context* ctx, const float* a, int m, int k, uint8_t* qa,
+                        int ldq, float* row_scales) {
+  if (m < 0 || k < 1) return fail(RH_ERR_INVALID, "bad m/k");
+  if (ldq < k || ldq % 16 != 0) return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+  if (m > 0 && (!a || !qa || !row_scales)) return fail(RH_ERR_INVALID, "null argument");
+  CTX_GUARD(ctx);
+  RH_HIP(launch_quantize_rows_u8(a, k, m, k, qa, ldq, row_scales, ctx->stream));
+  return RH_OK;
+}
+
+static int check_gemm(const rh_weight* w, int mode, const float* a, const void* dst, int m) {
+  if (!w) return fail(RH_ERR_INVALID, "null weight");
+  if (mode >= 0 && w->mode != mode) return fail(RH_ERR_INVALID, "weight packed for another mode");
+  if (m < 0) return fail(RH_ERR_INVALID, "negative m");
+  if (m > 0 && (!a || !dst)) return fail(RH_ERR_INVALID, "null argument");
+  return RH_OK;
+}
+
+int rh_matmul_packed(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m) {
+  int st = check_gemm(w, RH_MODE_F32, a, dst, m);
+  if (st) return st;
+  CTX_GUARD(ctx);
+  return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
+                    nullptr, false, nullptr);
+}
+
+int rh_matmul_packed8(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m) {
+  int st = check_gemm(w, RH_MODE_W8, a, dst, m);
+  if (st) return st;
+  CTX_GUARD(ctx);
+  return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
+                    nullptr, false, nullptr);
+}
+
+int rh_matmul_packed_vnni(rh_context* ctx, float* dst, const float* a, const rh_weight* w,
+                          int m, uint8_t* qa, int ldq, float* row_scales) {
+  int st = check_gemm(w, RH_MODE_A8W8, a, dst, m);
+  if (st) return st;
+  if (m > 0 && (!qa || !row_scales)) return fail(RH_ERR_INVALID, "null scratch");
+  if (ldq < w->k || ldq % 16 != 0)
+    return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+  CTX_GUARD(ctx);
+  return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, qa, ldq,
+                    row_scales, true, nullptr);
+}
+
+int rh_gemm_u8s8_i32(rh_context* ctx, int32_t* acc, const uint8_t* qa, int ldq,
+                     const rh_weight* w, int m) {
+  if (!w) return fail(RH_ERR_INVALID, "null weight");
+  if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight packed for another mode");
+  if (m < 0) return fail(RH_ERR_INVALID, "negative m");
+  if (m > 0 && (!acc || !qa)) return fail(RH_ERR_INVALID, "null argument");
+  if (ldq < w->k || ldq % 16 != 0)
+    return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+  CTX_GUARD(ctx);
+  return run_linear(ctx, w, nullptr, 0, m, nullptr, w->n, ACT_NONE, nullptr,
+                    const_cast<uint8_t*>(qa), ldq, nullptr, false, acc);
+}
+
+int rh_linear(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m,
+              int act, uint8_t* qa, int ldq, float* row_scales) {
+  int st = check_gemm(w, -1, a, dst, m);
+  if (st) return st;
+  if (act != RH_ACT_NONE && act != RH_ACT_GELU) return fail(RH_ERR_INVALID, "unknown act");
+  if (w->mode == RH_MODE_A8W8) {
+    if (m > 0 && (!qa || !row_scales)) return fail(RH_ERR_INVALID, "null scratch");
+    if (ldq < w->k || ldq % 16 != 0)
+      return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+  }
+  CTX_GUARD(ctx);
+  return run_linear(ctx, w, a, w->k, m, dst, w->n, act, w->d_bias, qa, ldq, row_scales,
+                    true, nullptr);
+}
+
+int rh_gelu(rh_context* ctx, float* x, size_t n) {
+  if (n > 0 && !x) return fail(RH_ERR_INVALID, "null x");
+  CTX_GUARD(ctx);
+  RH_HIP(launch_gelu(x, n, ctx->stream));
+  return RH_OK;
+}
+
+int rh_layernorm(rh_context* ctx, float* x, const float* gamma, const float* beta, int m,
+                 int n, float eps) {
+  if (m < 0 || n < 1 || n > 2048) return fail(RH_ERR_INVALID, "bad shape (n <= 2048)");
+  if (m > 0 && (!x || !gamma || !beta)) return fail(RH_ERR_INVALID, "null argument");
+  CTX_GUARD(ctx);
+  RH_HIP(launch_layernorm(x, gamma, beta, m, n, eps, ctx->stream));
+  return RH_OK;
+}
+
+}  // extern "C"

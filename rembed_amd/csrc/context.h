@@ -1,0 +1,57 @@
+// context.h — host-side objects behind the C ABI handles.
+#pragma once
+
+#include <mutex>
+#include <vector>
+
+#include "rh_internal.h"
+
+// rh_context: one device, one stream (default priority), a mutex that
+// serializes the calls made on it, GEMM strategy switches, and the optional
+// per-launch event timing used by the benchmark.
+struct rh_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  int f32_algo = rh::F32_SPLIT3;
+  int w8_terms = 2;  // bf16 terms of the fp32 activations in weight-only int8
+
+  struct ProfRec {
+    hipEvent_t a, b;
+    int kind;
+    double ops, bytes;
+  };
+  bool profiling = false;
+  std::vector<ProfRec> recs;
+
+  hipError_t prof_begin(int kind, double ops, double bytes, int* slot);
+  hipError_t prof_end(int slot);
+  void prof_clear();
+};
+
+// rh_weight: a packed dense weight resident in HBM. d_data is [np][kp]
+// (fp32 for RH_MODE_F32, int8 otherwise), zero outside the [n][k] corner.
+struct rh_weight {
+  rh_context* ctx = nullptr;
+  int mode = 0;
+  int k = 0, n = 0, kp = 0, np = 0;
+  void* d_data = nullptr;
+  float* d_scales = nullptr;
+  int32_t* d_colsum = nullptr;
+  float* d_bias = nullptr;
+};
+
+namespace rh {
+using Context = rh_context;
+
+int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
+                int n, rh_weight** out);
+void destroy_weight(rh_weight* w);
+int quantize_b8(const float* bT, int k, int n, std::vector<int8_t>& q,
+                std::vector<float>& scales);
+int quantize_b8_vnni(const float* bT, int k, int n, std::vector<int8_t>& q,
+                     std::vector<float>& scales, std::vector<int32_t>& colsum);
+int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
+               float* dst, int ldc, int act, const float* bias, uint8_t* qa, int ldq,
+               float* rs, bool quantize_first, int32_t* acc_out);
+}  // namespace rh

@@ -1,0 +1,365 @@
+// gemm_bf16.hip — the floating-point GEMMs for gfx950 on bf16 MFMA
+// (v_mfma_f32_32x32x16_bf16, fp32 accumulation), plus a native
+// v_mfma_f32_32x32x2_f32 variant of the fp32 GEMM.
+//
+//  * Weight-only int8 (replaces MatMulPacked8, internal/tensor/pack8.go:80-126
+//    and gemm4x16i8, gemm8_amd64.s:14-79): int8 weight tiles are dequantised
+//    to bf16 (exact: |q| <= 127 needs 7 significant bits) while they are
+//    staged into LDS; the fp32 activations are split into A_TERMS bf16 terms
+//    (hi, lo) so a·q keeps ~16 significant bits of a; the per-channel scale
+//    multiplies the fp32 accumulator in the epilogue, as the reference does.
+//  * fp32 (replaces MatMulPacked, pack.go:123-210 and gemm4x16,
+//    gemm_amd64.s:14-64): both operands split into bf16 hi + lo, three MFMA
+//    products hi·hi + hi·lo + lo·hi (the lo·lo term is below fp32 rounding
+//    of the sum for these magnitudes), or native f32 MFMA.
+//
+// Same tiling scheme as gemm_i8.hip: 256 threads as 2x2 waves, LDS rows of
+// 128 bytes (64 bf16 of k per stage), XOR swizzle, double buffering.
+#include "gemm_common.h"
+
+namespace rh {
+
+__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
+  hi = (__bf16)x;
+  lo = (__bf16)(x - (float)hi);
+}
+
+// Load 8 consecutive fp32 activations of row r starting at column k (zeros
+// past K; vector path when the row stride and base allow 16-byte loads).
+__device__ __forceinline__ void load_a8(const float* A, int lda, int r, int M,
+                                        int k, int K, bool vec, float (&v)[8]) {
+  if (r < M && vec && k + 8 <= K) {
+    const v4f* src = reinterpret_cast<const v4f*>(A + (size_t)r * lda + k);
+    v4f x0 = src[0], x1 = src[1];
+    v[0] = x0[0]; v[1] = x0[1]; v[2] = x0[2]; v[3] = x0[3];
+    v[4] = x1[0]; v[5] = x1[1]; v[6] = x1[2]; v[7] = x1[3];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+      v[e] = (r < M && k + e < K) ? A[(size_t)r * lda + k + e] : 0.0f;
+  }
+}
+
+template <int BM, int BN, int A_TERMS, bool B_INT8>
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec) {
+  constexpr int B_TERMS = B_INT8 ? 1 : 2;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int AP = BM / 32, BP = BN / 32;
+  constexpr int kA = BM * 128, kB = BN * 128;
+  constexpr int kStage = A_TERMS * kA + B_TERMS * kB;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int row0 = (tile / tiles_n) * BM;
+  const int col0 = (tile % tiles_n) * BN;
+
+  const int lrow = tid >> 3, lchunk = tid & 7;
+  const int nk = (p.K + 63) >> 6;
+  const bool vec = a_vec != 0;
+
+  float ra[AP][8];
+  // B staging registers: int8 -> 8 bytes (2 dwords); fp32 -> 8 floats.
+  int rbi[B_INT8 ? BP : 1][2];
+  float rbf[B_INT8 ? 1 : BP][8];
+
+  auto gload = [&](int kt) {
+    const int k = (kt << 6) + (lchunk << 3);
+#pragma unroll
+    for (int i = 0; i < AP; i++)
+      load_a8(p.A, p.lda, row0 + i * 32 + lrow, p.M, k, p.K, vec, ra[i]);
+#pragma unroll
+    for (int i = 0; i < BP; i++) {
+      const int c = col0 + i * 32 + lrow;  // zero-padded rows, in bounds
+      if constexpr (B_INT8) {
+        const int* src = reinterpret_cast<const int*>(
+            static_cast<const int8_t*>(p.B) + (size_t)c * p.ldb + k);
+        rbi[i][0] = src[0];
+        rbi[i][1] = src[1];
+      } else {
+        const v4f* src = reinterpret_cast<const v4f*>(
+            static_cast<const float*>(p.B) + (size_t)c * p.ldb + k);
+        v4f x0 = src[0], x1 = src[1];
+        rbf[i][0] = x0[0]; rbf[i][1] = x0[1]; rbf[i][2] = x0[2]; rbf[i][3] = x0[3];
+        rbf[i][4] = x1[0]; rbf[i][5] = x1[1]; rbf[i][6] = x1[2]; rbf[i][7] = x1[3];
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    uint8_t* s = lds + buf * kStage;
+#pragma unroll
+    for (int i = 0; i < AP; i++) {
+      const int r = i * 32 + lrow;
+      v8bf hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        __bf16 h, l;
+        split_bf16(ra[i][e], h, l);
+        hi[e] = h;
+        lo[e] = l;
+      }
+      *reinterpret_cast<v8bf*>(s + lds_off(r, lchunk)) = hi;
+      if constexpr (A_TERMS == 2)
+        *reinterpret_cast<v8bf*>(s + kA + lds_off(r, lchunk)) = lo;
+    }
+    uint8_t* sb = s + A_TERMS * kA;
+#pragma unroll
+    for (int i = 0; i < BP; i++) {
+      const int r = i * 32 + lrow;
+      if constexpr (B_INT8) {
+        v8bf q;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int byte = (rbi[i][e >> 2] >> (8 * (e & 3))) & 0xff;
+          q[e] = (__bf16)(float)(int)(int8_t)byte;
+        }
+        *reinterpret_cast<v8bf*>(sb + lds_off(r, lchunk)) = q;
+      } else {
+        v8bf hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          __bf16 h, l;
+          split_bf16(rbf[i][e], h, l);
+          hi[e] = h;
+          lo[e] = l;
+        }
+        *reinterpret_cast<v8bf*>(sb + lds_off(r, lchunk)) = hi;
+        *reinterpret_cast<v8bf*>(sb + kB + lds_off(r, lchunk)) = lo;
+      }
+    }
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  const int fr = lane & 31, fg = lane >> 5;
+  for (int kt = 0; kt < nk; kt++) {
+    if (kt + 1 < nk) gload(kt + 1);
+    const uint8_t* s = lds + (kt & 1) * kStage;
+    const uint8_t* sB = s + A_TERMS * kA;
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      const int c = 2 * st + fg;
+      v8bf fah[TM], fal[TM], fbh[TN], fbl[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int r = wm * WM + i * 32 + fr;
+        fah[i] = *reinterpret_cast<const v8bf*>(s + lds_off(r, c));
+        if constexpr (A_TERMS == 2)
+          fal[i] = *reinterpret_cast<const v8bf*>(s + kA + lds_off(r, c));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int r = wn * WN + j * 32 + fr;
+        fbh[j] = *reinterpret_cast<const v8bf*>(sB + lds_off(r, c));
+        if constexpr (!B_INT8)
+          fbl[j] = *reinterpret_cast<const v8bf*>(sB + kB + lds_off(r, c));
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fah[i], fbh[j],
+                                                              acc[i][j], 0, 0, 0);
+          if constexpr (!B_INT8)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                fah[i], fbl[j], acc[i][j], 0, 0, 0);
+          if constexpr (A_TERMS == 2)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                fal[i], fbh[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    if (kt + 1 < nk) lstore((kt + 1) & 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int col = col0 + wn * WN + j * 32 + fr;
+    if (col >= p.N) continue;
+    const float cs = p.col_scales ? p.col_scales[col] : 1.0f;
+    const float b = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const int row = row0 + wm * WM + i * 32 + ii * 8 + fg * 4 + jj;
+          if (row >= p.M) continue;
+          float v = acc[i][j][ii * 4 + jj];
+          if (p.col_scales) v = v * cs;
+          if (p.bias) v = v + b;
+          p.C[(size_t)row * p.ldc + col] = apply_act(v, p.act);
+        }
+  }
+}
+
+// Native fp32: v_mfma_f32_32x32x2_f32. LDS rows hold 32 fp32 of k per stage
+// (8 chunks of 4); lane half g takes chunk 2s+g and feeds its 4 elements to
+// 4 consecutive MFMAs, identically for A and B, so the k pairing agrees.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_f32_native_kernel(GemmBfArgs p,
+                                                              int a_vec) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int AP = BM / 32, BP = BN / 32;
+  constexpr int kStage = (BM + BN) * 128;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int row0 = (tile / tiles_n) * BM;
+  const int col0 = (tile % tiles_n) * BN;
+  const int lrow = tid >> 3, lchunk = tid & 7;
+  const int nk = (p.K + 31) >> 5;
+  const bool vec = a_vec != 0;
+
+  v4f ra[AP], rb[BP];
+  auto gload = [&](int kt) {
+    const int k = (kt << 5) + (lchunk << 2);
+#pragma unroll
+    for (int i = 0; i < AP; i++) {
+      const int r = row0 + i * 32 + lrow;
+      if (r < p.M && vec && k + 4 <= p.K) {
+        ra[i] = *reinterpret_cast<const v4f*>(p.A + (size_t)r * p.lda + k);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          ra[i][e] = (r < p.M && k + e < p.K) ? p.A[(size_t)r * p.lda + k + e] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BP; i++) {
+      const int c = col0 + i * 32 + lrow;
+      rb[i] = *reinterpret_cast<const v4f*>(static_cast<const float*>(p.B) +
+                                            (size_t)c * p.ldb + k);
+    }
+  };
+  auto lstore = [&](int buf) {
+    uint8_t* s = lds + buf * kStage;
+#pragma unroll
+    for (int i = 0; i < AP; i++)
+      *reinterpret_cast<v4f*>(s + lds_off(i * 32 + lrow, lchunk)) = ra[i];
+#pragma unroll
+    for (int i = 0; i < BP; i++)
+      *reinterpret_cast<v4f*>(s + lds_off(BM + i * 32 + lrow, lchunk)) = rb[i];
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int fr = lane & 31, fg = lane >> 5;
+  for (int kt = 0; kt < nk; kt++) {
+    if (kt + 1 < nk) gload(kt + 1);
+    const uint8_t* sA = lds + (kt & 1) * kStage;
+    const uint8_t* sB = sA + BM * 128;
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      const int c = 2 * st + fg;
+      v4f fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        fa[i] = *reinterpret_cast<const v4f*>(sA + lds_off(wm * WM + i * 32 + fr, c));
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+        fb[j] = *reinterpret_cast<const v4f*>(sB + lds_off(wn * WN + j * 32 + fr, c));
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e],
+                                                             acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) lstore((kt + 1) & 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int col = col0 + wn * WN + j * 32 + fr;
+    if (col >= p.N) continue;
+    const float b = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const int row = row0 + wm * WM + i * 32 + ii * 8 + fg * 4 + jj;
+          if (row >= p.M) continue;
+          float v = acc[i][j][ii * 4 + jj];
+          if (p.bias) v = v + b;
+          p.C[(size_t)row * p.ldc + col] = apply_act(v, p.act);
+        }
+  }
+}
+
+static int a_vec_ok(const GemmBfArgs& a) {
+  return (a.lda % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.A) & 15) == 0);
+}
+
+template <int BM, int BN, int AT, bool BI8>
+static hipError_t launch_bf(const GemmBfArgs& a, hipStream_t s) {
+  const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, AT, BI8>), dim3(tiles), dim3(256),
+                     0, s, a, a_vec_ok(a));
+  return hipGetLastError();
+}
+
+// Prefer the larger tile when it still fills the 256 CUs.
+static bool big_tile(const GemmBfArgs& a, int bm, int bn) {
+  return ceil_div(a.M, bm) * ceil_div(a.N, bn) >= 256;
+}
+
+hipError_t launch_gemm_w8(const GemmBfArgs& a, int a_terms, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a_terms == 1) {
+    if (big_tile(a, 256, 256)) return launch_bf<256, 256, 1, true>(a, s);
+    return launch_bf<128, 128, 1, true>(a, s);
+  }
+  if (big_tile(a, 256, 128)) return launch_bf<256, 128, 2, true>(a, s);
+  return launch_bf<128, 128, 2, true>(a, s);
+}
+
+hipError_t launch_gemm_f32(const GemmBfArgs& a, int algo, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (algo == F32_NATIVE) {
+    const int tiles = ceil_div(a.M, 128) * ceil_div(a.N, 128);
+    hipLaunchKernelGGL((gemm_f32_native_kernel<128, 128>), dim3(tiles), dim3(256),
+                       0, s, a, a_vec_ok(a));
+    return hipGetLastError();
+  }
+  return launch_bf<128, 128, 2, false>(a, s);
+}
+
+}  // namespace rh

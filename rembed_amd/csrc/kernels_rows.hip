@@ -1,0 +1,282 @@
+// kernels_rows.hip — row-wise kernels that keep activations in HBM between
+// the GEMMs: activation quantization, embeddings + LayerNorm, residual add +
+// LayerNorm (each optionally fused with the next GEMM's u8 quantization),
+// pooling + L2 normalization, and the standalone GELU / bias passes.
+//
+// One 64-lane wave owns one row; lane l holds columns l, l+64, l+128, ...
+#include "gemm_common.h"
+
+namespace rh {
+
+constexpr int kRowsPerBlock = 4;  // 256 threads = 4 waves = 4 rows
+constexpr int kMaxPerLane = 32;   // rows up to 2048 wide stay in registers
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// QuantizeRowU8 (internal/tensor/pack_vnni.go:85-117) for one row already
+// held by the wave: absmax, s = absmax/127 (1 if 0), inv = 1/s (IEEE float32
+// divisions), q = clamp(rint(v*inv) + 128, 0, 255). rint is round-half-even
+// as math.RoundToEven on the exactly-widened float32 product.
+__device__ __forceinline__ uint8_t quant_u8(float v, float inv) {
+  int q = (int)rintf(v * inv) + 128;
+  q = q < 0 ? 0 : (q > 255 ? 255 : q);
+  return (uint8_t)q;
+}
+
+// Generic quantizer over rows of any width (two passes over the row; the
+// second pass hits L2). Writes ldq bytes per row: k quantized + zero tail.
+__global__ __launch_bounds__(256) void quantize_rows_kernel(
+    const float* __restrict__ a, int lda, int m, int k, uint8_t* __restrict__ qa,
+    int ldq, float* __restrict__ row_scales, int vec) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= m) return;
+  const float* src = a + (size_t)row * lda;
+  float mx = 0.0f;
+  for (int i = lane; i < k; i += 64) mx = fmaxf(mx, fabsf(src[i]));
+  mx = wave_max(mx);
+  float scale = mx / 127.0f;
+  if (scale == 0.0f) scale = 1.0f;
+  const float inv = 1.0f / scale;
+  uint8_t* dst = qa + (size_t)row * ldq;
+  if (vec) {
+    for (int i = lane * 4; i < k; i += 256) {
+      v4f v = *reinterpret_cast<const v4f*>(src + i);
+      uint32_t w = (uint32_t)quant_u8(v[0], inv) | ((uint32_t)quant_u8(v[1], inv) << 8) |
+                   ((uint32_t)quant_u8(v[2], inv) << 16) |
+                   ((uint32_t)quant_u8(v[3], inv) << 24);
+      *reinterpret_cast<uint32_t*>(dst + i) = w;
+    }
+  } else {
+    for (int i = lane; i < k; i += 64) dst[i] = quant_u8(src[i], inv);
+  }
+  for (int i = k + lane; i < ldq; i += 64) dst[i] = 0;
+  if (lane == 0) row_scales[row] = scale;
+}
+
+hipError_t launch_quantize_rows_u8(const float* a, int lda, int m, int k,
+                                   uint8_t* qa, int ldq, float* row_scales,
+                                   hipStream_t s) {
+  if (m <= 0) return hipSuccess;
+  // 16-byte row loads and 4-byte stores need aligned rows.
+  const int vec = (k % 4 == 0) && (lda % 4 == 0) && (ldq % 4 == 0) &&
+                  ((reinterpret_cast<uintptr_t>(a) & 15) == 0) &&
+                  ((reinterpret_cast<uintptr_t>(qa) & 3) == 0);
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3(ceil_div(m, kRowsPerBlock)),
+                     dim3(256), 0, s, a, lda, m, k, qa, ldq, row_scales, vec);
+  return hipGetLastError();
+}
+
+// LayerNorm of the row held in v[] (tensor.go:433-452: biased variance,
+// inv = 1/float32(sqrt(var+eps)), out = (v-mean)*inv*g + b), then optional
+// quantization of the normalized row into qa/row_scales.
+__device__ __forceinline__ void ln_row_finish(float (&v)[kMaxPerLane], int lane,
+                                              int H, const float* gamma,
+                                              const float* beta, float eps,
+                                              float* out, uint8_t* qa, int ldq,
+                                              float* rs_out) {
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kMaxPerLane; e++)
+    if (lane + 64 * e < H) s += v[e];
+  const float mean = wave_sum(s) / (float)H;
+  float s2 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kMaxPerLane; e++)
+    if (lane + 64 * e < H) {
+      const float d = v[e] - mean;
+      s2 += d * d;
+    }
+  const float var = wave_sum(s2) / (float)H;
+  const float inv = 1.0f / sqrtf(var + eps);
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kMaxPerLane; e++) {
+    const int j = lane + 64 * e;
+    if (j < H) {
+      const float y = (v[e] - mean) * inv * gamma[j] + beta[j];
+      v[e] = y;
+      out[j] = y;
+      mx = fmaxf(mx, fabsf(y));
+    }
+  }
+  if (qa) {
+    mx = wave_max(mx);
+    float scale = mx / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    const float qinv = 1.0f / scale;
+#pragma unroll
+    for (int e = 0; e < kMaxPerLane; e++) {
+      const int j = lane + 64 * e;
+      if (j < H) qa[j] = quant_u8(v[e], qinv);
+    }
+    for (int j = H + lane; j < ldq; j += 64) qa[j] = 0;
+    if (lane == 0) *rs_out = scale;
+  }
+}
+
+__global__ __launch_bounds__(256) void embed_ln_kernel(EmbedArgs p, int total) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= total) return;
+  // text b with cu[b] <= row < cu[b+1]
+  int lo = 0, hi = p.batch;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (p.cu[mid] <= row) lo = mid;
+    else hi = mid;
+  }
+  const int b = lo, t = row - p.cu[b];
+  int id = p.ids[(size_t)b * p.stride + t];
+  if (id < 0 || id >= p.vocab) {
+    if (lane == 0) *p.err_flag = 1;
+    id = id < 0 ? 0 : p.vocab - 1;  // stay in bounds; the call reports failure
+  }
+  const float* w = p.word + (size_t)id * p.H;
+  const float* ps = p.pos + (size_t)(t + p.pos_off) * p.H;
+  float v[kMaxPerLane];
+#pragma unroll
+  for (int e = 0; e < kMaxPerLane; e++) {
+    const int j = lane + 64 * e;
+    // bert.go:801-812: row = w + p (+ t)
+    if (j < p.H) v[e] = p.type0 ? (w[j] + ps[j]) + p.type0[j] : w[j] + ps[j];
+    else v[e] = 0.0f;
+  }
+  ln_row_finish(v, lane, p.H, p.gamma, p.beta, p.eps, p.x + (size_t)row * p.H,
+                p.qa ? p.qa + (size_t)row * p.ldq : nullptr, p.ldq,
+                p.row_scales ? p.row_scales + row : nullptr);
+}
+
+hipError_t launch_embed_layernorm(const EmbedArgs& a, int total, hipStream_t s) {
+  if (total <= 0) return hipSuccess;
+  if (a.H > 64 * kMaxPerLane) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(embed_ln_kernel, dim3(ceil_div(total, kRowsPerBlock)),
+                     dim3(256), 0, s, a, total);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void add_ln_kernel(
+    float* __restrict__ x, const float* __restrict__ y, int ldy,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int m,
+    int H, float eps, uint8_t* __restrict__ qa, int ldq,
+    float* __restrict__ row_scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= m) return;
+  float* xr = x + (size_t)row * H;
+  const float* yr = y ? y + (size_t)row * ldy : nullptr;
+  float v[kMaxPerLane];
+#pragma unroll
+  for (int e = 0; e < kMaxPerLane; e++) {
+    const int j = lane + 64 * e;
+    v[e] = j < H ? (yr ? xr[j] + yr[j] : xr[j]) : 0.0f;  // Add, tensor.go:383-387
+  }
+  ln_row_finish(v, lane, H, gamma, beta, eps, xr,
+                qa ? qa + (size_t)row * ldq : nullptr, ldq,
+                row_scales ? row_scales + row : nullptr);
+}
+
+hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
+                                const float* gamma, const float* beta, int m,
+                                int H, float eps, uint8_t* qa, int ldq,
+                                float* row_scales, hipStream_t s) {
+  if (m <= 0) return hipSuccess;
+  if (H > 64 * kMaxPerLane) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(add_ln_kernel, dim3(ceil_div(m, kRowsPerBlock)), dim3(256),
+                     0, s, x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_layernorm(float* x, const float* gamma, const float* beta,
+                            int m, int H, float eps, hipStream_t s) {
+  return launch_add_layernorm(x, nullptr, 0, gamma, beta, m, H, eps, nullptr, 0,
+                              nullptr, s);
+}
+
+// Pooling per text (bert.go:669-703) + L2Normalize (tensor.go:542-554).
+// Mean pooling sums each column over the text's rows in ascending order —
+// the reference's poolMean order — then multiplies by 1/float32(len).
+__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x,
+                                                   int H,
+                                                   const int32_t* __restrict__ cu,
+                                                   int pooling, int normalize,
+                                                   float* __restrict__ out) {
+  __shared__ double red[256];
+  const int b = blockIdx.x;
+  const int r0 = cu[b], len = cu[b + 1] - cu[b];
+  float* o = out + (size_t)b * H;
+  double ss = 0.0;
+  for (int j = threadIdx.x; j < H; j += 256) {
+    float v;
+    if (pooling == RH_POOL_CLS) {
+      v = x[(size_t)r0 * H + j];
+    } else if (pooling == RH_POOL_LAST) {
+      v = x[(size_t)(r0 + len - 1) * H + j];
+    } else {
+      float s = 0.0f;
+      for (int i = 0; i < len; i++) s += x[(size_t)(r0 + i) * H + j];
+      v = s * (1.0f / (float)len);
+    }
+    o[j] = v;
+    ss += (double)v * (double)v;
+  }
+  if (!normalize) return;
+  red[threadIdx.x] = ss;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  const double sum = red[0];
+  if (sum == 0.0) return;
+  const float inv = (float)(1.0 / sqrt(sum));
+  for (int j = threadIdx.x; j < H; j += 256) o[j] = o[j] * inv;
+}
+
+hipError_t launch_pool(const float* x, int H, const int32_t* cu, int batch,
+                       int pooling, int normalize, float* out, hipStream_t s) {
+  if (batch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(pool_kernel, dim3(batch), dim3(256), 0, s, x, H, cu, pooling,
+                     normalize, out);
+  return hipGetLastError();
+}
+
+__global__ void gelu_kernel(float* x, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = gelu_ref(x[i]);
+}
+
+hipError_t launch_gelu(float* x, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(gelu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     s, x, n);
+  return hipGetLastError();
+}
+
+__global__ void add_bias_kernel(float* x, const float* bias, int m, int n,
+                                int ldx) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)m * n) return;
+  const int r = (int)(i / n), c = (int)(i % n);
+  x[(size_t)r * ldx + c] += bias[c];
+}
+
+hipError_t launch_add_bias(float* x, const float* bias, int m, int n, int ldx,
+                           hipStream_t s) {
+  const size_t tot = (size_t)m * n;
+  if (tot == 0) return hipSuccess;
+  hipLaunchKernelGGL(add_bias_kernel, dim3((unsigned)((tot + 255) / 256)),
+                     dim3(256), 0, s, x, bias, m, n, ldx);
+  return hipGetLastError();
+}
+
+}  // namespace rh

@@ -1,0 +1,597 @@
+// model.cpp — the device-resident encoder behind rh_model_*: the mirror of
+// model.Load (internal/model/bert.go:307-524), encodeWorkers
+// (bert.go:740-923), Forward/ForwardTokens (bert.go:649-731) and Embed's
+// batch loop (rembed.go:287-411).
+//
+// Where the reference runs one unpadded forward per text, this runtime packs
+// the batch's texts back to back into M = sum(len) rows: every linear is
+// one GEMM over all texts, attention and pooling walk each text's own rows
+// (cu offsets), so no pad token is ever computed or attended and each
+// text's result equals its unpadded forward.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "context.h"
+
+using namespace rh;
+
+namespace {
+
+struct HostTensor {
+  std::vector<int64_t> shape;
+  std::vector<float> data;
+};
+
+struct Layer {
+  rh_weight* qkv = nullptr;  // fused [3H][H] (bert.go:479-485)
+  rh_weight* o = nullptr;
+  rh_weight* f1 = nullptr;
+  rh_weight* f2 = nullptr;
+  float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
+};
+
+template <class T>
+hipError_t dalloc(T** p, size_t count) {
+  return hipMalloc((void**)p, count * sizeof(T) + 16);
+}
+
+}  // namespace
+
+struct rh_model {
+  rh_context* ctx = nullptr;
+  rh_model_config cfg{};
+  int quant = 0;
+  bool finalized = false;
+  std::map<std::string, HostTensor> pending;
+  std::mutex mu;
+
+  float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_g = nullptr,
+        *emb_b = nullptr;
+  std::vector<Layer> layers;
+  int attn_precision = 3;
+
+  // workspace, sized for cap rows / cap_batch texts
+  int cap = 0, cap_batch = 0, cap_ids = 0;
+  float *x = nullptr, *qkv = nullptr, *ctxb = nullptr, *y = nullptr, *hid = nullptr;
+  uint8_t* qa = nullptr;
+  float* rs = nullptr;
+  int32_t* cu_d = nullptr;
+  int32_t* ids_d = nullptr;
+  float* out_d = nullptr;
+  int* err_d = nullptr;
+  int32_t* cu_pinned = nullptr;
+  hipEvent_t cu_evt = nullptr;
+  int cu_pinned_cap = 0;
+
+  ~rh_model() { release(); }
+
+  void release_ws() {
+    for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
+                    (void*)rs, (void*)cu_d, (void*)ids_d, (void*)out_d})
+      if (p) (void)hipFree(p);
+    x = qkv = ctxb = y = hid = rs = out_d = nullptr;
+    qa = nullptr;
+    cu_d = ids_d = nullptr;
+    cap = cap_batch = cap_ids = 0;
+  }
+  void release() {
+    if (ctx) {
+      (void)hipSetDevice(ctx->device);
+      (void)hipStreamSynchronize(ctx->stream);
+    }
+    release_ws();
+    for (auto& L : layers) {
+      destroy_weight(L.qkv);
+      destroy_weight(L.o);
+      destroy_weight(L.f1);
+      destroy_weight(L.f2);
+      for (float* p : {L.ln1_g, L.ln1_b, L.ln2_g, L.ln2_b})
+        if (p) (void)hipFree(p);
+    }
+    layers.clear();
+    for (float* p : {word, pos, type0, emb_g, emb_b})
+      if (p) (void)hipFree(p);
+    word = pos = type0 = emb_g = emb_b = nullptr;
+    if (err_d) (void)hipFree(err_d);
+    err_d = nullptr;
+    if (cu_pinned) (void)hipHostFree(cu_pinned);
+    cu_pinned = nullptr;
+    if (cu_evt) (void)hipEventDestroy(cu_evt);
+    cu_evt = nullptr;
+  }
+
+  int H() const { return cfg.hidden; }
+  int I() const { return cfg.intermediate; }
+  int ldq_for(int k) const { return (int)round_up(k, 16); }
+  float eps() const { return cfg.layer_norm_eps == 0.0f ? 1e-12f : cfg.layer_norm_eps; }
+  int max_seq() const { return cfg.max_position - cfg.position_offset; }
+
+  int ensure_ws(int rows, int batch, int ids_elems) {
+    const int H = this->H(), I = this->I();
+    if (rows > cap || batch > cap_batch || ids_elems > cap_ids)
+      RH_HIP(hipStreamSynchronize(ctx->stream));  // buffers may be in flight
+    if (rows > cap) {
+      int newcap = (int)round_up(rows, 256);
+      for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
+                      (void*)rs})
+        if (p) RH_HIP(hipFree(p));
+      x = qkv = ctxb = y = hid = rs = nullptr;
+      qa = nullptr;
+      const size_t r = newcap;
+      RH_HIP(dalloc(&x, r * H));
+      RH_HIP(dalloc(&qkv, r * 3 * H));
+      RH_HIP(dalloc(&ctxb, r * H));
+      RH_HIP(dalloc(&y, r * H));
+      RH_HIP(dalloc(&hid, r * I));
+      RH_HIP(dalloc(&qa, r * round_up(std::max(H, I), 16)));
+      RH_HIP(dalloc(&rs, r));
+      cap = newcap;
+    }
+    if (batch > cap_batch) {
+      if (cu_d) RH_HIP(hipFree(cu_d));
+      if (out_d) RH_HIP(hipFree(out_d));
+      cu_d = nullptr;
+      out_d = nullptr;
+      const int nb = (int)round_up(batch, 64);
+      RH_HIP(dalloc(&cu_d, nb + 1));
+      RH_HIP(dalloc(&out_d, (size_t)nb * H));
+      cap_batch = nb;
+    }
+    if (ids_elems > cap_ids) {
+      if (ids_d) RH_HIP(hipFree(ids_d));
+      ids_d = nullptr;
+      const int n = (int)round_up(ids_elems, 4096);
+      RH_HIP(dalloc(&ids_d, n));
+      cap_ids = n;
+    }
+    if (batch + 1 > cu_pinned_cap) {
+      if (cu_pinned) {
+        if (cu_evt) RH_HIP(hipEventSynchronize(cu_evt));
+        RH_HIP(hipHostFree(cu_pinned));
+      }
+      cu_pinned = nullptr;
+      const int n = (int)round_up(batch + 1, 256);
+      RH_HIP(hipHostMalloc((void**)&cu_pinned, n * sizeof(int32_t)));
+      cu_pinned_cap = n;
+    }
+    if (!cu_evt) RH_HIP(hipEventCreateWithFlags(&cu_evt, hipEventDisableTiming));
+    if (!err_d) {
+      RH_HIP(dalloc(&err_d, 1));
+      RH_HIP(hipMemset(err_d, 0, sizeof(int)));
+    }
+    return RH_OK;
+  }
+
+  // Validate lengths (bert.go:741-747) and build packed row offsets.
+  int plan(const int32_t* lens, int batch, std::vector<int32_t>& cu, int* max_len) {
+    cu.assign(batch + 1, 0);
+    int mx = 0;
+    for (int b = 0; b < batch; b++) {
+      char buf[160];
+      if (lens[b] <= 0) {
+        snprintf(buf, sizeof buf, "text %d: empty token sequence", b);
+        return fail(RH_ERR_SEQ, buf);
+      }
+      if (lens[b] > max_seq()) {
+        snprintf(buf, sizeof buf,
+                 "text %d: sequence length %d exceeds the model's maximum %d", b,
+                 lens[b], max_seq());
+        return fail(RH_ERR_SEQ, buf);
+      }
+      cu[b + 1] = cu[b] + lens[b];
+      mx = std::max(mx, (int)lens[b]);
+    }
+    *max_len = mx;
+    return RH_OK;
+  }
+
+  // The forward over rows already planned; ids_dev is [batch][stride].
+  int forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
+              int max_len, bool pool, float* out_dev);
+};
+
+static bool needs_q(const rh_weight* w) { return w->mode == RH_MODE_A8W8; }
+
+int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
+                      int max_len, bool pool, float* out_dev) {
+  hipStream_t s = ctx->stream;
+  const int batch = (int)cu.size() - 1;
+  const int M = cu[batch];
+  const int H = this->H(), I = this->I();
+  const int heads = cfg.heads, dh = H / heads;
+  int st = ensure_ws(M, batch, 0);
+  if (st) return st;
+  // Row offsets: reuse the pinned buffer once its previous copy finished.
+  RH_HIP(hipEventSynchronize(cu_evt));
+  memcpy(cu_pinned, cu.data(), (batch + 1) * sizeof(int32_t));
+  RH_HIP(hipMemcpyAsync(cu_d, cu_pinned, (batch + 1) * sizeof(int32_t),
+                        hipMemcpyHostToDevice, s));
+  RH_HIP(hipEventRecord(cu_evt, s));
+
+  // Embeddings + LayerNorm (+ u8 quantization when the first QKV is int8).
+  const bool q0 = !layers.empty() && needs_q(layers[0].qkv);
+  EmbedArgs ea{};
+  ea.ids = ids_dev;
+  ea.stride = stride;
+  ea.cu = cu_d;
+  ea.batch = batch;
+  ea.word = word;
+  ea.pos = pos;
+  ea.type0 = type0;
+  ea.gamma = emb_g;
+  ea.beta = emb_b;
+  ea.H = H;
+  ea.vocab = cfg.vocab;
+  ea.pos_off = cfg.position_offset;
+  ea.eps = eps();
+  ea.x = x;
+  ea.qa = q0 ? qa : nullptr;
+  ea.ldq = ldq_for(H);
+  ea.row_scales = q0 ? rs : nullptr;
+  ea.err_flag = err_d;
+  RH_HIP(launch_embed_layernorm(ea, M, s));
+
+  double attn_ops = 0;
+  for (int b = 0; b < batch; b++) {
+    const double L = cu[b + 1] - cu[b];
+    attn_ops += 4.0 * L * L * dh * heads;
+  }
+
+  for (size_t li = 0; li < layers.size(); li++) {
+    const Layer& L = layers[li];
+    // x already quantized into qa/rs if the QKV weight is int8-activation.
+    st = run_linear(ctx, L.qkv, x, H, M, qkv, 3 * H, ACT_NONE, L.qkv->d_bias, qa,
+                    ldq_for(H), rs, false, nullptr);
+    if (st) return st;
+    AttnArgs aa{};
+    aa.qkv = qkv;
+    aa.ldqkv = 3 * H;
+    aa.q_off = 0;
+    aa.k_off = H;
+    aa.v_off = 2 * H;
+    aa.cu = cu_d;
+    aa.batch = batch;
+    aa.max_len = max_len;
+    aa.heads = heads;
+    aa.kv_heads = heads;
+    aa.dh = dh;
+    aa.scale = (float)(1.0 / std::sqrt((double)dh));
+    aa.ctx = ctxb;
+    aa.ldctx = H;
+    int slot = -1;
+    RH_HIP(ctx->prof_begin(3, attn_ops, 0.0, &slot));
+    RH_HIP(launch_attention(aa, attn_precision, s));
+    RH_HIP(ctx->prof_end(slot));
+    st = run_linear(ctx, L.o, ctxb, H, M, y, H, ACT_NONE, L.o->d_bias, qa, ldq_for(H),
+                    rs, needs_q(L.o), nullptr);
+    if (st) return st;
+    const bool qf1 = needs_q(L.f1);
+    RH_HIP(launch_add_layernorm(x, y, H, L.ln1_g, L.ln1_b, M, H, eps(),
+                                qf1 ? qa : nullptr, ldq_for(H), qf1 ? rs : nullptr, s));
+    st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_GELU, L.f1->d_bias, qa, ldq_for(H),
+                    rs, false, nullptr);
+    if (st) return st;
+    st = run_linear(ctx, L.f2, hid, I, M, y, H, ACT_NONE, L.f2->d_bias, qa, ldq_for(I),
+                    rs, needs_q(L.f2), nullptr);
+    if (st) return st;
+    const bool qn = li + 1 < layers.size() && needs_q(layers[li + 1].qkv);
+    RH_HIP(launch_add_layernorm(x, y, H, L.ln2_g, L.ln2_b, M, H, eps(),
+                                qn ? qa : nullptr, ldq_for(H), qn ? rs : nullptr, s));
+  }
+  if (pool) {
+    RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
+  }
+  return RH_OK;
+}
+
+// ---- tensor bookkeeping ----------------------------------------------------------
+
+static const char* kPrefixes[] = {"", "bert.", "roberta.", "distilbert."};
+
+static int find_tensor(rh_model* m, const std::string& prefix, const std::string& name,
+                       std::initializer_list<int64_t> shape, const HostTensor** out) {
+  auto it = m->pending.find(prefix + name);
+  char buf[256];
+  if (it == m->pending.end()) {
+    snprintf(buf, sizeof buf, "missing tensor \"%s\"", (prefix + name).c_str());
+    return fail(RH_ERR_MISSING, buf);
+  }
+  const HostTensor& t = it->second;
+  bool ok = t.shape.size() == shape.size();
+  size_t i = 0;
+  for (int64_t d : shape) {
+    if (!ok) break;
+    if (d >= 0 && t.shape[i] != d) ok = false;
+    i++;
+  }
+  if (!ok) {
+    snprintf(buf, sizeof buf, "tensor \"%s\" has the wrong shape", (prefix + name).c_str());
+    return fail(RH_ERR_MISSING, buf);
+  }
+  *out = &t;
+  return RH_OK;
+}
+
+static int upload(const float* src, size_t n, float** dst) {
+  RH_HIP(hipMalloc((void**)dst, n * sizeof(float)));
+  RH_HIP(hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice));
+  return RH_OK;
+}
+
+// newDense (bert.go:263-278): requested mode, then the fallback chain
+// A8W8 -> W8 -> F32 on a pack error.
+static int new_dense(rh_model* m, const float* raw, const float* bias, int in, int out,
+                     rh_weight** w) {
+  if (m->quant == RH_QUANT_FULL &&
+      pack_weight(m->ctx, RH_MODE_A8W8, raw, bias, in, out, w) == RH_OK)
+    return RH_OK;
+  if (m->quant >= RH_QUANT_WEIGHTS &&
+      pack_weight(m->ctx, RH_MODE_W8, raw, bias, in, out, w) == RH_OK)
+    return RH_OK;
+  return pack_weight(m->ctx, RH_MODE_F32, raw, bias, in, out, w);
+}
+
+static int finalize_bert(rh_model* m) {
+  const int H = m->cfg.hidden, I = m->cfg.intermediate;
+  std::string prefix;
+  for (const char* p : kPrefixes)
+    if (m->pending.count(std::string(p) + "embeddings.word_embeddings.weight")) prefix = p;
+  const HostTensor *we, *pe, *tt, *eg, *eb;
+  int st;
+  if ((st = find_tensor(m, prefix, "embeddings.word_embeddings.weight", {m->cfg.vocab, H}, &we)))
+    return st;
+  if ((st = find_tensor(m, prefix, "embeddings.position_embeddings.weight",
+                        {m->cfg.max_position, H}, &pe)))
+    return st;
+  if ((st = find_tensor(m, prefix, "embeddings.token_type_embeddings.weight", {-1, H}, &tt)))
+    return st;
+  if (tt->shape[0] < 1) return fail(RH_ERR_MISSING, "token_type_embeddings has no rows");
+  if ((st = find_tensor(m, prefix, "embeddings.LayerNorm.weight", {H}, &eg))) return st;
+  if ((st = find_tensor(m, prefix, "embeddings.LayerNorm.bias", {H}, &eb))) return st;
+  if ((st = upload(we->data.data(), we->data.size(), &m->word))) return st;
+  if ((st = upload(pe->data.data(), pe->data.size(), &m->pos))) return st;
+  if ((st = upload(tt->data.data(), H, &m->type0))) return st;
+  if ((st = upload(eg->data.data(), H, &m->emb_g))) return st;
+  if ((st = upload(eb->data.data(), H, &m->emb_b))) return st;
+
+  m->layers.resize(m->cfg.layers);
+  for (int l = 0; l < m->cfg.layers; l++) {
+    char p[64];
+    snprintf(p, sizeof p, "encoder.layer.%d.", l);
+    const std::string lp = p;
+    const HostTensor *qw, *qb, *kw, *kb, *vw, *vb, *ow, *ob, *g1, *b1, *f1w, *f1b, *f2w,
+        *f2b, *g2, *b2;
+    struct Need {
+      const char* name;
+      std::initializer_list<int64_t> shape;
+      const HostTensor** dst;
+    };
+    const Need needs[] = {
+        {"attention.self.query.weight", {H, H}, &qw},
+        {"attention.self.query.bias", {H}, &qb},
+        {"attention.self.key.weight", {H, H}, &kw},
+        {"attention.self.key.bias", {H}, &kb},
+        {"attention.self.value.weight", {H, H}, &vw},
+        {"attention.self.value.bias", {H}, &vb},
+        {"attention.output.dense.weight", {H, H}, &ow},
+        {"attention.output.dense.bias", {H}, &ob},
+        {"attention.output.LayerNorm.weight", {H}, &g1},
+        {"attention.output.LayerNorm.bias", {H}, &b1},
+        {"intermediate.dense.weight", {I, H}, &f1w},
+        {"intermediate.dense.bias", {I}, &f1b},
+        {"output.dense.weight", {H, I}, &f2w},
+        {"output.dense.bias", {H}, &f2b},
+        {"output.LayerNorm.weight", {H}, &g2},
+        {"output.LayerNorm.bias", {H}, &b2},
+    };
+    for (const Need& n : needs)
+      if ((st = find_tensor(m, prefix, lp + n.name, n.shape, n.dst))) return st;
+    // Fuse Q|K|V rows into [3H][H] and the biases into [3H] (bert.go:479-485).
+    std::vector<float> qkvw((size_t)3 * H * H), qkvb((size_t)3 * H);
+    memcpy(qkvw.data(), qw->data.data(), sizeof(float) * H * H);
+    memcpy(qkvw.data() + (size_t)H * H, kw->data.data(), sizeof(float) * H * H);
+    memcpy(qkvw.data() + (size_t)2 * H * H, vw->data.data(), sizeof(float) * H * H);
+    memcpy(qkvb.data(), qb->data.data(), sizeof(float) * H);
+    memcpy(qkvb.data() + H, kb->data.data(), sizeof(float) * H);
+    memcpy(qkvb.data() + 2 * H, vb->data.data(), sizeof(float) * H);
+    Layer& L = m->layers[l];
+    if ((st = new_dense(m, qkvw.data(), qkvb.data(), H, 3 * H, &L.qkv))) return st;
+    if ((st = new_dense(m, ow->data.data(), ob->data.data(), H, H, &L.o))) return st;
+    if ((st = new_dense(m, f1w->data.data(), f1b->data.data(), H, I, &L.f1))) return st;
+    if ((st = new_dense(m, f2w->data.data(), f2b->data.data(), I, H, &L.f2))) return st;
+    if ((st = upload(g1->data.data(), H, &L.ln1_g))) return st;
+    if ((st = upload(b1->data.data(), H, &L.ln1_b))) return st;
+    if ((st = upload(g2->data.data(), H, &L.ln2_g))) return st;
+    if ((st = upload(b2->data.data(), H, &L.ln2_b))) return st;
+  }
+  return RH_OK;
+}
+
+// ---- C ABI ------------------------------------------------------------------------
+
+#define MODEL_GUARD(m)                                                   \
+  if (!(m)) return fail(RH_ERR_INVALID, "null model");                  \
+  std::lock_guard<std::mutex> mlk_((m)->mu);                            \
+  std::lock_guard<std::mutex> clk_((m)->ctx->mu);                       \
+  RH_HIP(hipSetDevice((m)->ctx->device))
+
+extern "C" {
+
+int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_model** out) {
+  if (!ctx || !cfg || !out) return fail(RH_ERR_INVALID, "null argument");
+  if (cfg->arch != RH_ARCH_BERT) return fail(RH_ERR_INVALID, "unsupported arch");
+  if (cfg->hidden <= 0 || cfg->heads <= 0 || cfg->hidden % cfg->heads != 0)
+    return fail(RH_ERR_INVALID, "hidden_size not divisible by num_attention_heads");
+  const int dh = cfg->hidden / cfg->heads;
+  if (dh != 32 && dh != 64 && dh != 128) return fail(RH_ERR_INVALID, "head dim must be 32, 64 or 128");
+  if (cfg->hidden % 64 != 0 || cfg->hidden > 2048)
+    return fail(RH_ERR_INVALID, "hidden must be a multiple of 64 and <= 2048");
+  if (cfg->intermediate <= 0 || cfg->layers <= 0 || cfg->vocab <= 0 || cfg->max_position <= 0)
+    return fail(RH_ERR_INVALID, "bad config sizes");
+  if (quant < RH_QUANT_NONE || quant > RH_QUANT_FULL) return fail(RH_ERR_INVALID, "bad quant");
+  auto* m = new rh_model();
+  m->ctx = ctx;
+  m->cfg = *cfg;
+  m->quant = quant;
+  m->attn_precision = quant == RH_QUANT_NONE ? 3 : 1;
+  *out = m;
+  return RH_OK;
+}
+
+int rh_model_set_option(rh_model* m, int option, int value) {
+  if (!m) return fail(RH_ERR_INVALID, "null model");
+  std::lock_guard<std::mutex> lk(m->mu);
+  if (option == RH_OPT_ATTN_PRECISION) {
+    if (value != 1 && value != 3) return fail(RH_ERR_INVALID, "attn precision must be 1 or 3");
+    m->attn_precision = value;
+    return RH_OK;
+  }
+  return fail(RH_ERR_INVALID, "unknown option");
+}
+
+int rh_model_set_tensor(rh_model* m, const char* name, const float* host,
+                        const int64_t* shape, int ndim) {
+  if (!m || !name || !host || (ndim > 0 && !shape) || ndim < 0 || ndim > 4)
+    return fail(RH_ERR_INVALID, "bad argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  if (m->finalized) return fail(RH_ERR_INVALID, "model already finalized");
+  HostTensor t;
+  size_t n = 1;
+  for (int i = 0; i < ndim; i++) {
+    if (shape[i] < 0) return fail(RH_ERR_INVALID, "negative dim");
+    t.shape.push_back(shape[i]);
+    n *= (size_t)shape[i];
+  }
+  t.data.assign(host, host + n);
+  m->pending[name] = std::move(t);
+  return RH_OK;
+}
+
+int rh_model_finalize(rh_model* m) {
+  MODEL_GUARD(m);
+  if (m->finalized) return fail(RH_ERR_INVALID, "model already finalized");
+  int st = finalize_bert(m);
+  if (st) {
+    std::string msg = rh_last_error();
+    m->release();
+    set_error(msg);
+    return st;
+  }
+  m->pending.clear();
+  m->finalized = true;
+  return RH_OK;
+}
+
+void rh_model_destroy(rh_model* m) {
+  if (!m) return;
+  {
+    std::lock_guard<std::mutex> lk(m->ctx->mu);
+    m->release();
+  }
+  delete m;
+}
+
+int rh_model_quantized(const rh_model* m) {
+  if (!m || m->layers.empty()) return 0;
+  for (const Layer& L : m->layers)
+    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2})
+      if (w->mode == RH_MODE_F32) return 0;
+  return 1;
+}
+
+int rh_model_quantized_activations(const rh_model* m) {
+  if (!m || m->layers.empty()) return 0;
+  for (const Layer& L : m->layers)
+    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2})
+      if (w->mode != RH_MODE_A8W8) return 0;
+  return 1;
+}
+
+static int embed_common(rh_model* m, const int32_t* ids, const int32_t* lens, int batch,
+                        int stride, float* out, bool pool) {
+  if (!ids || !lens || !out || batch < 0 || stride < 1)
+    return fail(RH_ERR_INVALID, "bad argument");
+  if (!m->finalized) return fail(RH_ERR_INVALID, "model not finalized");
+  if (batch == 0) return RH_OK;
+  std::vector<int32_t> cu;
+  int max_len = 0;
+  int st = m->plan(lens, batch, cu, &max_len);
+  if (st) return st;
+  for (int b = 0; b < batch; b++) {
+    if (lens[b] > stride) return fail(RH_ERR_INVALID, "length exceeds row stride");
+    for (int t = 0; t < lens[b]; t++) {
+      const int32_t id = ids[(size_t)b * stride + t];
+      if (id < 0 || id >= m->cfg.vocab) {
+        char buf[160];
+        snprintf(buf, sizeof buf, "text %d: token id %d out of vocab range %d", b, id,
+                 m->cfg.vocab);
+        return fail(RH_ERR_VOCAB, buf);
+      }
+    }
+  }
+  const int M = cu[batch], H = m->cfg.hidden;
+  if ((st = m->ensure_ws(M, batch, batch * stride))) return st;
+  hipStream_t s = m->ctx->stream;
+  RH_HIP(hipMemcpyAsync(m->ids_d, ids, (size_t)batch * stride * sizeof(int32_t),
+                        hipMemcpyHostToDevice, s));
+  if ((st = m->forward(m->ids_d, stride, cu, max_len, pool, m->out_d))) return st;
+  if (pool)
+    RH_HIP(hipMemcpyAsync(out, m->out_d, (size_t)batch * H * sizeof(float),
+                          hipMemcpyDeviceToHost, s));
+  else
+    RH_HIP(hipMemcpyAsync(out, m->x, (size_t)M * H * sizeof(float), hipMemcpyDeviceToHost,
+                          s));
+  RH_HIP(hipStreamSynchronize(s));
+  return RH_OK;
+}
+
+int rh_model_embed(rh_model* m, const int32_t* ids, const int32_t* lens, int batch,
+                   int stride, float* out) {
+  MODEL_GUARD(m);
+  return embed_common(m, ids, lens, batch, stride, out, true);
+}
+
+int rh_model_embed_tokens(rh_model* m, const int32_t* ids, const int32_t* lens, int batch,
+                          int stride, float* out) {
+  MODEL_GUARD(m);
+  return embed_common(m, ids, lens, batch, stride, out, false);
+}
+
+int rh_model_embed_device(rh_model* m, const int32_t* ids_dev, const int32_t* lens,
+                          int batch, int stride, float* out_dev) {
+  MODEL_GUARD(m);
+  if (!ids_dev || !lens || !out_dev || batch < 0 || stride < 1)
+    return fail(RH_ERR_INVALID, "bad argument");
+  if (!m->finalized) return fail(RH_ERR_INVALID, "model not finalized");
+  if (batch == 0) return RH_OK;
+  std::vector<int32_t> cu;
+  int max_len = 0;
+  int st = m->plan(lens, batch, cu, &max_len);
+  if (st) return st;
+  for (int b = 0; b < batch; b++)
+    if (lens[b] > stride) return fail(RH_ERR_INVALID, "length exceeds row stride");
+  return m->forward(ids_dev, stride, cu, max_len, true, out_dev);
+}
+
+int rh_model_check(rh_model* m) {
+  MODEL_GUARD(m);
+  RH_HIP(hipStreamSynchronize(m->ctx->stream));
+  if (!m->err_d) return RH_OK;
+  int flag = 0;
+  RH_HIP(hipMemcpy(&flag, m->err_d, sizeof(int), hipMemcpyDeviceToHost));
+  if (flag) {
+    RH_HIP(hipMemset(m->err_d, 0, sizeof(int)));
+    return fail(RH_ERR_VOCAB, "a token id was out of vocab range (clamped on device)");
+  }
+  return RH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,167 @@
+// rh_internal.h — shared definitions for the rembed HIP backend (gfx950).
+//
+// Everything here is device-agnostic plumbing: status handling, vector
+// types for the CDNA4 MFMA builtins, and the kernel launch entry points
+// that the C-ABI layer (capi.cpp) and the model runtime (model.cpp) call.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/rembed_hip.h"
+
+namespace rh {
+
+// ---- status ----------------------------------------------------------------
+// A thread-local message backs rh_last_error(); every C entry point returns
+// one of the RH_* codes and never aborts the host.
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what, const char* file, int line);
+
+#define RH_HIP(call)                                                   \
+  do {                                                                 \
+    hipError_t rh_e_ = (call);                                         \
+    if (rh_e_ != hipSuccess)                                           \
+      return ::rh::hip_fail(rh_e_, #call, __FILE__, __LINE__);         \
+  } while (0)
+
+#define RH_CHECK(cond, code, msg)                                      \
+  do {                                                                 \
+    if (!(cond)) return ::rh::fail((code), (msg));                     \
+  } while (0)
+
+// ---- MFMA operand types ----------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Padding of packed weights in HBM: rows (output channels) to a multiple of
+// the widest N tile, columns (k) to a multiple of the deepest K tile, so
+// every tile load of B stays inside the allocation with zero padding.
+constexpr int kWeightRowPad = 256;
+constexpr int kWeightKPad = 128;
+
+// ---- GEMM launch descriptors -------------------------------------------------
+// act codes for the fused epilogue (reference applies these as separate
+// passes after AddBias: internal/model/bert.go:913-915, qwen3.go:530-539).
+enum Act : int { ACT_NONE = 0, ACT_GELU = 1 };
+
+struct GemmI8Args {
+  const uint8_t* A;  // u8 activations (+128 offset, QuantizeRowU8 format) [M][lda]
+  int lda;           // bytes, multiple of 16
+  const int8_t* B;   // s8 weights [Np][ldb], zero padded
+  int ldb;           // bytes, multiple of kWeightKPad
+  int M, N, K;
+  const float* row_scales;  // [M]
+  const float* col_scales;  // [N]
+  const int32_t* colsum;    // [N]
+  const float* bias;        // [N] or null
+  float* C;                 // [M][ldc] fp32 or null
+  int32_t* Cacc;            // [M][ldc] reference-form accumulators or null
+  int ldc;
+  int act;
+};
+
+// B formats of the bf16-MFMA GEMM family.
+enum BKind : int {
+  BK_I8 = 0,     // int8 weights, dequantised to bf16 on the way into LDS
+  BK_BF16X2 = 1  // fp32 weights stored as bf16 hi + bf16 lo planes
+};
+
+struct GemmBfArgs {
+  const float* A;  // fp32 activations [M][lda]
+  int lda;         // floats, multiple of 4
+  const void* B;   // BK_I8: int8 [Np][ldb]; BK_BF16X2: bf16 hi plane [Np][ldb]
+  const void* Blo; // BK_BF16X2: bf16 lo plane
+  int ldb;         // elements
+  int M, N, K;
+  const float* col_scales;  // BK_I8: [N]; else null
+  const float* bias;        // [N] or null
+  float* C;
+  int ldc;
+  int act;
+};
+
+// fp32 GEMM strategies (selected per model/context; both kept so the
+// choice can be re-measured): three bf16 products or native f32 MFMA.
+enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
+
+// Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
+hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t s);
+// a_terms: 1 or 2 bf16 terms for the fp32 activations.
+hipError_t launch_gemm_w8(const GemmBfArgs& a, int a_terms, hipStream_t s);
+hipError_t launch_gemm_f32(const GemmBfArgs& a, int algo, hipStream_t s);
+
+// ---- elementwise / norm / attention launchers (kernels_misc.hip, attention.hip)
+hipError_t launch_quantize_rows_u8(const float* a, int lda, int m, int k,
+                                   uint8_t* qa, int ldq, float* row_scales,
+                                   hipStream_t s);
+hipError_t launch_gelu(float* x, size_t n, hipStream_t s);
+hipError_t launch_add_bias(float* x, const float* bias, int m, int n, int ldx,
+                           hipStream_t s);
+
+// BERT embeddings: x[t] = word[id] + pos[t - start + pos_off] + type0, then
+// LayerNorm; optionally also quantizes x rows for the next full-int8 GEMM.
+struct EmbedArgs {
+  const int32_t* ids;      // padded [batch][stride]
+  int stride;
+  const int32_t* cu;       // [batch+1] packed row offsets
+  int batch;
+  const float* word;       // [vocab][H]
+  const float* pos;        // [max_pos][H]
+  const float* type0;      // [H] or null
+  const float* gamma;
+  const float* beta;
+  int H, vocab, pos_off;
+  float eps;
+  float* x;                // [M][H]
+  uint8_t* qa;             // optional [M][ldq]
+  int ldq;
+  float* row_scales;       // optional [M]
+  int* err_flag;           // set to 1 on an out-of-range id
+};
+hipError_t launch_embed_layernorm(const EmbedArgs& a, int total_rows,
+                                  hipStream_t s);
+
+// x = LayerNorm(x + y) (bert.go:906-907,917-918); optional u8 quantization
+// of the result for the next full-int8 GEMM.
+hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
+                                const float* gamma, const float* beta, int m,
+                                int H, float eps, uint8_t* qa, int ldq,
+                                float* row_scales, hipStream_t s);
+// standalone LayerNorm (tests)
+hipError_t launch_layernorm(float* x, const float* gamma, const float* beta,
+                            int m, int H, float eps, hipStream_t s);
+
+// pooling + optional L2 per text (bert.go:669-703, tensor.go:542-554)
+hipError_t launch_pool(const float* x, int H, const int32_t* cu, int batch,
+                       int pooling, int normalize, float* out, hipStream_t s);
+
+// Multi-head attention over a packed varlen batch (bert.go:853-902 per
+// text): q/k/v read from the fused QKV rows, ctx written [M][H].
+struct AttnArgs {
+  const float* qkv;  // [M][ldqkv]
+  int ldqkv;
+  int q_off, k_off, v_off;  // column offsets of head 0
+  const int32_t* cu;        // [batch+1]
+  int batch;
+  int max_len;
+  int heads, kv_heads, dh;
+  float scale;
+  float* ctx;  // [M][ldctx]
+  int ldctx;
+};
+// precision: 1 = bf16 MFMA, 3 = three-term bf16 split (fp32-grade)
+hipError_t launch_attention(const AttnArgs& a, int precision, hipStream_t s);
+
+}  // namespace rh

@@ -1,0 +1,116 @@
+"""Python mirror of rembed's encoder API over the C ABI.
+
+Model follows internal/model (Load, Forward/ForwardTokens, Quantized,
+QuantizedActivations); embed()/embed_tokens() take token ids the way
+Embedder.Embed/EmbedTokens feed them (rembed.go:287-411), batched.
+"""
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+
+QUANT_NONE = _lib.RH_QUANT_NONE       # default fp32
+QUANT_WEIGHTS = _lib.RH_QUANT_WEIGHTS  # WithInt8 (rembed.go:67-69)
+QUANT_FULL = _lib.RH_QUANT_FULL        # WithInt8Activations (rembed.go:79-81)
+
+
+def make_config(shape):
+    """rh_model_config from a synthetic.BertShape-like object."""
+    c = _lib.ModelConfig()
+    c.arch = _lib.RH_ARCH_BERT
+    c.hidden = shape.hidden
+    c.layers = shape.layers
+    c.heads = shape.heads
+    c.intermediate = shape.intermediate
+    c.vocab = shape.vocab
+    c.max_position = shape.max_position
+    c.position_offset = getattr(shape, "position_offset", 0)
+    c.type_vocab = shape.type_vocab
+    c.layer_norm_eps = shape.eps
+    c.pooling = shape.pooling
+    c.normalize = shape.normalize
+    return c
+
+
+class Model:
+    """A loaded encoder resident in HBM (rh_model)."""
+
+    def __init__(self, ctx, shape, tensors, quant=QUANT_NONE):
+        self.ctx = ctx
+        self.shape = shape
+        cfg = make_config(shape)
+        h = ctypes.c_void_p()
+        check(lib.rh_model_create(ctx.h, ctypes.byref(cfg), quant, ctypes.byref(h)))
+        self.h = h
+        try:
+            for name, arr in tensors.items():
+                arr = np.ascontiguousarray(arr, dtype=np.float32)
+                dims = (ctypes.c_int64 * arr.ndim)(*arr.shape)
+                check(lib.rh_model_set_tensor(h, name.encode(), arr.ctypes.data,
+                                              dims, arr.ndim))
+            check(lib.rh_model_finalize(h))
+        except Exception:
+            self.close()
+            raise
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib.rh_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_attention_precision(self, prec):
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_ATTN_PRECISION, prec))
+
+    def quantized(self):
+        return bool(lib.rh_model_quantized(self.h))
+
+    def quantized_activations(self):
+        return bool(lib.rh_model_quantized_activations(self.h))
+
+    @staticmethod
+    def _pack(ids, lens):
+        if lens is None:  # list of sequences
+            seqs = [np.asarray(s, np.int32) for s in ids]
+            lens = np.array([len(s) for s in seqs], np.int32)
+            stride = max(1, int(lens.max())) if len(seqs) else 1
+            arr = np.zeros((len(seqs), stride), np.int32)
+            for i, s in enumerate(seqs):
+                arr[i, : len(s)] = s
+            return arr, lens
+        return (np.ascontiguousarray(ids, np.int32),
+                np.ascontiguousarray(lens, np.int32))
+
+    def embed(self, ids, lens=None):
+        """Pooled (and L2-normalized per config) vectors, [batch][H]."""
+        ids, lens = self._pack(ids, lens)
+        out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
+        check(lib.rh_model_embed(self.h, ids.ctypes.data, lens.ctypes.data,
+                                 ids.shape[0], ids.shape[1], out.ctypes.data))
+        return out
+
+    def embed_tokens(self, ids, lens=None):
+        """Per-token final hidden states, one [len][H] array per text."""
+        ids, lens = self._pack(ids, lens)
+        tot = int(lens.sum())
+        out = np.empty((tot, self.shape.hidden), np.float32)
+        check(lib.rh_model_embed_tokens(self.h, ids.ctypes.data, lens.ctypes.data,
+                                        ids.shape[0], ids.shape[1], out.ctypes.data))
+        offs = np.concatenate([[0], np.cumsum(lens)])
+        return [out[offs[i]: offs[i + 1]] for i in range(len(lens))]
+
+    def embed_device(self, ids_dev, lens, batch, stride, out_dev):
+        """Enqueue a forward over HBM-resident ids; no host sync."""
+        lens = np.ascontiguousarray(lens, np.int32)
+        check(lib.rh_model_embed_device(self.h, ids_dev.ptr, lens.ctypes.data, batch,
+                                        stride, out_dev.ptr))
+
+    def check(self):
+        check(lib.rh_model_check(self.h))

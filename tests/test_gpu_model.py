@@ -1,0 +1,171 @@
+"""GPU parity of the device-resident encoder against the oracle's per-text,
+unpadded forward on identical synthetic weights and token ids.
+
+Contracts: fp32 max |err| <= 1e-4 on final embeddings; weight-only int8
+cosine >= 0.9999 against the oracle's int8 path; full int8 cosine against
+the oracle's full-int8 path (and >= 0.991 against fp32, the reference's own
+floor, rembed_test.go:107-166); batch results equal single-text results.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+SHAPES = {}
+
+
+def minilm_small():
+    from rembed_amd.synthetic import MINILM_L6
+    return MINILM_L6
+
+
+def bert_base():
+    from rembed_amd.synthetic import BERT_BASE
+    return BERT_BASE
+
+
+@pytest.fixture(scope="module")
+def minilm():
+    from rembed_amd.synthetic import bert_tensors, token_batch
+    shape = minilm_small()
+    t = bert_tensors(shape, seed=0x5EED0001)
+    ids, lens = token_batch(12, 128, 16, 128, seed=0x5EED0002)
+    return shape, t, ids, lens
+
+
+def gpu_embed(ctx, shape, t, quant, ids, lens, prec=None):
+    from rembed_amd.model import Model
+    m = Model(ctx, shape, t, quant)
+    if prec:
+        m.set_attention_precision(prec)
+    out = m.embed(ids, lens)
+    return m, out
+
+
+def cos_rows(a, b):
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    return np.sum(a * b, 1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+
+
+def test_minilm_fp32_max_abs_1e4(gpu_ctx, minilm):
+    shape, t, ids, lens = minilm
+    say("minilm fp32")
+    m, got = gpu_embed(gpu_ctx, shape, t, 0, ids, lens)
+    assert not m.quantized()
+    want = O.BertOracle(shape, t, 0).embed_batch(ids, lens, threads=8)
+    err = np.abs(got - want).max()
+    say(f"  max abs err {err:.3e}")
+    assert err <= 1e-4
+
+
+def test_minilm_weight_only_cosine(gpu_ctx, minilm):
+    shape, t, ids, lens = minilm
+    say("minilm w8")
+    m, got = gpu_embed(gpu_ctx, shape, t, 1, ids, lens)
+    assert m.quantized() and not m.quantized_activations()
+    want = O.BertOracle(shape, t, 1).embed_batch(ids, lens, threads=8)
+    c = cos_rows(got, want)
+    say(f"  min cos {c.min():.7f} max abs {np.abs(got - want).max():.3e}")
+    assert c.min() >= 0.9999
+
+
+def test_minilm_full_int8_cosine(gpu_ctx, minilm):
+    shape, t, ids, lens = minilm
+    say("minilm a8w8")
+    m, got = gpu_embed(gpu_ctx, shape, t, 2, ids, lens)
+    assert m.quantized() and m.quantized_activations()
+    want = O.BertOracle(shape, t, 2).embed_batch(ids, lens, threads=8)
+    fp = O.BertOracle(shape, t, 0).embed_batch(ids, lens, threads=8)
+    c = cos_rows(got, want)
+    c32 = cos_rows(got, fp)
+    say(f"  min cos vs oracle int8 {c.min():.6f}, vs fp32 {c32.min():.6f}")
+    assert c.min() >= 0.999
+    assert c32.min() >= 0.991
+    # the int8 path is really active (rembed_test.go:107-174)
+    assert np.abs(got - fp).max() >= 1e-4
+
+
+@pytest.mark.parametrize("quant", [0, 1, 2])
+def test_batch_matches_single(gpu_ctx, minilm, quant):
+    """TestEmbedBatchMatchesSingle (rembed_test.go:1262-1315): a text's vector
+    does not depend on the other texts in the batch."""
+    shape, t, ids, lens = minilm
+    from rembed_amd.model import Model
+    m = Model(gpu_ctx, shape, t, quant)
+    batch = m.embed(ids, lens)
+    for b in (0, 5, 11):
+        single = m.embed(ids[b: b + 1, : lens[b]], lens[b: b + 1])
+        assert np.array_equal(single[0], batch[b]), b
+
+
+def test_embed_tokens_matches_oracle_hidden(gpu_ctx, minilm):
+    shape, t, ids, lens = minilm
+    from rembed_amd.model import Model
+    m = Model(gpu_ctx, shape, t, 0)
+    toks = m.embed_tokens(ids[:3], lens[:3])
+    orc = O.BertOracle(shape, t, 0)
+    for b in range(3):
+        want = orc.encode(ids[b, : lens[b]])
+        assert toks[b].shape == want.shape
+        assert np.abs(toks[b] - want).max() <= 1e-4
+
+
+def test_model_errors(gpu_ctx, minilm):
+    from rembed_amd._lib import RembedError, RH_ERR_SEQ, RH_ERR_VOCAB, RH_ERR_MISSING
+    from rembed_amd.model import Model
+    shape, t, ids, lens = minilm
+    m = Model(gpu_ctx, shape, t, 0)
+    with pytest.raises(RembedError) as e:
+        m.embed([[1, 2, shape.vocab]])
+    assert e.value.code == RH_ERR_VOCAB
+    with pytest.raises(RembedError) as e:
+        m.embed(np.zeros((1, 4), np.int32), np.array([0], np.int32))
+    assert e.value.code == RH_ERR_SEQ
+    with pytest.raises(RembedError) as e:
+        m.embed(np.zeros((1, 600), np.int32), np.array([600], np.int32))
+    assert e.value.code == RH_ERR_SEQ
+    t2 = dict(t)
+    del t2["encoder.layer.3.output.dense.bias"]
+    with pytest.raises(RembedError) as e:
+        Model(gpu_ctx, shape, t2, 0)
+    assert e.value.code == RH_ERR_MISSING
+
+
+@pytest.fixture(scope="module")
+def bertbase():
+    from rembed_amd.synthetic import bert_tensors, token_batch
+    shape = bert_base()
+    t = bert_tensors(shape, seed=0x5EED0001)
+    ids, lens = token_batch(64, 256, 64, 256, seed=0x5EED0002)
+    return shape, t, ids, lens
+
+
+@pytest.mark.parametrize("quant", [0, 2])
+def test_bert_base_full_batch_parity(gpu_ctx, bertbase, quant):
+    """The benchmark workload (64 texts x up to 256 tokens) on the GPU; a
+    sample of texts re-run on the oracle."""
+    shape, t, ids, lens = bertbase
+    say(f"bert-base quant={quant}")
+    m, got = gpu_embed(gpu_ctx, shape, t, quant, ids, lens)
+    assert np.all(np.abs(np.linalg.norm(got.astype(np.float64), axis=1) - 1) < 1e-5)
+    sample = [0, 17, 63]
+    want = O.BertOracle(shape, t, quant).embed_batch(ids[sample], lens[sample], threads=8)
+    if quant == 0:
+        err = np.abs(got[sample] - want).max()
+        say(f"  max abs err {err:.3e}")
+        assert err <= 1e-4
+    else:
+        c = cos_rows(got[sample], want)
+        say(f"  min cos {c.min():.6f}")
+        assert c.min() >= 0.999

@@ -1,0 +1,256 @@
+"""GPU parity of the tensor-level entry points against the pinned oracle.
+
+Integer work (activation quantization, u8 x s8 accumulators, the full-int8
+epilogue, GELU) must be bit-exact; the floating-point GEMMs are held to the
+reference's own float64 tolerance (internal/tensor/pack_test.go:55-67).
+"""
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                   "reference_kats.json")))
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "vnni_vectors.npz")
+GUARD = 64  # canary floats past the end of every output
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def T():
+    from rembed_amd import tensor
+    return tensor
+
+
+def vnni_case(rng, m, k, n):
+    a = (rng.random((m, k), dtype=np.float32) * 4 - 2).astype(np.float32)
+    bT = (rng.random((n, k), dtype=np.float32) * 2 - 1).astype(np.float32)
+    if k > 2:
+        a[0, :3] = KATS["vnni_exact_shapes"]["rail_row"]
+    return a, bT
+
+
+def run_vnni(ctx, a, pb, m):
+    """MatMulPackedVNNI on device with guard canaries; returns dst, qa, rs."""
+    t = T()
+    k, n = pb.K, pb.N
+    ldq = t.ldq_for(k)
+    da = ctx.upload(a)
+    dst = ctx.upload(np.full(m * n + GUARD, -999, np.float32))
+    qa = ctx.upload(np.full(m * ldq + GUARD, 0xAB, np.uint8))
+    rs = ctx.upload(np.full(m + GUARD, -7, np.float32))
+    t.MatMulPackedVNNI(ctx, dst, da, pb, m, qa, ldq, rs)
+    ctx.sync()
+    d = dst.download(np.float32, (m * n + GUARD,))
+    q = qa.download(np.uint8, (m * ldq + GUARD,))
+    r = rs.download(np.float32, (m + GUARD,))
+    assert np.all(d[m * n:] == -999), "dst guard overwritten"
+    assert np.all(q[m * ldq:] == 0xAB), "qa guard overwritten"
+    assert np.all(r[m:] == -7), "row-scale guard overwritten"
+    qm = q[: m * ldq].reshape(m, ldq)
+    assert np.all(qm[:, k:] == 0), "tail bytes not zeroed"
+    return d[: m * n].reshape(m, n), qm[:, :k], r[:m]
+
+
+@pytest.mark.parametrize("shape", KATS["vnni_exact_shapes"]["shapes"])
+def test_vnni_bit_exact_reference_shapes(gpu_ctx, shape):
+    m, k, n = shape
+    say(f"vnni shape m={m} k={k} n={n}")
+    rng = np.random.default_rng(1000 + m * 31 + k)
+    a, bT = vnni_case(rng, m, k, n)
+    pb = T().PackB8VNNI(gpu_ctx, bT, k, n)
+    q, sc, cs = pb.export()
+    st, q_o, sc_o, cs_o = O.pack_b8_vnni(bT, k, n)
+    assert np.array_equal(q, q_o) and np.array_equal(sc, sc_o) and np.array_equal(cs, cs_o)
+    dst, qa, rs = run_vnni(gpu_ctx, a, pb, m)
+    dst_o, qa_o, rs_o, acc_o = O.matmul_vnni(a, q_o, cs_o, sc_o)
+    assert np.array_equal(qa, qa_o), "QuantizeRowU8 bytes differ"
+    assert np.array_equal(rs, rs_o), "row scales differ"
+    assert np.array_equal(dst, dst_o), "dequantized output not bit-exact"
+
+
+def test_vnni_golden_fixture(gpu_ctx):
+    g = np.load(GOLDEN)
+    tags = sorted({k.split("/")[0] for k in g.files if "/" in k})
+    for tag in tags:
+        m, k, n = map(int, tag.split("x"))
+        say(f"golden {tag}")
+        pb = T().PackB8VNNI(gpu_ctx, g[f"{tag}/bT"], k, n)
+        q, sc, cs = pb.export()
+        assert np.array_equal(q, g[f"{tag}/q"])
+        assert np.array_equal(sc, g[f"{tag}/scales"])
+        assert np.array_equal(cs, g[f"{tag}/colsum"])
+        dst, qa, rs = run_vnni(gpu_ctx, g[f"{tag}/a"], pb, m)
+        assert np.array_equal(qa, g[f"{tag}/qa"])
+        assert np.array_equal(rs, g[f"{tag}/rs"])
+        assert np.array_equal(dst, g[f"{tag}/dst"])
+        # raw accumulators in the reference's u8·s8 form
+        t = T()
+        ldq = t.ldq_for(k)
+        qpad = np.zeros((m, ldq), np.uint8)
+        qpad[:, :k] = g[f"{tag}/qa"]
+        dq = gpu_ctx.upload(qpad)
+        acc = gpu_ctx.upload(np.zeros(m * n, np.int32))
+        t.GemmU8S8I32(gpu_ctx, acc, dq, ldq, pb, m)
+        gpu_ctx.sync()
+        assert np.array_equal(acc.download(np.int32, (m, n)), g[f"{tag}/acc"])
+
+
+@pytest.mark.parametrize("kn", [(768, 2304), (768, 768), (768, 3072), (3072, 768)])
+@pytest.mark.parametrize("m", [2048, 16384])
+def test_i32_accumulators_bert_base_bit_exact(gpu_ctx, m, kn):
+    """int32 accumulators bit-exact at the BERT-base GEMM shapes."""
+    k, n = kn
+    say(f"i32 acc m={m} k={k} n={n}")
+    t = T()
+    rng = np.random.default_rng(m + k + n)
+    bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
+    pb = t.PackB8VNNI(gpu_ctx, bT, k, n)
+    q, _, _ = pb.export()
+    qa = rng.integers(0, 256, size=(m, k), dtype=np.uint8)
+    ldq = t.ldq_for(k)
+    dq = gpu_ctx.upload(qa)
+    acc = gpu_ctx.upload(np.full(m * n + GUARD, 0x7EADBEEF, np.int32))
+    t.GemmU8S8I32(gpu_ctx, acc, dq, ldq, pb, m)
+    gpu_ctx.sync()
+    got = acc.download(np.int32, (m * n + GUARD,))
+    assert np.all(got[m * n:] == 0x7EADBEEF)
+    want = O.gemm_u8s8_i32(qa, q)
+    assert np.array_equal(got[: m * n].reshape(m, n), want)
+
+
+def test_quantize_rows_bit_exact(gpu_ctx):
+    t = T()
+    rng = np.random.default_rng(77)
+    for k in (1, 3, 5, 7, 33, 129, 384, 768, 1536, 3072):
+        m = 37
+        say(f"quantize k={k}")
+        a = (rng.standard_normal((m, k), dtype=np.float32) *
+             np.exp(rng.integers(-8, 8, size=(m, 1))).astype(np.float32)).astype(np.float32)
+        a[3] = 0
+        if k >= 4:
+            a[5, :4] = [127, -127, 0, 63.5]
+        ldq = t.ldq_for(k)
+        da = gpu_ctx.upload(a)
+        qa = gpu_ctx.upload(np.full(m * ldq, 0xCD, np.uint8))
+        rs = gpu_ctx.alloc(m * 4)
+        t.QuantizeRowsU8(gpu_ctx, da, m, k, qa, ldq, rs)
+        gpu_ctx.sync()
+        q = qa.download(np.uint8, (m, ldq))
+        r = rs.download(np.float32, (m,))
+        for i in range(m):
+            qo, so = O.quantize_row_u8(a[i], ldq)
+            assert np.array_equal(q[i], qo), (k, i)
+            assert r[i] == so, (k, i)
+
+
+def test_linear_a8w8_bias_gelu_bit_exact(gpu_ctx):
+    """Fused bias + erf-GELU epilogue equals AddBias then GELU (bert.go:297-300,913-915)."""
+    t = T()
+    rng = np.random.default_rng(5)
+    m, k, n = 300, 384, 1536
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.05).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    pb = t.PackB8VNNI(gpu_ctx, bT, k, n, bias=bias)
+    got, _ = t.matmul_host(gpu_ctx, a, pb, act=1)
+    st, q, sc, cs = O.pack_b8_vnni(bT, k, n)
+    dst, _, _, _ = O.matmul_vnni(a, q, cs, sc)
+    want = O.gelu((dst + bias[None, :]).astype(np.float32))
+    assert np.array_equal(got, want)
+
+
+def f64_tol(k):
+    return max(KATS["packed_f32_shapes"]["tol_base"],
+               KATS["packed_f32_shapes"]["tol_sqrtk"] * math.sqrt(k))
+
+
+@pytest.mark.parametrize("shape", KATS["packed_f32_shapes"]["shapes"])
+def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape):
+    m, k, n = shape
+    say(f"w8 shape {shape}")
+    t = T()
+    rng = np.random.default_rng(23 + k)
+    a = (rng.random((m, k), dtype=np.float32) * 2 - 1).astype(np.float32)
+    bT = (rng.random((n, k), dtype=np.float32) * 2 - 1).astype(np.float32)
+    bT[n // 2] = 0  # the scale-1 branch
+    pb = t.PackB8(gpu_ctx, bT, k, n)
+    q, sc, _ = pb.export()
+    st, q_o, sc_o = O.pack_b8(bT, k, n)
+    assert np.array_equal(q, q_o) and np.array_equal(sc, sc_o)
+    got = t.matmul_host(gpu_ctx, a, pb)
+    deq = q.astype(np.float64) * sc.astype(np.float64)[:, None]
+    want = a.astype(np.float64) @ deq.T
+    err = np.abs(got - want) / (1 + np.abs(want))
+    assert err.max() <= f64_tol(k), err.max()
+
+
+@pytest.mark.parametrize("algo", [0, 1])
+@pytest.mark.parametrize("shape", KATS["packed_f32_shapes"]["shapes"])
+def test_matmul_packed_f32_against_float64(gpu_ctx, shape, algo):
+    m, k, n = shape
+    say(f"f32 shape {shape} algo {algo}")
+    t = T()
+    rng = np.random.default_rng(11 + k)
+    a = (rng.random((m, k), dtype=np.float32) * 2 - 1).astype(np.float32)
+    bT = (rng.random((n, k), dtype=np.float32) * 2 - 1).astype(np.float32)
+    gpu_ctx.set_f32_algo(algo)
+    try:
+        pb = t.PackB(gpu_ctx, bT, k, n)
+        got = t.matmul_host(gpu_ctx, a, pb)
+    finally:
+        gpu_ctx.set_f32_algo(0)
+    want = a.astype(np.float64) @ bT.astype(np.float64).T
+    err = np.abs(got - want) / (1 + np.abs(want))
+    assert err.max() <= f64_tol(k), err.max()
+
+
+def test_gelu_bit_exact(gpu_ctx):
+    from rembed_amd._lib import check, lib
+    xs = np.concatenate([np.arange(-30, 30, 0.2337, dtype=np.float32),
+                         np.array([0, -0.0, 1e-20, -1e-20, 90, -90, 12.5, -12.5],
+                                  np.float32)]).astype(np.float32)
+    d = gpu_ctx.upload(xs)
+    check(lib.rh_gelu(gpu_ctx.h, d.ptr, xs.size))
+    gpu_ctx.sync()
+    assert np.array_equal(d.download(np.float32, xs.shape), O.gelu(xs))
+
+
+def test_layernorm_matches_oracle(gpu_ctx):
+    from rembed_amd._lib import check, lib
+    rng = np.random.default_rng(3)
+    for n in (3, 384, 768, 1024):
+        x = rng.standard_normal((50, n), dtype=np.float32) * 3 + 1
+        g = rng.standard_normal(n, dtype=np.float32)
+        b = rng.standard_normal(n, dtype=np.float32)
+        dx, dg, db = gpu_ctx.upload(x), gpu_ctx.upload(g), gpu_ctx.upload(b)
+        check(lib.rh_layernorm(gpu_ctx.h, dx.ptr, dg.ptr, db.ptr, 50, n,
+                               np.float32(1e-12)))
+        gpu_ctx.sync()
+        got = dx.download(np.float32, x.shape)
+        want = O.layernorm(x, g, b, 1e-12)
+        assert np.max(np.abs(got - want)) <= 1e-5 * (1 + np.abs(want)).max()
+
+
+def test_pack_errors_surface_as_status(gpu_ctx):
+    from rembed_amd._lib import RembedError, RH_ERR_NONFINITE, RH_ERR_SHAPE
+    t = T()
+    with pytest.raises(RembedError) as e:
+        t.PackB8(gpu_ctx, np.zeros((15, 3), np.float32), 3, 15)
+    assert e.value.code == RH_ERR_SHAPE
+    bad = np.zeros((16, 4), np.float32)
+    bad[1, 2] = np.nan
+    for fn in (t.PackB8, t.PackB8VNNI):
+        with pytest.raises(RembedError) as e:
+            fn(gpu_ctx, bad, 4, 16)
+        assert e.value.code == RH_ERR_NONFINITE
