@@ -55,9 +55,16 @@ void rh_context_destroy(rh_context *ctx);
 int rh_context_sync(rh_context *ctx);
 /* The context's hipStream_t, for callers that time or order work around it. */
 void *rh_context_stream(rh_context *ctx);
-/* fp32 GEMM strategy: 0 = three bf16 MFMA products (default), 1 = native
- * f32 MFMA. Both meet the fp32 contract; this exists to re-measure. */
-int rh_context_set_f32_algo(rh_context *ctx, int algo);
+/* GEMM strategy switches of a context (kept so choices can be re-measured):
+ *   RH_CTX_F32_ALGO  0 = three bf16 MFMA products (default), 1 = native f32
+ *   RH_CTX_W8_TERMS  bf16 terms of the fp32 activations in the weight-only
+ *                    int8 GEMM: 1 or 2 (default 2)
+ *   RH_CTX_I8_TILE   int8 GEMM tile: 0 = automatic, else a fixed
+ *                    configuration index (see DESIGN notes of the kernel) */
+#define RH_CTX_F32_ALGO 1
+#define RH_CTX_W8_TERMS 2
+#define RH_CTX_I8_TILE 3
+int rh_context_set_option(rh_context *ctx, int option, int value);
 
 /* Device memory helpers (the Go host has no other allocator for HBM). */
 int rh_malloc(rh_context *ctx, size_t bytes, void **dev);

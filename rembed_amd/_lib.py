@@ -28,12 +28,13 @@ RH_POOL_MEAN, RH_POOL_CLS, RH_POOL_LAST = 0, 1, 2
 RH_ACT_NONE, RH_ACT_GELU = 0, 1
 RH_ARCH_BERT = 0
 RH_OPT_ATTN_PRECISION = 1
+RH_CTX_F32_ALGO, RH_CTX_W8_TERMS, RH_CTX_I8_TILE = 1, 2, 3
 
 # Symbols the header declares (checked by the CPU test suite).
 EXPORTS = [
     "rh_last_error", "rh_version", "rh_device_count", "rh_context_create",
     "rh_context_destroy", "rh_context_sync", "rh_context_stream",
-    "rh_context_set_f32_algo", "rh_malloc", "rh_free", "rh_memcpy_h2d",
+    "rh_context_set_option", "rh_malloc", "rh_free", "rh_memcpy_h2d",
     "rh_memcpy_d2h", "rh_profile_enable", "rh_profile_read", "rh_pack_weight",
     "rh_weight_destroy", "rh_weight_info", "rh_weight_export",
     "rh_quantize_rows_u8", "rh_matmul_packed", "rh_matmul_packed8",
@@ -85,7 +86,7 @@ def _load():
         "rh_context_destroy": (None, [P]),
         "rh_context_sync": (I, [P]),
         "rh_context_stream": (P, [P]),
-        "rh_context_set_f32_algo": (I, [P, I]),
+        "rh_context_set_option": (I, [P, I, I]),
         "rh_malloc": (I, [P, S, ctypes.POINTER(P)]),
         "rh_free": (I, [P, P]),
         "rh_memcpy_h2d": (I, [P, P, P, S]),

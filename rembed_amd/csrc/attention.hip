@@ -78,21 +78,20 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     for (int it = tid; it < kAttnKV * kChunksPerRow; it += 256) {
       const int key = it / kChunksPerRow, ch = it % kChunksPerRow;
       const int kg = key0 + key;
-      const float* krow = p.qkv + (size_t)(r0 + kg) * p.ldqkv + p.k_off + kvh * DH + ch * 8;
-      const float* vrow = p.qkv + (size_t)(r0 + kg) * p.ldqkv + p.v_off + kvh * DH + ch * 8;
+      // Unconditional loads from a clamped in-text row; keys past the text
+      // are zeroed after the loads (and masked out of the softmax below).
+      const bool kok = kg < len;
+      const size_t rowk = (size_t)(r0 + (kok ? kg : len - 1)) * p.ldqkv;
+      const v4f* k4 = reinterpret_cast<const v4f*>(p.qkv + rowk + p.k_off + kvh * DH + ch * 8);
+      const v4f* v4 = reinterpret_cast<const v4f*>(p.qkv + rowk + p.v_off + kvh * DH + ch * 8);
+      const v4f a0 = k4[0], a1 = k4[1], c0 = v4[0], c1 = v4[1];
       float kx[8], vx[8];
-      if (kg < len) {
-        const v4f* k4 = reinterpret_cast<const v4f*>(krow);
-        const v4f* v4 = reinterpret_cast<const v4f*>(vrow);
-        v4f a0 = k4[0], a1 = k4[1], c0 = v4[0], c1 = v4[1];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          kx[e] = a0[e]; kx[4 + e] = a1[e];
-          vx[e] = c0[e]; vx[4 + e] = c1[e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) kx[e] = vx[e] = 0.0f;
+      for (int e = 0; e < 4; e++) {
+        kx[e] = kok ? a0[e] : 0.0f;
+        kx[4 + e] = kok ? a1[e] : 0.0f;
+        vx[e] = kok ? c0[e] : 0.0f;
+        vx[4 + e] = kok ? c1[e] : 0.0f;
       }
       v8bf khi, klo;
 #pragma unroll

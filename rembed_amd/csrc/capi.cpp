@@ -200,10 +200,13 @@ int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int 
     destroy_weight(w);
     return hip_fail(e, "weight upload", __FILE__, __LINE__);
   }
+  ctx_retain(ctx);
   *out = w;
   return RH_OK;
 }
 
+// Frees the device copy; the caller holds the context's mutex (or is the
+// last owner) and then drops the weight's context reference.
 void destroy_weight(rh_weight* w) {
   if (!w) return;
   if (w->d_data) (void)hipFree(w->d_data);
@@ -211,6 +214,17 @@ void destroy_weight(rh_weight* w) {
   if (w->d_colsum) (void)hipFree(w->d_colsum);
   if (w->d_bias) (void)hipFree(w->d_bias);
   delete w;
+}
+
+void ctx_retain(Context* ctx) { ctx->refs.fetch_add(1); }
+
+void ctx_release(Context* ctx) {
+  if (ctx->refs.fetch_sub(1) != 1) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  ctx->prof_clear();
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
 }
 
 // One linear: the GEMM family dispatch of applyDense (bert.go:282-301) with
@@ -249,7 +263,7 @@ int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
     g.act = act;
     const double bytes = M * K + K * N + M * N * 4 + 4 * M + 8 * N + (bias ? 4 * N : 0);
     e = ctx->prof_begin(0, ops, bytes, &slot);
-    if (e == hipSuccess) e = launch_gemm_i8(g, s);
+    if (e == hipSuccess) e = launch_gemm_i8(g, ctx->i8_tile, s);
     if (e == hipSuccess) e = ctx->prof_end(slot);
   } else {
     GemmBfArgs g{};
@@ -329,11 +343,7 @@ int rh_context_create(int device, rh_context** out) {
 
 void rh_context_destroy(rh_context* ctx) {
   if (!ctx) return;
-  (void)hipSetDevice(ctx->device);
-  (void)hipStreamSynchronize(ctx->stream);
-  ctx->prof_clear();
-  (void)hipStreamDestroy(ctx->stream);
-  delete ctx;
+  ctx_release(ctx);
 }
 
 int rh_context_sync(rh_context* ctx) {
@@ -344,12 +354,25 @@ int rh_context_sync(rh_context* ctx) {
 
 void* rh_context_stream(rh_context* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
 
-int rh_context_set_f32_algo(rh_context* ctx, int algo) {
+int rh_context_set_option(rh_context* ctx, int option, int value) {
   if (!ctx) return fail(RH_ERR_INVALID, "null context");
-  if (algo != F32_SPLIT3 && algo != F32_NATIVE) return fail(RH_ERR_INVALID, "unknown fp32 algo");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  ctx->f32_algo = algo;
-  return RH_OK;
+  switch (option) {
+    case RH_CTX_F32_ALGO:
+      if (value != F32_SPLIT3 && value != F32_NATIVE) return fail(RH_ERR_INVALID, "unknown fp32 algo");
+      ctx->f32_algo = value;
+      return RH_OK;
+    case RH_CTX_W8_TERMS:
+      if (value != 1 && value != 2) return fail(RH_ERR_INVALID, "w8 terms must be 1 or 2");
+      ctx->w8_terms = value;
+      return RH_OK;
+    case RH_CTX_I8_TILE:
+      if (value < 0 || value > kI8TileConfigs) return fail(RH_ERR_INVALID, "unknown int8 tile");
+      ctx->i8_tile = value;
+      return RH_OK;
+    default:
+      return fail(RH_ERR_INVALID, "unknown context option");
+  }
 }
 
 int rh_malloc(rh_context* ctx, size_t bytes, void** dev) {
@@ -416,10 +439,14 @@ int rh_pack_weight(rh_context* ctx, int mode, const float* bT, const float* bias
 
 void rh_weight_destroy(rh_weight* w) {
   if (!w) return;
-  std::lock_guard<std::mutex> lk(w->ctx->mu);
-  (void)hipSetDevice(w->ctx->device);
-  (void)hipStreamSynchronize(w->ctx->stream);
-  destroy_weight(w);
+  Context* ctx = w->ctx;
+  {
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    destroy_weight(w);
+  }
+  ctx_release(ctx);
 }
 
 int rh_weight_info(const rh_weight* w, int* mode, int* k, int* n) {

@@ -1,6 +1,7 @@
 // context.h — host-side objects behind the C ABI handles.
 #pragma once
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -13,8 +14,13 @@ struct rh_context {
   int device = 0;
   hipStream_t stream = nullptr;
   std::mutex mu;
+  // Weights and models created on the context hold a reference, so the
+  // context (stream included) lives until rh_context_destroy has been called
+  // AND every object created from it has been destroyed, in any order.
+  std::atomic<int> refs{1};
   int f32_algo = rh::F32_SPLIT3;
   int w8_terms = 2;  // bf16 terms of the fp32 activations in weight-only int8
+  int i8_tile = 0;   // 0 = automatic int8 GEMM tile choice
 
   struct ProfRec {
     hipEvent_t a, b;
@@ -44,6 +50,8 @@ struct rh_weight {
 namespace rh {
 using Context = rh_context;
 
+void ctx_retain(Context* ctx);
+void ctx_release(Context* ctx);  // frees the context on the last reference
 int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
                 int n, rh_weight** out);
 void destroy_weight(rh_weight* w);

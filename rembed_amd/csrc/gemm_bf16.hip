@@ -24,20 +24,29 @@ __device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
   lo = (__bf16)(x - (float)hi);
 }
 
-// Load 8 consecutive fp32 activations of row r starting at column k (zeros
-// past K; vector path when the row stride and base allow 16-byte loads).
-__device__ __forceinline__ void load_a8(const float* A, int lda, int r, int M,
-                                        int k, int K, bool vec, float (&v)[8]) {
-  if (r < M && vec && k + 8 <= K) {
-    const v4f* src = reinterpret_cast<const v4f*>(A + (size_t)r * lda + k);
-    v4f x0 = src[0], x1 = src[1];
-    v[0] = x0[0]; v[1] = x0[1]; v[2] = x0[2]; v[3] = x0[3];
-    v[4] = x1[0]; v[5] = x1[1]; v[6] = x1[2]; v[7] = x1[3];
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-      v[e] = (r < M && k + e < K) ? A[(size_t)r * lda + k + e] : 0.0f;
+// Load 8 consecutive fp32 activations of row r starting at column k (k a
+// multiple of 8). Vector path (K and lda multiples of 4, 16-byte aligned
+// base): two unconditional 16-byte loads from clamped in-bounds addresses,
+// so a stage's loads all issue before any wait; halves past M or K are
+// zeroed later through the returned mask bits. Scalar path otherwise.
+__device__ __forceinline__ uint32_t load_a8(const float* A, int lda, int r, int M,
+                                            int k, int K, bool vec, v4f& x0,
+                                            v4f& x1) {
+  if (vec) {
+    const bool rok = r < M;
+    const float* row = A + (size_t)(rok ? r : M - 1) * lda;
+    const bool h0 = rok && k < K;      // k+4 <= K since both are multiples of 4
+    const bool h1 = rok && k + 4 < K;  // k+8 <= K
+    x0 = *reinterpret_cast<const v4f*>(row + (h0 ? k : 0));
+    x1 = *reinterpret_cast<const v4f*>(row + (h1 ? k + 4 : 0));
+    return (uint32_t)h0 | ((uint32_t)h1 << 1);
   }
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    x0[e] = (r < M && k + e < K) ? A[(size_t)r * lda + k + e] : 0.0f;
+    x1[e] = (r < M && k + 4 + e < K) ? A[(size_t)r * lda + k + 4 + e] : 0.0f;
+  }
+  return 3u;
 }
 
 template <int BM, int BN, int A_TERMS, bool B_INT8>
@@ -64,16 +73,19 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec)
   const int nk = (p.K + 63) >> 6;
   const bool vec = a_vec != 0;
 
-  float ra[AP][8];
+  v4f ra0[AP], ra1[AP];
+  uint32_t amask = 0;
   // B staging registers: int8 -> 8 bytes (2 dwords); fp32 -> 8 floats.
   int rbi[B_INT8 ? BP : 1][2];
-  float rbf[B_INT8 ? 1 : BP][8];
+  v4f rbf0[B_INT8 ? 1 : BP], rbf1[B_INT8 ? 1 : BP];
 
   auto gload = [&](int kt) {
     const int k = (kt << 6) + (lchunk << 3);
+    amask = 0;
 #pragma unroll
     for (int i = 0; i < AP; i++)
-      load_a8(p.A, p.lda, row0 + i * 32 + lrow, p.M, k, p.K, vec, ra[i]);
+      amask |= load_a8(p.A, p.lda, row0 + i * 32 + lrow, p.M, k, p.K, vec, ra0[i],
+                       ra1[i]) << (2 * i);
 #pragma unroll
     for (int i = 0; i < BP; i++) {
       const int c = col0 + i * 32 + lrow;  // zero-padded rows, in bounds
@@ -85,9 +97,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec)
       } else {
         const v4f* src = reinterpret_cast<const v4f*>(
             static_cast<const float*>(p.B) + (size_t)c * p.ldb + k);
-        v4f x0 = src[0], x1 = src[1];
-        rbf[i][0] = x0[0]; rbf[i][1] = x0[1]; rbf[i][2] = x0[2]; rbf[i][3] = x0[3];
-        rbf[i][4] = x1[0]; rbf[i][5] = x1[1]; rbf[i][6] = x1[2]; rbf[i][7] = x1[3];
+        rbf0[i] = src[0];
+        rbf1[i] = src[1];
       }
     }
   };
@@ -96,11 +107,14 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec)
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const int r = i * 32 + lrow;
+      const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+      const v4f x0 = ((amask >> (2 * i)) & 1) ? ra0[i] : z;
+      const v4f x1 = ((amask >> (2 * i + 1)) & 1) ? ra1[i] : z;
       v8bf hi, lo;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         __bf16 h, l;
-        split_bf16(ra[i][e], h, l);
+        split_bf16(e < 4 ? x0[e] : x1[e - 4], h, l);
         hi[e] = h;
         lo[e] = l;
       }
@@ -125,7 +139,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec)
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           __bf16 h, l;
-          split_bf16(rbf[i][e], h, l);
+          split_bf16(e < 4 ? rbf0[i][e] : rbf1[i][e - 4], h, l);
           hi[e] = h;
           lo[e] = l;
         }
@@ -235,17 +249,23 @@ __global__ __launch_bounds__(256) void gemm_f32_native_kernel(GemmBfArgs p,
   const bool vec = a_vec != 0;
 
   v4f ra[AP], rb[BP];
+  uint32_t amask = 0;
   auto gload = [&](int kt) {
     const int k = (kt << 5) + (lchunk << 2);
+    amask = 0;
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const int r = row0 + i * 32 + lrow;
-      if (r < p.M && vec && k + 4 <= p.K) {
-        ra[i] = *reinterpret_cast<const v4f*>(p.A + (size_t)r * p.lda + k);
+      if (vec) {  // unconditional load from a clamped address, masked later
+        const bool ok = r < p.M && k < p.K;
+        const float* row = p.A + (size_t)(r < p.M ? r : p.M - 1) * p.lda;
+        ra[i] = *reinterpret_cast<const v4f*>(row + (ok ? k : 0));
+        amask |= (uint32_t)ok << i;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; e++)
           ra[i][e] = (r < p.M && k + e < p.K) ? p.A[(size_t)r * p.lda + k + e] : 0.0f;
+        amask |= 1u << i;
       }
     }
 #pragma unroll
@@ -257,9 +277,11 @@ __global__ __launch_bounds__(256) void gemm_f32_native_kernel(GemmBfArgs p,
   };
   auto lstore = [&](int buf) {
     uint8_t* s = lds + buf * kStage;
+    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < AP; i++)
-      *reinterpret_cast<v4f*>(s + lds_off(i * 32 + lrow, lchunk)) = ra[i];
+      *reinterpret_cast<v4f*>(s + lds_off(i * 32 + lrow, lchunk)) =
+          ((amask >> i) & 1) ? ra[i] : z;
 #pragma unroll
     for (int i = 0; i < BP; i++)
       *reinterpret_cast<v4f*>(s + lds_off(BM + i * 32 + lrow, lchunk)) = rb[i];
@@ -324,8 +346,11 @@ __global__ __launch_bounds__(256) void gemm_f32_native_kernel(GemmBfArgs p,
   }
 }
 
+// The vector load path needs 16-byte aligned rows and K a multiple of 4 (so a
+// 4-float group is either wholly inside [0, K) or wholly past it).
 static int a_vec_ok(const GemmBfArgs& a) {
-  return (a.lda % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.A) & 15) == 0);
+  return (a.lda % 4 == 0) && (a.K % 4 == 0) &&
+         ((reinterpret_cast<uintptr_t>(a.A) & 15) == 0);
 }
 
 template <int BM, int BN, int AT, bool BI8>

@@ -89,10 +89,11 @@ struct rh_model {
     }
     release_ws();
     for (auto& L : layers) {
-      destroy_weight(L.qkv);
-      destroy_weight(L.o);
-      destroy_weight(L.f1);
-      destroy_weight(L.f2);
+      for (rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) {
+        if (!w) continue;
+        destroy_weight(w);
+        ctx_release(ctx);  // never the last reference: the model holds one
+      }
       for (float* p : {L.ln1_g, L.ln1_b, L.ln2_g, L.ln2_b})
         if (p) (void)hipFree(p);
     }
@@ -439,6 +440,7 @@ int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_m
   if (quant < RH_QUANT_NONE || quant > RH_QUANT_FULL) return fail(RH_ERR_INVALID, "bad quant");
   auto* m = new rh_model();
   m->ctx = ctx;
+  ctx_retain(ctx);
   m->cfg = *cfg;
   m->quant = quant;
   m->attn_precision = quant == RH_QUANT_NONE ? 3 : 1;
@@ -492,11 +494,14 @@ int rh_model_finalize(rh_model* m) {
 
 void rh_model_destroy(rh_model* m) {
   if (!m) return;
+  rh_context* ctx = m->ctx;
   {
-    std::lock_guard<std::mutex> lk(m->ctx->mu);
+    std::lock_guard<std::mutex> lk(ctx->mu);
     m->release();
   }
+  m->ctx = nullptr;
   delete m;
+  ctx_release(ctx);
 }
 
 int rh_model_quantized(const rh_model* m) {

@@ -97,7 +97,9 @@ struct GemmBfArgs {
 enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 
 // Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
-hipError_t launch_gemm_i8(const GemmI8Args& a, hipStream_t s);
+// tile: 0 = automatic, 1..kI8TileConfigs = a fixed configuration.
+constexpr int kI8TileConfigs = 6;
+hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
 // a_terms: 1 or 2 bf16 terms for the fp32 activations.
 hipError_t launch_gemm_w8(const GemmBfArgs& a, int a_terms, hipStream_t s);
 hipError_t launch_gemm_f32(const GemmBfArgs& a, int algo, hipStream_t s);

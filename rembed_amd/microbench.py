@@ -1,0 +1,87 @@
+"""GEMM microbenchmarks on one GPU — the device counterpart of the
+reference's BenchmarkMatMulPacked* (internal/tensor/pack8_test.go,
+tensor_test.go benchmarks), at the encoder's real shapes.
+
+Each case is timed with the library's per-launch HIP events on its own
+stream. Usage:
+    python -m rembed_amd.microbench [--m 10102] [--iters 20] [--modes i8,w8,f32]
+"""
+import argparse
+import json
+import sys
+
+import numpy as np
+
+from . import _lib
+from . import tensor as T
+
+BERT_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+PEAK = {"i8": 5000.0, "w8": 2500.0, "f32": 2500.0}  # TOP/s of the MFMA used
+
+
+def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False):
+    rng = np.random.default_rng(k * 7 + n)
+    bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32) * 0.02
+    pack = {"i8": T.PackB8VNNI, "w8": T.PackB8, "f32": T.PackB}[mode]
+    pb = pack(ctx, bT, k, n, bias=bias)
+    a = ctx.upload(rng.standard_normal((m, k), dtype=np.float32))
+    dst = ctx.alloc(m * n * 4)
+    ldq = T.ldq_for(k)
+    qa = ctx.alloc(m * ldq)
+    rs = ctx.alloc(m * 4)
+    kind = {"i8": 0, "w8": 1, "f32": 2}[mode]
+    ctx.set_option(_lib.RH_CTX_I8_TILE, tile)
+    if mode == "i8":
+        T.QuantizeRowsU8(ctx, a, m, k, qa, ldq, rs)
+
+    def run():
+        if mode == "i8":
+            if acc_only:  # int32 accumulators only: the GEMM core
+                T.GemmU8S8I32(ctx, dst, qa, ldq, pb, m)
+            else:  # fp32 dequant epilogue (+bias, +GELU); quantize is not timed
+                T.Linear(ctx, dst, a, pb, m, act, qa, ldq, rs)
+        else:
+            T.Linear(ctx, dst, a, pb, m, act)
+
+    for _ in range(3):
+        run()
+    ctx.sync()
+    ctx.profile(True)
+    for _ in range(iters):
+        run()
+    ctx.sync()
+    st = ctx.profile_read(kind)
+    ctx.profile(False)
+    ctx.set_option(_lib.RH_CTX_I8_TILE, 0)
+    us = st["total_ms"] * 1e3 / st["launches"]
+    tops = st["total_ops"] / (st["total_ms"] * 1e-3) / 1e12
+    return {"mode": mode, "m": m, "k": k, "n": n, "act": act, "tile": tile,
+            "acc_only": acc_only, "us": round(us, 2), "tops": round(tops, 1),
+            "frac": round(tops / PEAK[mode], 4),
+            "gbps": round(st["total_bytes"] / (st["total_ms"] * 1e-3) / 1e9, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--m", type=int, default=10102)
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--modes", default="i8")
+    ap.add_argument("--tiles", default="0")
+    args = ap.parse_args()
+    ctx = T.Context(0)
+    for mode in args.modes.split(","):
+        for (k, n) in BERT_SHAPES:
+            for tile in [int(t) for t in args.tiles.split(",")]:
+                variants = [dict(acc_only=True), dict()] if mode == "i8" else [dict()]
+                if n == 3072:
+                    variants.append(dict(act=1))
+                for v in variants:
+                    r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile, **v)
+                    print(json.dumps(r), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

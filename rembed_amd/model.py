@@ -5,6 +5,7 @@ QuantizedActivations); embed()/embed_tokens() take token ids the way
 Embedder.Embed/EmbedTokens feed them (rembed.go:287-411), batched.
 """
 import ctypes
+import sys
 
 import numpy as np
 
@@ -61,6 +62,8 @@ class Model:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return  # the HIP runtime may already be torn down
         try:
             self.close()
         except Exception:

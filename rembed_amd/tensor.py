@@ -7,6 +7,7 @@ Errors surface as RembedError carrying the RH_* code, where the reference
 returns `error` (pack time) or panics (contract violations).
 """
 import ctypes
+import sys
 
 import numpy as np
 
@@ -40,8 +41,11 @@ class Context:
     def stream(self):
         return lib.rh_context_stream(self.h)
 
+    def set_option(self, option, value):
+        check(lib.rh_context_set_option(self.h, option, value))
+
     def set_f32_algo(self, algo):
-        check(lib.rh_context_set_f32_algo(self.h, algo))
+        self.set_option(_lib.RH_CTX_F32_ALGO, algo)
 
     def alloc(self, nbytes):
         return DeviceBuffer(self, nbytes)
@@ -85,6 +89,8 @@ class DeviceBuffer:
         self.ptr = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return  # the HIP runtime may already be torn down
         try:
             self.free()
         except Exception:
@@ -125,6 +131,8 @@ class PackedWeight:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return  # the HIP runtime may already be torn down
         try:
             self.close()
         except Exception:

@@ -2,7 +2,9 @@
 
 Integer work (activation quantization, u8 x s8 accumulators, the full-int8
 epilogue, GELU) must be bit-exact; the floating-point GEMMs are held to the
-reference's own float64 tolerance (internal/tensor/pack_test.go:55-67).
+reference's own float64 tolerance (internal/tensor/pack_test.go:55-67) or,
+for the bf16-split MFMA paths, to that tolerance plus the split's derived
+error bound (split_bound below).
 """
 import json
 import math
@@ -129,6 +131,39 @@ def test_i32_accumulators_bert_base_bit_exact(gpu_ctx, m, kn):
     assert np.array_equal(got[: m * n].reshape(m, n), want)
 
 
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6])
+def test_every_int8_tile_config_bit_exact(gpu_ctx, tile):
+    """Each int8 GEMM tile configuration (forced) gives the oracle's exact
+    accumulators and dequantized outputs, including M/N/K tails."""
+    from rembed_amd._lib import RH_CTX_I8_TILE
+    t = T()
+    rng = np.random.default_rng(40 + tile)
+    gpu_ctx.set_option(RH_CTX_I8_TILE, tile)
+    try:
+        for (m, k, n) in [(1, 1, 16), (13, 129, 64), (300, 384, 1536), (517, 100, 272),
+                          (2048, 768, 2304), (1999, 3072, 768)]:
+            say(f"tile {tile} m={m} k={k} n={n}")
+            a = rng.standard_normal((m, k), dtype=np.float32)
+            bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.05).astype(np.float32)
+            pb = t.PackB8VNNI(gpu_ctx, bT, k, n)
+            dst, qa, rs = run_vnni(gpu_ctx, a, pb, m)
+            st, q, sc, cs = O.pack_b8_vnni(bT, k, n)
+            want, qa_o, rs_o, acc_o = O.matmul_vnni(a, q, cs, sc)
+            assert np.array_equal(dst, want)
+            ldq = t.ldq_for(k)
+            qpad = np.zeros((m, ldq), np.uint8)
+            qpad[:, :k] = qa_o
+            dq = gpu_ctx.upload(qpad)
+            acc = gpu_ctx.upload(np.full(m * n + GUARD, 0x7EADBEEF, np.int32))
+            t.GemmU8S8I32(gpu_ctx, acc, dq, ldq, pb, m)
+            gpu_ctx.sync()
+            got = acc.download(np.int32, (m * n + GUARD,))
+            assert np.all(got[m * n:] == 0x7EADBEEF)
+            assert np.array_equal(got[: m * n].reshape(m, n), acc_o)
+    finally:
+        gpu_ctx.set_option(RH_CTX_I8_TILE, 0)
+
+
 def test_quantize_rows_bit_exact(gpu_ctx):
     t = T()
     rng = np.random.default_rng(77)
@@ -175,6 +210,19 @@ def f64_tol(k):
                KATS["packed_f32_shapes"]["tol_sqrtk"] * math.sqrt(k))
 
 
+# Error bounds of the bf16-split MFMA paths. A float x split into bf16 terms
+# hi = rne8(x), lo = rne8(x - hi) keeps |x - hi - lo| <= 2^-16 |x| (each
+# rounding to 8 significant bits loses at most 2^-8 relative). Weight-only
+# int8: q is exact in bf16, so |err| <= 2^-16 sum|a·deq|. fp32 via three
+# products hi·hi + hi·lo + lo·hi: |err| <= ~3·2^-16 sum|a·b|. Both get a
+# factor-2 margin plus the reference's fp32 tolerance for the accumulation.
+# An indexing mistake moves a result by a whole product |a_p·b_p|, far
+# above these bounds.
+def split_bound(a, b, k, eps, want):
+    mag = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64)).T
+    return eps * mag + f64_tol(k) * (1 + np.abs(want))
+
+
 @pytest.mark.parametrize("shape", KATS["packed_f32_shapes"]["shapes"])
 def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape):
     m, k, n = shape
@@ -191,8 +239,10 @@ def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape):
     got = t.matmul_host(gpu_ctx, a, pb)
     deq = q.astype(np.float64) * sc.astype(np.float64)[:, None]
     want = a.astype(np.float64) @ deq.T
-    err = np.abs(got - want) / (1 + np.abs(want))
-    assert err.max() <= f64_tol(k), err.max()
+    bound = split_bound(a, deq, k, 2.0 ** -15, want)
+    err = np.abs(got - want)
+    say(f"  max err {err.max():.3e}  worst err/bound {(err / bound).max():.3f}")
+    assert np.all(err <= bound)
 
 
 @pytest.mark.parametrize("algo", [0, 1])
@@ -211,8 +261,13 @@ def test_matmul_packed_f32_against_float64(gpu_ctx, shape, algo):
     finally:
         gpu_ctx.set_f32_algo(0)
     want = a.astype(np.float64) @ bT.astype(np.float64).T
-    err = np.abs(got - want) / (1 + np.abs(want))
-    assert err.max() <= f64_tol(k), err.max()
+    err = np.abs(got - want)
+    if algo == 1:  # native f32 MFMA: the reference's own tolerance
+        bound = f64_tol(k) * (1 + np.abs(want))
+    else:
+        bound = split_bound(a, bT, k, 2.0 ** -14, want)
+    say(f"  max err {err.max():.3e}  worst err/bound {(err / bound).max():.3f}")
+    assert np.all(err <= bound)
 
 
 def test_gelu_bit_exact(gpu_ctx):
