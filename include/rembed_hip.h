@@ -142,6 +142,17 @@ int rh_gemm_u8s8_i32(rh_context *ctx, int32_t *acc, const uint8_t *qa, int ldq,
 int rh_linear(rh_context *ctx, float *dst, const float *a, const rh_weight *w,
               int m, int act, uint8_t *qa, int ldq, float *row_scales);
 
+/* applyDense followed by QuantizeRowU8 of its output rows, for chaining
+ * full-int8 linears (bert.go:910-916: FFN1, GELU, then FFN2's row
+ * quantization) without an fp32 intermediate. Input rows are already
+ * quantized (qa/row_scales as produced by rh_quantize_rows_u8); output rows
+ * go to qa_out [m][ldq_out] (ldq_out >= n, multiple of 16) and rs_out [m].
+ * absmax_scratch holds m floats of caller scratch. The weight must be
+ * RH_MODE_A8W8. Output bytes equal QuantizeRowU8(act(a·Wᵀ + bias)) exactly. */
+int rh_linear_u8(rh_context *ctx, const uint8_t *qa, int ldq, const float *row_scales,
+                 const rh_weight *w, int m, int act, uint8_t *qa_out, int ldq_out,
+                 float *rs_out, float *absmax_scratch);
+
 /* Elementwise entry points used by parity tests (dev pointers). */
 int rh_gelu(rh_context *ctx, float *x, size_t n);          /* tensor.go:508-538 */
 int rh_layernorm(rh_context *ctx, float *x, const float *gamma,
@@ -189,8 +200,12 @@ int rh_model_set_tensor(rh_model *m, const char *name, const float *host,
 int rh_model_finalize(rh_model *m);
 void rh_model_destroy(rh_model *m);
 /* Per-model switches. RH_OPT_ATTN_PRECISION: 1 = bf16 attention operands,
- * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE). */
+ * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE).
+ * RH_OPT_FUSED_FFN1: 1 = full-int8 FFN1 writes u8 rows directly (two GEMM
+ * passes, no fp32 intermediate), 0 = fp32 GELU rows then QuantizeRowU8
+ * (default); both give identical bytes. */
 #define RH_OPT_ATTN_PRECISION 1
+#define RH_OPT_FUSED_FFN1 2
 int rh_model_set_option(rh_model *m, int option, int value);
 /* Model.Quantized / QuantizedActivations (bert.go:526-644). */
 int rh_model_quantized(const rh_model *m);

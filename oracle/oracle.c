@@ -431,6 +431,51 @@ void or_gelu(float *x, int n) {
   }
 }
 
+/* geluAVX2's per-lane sequence (internal/tensor/gelu_amd64.s:37-123): the
+ * same constants as geluScalar with FMAs where the assembly fuses (erf
+ * denominator, both Horner chains, the exponent rounding, the two-part ln2
+ * reduction, y*z+xe and 1-poly*e) and an exact division for t. */
+float or_gelu_avx2_lane(float v) {
+  float a = v * 0.7071067811865476f;
+  float aa = fabsf(a);
+  float t = 1.0f / fmaf(0.3275911f, aa, 1.0f);
+  float h = 1.061405429f;
+  h = fmaf(h, t, -1.453152027f);
+  h = fmaf(h, t, 1.421413741f);
+  h = fmaf(h, t, -0.284496736f);
+  h = fmaf(h, t, 0.254829592f);
+  float poly = h * t;
+  float xe = -(aa * aa);
+  if (xe < -87.33f) xe = -87.33f;
+  int32_t nfi = (int32_t)fmaf(EXP_LOG2E, xe, -0.5f);
+  float nf = (float)nfi;
+  xe = fmaf(-(EXP_C1), nf, xe);
+  xe = fmaf(-(EXP_C2), nf, xe);
+  float z = xe * xe;
+  float y = 1.9875691500e-4f;
+  y = fmaf(y, xe, 1.3981999507e-3f);
+  y = fmaf(y, xe, 8.3334519073e-3f);
+  y = fmaf(y, xe, 4.1665795894e-2f);
+  y = fmaf(y, xe, 1.6666665459e-1f);
+  y = fmaf(y, xe, 5.0000001201e-1f);
+  y = fmaf(y, z, xe);
+  y = y + 1.0f;
+  float e = y * pow2i(nfi);
+  float val = fmaf(-poly, e, 1.0f);
+  float erf = a < 0 ? -val : val; /* sign bit of a xor-ed in */
+  if (a == 0 && signbit(a)) erf = -val;
+  return (v * 0.5f) * (1.0f + erf);
+}
+
+/* GELU as the reference runs it on amd64 (internal/tensor/gelu_amd64.go:
+ * 16-26): the AVX2 body over the first n&~7 elements, geluScalar for the
+ * tail. */
+void or_gelu_ref(float *x, int n) {
+  int m = n & ~7;
+  for (int i = 0; i < m; i++) x[i] = or_gelu_avx2_lane(x[i]);
+  if (m < n) or_gelu(x + m, n - m);
+}
+
 /* GELUTanh, tensor.go:490-497 (float64 inside) */
 void or_gelu_tanh(float *x, int n) {
   const double c = 0.7978845608028654;
@@ -704,7 +749,7 @@ int or_bert_encode(const or_bert_model *m, const int32_t *ids, int seq,
     or_add(x, att, seq * H);
     or_layernorm(x, L->ln1_g, L->ln1_b, seq, H, c->eps);
     dense_apply(&L->ffn1, hid, x, seq);
-    for (int i = 0; i < seq; i++) or_gelu(hid + (size_t)i * I, I);
+    for (int i = 0; i < seq; i++) or_gelu_ref(hid + (size_t)i * I, I);
     dense_apply(&L->ffn2, att, hid, seq);
     or_add(x, att, seq * H);
     or_layernorm(x, L->ln2_g, L->ln2_b, seq, H, c->eps);

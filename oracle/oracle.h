@@ -82,6 +82,8 @@ void or_layernorm(float *x, const float *g, const float *b, int m, int n,
                   float eps);
 void or_rmsnorm(float *x, const float *g, int m, int n, float eps);
 void or_gelu(float *x, int n);      /* geluScalar, tensor.go:508-538 */
+float or_gelu_avx2_lane(float v);   /* geluAVX2 lane, gelu_amd64.s:37-123 */
+void or_gelu_ref(float *x, int n);  /* GELU on amd64, gelu_amd64.go:16-26 */
 void or_gelu_tanh(float *x, int n); /* tensor.go:490-497 */
 void or_silu(float *x, int n);      /* tensor.go:477-481 */
 void or_l2normalize(float *x, int n);

@@ -39,6 +39,8 @@ def _load():
         "or_layernorm": (None, [P, P, P, I, I, F]),
         "or_rmsnorm": (None, [P, P, I, I, F]),
         "or_gelu": (None, [P, I]),
+        "or_gelu_ref": (None, [P, I]),
+        "or_gelu_avx2_lane": (F, [F]),
         "or_gelu_tanh": (None, [P, I]),
         "or_silu": (None, [P, I]),
         "or_l2normalize": (None, [P, I]),
@@ -150,8 +152,17 @@ def rowwise(fn, x, *args):
 
 
 def gelu(x):
+    """geluScalar (internal/tensor/tensor.go:508-538)."""
     x = f32(x).copy()
     lib.or_gelu(_p(x), x.size)
+    return x
+
+
+def gelu_ref(x):
+    """GELU as rembed runs it on amd64: geluAVX2 over whole 8-lane groups of
+    the array, geluScalar for the tail (internal/tensor/gelu_amd64.go:16-26)."""
+    x = f32(x).copy()
+    lib.or_gelu_ref(_p(x), x.size)
     return x
 
 

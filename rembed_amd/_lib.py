@@ -28,6 +28,7 @@ RH_POOL_MEAN, RH_POOL_CLS, RH_POOL_LAST = 0, 1, 2
 RH_ACT_NONE, RH_ACT_GELU = 0, 1
 RH_ARCH_BERT = 0
 RH_OPT_ATTN_PRECISION = 1
+RH_OPT_FUSED_FFN1 = 2
 RH_CTX_F32_ALGO, RH_CTX_W8_TERMS, RH_CTX_I8_TILE = 1, 2, 3
 
 # Symbols the header declares (checked by the CPU test suite).
@@ -38,7 +39,7 @@ EXPORTS = [
     "rh_memcpy_d2h", "rh_profile_enable", "rh_profile_read", "rh_pack_weight",
     "rh_weight_destroy", "rh_weight_info", "rh_weight_export",
     "rh_quantize_rows_u8", "rh_matmul_packed", "rh_matmul_packed8",
-    "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_gelu",
+    "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_linear_u8", "rh_gelu",
     "rh_layernorm", "rh_model_create", "rh_model_set_tensor",
     "rh_model_finalize", "rh_model_destroy", "rh_model_set_option",
     "rh_model_quantized", "rh_model_quantized_activations", "rh_model_embed",
@@ -103,6 +104,7 @@ def _load():
         "rh_matmul_packed_vnni": (I, [P, P, P, P, I, P, I, P]),
         "rh_gemm_u8s8_i32": (I, [P, P, P, I, P, I]),
         "rh_linear": (I, [P, P, P, P, I, I, P, I, P]),
+        "rh_linear_u8": (I, [P, P, I, P, P, I, I, P, I, P, P]),
         "rh_gelu": (I, [P, P, S]),
         "rh_layernorm": (I, [P, P, P, P, I, I, F]),
         "rh_model_create": (I, [P, ctypes.POINTER(ModelConfig), I, ctypes.POINTER(P)]),

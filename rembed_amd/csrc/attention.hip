@@ -20,8 +20,25 @@ namespace rh {
 constexpr int kAttnQ = 128;   // queries per workgroup (4 waves x 32)
 constexpr int kAttnKV = 64;   // keys per LDS block
 
-template <int DH, int PREC>
+// 8 consecutive activations as floats, from fp32 (two 16-byte loads) or bf16
+// (one 16-byte load; widening is exact).
+__device__ __forceinline__ void load8(const float* src, float (&x)[8]) {
+  const v4f a = reinterpret_cast<const v4f*>(src)[0], b = reinterpret_cast<const v4f*>(src)[1];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    x[e] = a[e];
+    x[4 + e] = b[e];
+  }
+}
+__device__ __forceinline__ void load8(const __bf16* src, float (&x)[8]) {
+  const v8bf a = *reinterpret_cast<const v8bf*>(src);
+#pragma unroll
+  for (int e = 0; e < 8; e++) x[e] = (float)a[e];
+}
+
+template <int DH, int PREC, typename TIn>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
+  const TIn* qkv = static_cast<const TIn*>(p.qkv);
   constexpr int T = PREC == 3 ? 2 : 1;        // bf16 planes per operand
   constexpr int KS = DH / 16;                 // k-steps over dh
   constexpr int DT = DH / 32;                 // 32-wide d tiles of O^T
@@ -49,16 +66,19 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   // Q[q][s*16 + fg*8 + e].
   v8bf qh[KS], ql[KS];
   {
-    const float* qrow = p.qkv + (size_t)(r0 + qi) * p.ldqkv + p.q_off + h * DH;
+    // rows past the text read its last row; their outputs are not stored
+    const TIn* qrow = qkv + (size_t)(r0 + (qi < len ? qi : len - 1)) * p.ldqkv + p.q_off + h * DH;
 #pragma unroll
-    for (int s = 0; s < KS; s++)
+    for (int s = 0; s < KS; s++) {
+      float xq[8];
+      load8(qrow + s * 16 + fg * 8, xq);
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const float x = qi < len ? qrow[s * 16 + fg * 8 + e] : 0.0f;
-        const __bf16 hi = (__bf16)x;
+        const __bf16 hi = (__bf16)xq[e];
         qh[s][e] = hi;
-        if constexpr (PREC == 3) ql[s][e] = (__bf16)(x - (float)hi);
+        if constexpr (PREC == 3) ql[s][e] = (__bf16)(xq[e] - (float)hi);
       }
+    }
   }
 
   v16f o[DT];
@@ -82,16 +102,13 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
       // are zeroed after the loads (and masked out of the softmax below).
       const bool kok = kg < len;
       const size_t rowk = (size_t)(r0 + (kok ? kg : len - 1)) * p.ldqkv;
-      const v4f* k4 = reinterpret_cast<const v4f*>(p.qkv + rowk + p.k_off + kvh * DH + ch * 8);
-      const v4f* v4 = reinterpret_cast<const v4f*>(p.qkv + rowk + p.v_off + kvh * DH + ch * 8);
-      const v4f a0 = k4[0], a1 = k4[1], c0 = v4[0], c1 = v4[1];
       float kx[8], vx[8];
+      load8(qkv + rowk + p.k_off + kvh * DH + ch * 8, kx);
+      load8(qkv + rowk + p.v_off + kvh * DH + ch * 8, vx);
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        kx[e] = kok ? a0[e] : 0.0f;
-        kx[4 + e] = kok ? a1[e] : 0.0f;
-        vx[e] = kok ? c0[e] : 0.0f;
-        vx[4 + e] = kok ? c1[e] : 0.0f;
+      for (int e = 0; e < 8; e++) {
+        kx[e] = kok ? kx[e] : 0.0f;
+        vx[e] = kok ? vx[e] : 0.0f;
       }
       v8bf khi, klo;
 #pragma unroll
@@ -228,10 +245,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
 template <int DH>
 static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s) {
   dim3 grid(ceil_div(a.max_len, kAttnQ), a.heads, a.batch);
-  if (precision == 3)
-    hipLaunchKernelGGL((attention_kernel<DH, 3>), grid, dim3(256), 0, s, a);
+  if (a.in_bf16)  // bf16 input carries no low half: one-term products
+    hipLaunchKernelGGL((attention_kernel<DH, 1, __bf16>), grid, dim3(256), 0, s, a);
+  else if (precision == 3)
+    hipLaunchKernelGGL((attention_kernel<DH, 3, float>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((attention_kernel<DH, 1>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attention_kernel<DH, 1, float>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -227,69 +227,87 @@ void ctx_release(Context* ctx) {
   delete ctx;
 }
 
-// One linear: the GEMM family dispatch of applyDense (bert.go:282-301) with
-// bias/activation fused. For A8W8 the input must already be quantized into
-// qa/rs (row stride ldq) unless `a` is given, in which case it is quantized
-// here first.
+// The int8 GEMM over already-quantized rows with an explicit epilogue.
+// Profiled as kind 0; `ops` is the algorithmic work credited to the launch
+// (a recompute pass credits 0 so the pair counts 2·M·K·N once).
+int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
+                const float* rs, int m, int epi, void* out, int ldo, int act,
+                const float* bias, float* row_absmax, float* rs_out, double ops) {
+  if (m <= 0) return RH_OK;
+  GemmI8Args g{};
+  g.A = qa;
+  g.lda = ldq;
+  g.B = static_cast<const int8_t*>(w->d_data);
+  g.ldb = w->kp;
+  g.M = m;
+  g.N = w->n;
+  g.K = w->k;
+  g.row_scales = rs;
+  g.col_scales = w->d_scales;
+  g.colsum = w->d_colsum;
+  g.bias = bias;
+  g.out = out;
+  g.ldo = ldo;
+  g.act = act;
+  g.epi = epi;
+  g.row_absmax = row_absmax;
+  g.rs_out = rs_out;
+  const double M = m, K = w->k, N = w->n;
+  static const double out_bytes[] = {4, 2, 0, 1, 4};  // per output element
+  const double bytes = M * K + K * N + M * N * out_bytes[epi] + 4 * M + 8 * N +
+                       (bias ? 4 * N : 0) + (epi == EPI_QUANT ? 4 * M : 0);
+  int slot = -1;
+  hipError_t e = ctx->prof_begin(0, ops, bytes, &slot);
+  if (e == hipSuccess) e = launch_gemm_i8(g, ctx->i8_tile, ctx->stream);
+  if (e == hipSuccess) e = ctx->prof_end(slot);
+  if (e != hipSuccess) return hip_fail(e, "int8 gemm launch", __FILE__, __LINE__);
+  return RH_OK;
+}
+
+// One linear with fp32 output: the GEMM family dispatch of applyDense
+// (bert.go:282-301) with bias/activation fused. For A8W8 the input must
+// already be quantized into qa/rs (row stride ldq) unless quantize_first,
+// in which case `a` is quantized here first.
 int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
                float* dst, int ldc, int act, const float* bias, uint8_t* qa,
-               int ldq, float* rs, bool quantize_first, int32_t* acc_out) {
+               int ldq, float* rs, bool quantize_first) {
   if (m <= 0) return RH_OK;
   hipStream_t s = ctx->stream;
   const double M = m, K = w->k, N = w->n;
   const double ops = 2.0 * M * K * N;
-  int slot = -1;
-  hipError_t e = hipSuccess;
   if (w->mode == RH_MODE_A8W8) {
     if (quantize_first) {
-      e = launch_quantize_rows_u8(a, lda, m, w->k, qa, ldq, rs, s);
+      hipError_t e = launch_quantize_rows_u8(a, lda, m, w->k, qa, ldq, rs, s);
       if (e != hipSuccess) return hip_fail(e, "quantize_rows_u8", __FILE__, __LINE__);
     }
-    GemmI8Args g{};
-    g.A = qa;
-    g.lda = ldq;
-    g.B = static_cast<const int8_t*>(w->d_data);
-    g.ldb = w->kp;
-    g.M = m;
-    g.N = w->n;
-    g.K = w->k;
-    g.row_scales = rs;
-    g.col_scales = w->d_scales;
-    g.colsum = w->d_colsum;
-    g.bias = bias;
-    g.C = acc_out ? nullptr : dst;
-    g.Cacc = acc_out;
-    g.ldc = ldc;
-    g.act = act;
-    const double bytes = M * K + K * N + M * N * 4 + 4 * M + 8 * N + (bias ? 4 * N : 0);
-    e = ctx->prof_begin(0, ops, bytes, &slot);
-    if (e == hipSuccess) e = launch_gemm_i8(g, ctx->i8_tile, s);
-    if (e == hipSuccess) e = ctx->prof_end(slot);
-  } else {
-    GemmBfArgs g{};
-    g.A = a;
-    g.lda = lda;
-    g.B = w->d_data;
-    g.ldb = w->kp;
-    g.M = m;
-    g.N = w->n;
-    g.K = w->k;
-    g.col_scales = w->mode == RH_MODE_W8 ? w->d_scales : nullptr;
-    g.bias = bias;
-    g.C = dst;
-    g.ldc = ldc;
-    g.act = act;
-    if (w->mode == RH_MODE_W8) {
-      const double bytes = M * K * 4 + K * N + M * N * 4 + 4 * N + (bias ? 4 * N : 0);
-      e = ctx->prof_begin(1, ops, bytes, &slot);
-      if (e == hipSuccess) e = launch_gemm_w8(g, ctx->w8_terms, s);
-    } else {
-      const double bytes = M * K * 4 + K * N * 4 + M * N * 4 + (bias ? 4 * N : 0);
-      e = ctx->prof_begin(2, ops, bytes, &slot);
-      if (e == hipSuccess) e = launch_gemm_f32(g, ctx->f32_algo, s);
-    }
-    if (e == hipSuccess) e = ctx->prof_end(slot);
+    return run_gemm_i8(ctx, w, qa, ldq, rs, m, EPI_F32, dst, ldc, act, bias, nullptr,
+                       nullptr, ops);
   }
+  int slot = -1;
+  hipError_t e = hipSuccess;
+  GemmBfArgs g{};
+  g.A = a;
+  g.lda = lda;
+  g.B = w->d_data;
+  g.ldb = w->kp;
+  g.M = m;
+  g.N = w->n;
+  g.K = w->k;
+  g.col_scales = w->mode == RH_MODE_W8 ? w->d_scales : nullptr;
+  g.bias = bias;
+  g.C = dst;
+  g.ldc = ldc;
+  g.act = act;
+  if (w->mode == RH_MODE_W8) {
+    const double bytes = M * K * 4 + K * N + M * N * 4 + 4 * N + (bias ? 4 * N : 0);
+    e = ctx->prof_begin(1, ops, bytes, &slot);
+    if (e == hipSuccess) e = launch_gemm_w8(g, ctx->w8_terms, s);
+  } else {
+    const double bytes = M * K * 4 + K * N * 4 + M * N * 4 + (bias ? 4 * N : 0);
+    e = ctx->prof_begin(2, ops, bytes, &slot);
+    if (e == hipSuccess) e = launch_gemm_f32(g, ctx->f32_algo, s);
+  }
+  if (e == hipSuccess) e = ctx->prof_end(slot);
   if (e != hipSuccess) return hip_fail(e, "gemm launch", __FILE__, __LINE__);
   return RH_OK;
 }
@@ -490,11 +508,16 @@ int rh_quantize_rows_u8(rh_context* ctx, const float* a, int m, int k, uint8_t* 
   return RH_OK;
 }
 
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 static int check_gemm(const rh_weight* w, int mode, const float* a, const void* dst, int m) {
   if (!w) return fail(RH_ERR_INVALID, "null weight");
   if (mode >= 0 && w->mode != mode) return fail(RH_ERR_INVALID, "weight packed for another mode");
   if (m < 0) return fail(RH_ERR_INVALID, "negative m");
   if (m > 0 && (!a || !dst)) return fail(RH_ERR_INVALID, "null argument");
+  // the int8 epilogue writes 16-byte vectors
+  if (w->mode == RH_MODE_A8W8 && !aligned16(dst))
+    return fail(RH_ERR_INVALID, "output must be 16-byte aligned");
   return RH_OK;
 }
 
@@ -503,7 +526,7 @@ int rh_matmul_packed(rh_context* ctx, float* dst, const float* a, const rh_weigh
   if (st) return st;
   CTX_GUARD(ctx);
   return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
-                    nullptr, false, nullptr);
+                    nullptr, false);
 }
 
 int rh_matmul_packed8(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m) {
@@ -511,7 +534,7 @@ int rh_matmul_packed8(rh_context* ctx, float* dst, const float* a, const rh_weig
   if (st) return st;
   CTX_GUARD(ctx);
   return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
-                    nullptr, false, nullptr);
+                    nullptr, false);
 }
 
 int rh_matmul_packed_vnni(rh_context* ctx, float* dst, const float* a, const rh_weight* w,
@@ -523,7 +546,7 @@ int rh_matmul_packed_vnni(rh_context* ctx, float* dst, const float* a, const rh_
     return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
   CTX_GUARD(ctx);
   return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, qa, ldq,
-                    row_scales, true, nullptr);
+                    row_scales, true);
 }
 
 int rh_gemm_u8s8_i32(rh_context* ctx, int32_t* acc, const uint8_t* qa, int ldq,
@@ -534,9 +557,10 @@ int rh_gemm_u8s8_i32(rh_context* ctx, int32_t* acc, const uint8_t* qa, int ldq,
   if (m > 0 && (!acc || !qa)) return fail(RH_ERR_INVALID, "null argument");
   if (ldq < w->k || ldq % 16 != 0)
     return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+  if (!aligned16(acc) || !aligned16(qa)) return fail(RH_ERR_INVALID, "buffers must be 16-byte aligned");
   CTX_GUARD(ctx);
-  return run_linear(ctx, w, nullptr, 0, m, nullptr, w->n, ACT_NONE, nullptr,
-                    const_cast<uint8_t*>(qa), ldq, nullptr, false, acc);
+  return run_gemm_i8(ctx, w, qa, ldq, nullptr, m, EPI_ACC, acc, w->n, ACT_NONE, nullptr,
+                     nullptr, nullptr, 2.0 * m * w->k * w->n);
 }
 
 int rh_linear(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m,
@@ -551,7 +575,31 @@ int rh_linear(rh_context* ctx, float* dst, const float* a, const rh_weight* w, i
   }
   CTX_GUARD(ctx);
   return run_linear(ctx, w, a, w->k, m, dst, w->n, act, w->d_bias, qa, ldq, row_scales,
-                    true, nullptr);
+                    true);
+}
+
+int rh_linear_u8(rh_context* ctx, const uint8_t* qa, int ldq, const float* row_scales,
+                 const rh_weight* w, int m, int act, uint8_t* qa_out, int ldq_out,
+                 float* rs_out, float* absmax_scratch) {
+  if (!w) return fail(RH_ERR_INVALID, "null weight");
+  if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight must be RH_MODE_A8W8");
+  if (m < 0) return fail(RH_ERR_INVALID, "negative m");
+  if (act != RH_ACT_NONE && act != RH_ACT_GELU) return fail(RH_ERR_INVALID, "unknown act");
+  if (m > 0 && (!qa || !row_scales || !qa_out || !rs_out || !absmax_scratch))
+    return fail(RH_ERR_INVALID, "null argument");
+  if (ldq < w->k || ldq % 16 != 0)
+    return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+  if (ldq_out < w->n || ldq_out % 16 != 0)
+    return fail(RH_ERR_INVALID, "ldq_out must be >= n and a multiple of 16");
+  if (!aligned16(qa) || !aligned16(qa_out)) return fail(RH_ERR_INVALID, "buffers must be 16-byte aligned");
+  CTX_GUARD(ctx);
+  if (m == 0) return RH_OK;
+  RH_HIP(launch_fill_zero(absmax_scratch, m, ctx->stream));
+  int st = run_gemm_i8(ctx, w, qa, ldq, row_scales, m, EPI_ABSMAX, nullptr, 0, act, w->d_bias,
+                       absmax_scratch, nullptr, 2.0 * m * w->k * w->n);
+  if (st) return st;
+  return run_gemm_i8(ctx, w, qa, ldq, row_scales, m, EPI_QUANT, qa_out, ldq_out, act,
+                     w->d_bias, absmax_scratch, rs_out, 0.0);
 }
 
 int rh_gelu(rh_context* ctx, float* x, size_t n) {

@@ -61,5 +61,8 @@ int quantize_b8_vnni(const float* bT, int k, int n, std::vector<int8_t>& q,
                      std::vector<float>& scales, std::vector<int32_t>& colsum);
 int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
                float* dst, int ldc, int act, const float* bias, uint8_t* qa, int ldq,
-               float* rs, bool quantize_first, int32_t* acc_out);
+               float* rs, bool quantize_first);
+int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
+                const float* rs, int m, int epi, void* out, int ldo, int act,
+                const float* bias, float* row_absmax, float* rs_out, double ops);
 }  // namespace rh

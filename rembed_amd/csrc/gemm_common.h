@@ -16,11 +16,13 @@ __device__ __forceinline__ int xcd_remap(int b, int nwg) {
   return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
-// LDS tiles hold rows of 128 bytes = 8 chunks of 16 bytes; chunk c of row r
-// lives at slot c ^ (r & 7) so that the 32 rows one MFMA fragment read
-// touches spread over all slots (bank-conflict avoidance).
+// LDS tiles hold rows of 128 bytes = 8 chunks of 16 bytes. A 16-byte
+// fragment read serves 16 consecutive rows per LDS cycle on gfx950 (64 banks
+// = 256 bytes, i.e. two rows per bank window), so chunk c of row r lives at
+// slot c ^ ((r ^ (r >> 3)) & 7): rows r and r+8 of one window then differ in
+// slot, and any 8 aligned rows stay distinct for a 32-bank phase too.
 __device__ __forceinline__ int lds_off(int r, int c) {
-  return (r << 7) + ((c ^ (r & 7)) << 4);
+  return (r << 7) + ((c ^ ((r ^ (r >> 3)) & 7)) << 4);
 }
 
 // erf-GELU with exactly the float32 operation sequence of the reference's
@@ -56,8 +58,47 @@ __device__ __forceinline__ float gelu_ref(float v) {
   return 0.5f * v * (1.0f + erf);
 }
 
+// erf-GELU as rembed computes it on amd64 for every whole 8-lane group of a
+// row (geluAVX2, internal/tensor/gelu_amd64.s:37-123): geluScalar's
+// constants with fused multiply-adds exactly where the assembly fuses them,
+// an IEEE division for t and trunc-toward-zero exponent rounding.
+__device__ __forceinline__ float gelu_avx2(float v) {
+  const float a = v * 0.7071067811865476f;
+  const float aa = fabsf(a);
+  const float t = 1.0f / __builtin_fmaf(0.3275911f, aa, 1.0f);
+  float h = 1.061405429f;
+  h = __builtin_fmaf(h, t, -1.453152027f);
+  h = __builtin_fmaf(h, t, 1.421413741f);
+  h = __builtin_fmaf(h, t, -0.284496736f);
+  h = __builtin_fmaf(h, t, 0.254829592f);
+  const float poly = h * t;
+  float xe = -(aa * aa);
+  if (xe < -87.33f) xe = -87.33f;
+  const int nfi = (int)__builtin_fmaf(1.44269504088896341f, xe, -0.5f);
+  const float nf = (float)nfi;
+  xe = __builtin_fmaf(-0.693359375f, nf, xe);
+  xe = __builtin_fmaf(2.12194440e-4f, nf, xe);
+  const float z = xe * xe;
+  float y = 1.9875691500e-4f;
+  y = __builtin_fmaf(y, xe, 1.3981999507e-3f);
+  y = __builtin_fmaf(y, xe, 8.3334519073e-3f);
+  y = __builtin_fmaf(y, xe, 4.1665795894e-2f);
+  y = __builtin_fmaf(y, xe, 1.6666665459e-1f);
+  y = __builtin_fmaf(y, xe, 5.0000001201e-1f);
+  y = __builtin_fmaf(y, z, xe);
+  y = y + 1.0f;
+  const float e = y * __int_as_float((nfi + 127) << 23);
+  const float val = __builtin_fmaf(-poly, e, 1.0f);
+  // the sign bit of a is xor-ed into val (covers a == -0 as well)
+  const float erf = __int_as_float(__float_as_int(val) ^ (__float_as_int(a) & 0x80000000));
+  return (v * 0.5f) * (1.0f + erf);
+}
+
+// GEMM epilogue activation. Output rows always have n % 16 == 0 columns
+// (the packers require it), so every element lies in a whole 8-lane group and
+// takes the geluAVX2 sequence, as the reference's GELU(row) does.
 __device__ __forceinline__ float apply_act(float v, int act) {
-  return act == ACT_GELU ? gelu_ref(v) : v;
+  return act == ACT_GELU ? gelu_avx2(v) : v;
 }
 
 }  // namespace rh

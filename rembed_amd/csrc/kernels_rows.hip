@@ -250,9 +250,23 @@ hipError_t launch_pool(const float* x, int H, const int32_t* cu, int batch,
   return hipGetLastError();
 }
 
+__global__ void fill_zero_kernel(float* x, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = 0.0f;
+}
+
+hipError_t launch_fill_zero(float* x, int n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, x, n);
+  return hipGetLastError();
+}
+
+// GELU over a flat array as tensor.GELU does on amd64 (gelu_amd64.go:16-26):
+// the geluAVX2 sequence for whole 8-element groups, geluScalar for the tail.
 __global__ void gelu_kernel(float* x, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) x[i] = gelu_ref(x[i]);
+  if (i >= n) return;
+  x[i] = i < (n & ~(size_t)7) ? gelu_avx2(x[i]) : gelu_ref(x[i]);
 }
 
 hipError_t launch_gelu(float* x, size_t n, hipStream_t s) {

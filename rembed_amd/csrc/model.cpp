@@ -57,12 +57,14 @@ struct rh_model {
         *emb_b = nullptr;
   std::vector<Layer> layers;
   int attn_precision = 3;
+  bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
 
   // workspace, sized for cap rows / cap_batch texts
   int cap = 0, cap_batch = 0, cap_ids = 0;
   float *x = nullptr, *qkv = nullptr, *ctxb = nullptr, *y = nullptr, *hid = nullptr;
-  uint8_t* qa = nullptr;
-  float* rs = nullptr;
+  __bf16* qkvh = nullptr;                 // bf16 QKV rows (full-int8 path)
+  uint8_t *qa = nullptr, *qa2 = nullptr;  // u8 activations: width H / width I
+  float *rs = nullptr, *rs2 = nullptr, *absmax = nullptr;
   int32_t* cu_d = nullptr;
   int32_t* ids_d = nullptr;
   float* out_d = nullptr;
@@ -75,10 +77,12 @@ struct rh_model {
 
   void release_ws() {
     for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
-                    (void*)rs, (void*)cu_d, (void*)ids_d, (void*)out_d})
+                    (void*)rs, (void*)cu_d, (void*)ids_d, (void*)out_d, (void*)qkvh,
+                    (void*)qa2, (void*)rs2, (void*)absmax})
       if (p) (void)hipFree(p);
-    x = qkv = ctxb = y = hid = rs = out_d = nullptr;
-    qa = nullptr;
+    x = qkv = ctxb = y = hid = rs = out_d = rs2 = absmax = nullptr;
+    qa = qa2 = nullptr;
+    qkvh = nullptr;
     cu_d = ids_d = nullptr;
     cap = cap_batch = cap_ids = 0;
   }
@@ -122,18 +126,23 @@ struct rh_model {
     if (rows > cap) {
       int newcap = (int)round_up(rows, 256);
       for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
-                      (void*)rs})
+                      (void*)rs, (void*)qkvh, (void*)qa2, (void*)rs2, (void*)absmax})
         if (p) RH_HIP(hipFree(p));
-      x = qkv = ctxb = y = hid = rs = nullptr;
-      qa = nullptr;
+      x = qkv = ctxb = y = hid = rs = rs2 = absmax = nullptr;
+      qa = qa2 = nullptr;
+      qkvh = nullptr;
       const size_t r = newcap;
       RH_HIP(dalloc(&x, r * H));
       RH_HIP(dalloc(&qkv, r * 3 * H));
+      RH_HIP(dalloc(&qkvh, r * 3 * H));
       RH_HIP(dalloc(&ctxb, r * H));
       RH_HIP(dalloc(&y, r * H));
       RH_HIP(dalloc(&hid, r * I));
-      RH_HIP(dalloc(&qa, r * round_up(std::max(H, I), 16)));
+      RH_HIP(dalloc(&qa, r * round_up(H, 16)));
+      RH_HIP(dalloc(&qa2, r * round_up(I, 16)));
       RH_HIP(dalloc(&rs, r));
+      RH_HIP(dalloc(&rs2, r));
+      RH_HIP(dalloc(&absmax, r));
       cap = newcap;
     }
     if (batch > cap_batch) {
@@ -246,14 +255,25 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     attn_ops += 4.0 * L * L * dh * heads;
   }
 
+  const double MH = M;
   for (size_t li = 0; li < layers.size(); li++) {
     const Layer& L = layers[li];
-    // x already quantized into qa/rs if the QKV weight is int8-activation.
-    st = run_linear(ctx, L.qkv, x, H, M, qkv, 3 * H, ACT_NONE, L.qkv->d_bias, qa,
-                    ldq_for(H), rs, false, nullptr);
+    // QKV projection. x was quantized into qa/rs by the producer if the
+    // weight is full-int8. When attention runs on bf16 operands, a full-int8
+    // QKV writes bf16 directly (attention would round the fp32 values to the
+    // same bf16 on load), halving the write.
+    const bool qkv_bf16 = needs_q(L.qkv) && attn_precision == 1;
+    if (qkv_bf16) {
+      st = run_gemm_i8(ctx, L.qkv, qa, ldq_for(H), rs, M, EPI_BF16, qkvh, 3 * H, ACT_NONE,
+                       L.qkv->d_bias, nullptr, nullptr, 2.0 * MH * H * 3 * H);
+    } else {
+      st = run_linear(ctx, L.qkv, x, H, M, qkv, 3 * H, ACT_NONE, L.qkv->d_bias, qa,
+                      ldq_for(H), rs, false);
+    }
     if (st) return st;
     AttnArgs aa{};
-    aa.qkv = qkv;
+    aa.qkv = qkv_bf16 ? (const void*)qkvh : (const void*)qkv;
+    aa.in_bf16 = qkv_bf16 ? 1 : 0;
     aa.ldqkv = 3 * H;
     aa.q_off = 0;
     aa.k_off = H;
@@ -272,17 +292,36 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     RH_HIP(launch_attention(aa, attn_precision, s));
     RH_HIP(ctx->prof_end(slot));
     st = run_linear(ctx, L.o, ctxb, H, M, y, H, ACT_NONE, L.o->d_bias, qa, ldq_for(H),
-                    rs, needs_q(L.o), nullptr);
+                    rs, needs_q(L.o));
     if (st) return st;
     const bool qf1 = needs_q(L.f1);
     RH_HIP(launch_add_layernorm(x, y, H, L.ln1_g, L.ln1_b, M, H, eps(),
                                 qf1 ? qa : nullptr, ldq_for(H), qf1 ? rs : nullptr, s));
-    st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_GELU, L.f1->d_bias, qa, ldq_for(H),
-                    rs, false, nullptr);
-    if (st) return st;
-    st = run_linear(ctx, L.f2, hid, I, M, y, H, ACT_NONE, L.f2->d_bias, qa, ldq_for(I),
-                    rs, needs_q(L.f2), nullptr);
-    if (st) return st;
+    if (fused_ffn1 && qf1 && needs_q(L.f2)) {
+      // FFN1 + GELU + QuantizeRowU8 without the fp32 intermediate: pass 1
+      // finds each row's |max| of the GELU output, pass 2 recomputes the
+      // identical values and writes the u8 bytes and row scales FFN2 reads.
+      // Both passes see the same int32 accumulators, so the bytes equal
+      // QuantizeRowU8 of the fp32 GELU row (bert.go:910-916).
+      const double ops1 = 2.0 * MH * H * I;
+      RH_HIP(launch_fill_zero(absmax, M, s));
+      st = run_gemm_i8(ctx, L.f1, qa, ldq_for(H), rs, M, EPI_ABSMAX, nullptr, 0, ACT_GELU,
+                       L.f1->d_bias, absmax, nullptr, ops1);
+      if (st) return st;
+      st = run_gemm_i8(ctx, L.f1, qa, ldq_for(H), rs, M, EPI_QUANT, qa2, ldq_for(I),
+                       ACT_GELU, L.f1->d_bias, absmax, rs2, 0.0);
+      if (st) return st;
+      st = run_gemm_i8(ctx, L.f2, qa2, ldq_for(I), rs2, M, EPI_F32, y, H, ACT_NONE,
+                       L.f2->d_bias, nullptr, nullptr, 2.0 * MH * I * H);
+      if (st) return st;
+    } else {
+      st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_GELU, L.f1->d_bias, qa, ldq_for(H),
+                      rs, false);
+      if (st) return st;
+      st = run_linear(ctx, L.f2, hid, I, M, y, H, ACT_NONE, L.f2->d_bias, qa2, ldq_for(I),
+                      rs2, needs_q(L.f2));
+      if (st) return st;
+    }
     const bool qn = li + 1 < layers.size() && needs_q(layers[li + 1].qkv);
     RH_HIP(launch_add_layernorm(x, y, H, L.ln2_g, L.ln2_b, M, H, eps(),
                                 qn ? qa : nullptr, ldq_for(H), qn ? rs : nullptr, s));
@@ -454,6 +493,11 @@ int rh_model_set_option(rh_model* m, int option, int value) {
   if (option == RH_OPT_ATTN_PRECISION) {
     if (value != 1 && value != 3) return fail(RH_ERR_INVALID, "attn precision must be 1 or 3");
     m->attn_precision = value;
+    return RH_OK;
+  }
+  if (option == RH_OPT_FUSED_FFN1) {
+    if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fused FFN1 must be 0 or 1");
+    m->fused_ffn1 = value != 0;
     return RH_OK;
   }
   return fail(RH_ERR_INVALID, "unknown option");

@@ -56,6 +56,17 @@ constexpr int kWeightKPad = 128;
 // passes after AddBias: internal/model/bert.go:913-915, qwen3.go:530-539).
 enum Act : int { ACT_NONE = 0, ACT_GELU = 1 };
 
+// Epilogue variants of the int8 GEMM. value = act(float32(real)·rs·cs + bias)
+enum I8Epi : int {
+  EPI_F32 = 0,     // out fp32 [M][ldo] = value
+  EPI_BF16 = 1,    // out bf16 [M][ldo] = value rounded to nearest even
+  EPI_ABSMAX = 2,  // no out: row_absmax[row] = max over the row of |value|
+                   // (atomic max on the float bits; zero it beforehand)
+  EPI_QUANT = 3,   // out u8 [M][ldo] = QuantizeRowU8(value row) using
+                   // row_absmax from a preceding EPI_ABSMAX pass; rs_out[M]
+  EPI_ACC = 4      // out int32 [M][ldo] = reference-form accumulators
+};
+
 struct GemmI8Args {
   const uint8_t* A;  // u8 activations (+128 offset, QuantizeRowU8 format) [M][lda]
   int lda;           // bytes, multiple of 16
@@ -66,10 +77,12 @@ struct GemmI8Args {
   const float* col_scales;  // [N]
   const int32_t* colsum;    // [N]
   const float* bias;        // [N] or null
-  float* C;                 // [M][ldc] fp32 or null
-  int32_t* Cacc;            // [M][ldc] reference-form accumulators or null
-  int ldc;
+  void* out;                // per epi; rows 16-byte aligned
+  int ldo;                  // elements, multiple of 4
   int act;
+  int epi;
+  float* row_absmax;        // EPI_ABSMAX target / EPI_QUANT input
+  float* rs_out;            // EPI_QUANT row scales
 };
 
 // B formats of the bf16-MFMA GEMM family.
@@ -97,9 +110,12 @@ struct GemmBfArgs {
 enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 
 // Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
-// tile: 0 = automatic, 1..kI8TileConfigs = a fixed configuration.
-constexpr int kI8TileConfigs = 6;
+// tile: 0 = automatic, 1 = 256x256, 2 = 256x128, 3 = 128x128.
+constexpr int kI8TileConfigs = 3;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
+int pick_i8_tile(int M, int N);
+// fills n floats with zero (graph-capture safe, unlike hipMemsetAsync)
+hipError_t launch_fill_zero(float* x, int n, hipStream_t s);
 // a_terms: 1 or 2 bf16 terms for the fp32 activations.
 hipError_t launch_gemm_w8(const GemmBfArgs& a, int a_terms, hipStream_t s);
 hipError_t launch_gemm_f32(const GemmBfArgs& a, int algo, hipStream_t s);
@@ -152,7 +168,8 @@ hipError_t launch_pool(const float* x, int H, const int32_t* cu, int batch,
 // Multi-head attention over a packed varlen batch (bert.go:853-902 per
 // text): q/k/v read from the fused QKV rows, ctx written [M][H].
 struct AttnArgs {
-  const float* qkv;  // [M][ldqkv]
+  const void* qkv;   // [M][ldqkv] fp32, or bf16 when in_bf16
+  int in_bf16;
   int ldqkv;
   int q_off, k_off, v_off;  // column offsets of head 0
   const int32_t* cu;        // [batch+1]

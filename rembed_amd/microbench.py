@@ -19,7 +19,7 @@ BERT_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
 PEAK = {"i8": 5000.0, "w8": 2500.0, "f32": 2500.0}  # TOP/s of the MFMA used
 
 
-def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False):
+def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u8=False):
     rng = np.random.default_rng(k * 7 + n)
     bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
     bias = rng.standard_normal(n, dtype=np.float32) * 0.02
@@ -35,9 +35,16 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False):
     if mode == "i8":
         T.QuantizeRowsU8(ctx, a, m, k, qa, ldq, rs)
 
+    ldo = T.ldq_for(n)
+    qout = ctx.alloc(m * ldo) if fused_u8 else None
+    rs_out = ctx.alloc(m * 4) if fused_u8 else None
+    absmax = ctx.alloc(m * 4) if fused_u8 else None
+
     def run():
         if mode == "i8":
-            if acc_only:  # int32 accumulators only: the GEMM core
+            if fused_u8:  # linear + QuantizeRowU8 of the outputs (two passes)
+                T.LinearU8(ctx, qa, ldq, rs, pb, m, act, qout, ldo, rs_out, absmax)
+            elif acc_only:  # int32 accumulators only: the GEMM core
                 T.GemmU8S8I32(ctx, dst, qa, ldq, pb, m)
             else:  # fp32 dequant epilogue (+bias, +GELU); quantize is not timed
                 T.Linear(ctx, dst, a, pb, m, act, qa, ldq, rs)
@@ -54,10 +61,11 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False):
     st = ctx.profile_read(kind)
     ctx.profile(False)
     ctx.set_option(_lib.RH_CTX_I8_TILE, 0)
-    us = st["total_ms"] * 1e3 / st["launches"]
+    per_call = 2 if fused_u8 else 1  # the fused variant launches two GEMM passes
+    us = st["total_ms"] * 1e3 / st["launches"] * per_call
     tops = st["total_ops"] / (st["total_ms"] * 1e-3) / 1e12
     return {"mode": mode, "m": m, "k": k, "n": n, "act": act, "tile": tile,
-            "acc_only": acc_only, "us": round(us, 2), "tops": round(tops, 1),
+            "acc_only": acc_only, "fused_u8": fused_u8, "us": round(us, 2), "tops": round(tops, 1),
             "frac": round(tops / PEAK[mode], 4),
             "gbps": round(st["total_bytes"] / (st["total_ms"] * 1e-3) / 1e9, 1)}
 
@@ -68,14 +76,23 @@ def main():
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--modes", default="i8")
     ap.add_argument("--tiles", default="0")
+    ap.add_argument("--shapes", default="", help="k,n;k,n;... (default: BERT-base)")
+    ap.add_argument("--variants", default="", help="comma list of acc,fp32,gelu")
     args = ap.parse_args()
+    shapes = BERT_SHAPES
+    if args.shapes:
+        shapes = [tuple(int(x) for x in s.split(",")) for s in args.shapes.split(";")]
     ctx = T.Context(0)
     for mode in args.modes.split(","):
-        for (k, n) in BERT_SHAPES:
+        for (k, n) in shapes:
             for tile in [int(t) for t in args.tiles.split(",")]:
                 variants = [dict(acc_only=True), dict()] if mode == "i8" else [dict()]
                 if n == 3072:
                     variants.append(dict(act=1))
+                if args.variants:
+                    table = {"acc": dict(acc_only=True), "fp32": dict(), "gelu": dict(act=1),
+                             "u8gelu": dict(act=1, fused_u8=True)}
+                    variants = [table[v] for v in args.variants.split(",")]
                 for v in variants:
                     r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile, **v)
                     print(json.dumps(r), flush=True)

@@ -72,6 +72,9 @@ class Model:
     def set_attention_precision(self, prec):
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_ATTN_PRECISION, prec))
 
+    def set_fused_ffn1(self, on):
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSED_FFN1, 1 if on else 0))
+
     def quantized(self):
         return bool(lib.rh_model_quantized(self.h))
 

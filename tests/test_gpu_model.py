@@ -109,6 +109,19 @@ def test_batch_matches_single(gpu_ctx, minilm, quant):
         assert np.array_equal(single[0], batch[b]), b
 
 
+def test_fused_ffn1_identical(gpu_ctx, minilm):
+    """The fused full-int8 FFN1 (u8 rows written by the GEMM, no fp32
+    intermediate) yields the same embeddings, bit for bit, as fp32 GELU rows
+    followed by QuantizeRowU8 (bert.go:910-916)."""
+    shape, t, ids, lens = minilm
+    from rembed_amd.model import Model
+    m = Model(gpu_ctx, shape, t, 2)
+    plain = m.embed(ids, lens)
+    m.set_fused_ffn1(True)
+    fused = m.embed(ids, lens)
+    assert np.array_equal(plain, fused)
+
+
 def test_embed_tokens_matches_oracle_hidden(gpu_ctx, minilm):
     shape, t, ids, lens = minilm
     from rembed_amd.model import Model

@@ -283,6 +283,27 @@ def test_gelu_and_tanh_against_float64():
     assert np.max(np.abs(silu - want_s)) <= 1e-6
 
 
+def test_gelu_avx2_restatement_tracks_scalar():
+    """TestGELUVectorMatchesScalar (internal/tensor/tensor_test.go:220-251):
+    the fused AVX2 sequence stays within 1e-6 of geluScalar over the range,
+    the clamp region and signed zeros, for every length class; and within
+    1e-6 of the float64 erf-GELU (tensor_test.go:186-200)."""
+    base = list(np.arange(-30, 30, 0.2337, dtype=np.float32)) + \
+        [0.0, -0.0, 1e-20, -1e-20, 90.0, -90.0, 12.5, -12.5]
+    base = np.array(base, np.float32)
+    for n in (1, 2, 7, 8, 9, 15, 16, 17, 64, 129, len(base)):
+        vec, scal = O.gelu_ref(base[:n]), O.gelu(base[:n])
+        assert np.max(np.abs(vec - scal)) <= 1e-6, n
+        if n >= 8:  # the vector body really ran (not the scalar fallback)
+            lanes = np.array([O.lib.or_gelu_avx2_lane(float(v)) for v in base[:n & ~7]],
+                             np.float32)
+            assert np.array_equal(vec[:n & ~7], lanes)
+    xs = np.arange(-6, 6.0001, 0.25, dtype=np.float32)
+    want = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in xs.astype(np.float64)])
+    lanes = np.array([O.lib.or_gelu_avx2_lane(float(v)) for v in xs], np.float32)
+    assert np.max(np.abs(lanes - want)) <= 1e-6
+
+
 def test_expf32_erff32_bounds():
     ke = KATS["expf32"]
     for x in np.arange(-87, 88, 0.013, dtype=np.float32):
