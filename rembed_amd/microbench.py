@@ -70,6 +70,22 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
             "gbps": round(st["total_bytes"] / (st["total_ms"] * 1e-3) / 1e9, 1)}
 
 
+def copy_calibration(mib, iters):
+    """A device-to-device copy of `mib` MiB through torch's elementwise copy
+    kernel: each launch reads and writes exactly mib MiB, so a profiler's
+    per-dispatch byte counters can be scaled against it."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_mib": mib, "launches": iters,
+                      "bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4}))
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--m", type=int, default=10102)
@@ -78,7 +94,12 @@ def main():
     ap.add_argument("--tiles", default="0")
     ap.add_argument("--shapes", default="", help="k,n;k,n;... (default: BERT-base)")
     ap.add_argument("--variants", default="", help="comma list of acc,fp32,gelu")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (calibrates "
+                         "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
     args = ap.parse_args()
+    if args.copy_mib:
+        return copy_calibration(args.copy_mib, args.iters)
     shapes = BERT_SHAPES
     if args.shapes:
         shapes = [tuple(int(x) for x in s.split(",")) for s in args.shapes.split(";")]

@@ -1,0 +1,86 @@
+"""Summaries of rocprofv3 output for the committed profiles.
+
+    python -m rembed_amd.profsummary stats  <kernel_stats.csv> <steps> <title> <command>
+    python -m rembed_amd.profsummary traffic <fetch_dir_csv> <write_dir_csv>
+                                     <copy_fetch_csv> <copy_write_csv> <copy_mib> <command>
+
+`stats` renders a --kernel-trace --stats table (per-kernel calls, average
+and per-step time). `traffic` turns two --pmc runs (FETCH_SIZE, then
+WRITE_SIZE, KiB per dispatch) into HBM bytes per launch, each counter scaled
+by what it reads for a plain device copy of known size, and prints the JSON
+that bench.py reads for the GEMM's `roofline.traffic`.
+"""
+import collections
+import csv
+import json
+import sys
+
+GEMM = "gemm_i8_kernel"
+
+
+def _kernel_means(path):
+    vals = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        vals[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return {k: (len(v), sum(v) / len(v)) for k, v in vals.items()}
+
+
+def stats(path, steps, title, command):
+    rows = list(csv.DictReader(open(path)))
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    print(f"# {title}\n\nCommand: `{command}`\n")
+    print("| kernel | calls | avg µs | µs per step | share |")
+    print("|---|---:|---:|---:|---:|")
+    for r in rows:
+        t = float(r["TotalDurationNs"])
+        print(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+              f"{t / 1e3 / steps:.1f} | {100 * t / total:.1f}% |")
+    gemm = [r for r in rows if GEMM in r["Name"]]
+    gt = sum(float(r["TotalDurationNs"]) for r in gemm)
+    gc = sum(int(r["Calls"]) for r in gemm)
+    if gc:
+        print(f"\nAll `{GEMM}` launches: {gc} calls, average {gt / gc / 1e3:.2f} µs, "
+              f"{gt / 1e3 / steps:.1f} µs per step ({steps} steps incl. warm-up).")
+
+
+def traffic(fetch, write, cfetch, cwrite, copy_mib, command):
+    f, w = _kernel_means(fetch), _kernel_means(write)
+    cf, cw = _kernel_means(cfetch), _kernel_means(cwrite)
+    copy_kib = copy_mib * 1024.0
+    # the copy kernel: the launch named "copy" that writes the most
+    ck = max((k for k in cw if "copy" in k.lower()), key=lambda k: cw[k][1])
+    f_scale = copy_kib / cf[ck][1]
+    w_scale = copy_kib / cw[ck][1]
+    print("# HBM traffic per launch (rocprofv3 --pmc)\n")
+    print(f"Command: `{command}`\n")
+    print(f"Calibration: a {copy_mib} MiB device copy (`{ck}`) reads FETCH_SIZE "
+          f"{cf[ck][1]:.0f} KiB and WRITE_SIZE {cw[ck][1]:.0f} KiB per launch, so the "
+          f"counters are scaled by {f_scale:.3f} (fetch) and {w_scale:.3f} (write).\n")
+    print("| kernel | launches | fetch MB | write MB | total MB |")
+    print("|---|---:|---:|---:|---:|")
+    g_n = g_b = 0.0
+    for k in f:
+        if k not in w:
+            continue
+        n = f[k][0]
+        fb = f[k][1] * 1024 * f_scale
+        wb = w[k][1] * 1024 * w_scale
+        print(f"| `{k[:90]}` | {n} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | {(fb + wb) / 1e6:.1f} |")
+        if GEMM in k:
+            g_n += n
+            g_b += n * (fb + wb)
+    out = {"bytes_per_launch": g_b / g_n if g_n else None, "launches": int(g_n),
+           "fetch_scale": f_scale, "write_scale": w_scale}
+    print(f"\nAverage over all `{GEMM}` launches: {out['bytes_per_launch'] / 1e6:.1f} MB "
+          "per launch.\n")
+    print("```json\n" + json.dumps(out) + "\n```")
+    return out
+
+
+if __name__ == "__main__":
+    if sys.argv[1] == "stats":
+        stats(sys.argv[2], int(sys.argv[3]), sys.argv[4], sys.argv[5])
+    elif sys.argv[1] == "traffic":
+        o = traffic(*sys.argv[2:6], int(sys.argv[6]), sys.argv[7])
+        if len(sys.argv) > 8:
+            json.dump(o, open(sys.argv[8], "w"))
