@@ -55,6 +55,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ffn1", choices=["fused", "split"], default="split",
+                    help="full-int8 FFN1: fused = GELU rows re-quantized inside the GEMM "
+                         "(two passes, no fp32 intermediate); split = fp32 rows + QuantizeRowU8")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path "
@@ -74,6 +77,7 @@ def main():
     ctx = T.Context(0)
     model = Model(ctx, shape, tensors, QUANT_FULL)
     assert model.quantized_activations(), "full-int8 path did not take"
+    model.set_fused_ffn1(args.ffn1 == "fused")
     ids_dev = ctx.upload(ids)
     out_dev = ctx.alloc(BATCH * shape.hidden * 4)
 
@@ -139,7 +143,7 @@ def main():
             "global_batch": BATCH, "seq_len": SEQ, "layers": shape.layers,
             "hidden": shape.hidden, "heads": shape.heads,
             "intermediate": shape.intermediate, "real_tokens": tokens,
-            "gemm_rows_M": tokens, "parallelism": "none (1 GPU)",
+            "gemm_rows_M": tokens, "ffn1": args.ffn1, "parallelism": "none (1 GPU)",
         },
         "roofline": {
             "bound": "mfma",

@@ -63,6 +63,49 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   if (lane == 0) row_scales[row] = scale;
 }
 
+// Single-pass variant for 16-byte aligned rows with k % 4 == 0 and
+// k <= 256 * V: the row stays in registers (V float4 per lane), so HBM sees
+// one read of the row and one write of its bytes.
+template <int V>
+__global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
+    const float* __restrict__ a, int lda, int m, int k, uint8_t* __restrict__ qa,
+    int ldq, float* __restrict__ row_scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= m) return;
+  const float* src = a + (size_t)row * lda;
+  v4f x[V];
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int i = (lane + 64 * e) * 4;
+    x[e] = i < k ? *reinterpret_cast<const v4f*>(src + i) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x[e][0]), fabsf(x[e][1])), fmaxf(fabsf(x[e][2]), fabsf(x[e][3]))));
+  }
+  mx = wave_max(mx);
+  float scale = mx / 127.0f;
+  if (scale == 0.0f) scale = 1.0f;
+  const float inv = 1.0f / scale;
+  uint8_t* dst = qa + (size_t)row * ldq;
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int i = (lane + 64 * e) * 4;
+    if (i < k)
+      *reinterpret_cast<uint32_t*>(dst + i) =
+          (uint32_t)quant_u8(x[e][0], inv) | ((uint32_t)quant_u8(x[e][1], inv) << 8) |
+          ((uint32_t)quant_u8(x[e][2], inv) << 16) | ((uint32_t)quant_u8(x[e][3], inv) << 24);
+  }
+  for (int i = k + lane * 4; i < ldq; i += 256) *reinterpret_cast<uint32_t*>(dst + i) = 0u;
+  if (lane == 0) row_scales[row] = scale;
+}
+
+template <int V>
+static void launch_qvec(const float* a, int lda, int m, int k, uint8_t* qa, int ldq,
+                        float* rs, hipStream_t s) {
+  hipLaunchKernelGGL((quantize_rows_vec_kernel<V>), dim3(ceil_div(m, kRowsPerBlock)),
+                     dim3(256), 0, s, a, lda, m, k, qa, ldq, rs);
+}
+
 hipError_t launch_quantize_rows_u8(const float* a, int lda, int m, int k,
                                    uint8_t* qa, int ldq, float* row_scales,
                                    hipStream_t s) {
@@ -71,6 +114,18 @@ hipError_t launch_quantize_rows_u8(const float* a, int lda, int m, int k,
   const int vec = (k % 4 == 0) && (lda % 4 == 0) && (ldq % 4 == 0) &&
                   ((reinterpret_cast<uintptr_t>(a) & 15) == 0) &&
                   ((reinterpret_cast<uintptr_t>(qa) & 3) == 0);
+  if (vec && k <= 4096) {
+    const int v = ceil_div(k, 256);
+    if (v <= 1) launch_qvec<1>(a, lda, m, k, qa, ldq, row_scales, s);
+    else if (v <= 2) launch_qvec<2>(a, lda, m, k, qa, ldq, row_scales, s);
+    else if (v <= 3) launch_qvec<3>(a, lda, m, k, qa, ldq, row_scales, s);
+    else if (v <= 4) launch_qvec<4>(a, lda, m, k, qa, ldq, row_scales, s);
+    else if (v <= 6) launch_qvec<6>(a, lda, m, k, qa, ldq, row_scales, s);
+    else if (v <= 8) launch_qvec<8>(a, lda, m, k, qa, ldq, row_scales, s);
+    else if (v <= 12) launch_qvec<12>(a, lda, m, k, qa, ldq, row_scales, s);
+    else launch_qvec<16>(a, lda, m, k, qa, ldq, row_scales, s);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(quantize_rows_kernel, dim3(ceil_div(m, kRowsPerBlock)),
                      dim3(256), 0, s, a, lda, m, k, qa, ldq, row_scales, vec);
   return hipGetLastError();
@@ -185,12 +240,105 @@ __global__ __launch_bounds__(256) void add_ln_kernel(
                 row_scales ? row_scales + row : nullptr);
 }
 
+// float4 variant for H % 4 == 0 (every encoder width): lane l holds columns
+// 4(l + 64e) .. +3. Same operation order per element as ln_row_finish.
+template <int V>
+__global__ __launch_bounds__(256) void add_ln_vec_kernel(
+    float* __restrict__ x, const float* __restrict__ y, int ldy,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int m,
+    int H, float eps, uint8_t* __restrict__ qa, int ldq,
+    float* __restrict__ row_scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= m) return;
+  float* xr = x + (size_t)row * H;
+  const float* yr = y ? y + (size_t)row * ldy : nullptr;
+  v4f v[V];
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int j = (lane + 64 * e) * 4;
+    v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (j < H) {
+      t = *reinterpret_cast<const v4f*>(xr + j);
+      if (yr) t = t + *reinterpret_cast<const v4f*>(yr + j);  // Add, tensor.go:383-387
+    }
+    v[e] = t;
+    s += (t[0] + t[1]) + (t[2] + t[3]);
+  }
+  const float mean = wave_sum(s) / (float)H;
+  float s2 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int j = (lane + 64 * e) * 4;
+    if (j < H) {
+      const v4f d = v[e] - mean;
+      s2 += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+    }
+  }
+  const float var = wave_sum(s2) / (float)H;
+  const float inv = 1.0f / sqrtf(var + eps);
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int j = (lane + 64 * e) * 4;
+    if (j < H) {
+      const v4f g = *reinterpret_cast<const v4f*>(gamma + j);
+      const v4f b = *reinterpret_cast<const v4f*>(beta + j);
+      v4f o;
+#pragma unroll
+      for (int c = 0; c < 4; c++) o[c] = (v[e][c] - mean) * inv * g[c] + b[c];
+      v[e] = o;
+      *reinterpret_cast<v4f*>(xr + j) = o;
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
+    }
+  }
+  if (qa) {
+    mx = wave_max(mx);
+    float scale = mx / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    const float qinv = 1.0f / scale;
+    uint8_t* q = qa + (size_t)row * ldq;
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int j = (lane + 64 * e) * 4;
+      if (j < H)
+        *reinterpret_cast<uint32_t*>(q + j) =
+            (uint32_t)quant_u8(v[e][0], qinv) | ((uint32_t)quant_u8(v[e][1], qinv) << 8) |
+            ((uint32_t)quant_u8(v[e][2], qinv) << 16) | ((uint32_t)quant_u8(v[e][3], qinv) << 24);
+    }
+    for (int j = H + lane * 4; j < ldq; j += 256) *reinterpret_cast<uint32_t*>(q + j) = 0u;
+    if (lane == 0) row_scales[row] = scale;
+  }
+}
+
+template <int V>
+static void launch_alnv(float* x, const float* y, int ldy, const float* gamma,
+                        const float* beta, int m, int H, float eps, uint8_t* qa, int ldq,
+                        float* rs, hipStream_t s) {
+  hipLaunchKernelGGL((add_ln_vec_kernel<V>), dim3(ceil_div(m, kRowsPerBlock)), dim3(256),
+                     0, s, x, y, ldy, gamma, beta, m, H, eps, qa, ldq, rs);
+}
+
 hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
                                 const float* gamma, const float* beta, int m,
                                 int H, float eps, uint8_t* qa, int ldq,
                                 float* row_scales, hipStream_t s) {
   if (m <= 0) return hipSuccess;
   if (H > 64 * kMaxPerLane) return hipErrorInvalidValue;
+  const bool vec = H % 4 == 0 && (!y || ldy % 4 == 0) && (!qa || ldq % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                     reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) &
+                    15) == 0;
+  if (vec) {
+    const int v = ceil_div(H, 256);
+    if (v <= 1) launch_alnv<1>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
+    else if (v <= 2) launch_alnv<2>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
+    else if (v <= 3) launch_alnv<3>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
+    else if (v <= 4) launch_alnv<4>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
+    else launch_alnv<8>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(add_ln_kernel, dim3(ceil_div(m, kRowsPerBlock)), dim3(256),
                      0, s, x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales);
   return hipGetLastError();
