@@ -12,6 +12,7 @@
  * kernels rely on the same property, internal/tensor/pack_test.go:133-225).
  */
 #include "oracle.h"
+#include "oracle_int.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -329,7 +330,7 @@ float or_expf32(float x) {
 }
 
 /* expNonPos, fastmath.go:93-109 (the form Softmax and GELU inline). */
-static float exp_nonpos(float x) {
+float or__exp_nonpos(float x) {
   if (x < -87.33f) x = -87.33f;
   float nf = (float)(int32_t)(x * EXP_LOG2E - 0.5f);
   x -= nf * EXP_C1;
@@ -370,7 +371,7 @@ void or_softmax(float *x, int m, int n) {
       if (row[j] > maxv) maxv = row[j];
     float sum = 0.0f;
     for (int j = 0; j < n; j++) {
-      float e = exp_nonpos(row[j] - maxv);
+      float e = or__exp_nonpos(row[j] - maxv);
       row[j] = e;
       sum += e;
     }
@@ -425,7 +426,7 @@ void or_gelu(float *x, int n) {
         t * (0.254829592f +
              t * (-0.284496736f +
                   t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
-    float e = exp_nonpos(-a * a);
+    float e = or__exp_nonpos(-a * a);
     float erf = sign * (1.0f - poly * e);
     x[i] = 0.5f * v * (1.0f + erf);
   }
@@ -551,17 +552,6 @@ void or_matmul_serial(float *dst, const float *a, const float *bT, int m,
 
 /* denseWeight, internal/model/bert.go:32-39: exactly one of the three
  * layouts is populated (newDense's fallback chain, bert.go:263-278). */
-typedef struct {
-  int kind; /* 0 fp32, 1 weight-only int8, 2 full int8 */
-  int in, out;
-  const float *raw; /* fp32: borrowed bT */
-  float *rawcopy;   /* fp32 fused QKV copy owned here */
-  int8_t *q;
-  float *scales;
-  int32_t *colsum;
-  float *bias; /* owned (fused QKV) or NULL */
-  const float *bias_ref;
-} or_dense;
 
 typedef struct {
   or_dense qkv, attn_out, ffn1, ffn2;
@@ -575,7 +565,7 @@ struct or_bert_model {
   or_layer *layers;
 };
 
-static void dense_init(or_dense *d, const float *raw, int owned_raw,
+void or__dense_init(or_dense *d, const float *raw, int owned_raw,
                        const float *bias, int owned_bias, int in, int out,
                        int quant) {
   memset(d, 0, sizeof(*d));
@@ -617,7 +607,7 @@ static void dense_init(or_dense *d, const float *raw, int owned_raw,
   if (owned_raw) d->rawcopy = (float *)raw;
 }
 
-static void dense_free(or_dense *d) {
+void or__dense_free(or_dense *d) {
   free(d->q);
   free(d->scales);
   free(d->colsum);
@@ -627,7 +617,7 @@ static void dense_free(or_dense *d) {
 
 /* applyDense, bert.go:282-301: GEMM by the mode the weight took, then a
  * separate AddBias pass. */
-static void dense_apply(const or_dense *d, float *dst, const float *x,
+void or__dense_apply(const or_dense *d, float *dst, const float *x,
                         int seq) {
   if (d->kind == 2)
     or_matmul_vnni(dst, x, d->q, d->colsum, d->scales, seq, d->in, d->out,
@@ -667,12 +657,12 @@ or_bert_model *or_bert_create(const or_bert_config *cfg, int quant,
     memcpy(qkvb, t[1], sizeof(float) * H);
     memcpy(qkvb + H, t[3], sizeof(float) * H);
     memcpy(qkvb + 2 * H, t[5], sizeof(float) * H);
-    dense_init(&L->qkv, qkvw, 1, qkvb, 1, H, 3 * H, quant);
-    dense_init(&L->attn_out, t[6], 0, t[7], 0, H, H, quant);
+    or__dense_init(&L->qkv, qkvw, 1, qkvb, 1, H, 3 * H, quant);
+    or__dense_init(&L->attn_out, t[6], 0, t[7], 0, H, H, quant);
     L->ln1_g = t[8];
     L->ln1_b = t[9];
-    dense_init(&L->ffn1, t[10], 0, t[11], 0, H, I, quant);
-    dense_init(&L->ffn2, t[12], 0, t[13], 0, I, H, quant);
+    or__dense_init(&L->ffn1, t[10], 0, t[11], 0, H, I, quant);
+    or__dense_init(&L->ffn2, t[12], 0, t[13], 0, I, H, quant);
     L->ln2_g = t[14];
     L->ln2_b = t[15];
   }
@@ -682,10 +672,10 @@ or_bert_model *or_bert_create(const or_bert_config *cfg, int quant,
 void or_bert_free(or_bert_model *m) {
   if (!m) return;
   for (int l = 0; l < m->cfg.layers; l++) {
-    dense_free(&m->layers[l].qkv);
-    dense_free(&m->layers[l].attn_out);
-    dense_free(&m->layers[l].ffn1);
-    dense_free(&m->layers[l].ffn2);
+    or__dense_free(&m->layers[l].qkv);
+    or__dense_free(&m->layers[l].attn_out);
+    or__dense_free(&m->layers[l].ffn1);
+    or__dense_free(&m->layers[l].ffn2);
   }
   free(m->layers);
   free(m);
@@ -728,7 +718,7 @@ int or_bert_encode(const or_bert_model *m, const int32_t *ids, int seq,
   float scale = (float)(1.0 / sqrt((double)dh));
   for (int li = 0; li < c->layers; li++) {
     const or_layer *L = &m->layers[li];
-    dense_apply(&L->qkv, qkv, x, seq);
+    or__dense_apply(&L->qkv, qkv, x, seq);
     /* Per-head attention, bert.go:853-902. */
     for (int h = 0; h < heads; h++) {
       int off = h * dh;
@@ -745,12 +735,12 @@ int or_bert_encode(const or_bert_model *m, const int32_t *ids, int seq,
       for (int i = 0; i < seq; i++)
         memcpy(ctx + (size_t)i * H + off, ch + (size_t)i * dh, sizeof(float) * dh);
     }
-    dense_apply(&L->attn_out, att, ctx, seq);
+    or__dense_apply(&L->attn_out, att, ctx, seq);
     or_add(x, att, seq * H);
     or_layernorm(x, L->ln1_g, L->ln1_b, seq, H, c->eps);
-    dense_apply(&L->ffn1, hid, x, seq);
+    or__dense_apply(&L->ffn1, hid, x, seq);
     for (int i = 0; i < seq; i++) or_gelu_ref(hid + (size_t)i * I, I);
-    dense_apply(&L->ffn2, att, hid, seq);
+    or__dense_apply(&L->ffn2, att, hid, seq);
     or_add(x, att, seq * H);
     or_layernorm(x, L->ln2_g, L->ln2_b, seq, H, c->eps);
   }

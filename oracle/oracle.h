@@ -141,6 +141,53 @@ int or_bert_embed_batch(const or_bert_model *m, const int32_t *ids,
                         const int32_t *lens, int batch, int stride,
                         float *out, int threads);
 
+/* ---- decoder-family embedders (internal/model/qwen3.go, gemma3.go) ---- */
+#define OR_ARCH_QWEN3 1
+#define OR_ARCH_GEMMA3 2
+typedef struct {
+  int arch; /* OR_ARCH_* */
+  int vocab, hidden, layers, heads, kv_heads, head_dim, inter;
+  float eps;
+  double rope_theta;         /* Qwen3 RopeTheta; Gemma GlobalRopeTheta */
+  double rope_local_theta;   /* Gemma LocalRopeTheta */
+  int sliding_window;        /* Gemma: local layers keep |i-j| < window */
+  int sliding_pattern;       /* Gemma: layer l is global iff (l+1) % pattern == 0 */
+  int query_pre_attn_scalar; /* Gemma: scores scaled by 1/sqrt(scalar) */
+  int dense_hidden;          /* Gemma Dense head width (0: none) */
+  int pooling, normalize;
+  int max_seq;
+} or_dec_config;
+
+/* Per-layer tensors, HF layouts ([out][in] for projections):
+ * Qwen3 (11):  input_layernorm q_proj k_proj v_proj o_proj q_norm k_norm
+ *              post_attention_layernorm gate_proj up_proj down_proj
+ * Gemma3 (13): input_layernorm q_proj k_proj v_proj o_proj q_norm k_norm
+ *              post_attention_layernorm pre_feedforward_layernorm
+ *              post_feedforward_layernorm gate_proj up_proj down_proj
+ * Gemma norm weights are the checkpoint's (unit offset added at load). */
+#define OR_QWEN3_TENSORS_PER_LAYER 11
+#define OR_GEMMA3_TENSORS_PER_LAYER 13
+
+typedef struct or_dec_model or_dec_model;
+or_dec_model *or_dec_create(const or_dec_config *cfg, int quant,
+                            const float *embed, const float *final_norm,
+                            const float *const *layer_tensors,
+                            const float *dense1, const float *dense2);
+void or_dec_free(or_dec_model *m);
+/* 0 fp32, 1 weight-only int8, 2 full int8: the mode layer 0's q_proj took */
+int or_dec_quantized_kind(const or_dec_model *m);
+int or_dec_encode(const or_dec_model *m, const int32_t *ids, int seq, float *x);
+int or_dec_forward(const or_dec_model *m, const int32_t *ids, int seq, float *out);
+int or_dec_embed_batch(const or_dec_model *m, const int32_t *ids,
+                       const int32_t *lens, int batch, int stride, float *out,
+                       int threads);
+
+/* building blocks (exported for the unit tests) */
+void or_rope_table(float *cos_t, float *sin_t, int seq, int dh, double theta);
+void or_apply_rope(float *x, int seq, int dh, const float *cos_t, const float *sin_t);
+void or_flash_causal_head(const float *qh, const float *kh, const float *vh,
+                          float *out, int seq, int dh, float scale);
+
 /* Which int8 dot-product body the oracle picked at run time (for reports):
  * 2 = AVX-512-VNNI intrinsics, 0 = portable C. Both produce identical
  * integers. */

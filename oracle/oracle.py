@@ -52,6 +52,15 @@ def _load():
         "or_bert_forward": (I, [P, P, I, P]),
         "or_bert_embed_batch": (I, [P, P, P, I, I, P, I]),
         "or_vnni_kind": (I, []),
+        "or_dec_create": (P, [P, I, P, P, P, P, P]),
+        "or_dec_free": (None, [P]),
+        "or_dec_quantized_kind": (I, [P]),
+        "or_dec_encode": (I, [P, P, I, P]),
+        "or_dec_forward": (I, [P, P, I, P]),
+        "or_dec_embed_batch": (I, [P, P, P, I, I, P, I]),
+        "or_rope_table": (None, [P, P, I, I, ctypes.c_double]),
+        "or_apply_rope": (None, [P, I, I, P, P]),
+        "or_flash_causal_head": (None, [P, P, P, P, I, I, F]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -252,3 +261,118 @@ class BertOracle:
         if st:
             raise RuntimeError(f"oracle embed status {st}")
         return out
+
+
+# ---- decoder-family embedders (Qwen3, EmbeddingGemma) ------------------------------
+
+ARCH_QWEN3, ARCH_GEMMA3 = 1, 2
+
+
+class DecConfig(ctypes.Structure):
+    _fields_ = [("arch", ctypes.c_int), ("vocab", ctypes.c_int), ("hidden", ctypes.c_int),
+                ("layers", ctypes.c_int), ("heads", ctypes.c_int), ("kv_heads", ctypes.c_int),
+                ("head_dim", ctypes.c_int), ("inter", ctypes.c_int), ("eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_double), ("rope_local_theta", ctypes.c_double),
+                ("sliding_window", ctypes.c_int), ("sliding_pattern", ctypes.c_int),
+                ("query_pre_attn_scalar", ctypes.c_int), ("dense_hidden", ctypes.c_int),
+                ("pooling", ctypes.c_int), ("normalize", ctypes.c_int), ("max_seq", ctypes.c_int)]
+
+
+QWEN3_LAYER_ORDER = [
+    "input_layernorm.weight", "self_attn.q_proj.weight", "self_attn.k_proj.weight",
+    "self_attn.v_proj.weight", "self_attn.o_proj.weight", "self_attn.q_norm.weight",
+    "self_attn.k_norm.weight", "post_attention_layernorm.weight", "mlp.gate_proj.weight",
+    "mlp.up_proj.weight", "mlp.down_proj.weight",
+]
+GEMMA3_LAYER_ORDER = QWEN3_LAYER_ORDER[:8] + [
+    "pre_feedforward_layernorm.weight", "post_feedforward_layernorm.weight",
+    "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight",
+]
+
+
+class DecoderOracle:
+    """The reference's per-text unpadded Qwen3 / EmbeddingGemma forward on the
+    CPU (internal/model/qwen3.go, gemma3.go). `shape` is a
+    rembed_amd.synthetic.DecoderShape; tensors use HF names (Gemma's Dense
+    head as "2_Dense.linear.weight" / "3_Dense.linear.weight")."""
+
+    def __init__(self, shape, tensors, quant):
+        self._keep = {k: f32(v) for k, v in tensors.items()}
+        t = self._keep
+        gemma = shape.arch == ARCH_GEMMA3
+        cfg = DecConfig(shape.arch, shape.vocab, shape.hidden, shape.layers, shape.heads,
+                        shape.kv_heads, shape.head_dim, shape.intermediate, shape.eps,
+                        shape.rope_theta, shape.rope_local_theta, shape.sliding_window,
+                        shape.sliding_pattern, shape.query_pre_attn_scalar,
+                        shape.dense_hidden, shape.pooling, shape.normalize, shape.max_seq)
+        self.shape = shape
+        order = GEMMA3_LAYER_ORDER if gemma else QWEN3_LAYER_ORDER
+        ptrs = [t[f"layers.{l}.{n}"].ctypes.data for l in range(shape.layers) for n in order]
+        self._arr = (ctypes.c_void_p * len(ptrs))(*ptrs)
+        d1 = t.get("2_Dense.linear.weight")
+        d2 = t.get("3_Dense.linear.weight")
+        self.h = lib.or_dec_create(
+            ctypes.byref(cfg), quant, _p(t["embed_tokens.weight"]), _p(t["norm.weight"]),
+            ctypes.cast(self._arr, ctypes.c_void_p),
+            _p(d1) if d1 is not None else None, _p(d2) if d2 is not None else None)
+        if not self.h:
+            raise RuntimeError("oracle: bad decoder config")
+
+    def close(self):
+        if self.h:
+            lib.or_dec_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def quantized_kind(self):
+        return lib.or_dec_quantized_kind(self.h)
+
+    def encode(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
+        st = lib.or_dec_encode(self.h, _p(ids), ids.shape[0], _p(out))
+        if st:
+            raise RuntimeError(f"oracle encode status {st}")
+        return out
+
+    def forward(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty(self.shape.hidden, np.float32)
+        st = lib.or_dec_forward(self.h, _p(ids), ids.shape[0], _p(out))
+        if st:
+            raise RuntimeError(f"oracle forward status {st}")
+        return out
+
+    def embed_batch(self, ids, lens, threads=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        lens = np.ascontiguousarray(lens, np.int32)
+        out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
+        st = lib.or_dec_embed_batch(self.h, _p(ids), _p(lens), ids.shape[0], ids.shape[1],
+                                    _p(out), threads)
+        if st:
+            raise RuntimeError(f"oracle embed status {st}")
+        return out
+
+
+def rope_table(seq, dh, theta):
+    c = np.empty((seq, dh // 2), np.float32)
+    s = np.empty((seq, dh // 2), np.float32)
+    lib.or_rope_table(_p(c), _p(s), seq, dh, float(theta))
+    return c, s
+
+
+def apply_rope(x, cos_t, sin_t):
+    x = f32(x).copy()
+    seq, dh = x.shape
+    lib.or_apply_rope(_p(x), seq, dh, _p(f32(cos_t)), _p(f32(sin_t)))
+    return x
+
+
+def flash_causal_head(qh, kh, vh, scale):
+    qh, kh, vh = f32(qh), f32(kh), f32(vh)
+    seq, dh = qh.shape
+    out = np.empty((seq, dh), np.float32)
+    lib.or_flash_causal_head(_p(qh), _p(kh), _p(vh), _p(out), seq, dh, scale)
+    return out

@@ -82,3 +82,90 @@ def token_batch(batch, stride, len_lo, len_hi, vocab=30522, id_lo=1000,
         ids[b, : lens[b]] = rng.integers(id_lo, vocab, size=lens[b])
     return ids, lens
 
+
+
+# ---- decoder-family embedders (Qwen3, EmbeddingGemma) ------------------------------
+
+ARCH_QWEN3, ARCH_GEMMA3 = 1, 2
+
+
+@dataclass(frozen=True)
+class DecoderShape:
+    """Config of a Qwen3 / EmbeddingGemma embedder (internal/model/config.go:56-77)."""
+    name: str
+    arch: int
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    intermediate: int
+    vocab: int
+    eps: float = 1e-6
+    rope_theta: float = 1e6           # Qwen3 RopeTheta / Gemma GlobalRopeTheta
+    rope_local_theta: float = 1e4     # Gemma LocalRopeTheta
+    sliding_window: int = 0           # Gemma effective window: |i-j| < w
+    sliding_pattern: int = 1          # Gemma: layer l global iff (l+1) % pattern == 0
+    query_pre_attn_scalar: int = 0    # Gemma attention scale 1/sqrt(scalar)
+    dense_hidden: int = 0             # Gemma Dense head width
+    pooling: int = 2                  # 0 mean, 1 cls, 2 last token
+    normalize: int = 1
+    max_seq: int = 32768
+
+
+# Qwen3-Embedding-0.6B-shaped: 28 layers, hidden 1024, 16 Q / 8 KV heads of 128,
+# SwiGLU 3072, RoPE theta 1e6, last-token pooling.
+QWEN3_0_6B = DecoderShape("qwen3-0.6b", ARCH_QWEN3, 28, 1024, 16, 8, 128, 3072, 151669)
+# EmbeddingGemma-300m-shaped: 24 layers, hidden 768, 3 Q / 1 KV heads of 256,
+# GeGLU 1152, alternating sliding-window-512 (effective 257) / global layers,
+# mean pooling + Dense 768 -> 3072 -> 768.
+GEMMA3_300M = DecoderShape("embeddinggemma-300m", ARCH_GEMMA3, 24, 768, 3, 1, 256, 1152,
+                           262144, rope_theta=1e6, rope_local_theta=1e4,
+                           sliding_window=257, sliding_pattern=6,
+                           query_pre_attn_scalar=256, dense_hidden=3072, pooling=0)
+
+
+def decoder_tensors(shape: DecoderShape, seed: int = 0x5EED0001, bf16: bool = False):
+    """HF-named float32 tensors for a Qwen3 / Gemma3 backbone: projections and
+    the embedding table N(0, 0.02) (rounded through bf16 when `bf16`, as a
+    BF16 checkpoint widens, internal/safetensors/safetensors.go:199-203);
+    Qwen3 RMSNorm weights 1 + N(0, 0.02); Gemma norm weights N(0, 0.02)
+    (the checkpoint form, unit offset added at load)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    H, I, dh = shape.hidden, shape.intermediate, shape.head_dim
+    qdim, kvdim = shape.heads * dh, shape.kv_heads * dh
+    gemma = shape.arch == ARCH_GEMMA3
+
+    def normal(*dims):
+        w = rng.standard_normal(dims, dtype=np.float32) * np.float32(0.02)
+        if bf16:
+            w = (w.view(np.uint32) + np.uint32(0x7FFF) + ((w.view(np.uint32) >> 16) & 1)
+                 ) & np.uint32(0xFFFF0000)
+            w = w.view(np.float32)
+        return w.astype(np.float32)
+
+    def norm(n):
+        w = rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)
+        return (w if gemma else np.float32(1.0) + w).astype(np.float32)
+
+    t = {"embed_tokens.weight": normal(shape.vocab, H), "norm.weight": norm(H)}
+    for l in range(shape.layers):
+        p = f"layers.{l}."
+        t[p + "input_layernorm.weight"] = norm(H)
+        t[p + "self_attn.q_proj.weight"] = normal(qdim, H)
+        t[p + "self_attn.k_proj.weight"] = normal(kvdim, H)
+        t[p + "self_attn.v_proj.weight"] = normal(kvdim, H)
+        t[p + "self_attn.o_proj.weight"] = normal(H, qdim)
+        t[p + "self_attn.q_norm.weight"] = norm(dh)
+        t[p + "self_attn.k_norm.weight"] = norm(dh)
+        t[p + "post_attention_layernorm.weight"] = norm(H)
+        if gemma:
+            t[p + "pre_feedforward_layernorm.weight"] = norm(H)
+            t[p + "post_feedforward_layernorm.weight"] = norm(H)
+        t[p + "mlp.gate_proj.weight"] = normal(I, H)
+        t[p + "mlp.up_proj.weight"] = normal(I, H)
+        t[p + "mlp.down_proj.weight"] = normal(H, I)
+    if gemma and shape.dense_hidden:
+        t["2_Dense.linear.weight"] = normal(shape.dense_hidden, H)
+        t["3_Dense.linear.weight"] = normal(H, shape.dense_hidden)
+    return t
