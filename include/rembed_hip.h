@@ -100,6 +100,16 @@ typedef struct rh_weight rh_weight;
 int rh_pack_weight(rh_context *ctx, int mode, const float *bT, const float *bias,
                    int k, int n, rh_weight **out);
 void rh_weight_destroy(rh_weight *w);
+/* Gated-MLP weight (SwiGLU / GeGLU, qwen3.go:528-539, gemma3.go:363-374):
+ * gate and up are each [i][k] (HF gate_proj / up_proj). They are quantized
+ * per output channel exactly as two separate rh_pack_weight calls would, and
+ * stored interleaved (4 gate rows, then the matching 4 up rows) so one GEMM
+ * produces both halves and its epilogue writes act(gate) * up. Use it with
+ * rh_linear and RH_ACT_SWIGLU / RH_ACT_GEGLU; the output has i columns.
+ * i must be a multiple of 8. No counterpart call in the reference, which runs
+ * two applyDense calls and a loop. */
+int rh_pack_weight_gated(rh_context *ctx, int mode, const float *gate, const float *up,
+                         int k, int i, rh_weight **out);
 /* Shape and mode of a packed weight. */
 int rh_weight_info(const rh_weight *w, int *mode, int *k, int *n);
 /* Host copies of the quantization results, for parity checks: q is
@@ -139,6 +149,8 @@ int rh_gemm_u8s8_i32(rh_context *ctx, int32_t *acc, const uint8_t *qa, int ldq,
  * rh_matmul_packed_vnni (both may be NULL for the other modes). */
 #define RH_ACT_NONE 0
 #define RH_ACT_GELU 1
+#define RH_ACT_SWIGLU 2 /* silu(gate)*up, tensor.SiLU (tensor.go:477-481)       */
+#define RH_ACT_GEGLU 3  /* gelu_tanh(gate)*up, tensor.GELUTanh (tensor.go:490-497) */
 int rh_linear(rh_context *ctx, float *dst, const float *a, const rh_weight *w,
               int m, int act, uint8_t *qa, int ldq, float *row_scales);
 
@@ -162,7 +174,9 @@ int rh_layernorm(rh_context *ctx, float *x, const float *gamma,
  * Replaces model.Load + Model.Forward/ForwardTokens + the Embed batch loop
  * (internal/model/bert.go:307-524,649-731; rembed.go:287-411) with one
  * device-resident forward over a packed variable-length batch. */
-#define RH_ARCH_BERT 0 /* BERT / RoBERTa / DistilBERT-style post-LN encoder */
+#define RH_ARCH_BERT 0   /* BERT / RoBERTa / DistilBERT-style post-LN encoder */
+#define RH_ARCH_QWEN3 1  /* Qwen3 causal decoder embedder (qwen3.go:395-548) */
+#define RH_ARCH_GEMMA3 2 /* EmbeddingGemma: Gemma 3 run bidirectionally (gemma3.go:206-384) */
 #define RH_POOL_MEAN 0
 #define RH_POOL_CLS 1
 #define RH_POOL_LAST 2
@@ -185,7 +199,16 @@ typedef struct {
   float layer_norm_eps; /* 0 means 1e-12 (config.go:228-230) */
   int pooling;          /* RH_POOL_* */
   int normalize;        /* L2-normalize pooled vectors */
-  int reserved[8];      /* zero */
+  /* decoder family (config.go:56-77); ignored for RH_ARCH_BERT */
+  int kv_heads;              /* NumKeyValueHeads (GQA); 0 = heads */
+  int head_dim;              /* HeadDim; 0 = hidden / heads */
+  double rope_theta;         /* Qwen3 RopeTheta; Gemma GlobalRopeTheta */
+  double rope_local_theta;   /* Gemma LocalRopeTheta */
+  int sliding_window;        /* Gemma: local layers attend where |i-j| < window */
+  int sliding_pattern;       /* Gemma: layer l is global iff (l+1) % pattern == 0 */
+  int query_pre_attn_scalar; /* Gemma: scores scaled by 1/sqrt(scalar) */
+  int dense_hidden;          /* Gemma Dense head width (2_Dense/3_Dense); 0 = none */
+  int reserved[8];           /* zero */
 } rh_model_config;
 
 typedef struct rh_model rh_model;
@@ -193,10 +216,14 @@ typedef struct rh_model rh_model;
 int rh_model_create(rh_context *ctx, const rh_model_config *cfg, int quant,
                     rh_model **out);
 /* Hand one HF tensor (by its safetensors name, with or without the
- * "bert."/"roberta."/"distilbert." prefix) to the model; data is copied. */
+ * "bert."/"roberta."/"distilbert." prefix; decoders: embed_tokens.weight,
+ * norm.weight, layers.N.*, with or without "model.", and Gemma's Dense head
+ * as "2_Dense.linear.weight" / "3_Dense.linear.weight") to the model; data
+ * is copied. */
 int rh_model_set_tensor(rh_model *m, const char *name, const float *host,
                         const int64_t *shape, int ndim);
-/* Check every tensor is present, fuse Q|K|V, quantize/pack and upload. */
+/* Check every tensor is present, fuse Q|K|V (decoders: also gate|up into
+ * one gated weight), quantize/pack and upload. */
 int rh_model_finalize(rh_model *m);
 void rh_model_destroy(rh_model *m);
 /* Per-model switches. RH_OPT_ATTN_PRECISION: 1 = bf16 attention operands,

@@ -175,6 +175,28 @@ def gelu_ref(x):
     return x
 
 
+def silu(x):
+    """SiLU (internal/tensor/tensor.go:477-481)."""
+    x = f32(x).copy()
+    lib.or_silu(_p(x), x.size)
+    return x
+
+
+def gelu_tanh(x):
+    """GELUTanh (internal/tensor/tensor.go:490-497)."""
+    x = f32(x).copy()
+    lib.or_gelu_tanh(_p(x), x.size)
+    return x
+
+
+def rmsnorm(x, g, eps):
+    """RMSNorm (internal/tensor/tensor.go:459-471) over the rows of x."""
+    x = f32(x).copy()
+    m, n = x.shape
+    lib.or_rmsnorm(_p(x), _p(f32(g)), m, n, eps)
+    return x
+
+
 def layernorm(x, g, b, eps):
     x = f32(x).copy()
     m, n = x.shape

@@ -25,8 +25,8 @@ RH_ERR_MISSING = 9
 RH_MODE_F32, RH_MODE_W8, RH_MODE_A8W8 = 0, 1, 2
 RH_QUANT_NONE, RH_QUANT_WEIGHTS, RH_QUANT_FULL = 0, 1, 2
 RH_POOL_MEAN, RH_POOL_CLS, RH_POOL_LAST = 0, 1, 2
-RH_ACT_NONE, RH_ACT_GELU = 0, 1
-RH_ARCH_BERT = 0
+RH_ACT_NONE, RH_ACT_GELU, RH_ACT_SWIGLU, RH_ACT_GEGLU = 0, 1, 2, 3
+RH_ARCH_BERT, RH_ARCH_QWEN3, RH_ARCH_GEMMA3 = 0, 1, 2
 RH_OPT_ATTN_PRECISION = 1
 RH_OPT_FUSED_FFN1 = 2
 RH_CTX_F32_ALGO, RH_CTX_W8_TERMS, RH_CTX_I8_TILE = 1, 2, 3
@@ -37,6 +37,7 @@ EXPORTS = [
     "rh_context_destroy", "rh_context_sync", "rh_context_stream",
     "rh_context_set_option", "rh_malloc", "rh_free", "rh_memcpy_h2d",
     "rh_memcpy_d2h", "rh_profile_enable", "rh_profile_read", "rh_pack_weight",
+    "rh_pack_weight_gated",
     "rh_weight_destroy", "rh_weight_info", "rh_weight_export",
     "rh_quantize_rows_u8", "rh_matmul_packed", "rh_matmul_packed8",
     "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_linear_u8", "rh_gelu",
@@ -60,7 +61,12 @@ class ModelConfig(ctypes.Structure):
         ("vocab", ctypes.c_int), ("max_position", ctypes.c_int),
         ("position_offset", ctypes.c_int), ("type_vocab", ctypes.c_int),
         ("layer_norm_eps", ctypes.c_float), ("pooling", ctypes.c_int),
-        ("normalize", ctypes.c_int), ("reserved", ctypes.c_int * 8),
+        ("normalize", ctypes.c_int),
+        ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+        ("rope_theta", ctypes.c_double), ("rope_local_theta", ctypes.c_double),
+        ("sliding_window", ctypes.c_int), ("sliding_pattern", ctypes.c_int),
+        ("query_pre_attn_scalar", ctypes.c_int), ("dense_hidden", ctypes.c_int),
+        ("reserved", ctypes.c_int * 8),
     ]
 
 
@@ -95,6 +101,7 @@ def _load():
         "rh_profile_enable": (I, [P, I]),
         "rh_profile_read": (I, [P, I, ctypes.POINTER(ProfileStat)]),
         "rh_pack_weight": (I, [P, I, P, P, I, I, ctypes.POINTER(P)]),
+        "rh_pack_weight_gated": (I, [P, I, P, P, I, I, ctypes.POINTER(P)]),
         "rh_weight_destroy": (None, [P]),
         "rh_weight_info": (I, [P, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)]),
         "rh_weight_export": (I, [P, P, P, P]),

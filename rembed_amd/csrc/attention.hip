@@ -89,8 +89,16 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   float mrun = -INFINITY, lrun = 0.0f;
   const float l2e = 1.44269504088896341f;
 
-  const int nblk = (len + kAttnKV - 1) / kAttnKV;
-  for (int kb = 0; kb < nblk; kb++) {
+  // Key blocks this workgroup's queries can see: causal stops after the
+  // last query; a window bounds both ends (|i - j| < window).
+  int kb_lo = 0, kb_hi = (len + kAttnKV - 1) / kAttnKV;
+  const int qlast = min(q0 + kAttnQ, len) - 1;
+  if (p.causal) kb_hi = min(kb_hi, qlast / kAttnKV + 1);
+  if (p.window > 0) {
+    kb_lo = max(0, q0 - p.window + 1) / kAttnKV;
+    kb_hi = min(kb_hi, (qlast + p.window - 1) / kAttnKV + 1);
+  }
+  for (int kb = kb_lo; kb < kb_hi; kb++) {
     const int key0 = kb * kAttnKV;
     __syncthreads();  // previous block's LDS reads are done
     // Stage K (row-major [key][d], swizzled 16B chunks) and V^T ([d][key]).
@@ -162,20 +170,25 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
         for (int j = 0; j < 4; j++) {
           const int key = key0 + t2 * 32 + i * 8 + fg * 4 + j;
           float v = sc[t2][i * 4 + j] * p.scale;
-          if (key >= len) v = -INFINITY;
+          if (key >= len || (p.causal && key > qi) ||
+              (p.window > 0 && (key <= qi - p.window || key >= qi + p.window)))
+            v = -INFINITY;
           sc[t2][i * 4 + j] = v;
           mloc = fmaxf(mloc, v);
         }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    // A masked query can see no key of this block yet (mnew = -inf): use a
+    // finite reference so alpha = exp(-inf) = 0 and every p = 0, not NaN.
     const float mnew = fmaxf(mrun, mloc);
-    const float alpha = exp2f((mrun - mnew) * l2e);
+    const float mref = mnew == -INFINITY ? 0.0f : mnew;
+    const float alpha = exp2f((mrun - mref) * l2e);
     mrun = mnew;
     float psum = 0.0f;
 #pragma unroll
     for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const float pv = exp2f((sc[t2][e] - mnew) * l2e);
+        const float pv = exp2f((sc[t2][e] - mref) * l2e);
         sc[t2][e] = pv;
         psum += pv;
       }
@@ -260,6 +273,7 @@ hipError_t launch_attention(const AttnArgs& a, int precision, hipStream_t s) {
     case 32: return launch_attn_dh<32>(a, precision, s);
     case 64: return launch_attn_dh<64>(a, precision, s);
     case 128: return launch_attn_dh<128>(a, precision, s);
+    case 256: return launch_attn_dh<256>(a, precision, s);
     default: return hipErrorInvalidValue;
   }
 }

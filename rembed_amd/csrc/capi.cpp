@@ -230,6 +230,22 @@ void ctx_release(Context* ctx) {
 // The int8 GEMM over already-quantized rows with an explicit epilogue.
 // Profiled as kind 0; `ops` is the algorithmic work credited to the launch
 // (a recompute pass credits 0 so the pair counts 2·M·K·N once).
+int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up, int k,
+                      int i, rh_weight** out) {
+  if (i <= 0 || i % 8 != 0) return fail(RH_ERR_SHAPE, "gated weight: i must be a multiple of 8");
+  std::vector<float> inter((size_t)2 * i * k);
+  for (int t = 0; t < i / kGluGroup; t++)
+    for (int r = 0; r < kGluGroup; r++) {
+      memcpy(&inter[((size_t)2 * kGluGroup * t + r) * k], gate + ((size_t)kGluGroup * t + r) * k,
+             sizeof(float) * k);
+      memcpy(&inter[((size_t)2 * kGluGroup * t + kGluGroup + r) * k],
+             up + ((size_t)kGluGroup * t + r) * k, sizeof(float) * k);
+    }
+  int st = pack_weight(ctx, mode, inter.data(), nullptr, k, 2 * i, out);
+  if (st == RH_OK) (*out)->glu = true;
+  return st;
+}
+
 int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                 const float* rs, int m, int epi, void* out, int ldo, int act,
                 const float* bias, float* row_absmax, float* rs_out, double ops) {
@@ -327,7 +343,7 @@ extern "C" {
 
 const char* rh_last_error(void) { return g_err.c_str(); }
 
-int rh_version(void) { return 100; }
+int rh_version(void) { return 200; }
 
 int rh_device_count(int* count) {
   if (!count) return fail(RH_ERR_INVALID, "null count");
@@ -447,6 +463,14 @@ int rh_profile_read(rh_context* ctx, int kind, rh_profile_stat* out) {
   return RH_OK;
 }
 
+int rh_pack_weight_gated(rh_context* ctx, int mode, const float* gate,
+                                    const float* up, int k, int i, rh_weight** out) {
+  if (!out || !gate || !up) return fail(RH_ERR_INVALID, "null argument");
+  if (mode < RH_MODE_F32 || mode > RH_MODE_A8W8) return fail(RH_ERR_INVALID, "unknown mode");
+  CTX_GUARD(ctx);
+  return pack_weight_gated(ctx, mode, gate, up, k, i, out);
+}
+
 int rh_pack_weight(rh_context* ctx, int mode, const float* bT, const float* bias,
                    int k, int n, rh_weight** out) {
   if (!out || !bT) return fail(RH_ERR_INVALID, "null argument");
@@ -513,6 +537,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 static int check_gemm(const rh_weight* w, int mode, const float* a, const void* dst, int m) {
   if (!w) return fail(RH_ERR_INVALID, "null weight");
   if (mode >= 0 && w->mode != mode) return fail(RH_ERR_INVALID, "weight packed for another mode");
+  if (mode >= 0 && w->glu) return fail(RH_ERR_INVALID, "gated weight: use rh_linear with a gated act");
   if (m < 0) return fail(RH_ERR_INVALID, "negative m");
   if (m > 0 && (!a || !dst)) return fail(RH_ERR_INVALID, "null argument");
   // the int8 epilogue writes 16-byte vectors
@@ -567,15 +592,17 @@ int rh_linear(rh_context* ctx, float* dst, const float* a, const rh_weight* w, i
               int act, uint8_t* qa, int ldq, float* row_scales) {
   int st = check_gemm(w, -1, a, dst, m);
   if (st) return st;
-  if (act != RH_ACT_NONE && act != RH_ACT_GELU) return fail(RH_ERR_INVALID, "unknown act");
+  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU) return fail(RH_ERR_INVALID, "unknown act");
+  if (w->glu != is_glu(act))
+    return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
   if (w->mode == RH_MODE_A8W8) {
     if (m > 0 && (!qa || !row_scales)) return fail(RH_ERR_INVALID, "null scratch");
     if (ldq < w->k || ldq % 16 != 0)
       return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
   }
   CTX_GUARD(ctx);
-  return run_linear(ctx, w, a, w->k, m, dst, w->n, act, w->d_bias, qa, ldq, row_scales,
-                    true);
+  return run_linear(ctx, w, a, w->k, m, dst, w->glu ? w->n / 2 : w->n, act, w->d_bias, qa,
+                    ldq, row_scales, true);
 }
 
 int rh_linear_u8(rh_context* ctx, const uint8_t* qa, int ldq, const float* row_scales,
@@ -584,7 +611,9 @@ int rh_linear_u8(rh_context* ctx, const uint8_t* qa, int ldq, const float* row_s
   if (!w) return fail(RH_ERR_INVALID, "null weight");
   if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight must be RH_MODE_A8W8");
   if (m < 0) return fail(RH_ERR_INVALID, "negative m");
-  if (act != RH_ACT_NONE && act != RH_ACT_GELU) return fail(RH_ERR_INVALID, "unknown act");
+  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU) return fail(RH_ERR_INVALID, "unknown act");
+  if (w->glu != is_glu(act))
+    return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
   if (m > 0 && (!qa || !row_scales || !qa_out || !rs_out || !absmax_scratch))
     return fail(RH_ERR_INVALID, "null argument");
   if (ldq < w->k || ldq % 16 != 0)

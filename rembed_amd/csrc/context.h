@@ -45,6 +45,9 @@ struct rh_weight {
   float* d_scales = nullptr;
   int32_t* d_colsum = nullptr;
   float* d_bias = nullptr;
+  // gated (SwiGLU/GeGLU) weight: n = 2 * i rows, gate and up interleaved in
+  // groups of kGluGroup; rh_linear writes i = n / 2 output columns
+  bool glu = false;
 };
 
 namespace rh {
@@ -55,6 +58,10 @@ void ctx_release(Context* ctx);  // frees the context on the last reference
 int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
                 int n, rh_weight** out);
 void destroy_weight(rh_weight* w);
+// gate/up [i][k] -> one interleaved [2i][k] weight (rows 8t..8t+3 = gate
+// 4t..4t+3, rows 8t+4..8t+7 = up 4t..4t+3), packed in `mode`, glu = true
+int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up, int k,
+                      int i, rh_weight** out);
 int quantize_b8(const float* bT, int k, int n, std::vector<int8_t>& q,
                 std::vector<float>& scales);
 int quantize_b8_vnni(const float* bT, int k, int n, std::vector<int8_t>& q,

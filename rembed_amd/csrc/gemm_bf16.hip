@@ -49,7 +49,7 @@ __device__ __forceinline__ uint32_t load_a8(const float* A, int lda, int r, int 
   return 3u;
 }
 
-template <int BM, int BN, int A_TERMS, bool B_INT8>
+template <int BM, int BN, int A_TERMS, bool B_INT8, bool GLU>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec) {
   constexpr int B_TERMS = B_INT8 ? 1 : 2;
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -202,6 +202,33 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec)
     __syncthreads();
   }
 
+  if constexpr (GLU) {
+    // Gated weight (rows 8t..8t+3 gate, 8t+4..8t+7 up): lane fr holds one
+    // packed column; the gate lanes (fr % 8 < 4) fetch their up partner from
+    // lane + 4 and write act(gate) * up at column (packed / 8) * 4 + fr % 4.
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int col = col0 + wn * WN + j * 32 + fr;
+      const bool cok = col < p.N;
+      const float cs = (p.col_scales && cok) ? p.col_scales[col] : 1.0f;
+      const float b = (p.bias && cok) ? p.bias[col] : 0.0f;
+      const int ocol = (col >> 3) * 4 + (fr & 3);
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const int row = row0 + wm * WM + i * 32 + ii * 8 + fg * 4 + jj;
+            float v = acc[i][j][ii * 4 + jj];
+            if (p.col_scales) v = v * cs;
+            if (p.bias) v = v + b;
+            const float u = __shfl(v, lane + 4, 64);
+            if ((fr & 4) == 0 && cok && row < p.M) p.C[(size_t)row * p.ldc + ocol] = glu_act(v, u, p.act);
+          }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TN; j++) {
     const int col = col0 + wn * WN + j * 32 + fr;
@@ -227,7 +254,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmBfArgs p, int a_vec)
 // Native fp32: v_mfma_f32_32x32x2_f32. LDS rows hold 32 fp32 of k per stage
 // (8 chunks of 4); lane half g takes chunk 2s+g and feeds its 4 elements to
 // 4 consecutive MFMAs, identically for A and B, so the k pairing agrees.
-template <int BM, int BN>
+template <int BM, int BN, bool GLU>
 __global__ __launch_bounds__(256) void gemm_f32_native_kernel(GemmBfArgs p,
                                                               int a_vec) {
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -326,6 +353,28 @@ __global__ __launch_bounds__(256) void gemm_f32_native_kernel(GemmBfArgs p,
     __syncthreads();
   }
 
+  if constexpr (GLU) {  // gated weight, as in gemm_bf16_kernel
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int col = col0 + wn * WN + j * 32 + fr;
+      const bool cok = col < p.N;
+      const float b = (p.bias && cok) ? p.bias[col] : 0.0f;
+      const int ocol = (col >> 3) * 4 + (fr & 3);
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const int row = row0 + wm * WM + i * 32 + ii * 8 + fg * 4 + jj;
+            float v = acc[i][j][ii * 4 + jj];
+            if (p.bias) v = v + b;
+            const float u = __shfl(v, lane + 4, 64);
+            if ((fr & 4) == 0 && cok && row < p.M) p.C[(size_t)row * p.ldc + ocol] = glu_act(v, u, p.act);
+          }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TN; j++) {
     const int col = col0 + wn * WN + j * 32 + fr;
@@ -356,8 +405,12 @@ static int a_vec_ok(const GemmBfArgs& a) {
 template <int BM, int BN, int AT, bool BI8>
 static hipError_t launch_bf(const GemmBfArgs& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, AT, BI8>), dim3(tiles), dim3(256),
-                     0, s, a, a_vec_ok(a));
+  if (is_glu(a.act))
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, AT, BI8, true>), dim3(tiles), dim3(256),
+                       0, s, a, a_vec_ok(a));
+  else
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, AT, BI8, false>), dim3(tiles), dim3(256),
+                       0, s, a, a_vec_ok(a));
   return hipGetLastError();
 }
 
@@ -380,8 +433,12 @@ hipError_t launch_gemm_f32(const GemmBfArgs& a, int algo, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (algo == F32_NATIVE) {
     const int tiles = ceil_div(a.M, 128) * ceil_div(a.N, 128);
-    hipLaunchKernelGGL((gemm_f32_native_kernel<128, 128>), dim3(tiles), dim3(256),
-                       0, s, a, a_vec_ok(a));
+    if (is_glu(a.act))
+      hipLaunchKernelGGL((gemm_f32_native_kernel<128, 128, true>), dim3(tiles), dim3(256),
+                         0, s, a, a_vec_ok(a));
+    else
+      hipLaunchKernelGGL((gemm_f32_native_kernel<128, 128, false>), dim3(tiles), dim3(256),
+                         0, s, a, a_vec_ok(a));
     return hipGetLastError();
   }
   return launch_bf<128, 128, 2, false>(a, s);

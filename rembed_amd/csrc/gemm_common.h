@@ -94,6 +94,26 @@ __device__ __forceinline__ float gelu_avx2(float v) {
   return (v * 0.5f) * (1.0f + erf);
 }
 
+// SiLU as tensor.SiLU computes it (tensor.go:477-481): the sigmoid's
+// exponential in float64, one float32 rounding of 1 + e, float32 division.
+__device__ __forceinline__ float silu_ref(float v) {
+  return v / (float)(1.0 + exp(-(double)v));
+}
+
+// tanh-approximation GELU as tensor.GELUTanh computes it (tensor.go:490-497),
+// all in float64 with one rounding at the end.
+__device__ __forceinline__ float gelu_tanh_ref(float v) {
+  const double x = (double)v;
+  const double inner = 0.7978845608028654 * (x + 0.044715 * x * x * x);
+  return (float)(0.5 * x * (1.0 + tanh(inner)));
+}
+
+// Gated activation of one output: act(gate) * up, the float32 product of
+// the model loops (qwen3.go:530-539, gemma3.go:365-374).
+__device__ __forceinline__ float glu_act(float g, float u, int act) {
+  return (act == ACT_SWIGLU ? silu_ref(g) : gelu_tanh_ref(g)) * u;
+}
+
 // GEMM epilogue activation. Output rows always have n % 16 == 0 columns
 // (the packers require it), so every element lies in a whole 8-lane group and
 // takes the geluAVX2 sequence, as the reference's GELU(row) does.

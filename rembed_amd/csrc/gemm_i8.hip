@@ -191,6 +191,51 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     const int grow_base = row0 + wm * WM + i * 32;
+    if constexpr (EPI == EPI_F32) {
+      if (is_glu(p.act)) {
+        // Gated weight: tile columns 8t..8t+3 are gate rows, 8t+4..8t+7 the
+        // matching up rows. A lane reads both halves of one group of 8 and
+        // writes 4 outputs act(gate) * up at column (packed column) / 2.
+        constexpr int kL8 = WN / 8, kR8 = 64 / kL8;
+        const int c8 = (lane % kL8) * 8;
+        const int gpk = col0 + wn * WN + c8;
+        const bool pk_ok = gpk < p.N;
+        v4f csg = {1.0f, 1.0f, 1.0f, 1.0f}, csu = csg;
+        v4f bg = {0.0f, 0.0f, 0.0f, 0.0f}, bu = bg;
+        if (pk_ok) {
+          csg = *reinterpret_cast<const v4f*>(p.col_scales + gpk);
+          csu = *reinterpret_cast<const v4f*>(p.col_scales + gpk + 4);
+          if (p.bias) {
+            bg = *reinterpret_cast<const v4f*>(p.bias + gpk);
+            bu = *reinterpret_cast<const v4f*>(p.bias + gpk + 4);
+          }
+        }
+        for (int rr = lane / kL8; rr < 32; rr += kR8) {
+          const int grow = grow_base + rr;
+          const v4i ag = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8);
+          const v4i au = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8 + 4);
+          if (grow < p.M && pk_ok) {
+            const float rs = p.row_scales[grow];
+            v4f o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              float g = (float)ag[e] * rs;
+              g = g * csg[e];
+              float u = (float)au[e] * rs;
+              u = u * csu[e];
+              if (p.bias) {
+                g = g + bg[e];
+                u = u + bu[e];
+              }
+              o[e] = glu_act(g, u, p.act);
+            }
+            *reinterpret_cast<v4f*>(static_cast<float*>(p.out) + (size_t)grow * p.ldo + gpk / 2) = o;
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+        continue;
+      }
+    }
 #pragma unroll 2
     for (int rr = lane / kLanesPerRow; rr < 32; rr += kRowsPerPass) {
       const int grow = grow_base + rr;

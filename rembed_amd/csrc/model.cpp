@@ -38,6 +38,19 @@ struct Layer {
   float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
 };
 
+// One Qwen3 / Gemma3 layer on the device. q|k|v are fused into one weight
+// and gate|up into one gated weight; norm weights are uploaded as the
+// reference uses them (Gemma's with the unit offset folded in).
+struct DecLayer {
+  rh_weight* qkv = nullptr;  // [qdim + 2 kvdim][H]
+  rh_weight* o = nullptr;    // [H][qdim]
+  rh_weight* gu = nullptr;   // gated [2I][H]
+  rh_weight* down = nullptr; // [H][I]
+  float *in_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr,
+        *pre_ffn = nullptr, *post_ffn = nullptr;
+  bool global = true;
+};
+
 template <class T>
 hipError_t dalloc(T** p, size_t count) {
   return hipMalloc((void**)p, count * sizeof(T) + 16);
@@ -56,6 +69,12 @@ struct rh_model {
   float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_g = nullptr,
         *emb_b = nullptr;
   std::vector<Layer> layers;
+  // decoder family
+  std::vector<DecLayer> dlayers;
+  float *final_norm = nullptr, *dense1 = nullptr, *dense2 = nullptr;
+  float *cos_g = nullptr, *sin_g = nullptr, *cos_l = nullptr, *sin_l = nullptr;
+  float *normed = nullptr, *pooled = nullptr;
+  int32_t* pos_d = nullptr;
   int attn_precision = 3;
   bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
 
@@ -78,9 +97,11 @@ struct rh_model {
   void release_ws() {
     for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
                     (void*)rs, (void*)cu_d, (void*)ids_d, (void*)out_d, (void*)qkvh,
-                    (void*)qa2, (void*)rs2, (void*)absmax})
+                    (void*)qa2, (void*)rs2, (void*)absmax, (void*)normed, (void*)pooled,
+                    (void*)pos_d})
       if (p) (void)hipFree(p);
-    x = qkv = ctxb = y = hid = rs = out_d = rs2 = absmax = nullptr;
+    x = qkv = ctxb = y = hid = rs = out_d = rs2 = absmax = normed = pooled = nullptr;
+    pos_d = nullptr;
     qa = qa2 = nullptr;
     qkvh = nullptr;
     cu_d = ids_d = nullptr;
@@ -102,9 +123,21 @@ struct rh_model {
         if (p) (void)hipFree(p);
     }
     layers.clear();
-    for (float* p : {word, pos, type0, emb_g, emb_b})
+    for (auto& L : dlayers) {
+      for (rh_weight* w : {L.qkv, L.o, L.gu, L.down}) {
+        if (!w) continue;
+        destroy_weight(w);
+        ctx_release(ctx);
+      }
+      for (float* p : {L.in_norm, L.q_norm, L.k_norm, L.post_attn, L.pre_ffn, L.post_ffn})
+        if (p) (void)hipFree(p);
+    }
+    dlayers.clear();
+    for (float* p : {word, pos, type0, emb_g, emb_b, final_norm, dense1, dense2, cos_g, sin_g,
+                     cos_l, sin_l})
       if (p) (void)hipFree(p);
     word = pos = type0 = emb_g = emb_b = nullptr;
+    final_norm = dense1 = dense2 = cos_g = sin_g = cos_l = sin_l = nullptr;
     if (err_d) (void)hipFree(err_d);
     err_d = nullptr;
     if (cu_pinned) (void)hipHostFree(cu_pinned);
@@ -115,6 +148,17 @@ struct rh_model {
 
   int H() const { return cfg.hidden; }
   int I() const { return cfg.intermediate; }
+  bool decoder() const { return cfg.arch != RH_ARCH_BERT; }
+  bool gemma() const { return cfg.arch == RH_ARCH_GEMMA3; }
+  int nq() const { return cfg.heads; }
+  int nkv() const { return decoder() && cfg.kv_heads > 0 ? cfg.kv_heads : cfg.heads; }
+  int dh() const {
+    return decoder() && cfg.head_dim > 0 ? cfg.head_dim : cfg.hidden / cfg.heads;
+  }
+  int qdim() const { return nq() * dh(); }
+  int kvdim() const { return nkv() * dh(); }
+  int qkv_width() const { return decoder() ? qdim() + 2 * kvdim() : 3 * cfg.hidden; }
+  int ctx_width() const { return decoder() ? qdim() : cfg.hidden; }
   int ldq_for(int k) const { return (int)round_up(k, 16); }
   float eps() const { return cfg.layer_norm_eps == 0.0f ? 1e-12f : cfg.layer_norm_eps; }
   int max_seq() const { return cfg.max_position - cfg.position_offset; }
@@ -126,20 +170,26 @@ struct rh_model {
     if (rows > cap) {
       int newcap = (int)round_up(rows, 256);
       for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
-                      (void*)rs, (void*)qkvh, (void*)qa2, (void*)rs2, (void*)absmax})
+                      (void*)rs, (void*)qkvh, (void*)qa2, (void*)rs2, (void*)absmax,
+                      (void*)normed, (void*)pos_d})
         if (p) RH_HIP(hipFree(p));
-      x = qkv = ctxb = y = hid = rs = rs2 = absmax = nullptr;
+      x = qkv = ctxb = y = hid = rs = rs2 = absmax = normed = nullptr;
       qa = qa2 = nullptr;
       qkvh = nullptr;
+      pos_d = nullptr;
       const size_t r = newcap;
       RH_HIP(dalloc(&x, r * H));
-      RH_HIP(dalloc(&qkv, r * 3 * H));
-      RH_HIP(dalloc(&qkvh, r * 3 * H));
-      RH_HIP(dalloc(&ctxb, r * H));
+      RH_HIP(dalloc(&qkv, r * qkv_width()));
+      if (!decoder()) RH_HIP(dalloc(&qkvh, r * qkv_width()));
+      RH_HIP(dalloc(&ctxb, r * ctx_width()));
       RH_HIP(dalloc(&y, r * H));
       RH_HIP(dalloc(&hid, r * I));
-      RH_HIP(dalloc(&qa, r * round_up(H, 16)));
-      RH_HIP(dalloc(&qa2, r * round_up(I, 16)));
+      RH_HIP(dalloc(&qa, r * ldq_for(std::max(H, ctx_width()))));
+      RH_HIP(dalloc(&qa2, r * ldq_for(I)));
+      if (decoder()) {
+        RH_HIP(dalloc(&normed, r * H));
+        RH_HIP(dalloc(&pos_d, r));
+      }
       RH_HIP(dalloc(&rs, r));
       RH_HIP(dalloc(&rs2, r));
       RH_HIP(dalloc(&absmax, r));
@@ -148,11 +198,14 @@ struct rh_model {
     if (batch > cap_batch) {
       if (cu_d) RH_HIP(hipFree(cu_d));
       if (out_d) RH_HIP(hipFree(out_d));
+      if (pooled) RH_HIP(hipFree(pooled));
       cu_d = nullptr;
       out_d = nullptr;
+      pooled = nullptr;
       const int nb = (int)round_up(batch, 64);
       RH_HIP(dalloc(&cu_d, nb + 1));
       RH_HIP(dalloc(&out_d, (size_t)nb * H));
+      RH_HIP(dalloc(&pooled, (size_t)nb * H));
       cap_batch = nb;
     }
     if (ids_elems > cap_ids) {
@@ -206,12 +259,15 @@ struct rh_model {
   // The forward over rows already planned; ids_dev is [batch][stride].
   int forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
               int max_len, bool pool, float* out_dev);
+  int forward_dec(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
+                  int max_len, bool pool, float* out_dev);
 };
 
 static bool needs_q(const rh_weight* w) { return w->mode == RH_MODE_A8W8; }
 
 int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
                       int max_len, bool pool, float* out_dev) {
+  if (decoder()) return forward_dec(ids_dev, stride, cu, max_len, pool, out_dev);
   hipStream_t s = ctx->stream;
   const int batch = (int)cu.size() - 1;
   const int M = cu[batch];
@@ -328,6 +384,103 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
   }
   if (pool) {
     RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
+  }
+  return RH_OK;
+}
+
+
+// encodeQwen3 (qwen3.go:395-548) / encodeGemma3 (gemma3.go:206-384) over the
+// packed batch, then ForwardWorkers' pooling (bert.go:657-689).
+int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
+                          int max_len, bool pool, float* out_dev) {
+  hipStream_t s = ctx->stream;
+  const int batch = (int)cu.size() - 1;
+  const int M = cu[batch];
+  const int H = this->H(), I = this->I();
+  const int qd = qdim(), kvd = kvdim(), qkvw = qkv_width();
+  int st = ensure_ws(M, batch, 0);
+  if (st) return st;
+  RH_HIP(hipEventSynchronize(cu_evt));
+  memcpy(cu_pinned, cu.data(), (batch + 1) * sizeof(int32_t));
+  RH_HIP(hipMemcpyAsync(cu_d, cu_pinned, (batch + 1) * sizeof(int32_t),
+                        hipMemcpyHostToDevice, s));
+  RH_HIP(hipEventRecord(cu_evt, s));
+
+  const float emb_scale = gemma() ? (float)std::sqrt((double)H) : 1.0f;
+  RH_HIP(launch_embed_gather(ids_dev, stride, cu_d, batch, word, H, cfg.vocab, emb_scale, x,
+                             pos_d, err_d, M, s));
+  const float e = eps();
+  const int ldqH = ldq_for(std::max(H, qd)), ldqI = ldq_for(I);
+  const bool q0 = needs_q(dlayers[0].qkv);
+  RH_HIP(launch_rms_residual(x, nullptr, nullptr, dlayers[0].in_norm, normed, M, H, e,
+                             q0 ? qa : nullptr, ldqH, q0 ? rs : nullptr, s));
+  double attn_ops = 0;
+  for (int b = 0; b < batch; b++) {
+    const double L = cu[b + 1] - cu[b];
+    attn_ops += 4.0 * L * L * dh() * nq() * (cfg.arch == RH_ARCH_QWEN3 ? 0.5 : 1.0);
+  }
+  const int glu = gemma() ? ACT_GEGLU : ACT_SWIGLU;
+  for (size_t li = 0; li < dlayers.size(); li++) {
+    const DecLayer& L = dlayers[li];
+    // attention block: fused q|k|v, QK-norm + RoPE, GQA attention, o_proj
+    st = run_linear(ctx, L.qkv, normed, H, M, qkv, qkvw, ACT_NONE, nullptr, qa, ldqH, rs,
+                    false);
+    if (st) return st;
+    const bool local = gemma() && !L.global;
+    RH_HIP(launch_qk_norm_rope(qkv, qkvw, M, nq(), nkv(), dh(), L.q_norm, L.k_norm, e,
+                               local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d, s));
+    AttnArgs aa{};
+    aa.qkv = qkv;
+    aa.in_bf16 = 0;
+    aa.ldqkv = qkvw;
+    aa.q_off = 0;
+    aa.k_off = qd;
+    aa.v_off = qd + kvd;
+    aa.cu = cu_d;
+    aa.batch = batch;
+    aa.max_len = max_len;
+    aa.heads = nq();
+    aa.kv_heads = nkv();
+    aa.dh = dh();
+    aa.scale = gemma() ? (float)(1.0 / std::sqrt((double)cfg.query_pre_attn_scalar))
+                       : (float)(1.0 / std::sqrt((double)dh()));
+    aa.ctx = ctxb;
+    aa.ldctx = qd;
+    aa.causal = cfg.arch == RH_ARCH_QWEN3 ? 1 : 0;
+    aa.window = local ? cfg.sliding_window : 0;
+    int slot = -1;
+    RH_HIP(ctx->prof_begin(3, attn_ops, 0.0, &slot));
+    RH_HIP(launch_attention(aa, attn_precision, s));
+    RH_HIP(ctx->prof_end(slot));
+    st = run_linear(ctx, L.o, ctxb, qd, M, y, H, ACT_NONE, nullptr, qa, ldqH, rs, needs_q(L.o));
+    if (st) return st;
+    // x += [RMSNorm(attn, post_attn)]; normed = RMSNorm(x, pre-MLP norm)
+    const bool qg = needs_q(L.gu);
+    RH_HIP(launch_rms_residual(x, y, gemma() ? L.post_attn : nullptr,
+                               gemma() ? L.pre_ffn : L.post_attn, normed, M, H, e,
+                               qg ? qa : nullptr, ldqH, qg ? rs : nullptr, s));
+    // gated MLP: one GEMM over gate|up writes act(gate) * up, then down
+    st = run_linear(ctx, L.gu, normed, H, M, hid, I, glu, nullptr, qa, ldqH, rs, false);
+    if (st) return st;
+    st = run_linear(ctx, L.down, hid, I, M, y, H, ACT_NONE, nullptr, qa2, ldqI, rs2,
+                    needs_q(L.down));
+    if (st) return st;
+    // x += [RMSNorm(mlp, post_ffn)]; then the next layer's input norm, or the
+    // final RMSNorm in place (qwen3.go:543, gemma3.go:379)
+    const bool last = li + 1 == dlayers.size();
+    const bool qn = !last && needs_q(dlayers[li + 1].qkv);
+    RH_HIP(launch_rms_residual(x, y, gemma() ? L.post_ffn : nullptr,
+                               last ? final_norm : dlayers[li + 1].in_norm, last ? x : normed,
+                               M, H, e, qn ? qa : nullptr, ldqH, qn ? rs : nullptr, s));
+  }
+  if (pool) {
+    if (gemma() && dense1 && dense2) {
+      RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, 0, pooled, s));
+      RH_HIP(launch_dense_head(pooled, batch, H, cfg.dense_hidden, dense1, dense2,
+                               cfg.normalize, out_dev, s));
+    } else {
+      RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
+    }
   }
   return RH_OK;
 }
@@ -455,6 +608,130 @@ static int finalize_bert(rh_model* m) {
   return RH_OK;
 }
 
+
+// newDense for the gated gate|up pair: the same A8W8 -> W8 -> F32 chain.
+static int new_dense_gated(rh_model* m, const float* gate, const float* up, int in, int i,
+                           rh_weight** w) {
+  if (m->quant == RH_QUANT_FULL &&
+      pack_weight_gated(m->ctx, RH_MODE_A8W8, gate, up, in, i, w) == RH_OK)
+    return RH_OK;
+  if (m->quant >= RH_QUANT_WEIGHTS &&
+      pack_weight_gated(m->ctx, RH_MODE_W8, gate, up, in, i, w) == RH_OK)
+    return RH_OK;
+  return pack_weight_gated(m->ctx, RH_MODE_F32, gate, up, in, i, w);
+}
+
+// Upload a norm weight, adding Gemma's unit offset (gemma3.go:40-50).
+static int upload_norm(const HostTensor* t, int n, bool unit_offset, float** dst) {
+  std::vector<float> v(t->data.begin(), t->data.begin() + n);
+  if (unit_offset)
+    for (float& x : v) x = x + 1.0f;
+  return upload(v.data(), n, dst);
+}
+
+// ropeTable (modernbert.go:112-122) for positions [0, seq): float64 trig
+// rounded to float32, [seq][dh/2], uploaded once at load.
+static int upload_rope(int seq, int dh, double theta, float** cos_d, float** sin_d) {
+  const int half = dh / 2;
+  std::vector<float> c((size_t)seq * half), sn((size_t)seq * half);
+  for (int d = 0; d < half; d++) {
+    const double inv_freq = std::pow(theta, -2.0 * (double)d / (double)dh);
+    for (int p = 0; p < seq; p++) {
+      const double ang = (double)p * inv_freq;
+      c[(size_t)p * half + d] = (float)std::cos(ang);
+      sn[(size_t)p * half + d] = (float)std::sin(ang);
+    }
+  }
+  int st = upload(c.data(), c.size(), cos_d);
+  if (st) return st;
+  return upload(sn.data(), sn.size(), sin_d);
+}
+
+// loadQwen3 (qwen3.go:37-135) / loadGemma3 (gemma3.go:57-158).
+static int finalize_decoder(rh_model* m) {
+  const bool gemma = m->gemma();
+  const int H = m->cfg.hidden, I = m->cfg.intermediate, dh = m->dh();
+  const int qd = m->qdim(), kvd = m->kvdim();
+  std::string prefix;
+  if (m->pending.count("model.embed_tokens.weight")) prefix = "model.";
+  const HostTensor *emb, *fn;
+  int st;
+  if ((st = find_tensor(m, prefix, "embed_tokens.weight", {m->cfg.vocab, H}, &emb))) return st;
+  if ((st = find_tensor(m, prefix, "norm.weight", {H}, &fn))) return st;
+  if ((st = upload(emb->data.data(), emb->data.size(), &m->word))) return st;
+  if ((st = upload_norm(fn, H, gemma, &m->final_norm))) return st;
+  const int seq_cap = m->max_seq();
+  if ((st = upload_rope(seq_cap, dh, m->cfg.rope_theta, &m->cos_g, &m->sin_g))) return st;
+  if (gemma &&
+      (st = upload_rope(seq_cap, dh, m->cfg.rope_local_theta, &m->cos_l, &m->sin_l)))
+    return st;
+  if (gemma && m->cfg.dense_hidden > 0) {
+    const HostTensor *d1, *d2;
+    if ((st = find_tensor(m, "", "2_Dense.linear.weight", {m->cfg.dense_hidden, H}, &d1)))
+      return st;
+    if ((st = find_tensor(m, "", "3_Dense.linear.weight", {H, m->cfg.dense_hidden}, &d2)))
+      return st;
+    if ((st = upload(d1->data.data(), d1->data.size(), &m->dense1))) return st;
+    if ((st = upload(d2->data.data(), d2->data.size(), &m->dense2))) return st;
+  }
+  m->dlayers.resize(m->cfg.layers);
+  for (int l = 0; l < m->cfg.layers; l++) {
+    char buf[64];
+    snprintf(buf, sizeof buf, "layers.%d.", l);
+    const std::string lp = buf;
+    const HostTensor *in_n, *qw, *kw, *vw, *ow, *qn, *kn, *pa, *gw, *uw, *dw;
+    const HostTensor *pf = nullptr, *po = nullptr;
+    struct Need {
+      const char* name;
+      std::initializer_list<int64_t> shape;
+      const HostTensor** dst;
+    };
+    const Need needs[] = {
+        {"input_layernorm.weight", {H}, &in_n},
+        {"self_attn.q_proj.weight", {qd, H}, &qw},
+        {"self_attn.k_proj.weight", {kvd, H}, &kw},
+        {"self_attn.v_proj.weight", {kvd, H}, &vw},
+        {"self_attn.o_proj.weight", {H, qd}, &ow},
+        {"self_attn.q_norm.weight", {dh}, &qn},
+        {"self_attn.k_norm.weight", {dh}, &kn},
+        {"post_attention_layernorm.weight", {H}, &pa},
+        {"mlp.gate_proj.weight", {I, H}, &gw},
+        {"mlp.up_proj.weight", {I, H}, &uw},
+        {"mlp.down_proj.weight", {H, I}, &dw},
+    };
+    for (const Need& n : needs)
+      if ((st = find_tensor(m, prefix, lp + n.name, n.shape, n.dst))) return st;
+    if (gemma) {
+      if ((st = find_tensor(m, prefix, lp + "pre_feedforward_layernorm.weight", {H}, &pf)))
+        return st;
+      if ((st = find_tensor(m, prefix, lp + "post_feedforward_layernorm.weight", {H}, &po)))
+        return st;
+    }
+    DecLayer& L = m->dlayers[l];
+    L.global = !gemma || (l + 1) % m->cfg.sliding_pattern == 0;  // gemma3.go:87
+    // q|k|v rows fused: each output column is the same dot product as in the
+    // reference's three separate applyDense calls.
+    std::vector<float> qkvw((size_t)(qd + 2 * kvd) * H);
+    memcpy(qkvw.data(), qw->data.data(), sizeof(float) * (size_t)qd * H);
+    memcpy(qkvw.data() + (size_t)qd * H, kw->data.data(), sizeof(float) * (size_t)kvd * H);
+    memcpy(qkvw.data() + (size_t)(qd + kvd) * H, vw->data.data(),
+           sizeof(float) * (size_t)kvd * H);
+    if ((st = new_dense(m, qkvw.data(), nullptr, H, qd + 2 * kvd, &L.qkv))) return st;
+    if ((st = new_dense(m, ow->data.data(), nullptr, qd, H, &L.o))) return st;
+    if ((st = new_dense_gated(m, gw->data.data(), uw->data.data(), H, I, &L.gu))) return st;
+    if ((st = new_dense(m, dw->data.data(), nullptr, I, H, &L.down))) return st;
+    if ((st = upload_norm(in_n, H, gemma, &L.in_norm))) return st;
+    if ((st = upload_norm(qn, dh, gemma, &L.q_norm))) return st;
+    if ((st = upload_norm(kn, dh, gemma, &L.k_norm))) return st;
+    if ((st = upload_norm(pa, H, gemma, &L.post_attn))) return st;
+    if (gemma) {
+      if ((st = upload_norm(pf, H, true, &L.pre_ffn))) return st;
+      if ((st = upload_norm(po, H, true, &L.post_ffn))) return st;
+    }
+  }
+  return RH_OK;
+}
+
 // ---- C ABI ------------------------------------------------------------------------
 
 #define MODEL_GUARD(m)                                                   \
@@ -467,16 +744,36 @@ extern "C" {
 
 int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_model** out) {
   if (!ctx || !cfg || !out) return fail(RH_ERR_INVALID, "null argument");
-  if (cfg->arch != RH_ARCH_BERT) return fail(RH_ERR_INVALID, "unsupported arch");
-  if (cfg->hidden <= 0 || cfg->heads <= 0 || cfg->hidden % cfg->heads != 0)
-    return fail(RH_ERR_INVALID, "hidden_size not divisible by num_attention_heads");
-  const int dh = cfg->hidden / cfg->heads;
-  if (dh != 32 && dh != 64 && dh != 128) return fail(RH_ERR_INVALID, "head dim must be 32, 64 or 128");
-  if (cfg->hidden % 64 != 0 || cfg->hidden > 2048)
-    return fail(RH_ERR_INVALID, "hidden must be a multiple of 64 and <= 2048");
+  if (cfg->arch != RH_ARCH_BERT && cfg->arch != RH_ARCH_QWEN3 && cfg->arch != RH_ARCH_GEMMA3)
+    return fail(RH_ERR_INVALID, "unsupported arch");
+  if (cfg->hidden <= 0 || cfg->heads <= 0) return fail(RH_ERR_INVALID, "bad hidden/heads");
   if (cfg->intermediate <= 0 || cfg->layers <= 0 || cfg->vocab <= 0 || cfg->max_position <= 0)
     return fail(RH_ERR_INVALID, "bad config sizes");
+  if (cfg->hidden % 64 != 0 || cfg->hidden > 4096)
+    return fail(RH_ERR_INVALID, "hidden must be a multiple of 64 and <= 4096");
   if (quant < RH_QUANT_NONE || quant > RH_QUANT_FULL) return fail(RH_ERR_INVALID, "bad quant");
+  if (cfg->arch == RH_ARCH_BERT) {
+    if (cfg->hidden % cfg->heads != 0 || cfg->hidden > 2048)
+      return fail(RH_ERR_INVALID, "hidden must divide by heads and be <= 2048");
+    const int dh = cfg->hidden / cfg->heads;
+    if (dh != 32 && dh != 64 && dh != 128)
+      return fail(RH_ERR_INVALID, "head dim must be 32, 64 or 128");
+  } else {
+    const int nkv = cfg->kv_heads > 0 ? cfg->kv_heads : cfg->heads;
+    const int dh = cfg->head_dim > 0 ? cfg->head_dim : cfg->hidden / cfg->heads;
+    if (cfg->heads % nkv != 0) return fail(RH_ERR_INVALID, "heads must be a multiple of kv_heads");
+    if (dh != 64 && dh != 128 && dh != 256)
+      return fail(RH_ERR_INVALID, "head dim must be 64, 128 or 256");
+    if (cfg->intermediate % 8 != 0) return fail(RH_ERR_INVALID, "intermediate must divide by 8");
+    if (cfg->rope_theta <= 0) return fail(RH_ERR_INVALID, "rope_theta must be positive");
+    if (cfg->arch == RH_ARCH_GEMMA3) {
+      if (cfg->rope_local_theta <= 0 || cfg->sliding_pattern <= 0 || cfg->sliding_window <= 0 ||
+          cfg->query_pre_attn_scalar <= 0)
+        return fail(RH_ERR_INVALID, "gemma needs local theta, window, pattern, attn scalar");
+      if (cfg->dense_hidden < 0 || cfg->dense_hidden > 16384)
+        return fail(RH_ERR_INVALID, "bad dense_hidden");
+    }
+  }
   auto* m = new rh_model();
   m->ctx = ctx;
   ctx_retain(ctx);
@@ -524,7 +821,7 @@ int rh_model_set_tensor(rh_model* m, const char* name, const float* host,
 int rh_model_finalize(rh_model* m) {
   MODEL_GUARD(m);
   if (m->finalized) return fail(RH_ERR_INVALID, "model already finalized");
-  int st = finalize_bert(m);
+  int st = m->decoder() ? finalize_decoder(m) : finalize_bert(m);
   if (st) {
     std::string msg = rh_last_error();
     m->release();
@@ -548,19 +845,27 @@ void rh_model_destroy(rh_model* m) {
   ctx_release(ctx);
 }
 
-int rh_model_quantized(const rh_model* m) {
-  if (!m || m->layers.empty()) return 0;
+// Per-layer weight handles in load order (the same set for every arch).
+static std::vector<const rh_weight*> all_weights(const rh_model* m) {
+  std::vector<const rh_weight*> v;
   for (const Layer& L : m->layers)
-    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2})
-      if (w->mode == RH_MODE_F32) return 0;
+    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) v.push_back(w);
+  for (const DecLayer& L : m->dlayers)
+    for (const rh_weight* w : {L.qkv, L.o, L.gu, L.down}) v.push_back(w);
+  return v;
+}
+
+int rh_model_quantized(const rh_model* m) {
+  if (!m || !m->finalized) return 0;
+  for (const rh_weight* w : all_weights(m))
+    if (w->mode == RH_MODE_F32) return 0;
   return 1;
 }
 
 int rh_model_quantized_activations(const rh_model* m) {
-  if (!m || m->layers.empty()) return 0;
-  for (const Layer& L : m->layers)
-    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2})
-      if (w->mode != RH_MODE_A8W8) return 0;
+  if (!m || !m->finalized) return 0;
+  for (const rh_weight* w : all_weights(m))
+    if (w->mode != RH_MODE_A8W8) return 0;
   return 1;
 }
 

@@ -54,7 +54,12 @@ constexpr int kWeightKPad = 128;
 // ---- GEMM launch descriptors -------------------------------------------------
 // act codes for the fused epilogue (reference applies these as separate
 // passes after AddBias: internal/model/bert.go:913-915, qwen3.go:530-539).
-enum Act : int { ACT_NONE = 0, ACT_GELU = 1 };
+// ACT_SWIGLU / ACT_GEGLU apply to a gated weight (rows of gate and up
+// interleaved in groups of 4, see kGluGroup): the epilogue writes
+// act(gate) * up into n/2 output columns (qwen3.go:530-539, gemma3.go:365-374).
+enum Act : int { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2, ACT_GEGLU = 3 };
+constexpr int kGluGroup = 4;  // packed rows 8t..8t+3 = gate 4t.., 8t+4..8t+7 = up 4t..
+__host__ __device__ inline bool is_glu(int act) { return act == ACT_SWIGLU || act == ACT_GEGLU; }
 
 // Epilogue variants of the int8 GEMM. value = act(float32(real)·rs·cs + bias)
 enum I8Epi : int {
@@ -179,8 +184,36 @@ struct AttnArgs {
   float scale;
   float* ctx;  // [M][ldctx]
   int ldctx;
+  int causal;  // key j visible to query i only if j <= i (qwen3.go:307-390)
+  int window;  // > 0: key j visible only if |i - j| < window (gemma3.go:339-347)
 };
 // precision: 1 = bf16 MFMA, 3 = three-term bf16 split (fp32-grade)
 hipError_t launch_attention(const AttnArgs& a, int precision, hipStream_t s);
+
+// ---- decoder-family row kernels (kernels_dec.hip) ---------------------------
+// Token embeddings only (positions enter through RoPE): x[r] = word[id] * scale
+// (scale 1 for Qwen3, float32(sqrt(H)) for Gemma, gemma3.go:262-275); pos[r] =
+// the token's index in its text.
+hipError_t launch_embed_gather(const int32_t* ids, int stride, const int32_t* cu,
+                               int batch, const float* word, int H, int vocab,
+                               float scale, float* x, int32_t* pos, int* err_flag,
+                               int total_rows, hipStream_t s);
+// Residual + RMSNorm sandwich per row (tensor.go:459-471):
+//   y' = post_g ? RMSNorm(y, post_g) : y;  if (y) x += y';
+//   out = RMSNorm(x, pre_g) (out may alias x); optional u8 quantization of out.
+hipError_t launch_rms_residual(float* x, const float* y, const float* post_g,
+                               const float* pre_g, float* out, int m, int H, float eps,
+                               uint8_t* qa, int ldq, float* row_scales, hipStream_t s);
+// QK-norm (RMSNorm over each head's dh values) then rotate-half RoPE at the
+// row's position, in place on fused q|k rows (qwen3.go:484-516).
+hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, int dh,
+                               const float* q_g, const float* k_g, float eps,
+                               const float* cos_t, const float* sin_t,
+                               const int32_t* pos, hipStream_t s);
+// EmbeddingGemma Dense head (gemma3.go:174-198) on pooled [batch][H] rows:
+// out = W2 . (W1 . pooled), float32 sequential sums; optional L2.
+hipError_t launch_dense_head(const float* pooled, int batch, int H, int D,
+                             const float* w1, const float* w2, int normalize,
+                             float* out, hipStream_t s);
 
 }  // namespace rh

@@ -15,23 +15,35 @@ from ._lib import check, lib
 QUANT_NONE = _lib.RH_QUANT_NONE       # default fp32
 QUANT_WEIGHTS = _lib.RH_QUANT_WEIGHTS  # WithInt8 (rembed.go:67-69)
 QUANT_FULL = _lib.RH_QUANT_FULL        # WithInt8Activations (rembed.go:79-81)
+ARCH_BERT, ARCH_QWEN3, ARCH_GEMMA3 = _lib.RH_ARCH_BERT, _lib.RH_ARCH_QWEN3, _lib.RH_ARCH_GEMMA3
 
 
 def make_config(shape):
-    """rh_model_config from a synthetic.BertShape-like object."""
+    """rh_model_config from a synthetic.BertShape or DecoderShape."""
     c = _lib.ModelConfig()
-    c.arch = _lib.RH_ARCH_BERT
+    c.arch = getattr(shape, "arch", _lib.RH_ARCH_BERT)
     c.hidden = shape.hidden
     c.layers = shape.layers
     c.heads = shape.heads
     c.intermediate = shape.intermediate
     c.vocab = shape.vocab
-    c.max_position = shape.max_position
-    c.position_offset = getattr(shape, "position_offset", 0)
-    c.type_vocab = shape.type_vocab
     c.layer_norm_eps = shape.eps
     c.pooling = shape.pooling
     c.normalize = shape.normalize
+    if c.arch == _lib.RH_ARCH_BERT:
+        c.max_position = shape.max_position
+        c.position_offset = getattr(shape, "position_offset", 0)
+        c.type_vocab = shape.type_vocab
+    else:  # Qwen3 / Gemma3 (config.go:56-77)
+        c.max_position = shape.max_seq
+        c.kv_heads = shape.kv_heads
+        c.head_dim = shape.head_dim
+        c.rope_theta = shape.rope_theta
+        c.rope_local_theta = shape.rope_local_theta
+        c.sliding_window = shape.sliding_window
+        c.sliding_pattern = shape.sliding_pattern
+        c.query_pre_attn_scalar = shape.query_pre_attn_scalar
+        c.dense_hidden = shape.dense_hidden
     return c
 
 

@@ -154,6 +154,22 @@ def PackB8VNNI(ctx, bT, k, n, bias=None):
     return PackedWeight(ctx, _lib.RH_MODE_A8W8, bT, k, n, bias)
 
 
+class PackedGated(PackedWeight):
+    """Gated-MLP weight: gate and up [i][k] packed interleaved
+    (rh_pack_weight_gated); rh_linear with RH_ACT_SWIGLU / RH_ACT_GEGLU
+    writes act(gate) * up, i columns. N is the packed row count 2i."""
+
+    def __init__(self, ctx, mode, gate, up, k, i):
+        gate = np.ascontiguousarray(gate, dtype=np.float32)
+        up = np.ascontiguousarray(up, dtype=np.float32)
+        if gate.size != k * i or up.size != k * i:
+            raise _lib.RembedError(_lib.RH_ERR_SHAPE, f"gate/up must be [{i}][{k}]")
+        h = ctypes.c_void_p()
+        check(lib.rh_pack_weight_gated(ctx.h, mode, gate.ctypes.data, up.ctypes.data, k, i,
+                                       ctypes.byref(h)))
+        self.ctx, self.h, self.mode, self.K, self.N = ctx, h, mode, k, 2 * i
+
+
 def ldq_for(k):
     """Row stride of quantized activations: k rounded up to 16 bytes."""
     return (k + 15) // 16 * 16

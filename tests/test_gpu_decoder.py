@@ -1,0 +1,189 @@
+"""Decoder-family parity on the GPU (through the C ABI) against the oracle.
+
+* Gated GEMM (rh_pack_weight_gated + rh_linear with SwiGLU/GeGLU): the fp32
+  values of gate and up come out of the same epilogue arithmetic as
+  MatMulPacked/MatMulPacked8/MatMulPackedVNNI, then act(gate)*up as the model
+  loops compute it (qwen3.go:530-539, gemma3.go:365-374). Full int8 is
+  compared element-wise (the int32 accumulators and dequantization are exact;
+  only the float64 exp/tanh of the two libraries may differ in their last
+  bit before the float32 rounding); fp32 and weight-only int8 within the
+  GEMM tolerances.
+* Qwen3- and EmbeddingGemma-shaped models at full width (hidden 1024 /
+  16 Q, 8 KV heads of 128; hidden 768 / 3 Q, 1 KV head of 256, window 257,
+  Dense 3072), two layers: fp32 embeddings within 1e-4 of the oracle,
+  weight-only int8 cosine >= 0.9999 against the oracle's int8 path, full
+  int8 cosine >= 0.999, batch == single, per-token hidden states.
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from rembed_amd import _lib
+from rembed_amd import tensor as T
+from rembed_amd.model import QUANT_FULL, QUANT_NONE, QUANT_WEIGHTS, Model
+from rembed_amd.synthetic import GEMMA3_300M, QWEN3_0_6B, decoder_tensors, token_batch
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def oracle_dense(mode, bT, a):
+    """applyDense of the oracle for one weight (bert.go:282-301)."""
+    n, k = bT.shape
+    if mode == _lib.RH_MODE_F32:
+        return O.matmul_f32(a, bT)
+    if mode == _lib.RH_MODE_W8:
+        st, q, sc = O.pack_b8(bT, k, n)
+        return O.matmul_w8(a, q, sc)
+    st, q, sc, cs = O.pack_b8_vnni(bT, k, n)
+    return O.matmul_vnni(a, q, cs, sc)[0]
+
+
+@pytest.mark.parametrize("mode", [_lib.RH_MODE_F32, _lib.RH_MODE_W8, _lib.RH_MODE_A8W8])
+@pytest.mark.parametrize("act", [_lib.RH_ACT_SWIGLU, _lib.RH_ACT_GEGLU])
+def test_gated_linear_matches_oracle(gpu_ctx, mode, act):
+    ctx = gpu_ctx
+    rng = np.random.default_rng(10 * mode + act)
+    m, k, i = 301, 384, 520
+    say(f"gated linear mode={mode} act={act} m={m} k={k} i={i}")
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    gate = (rng.standard_normal((i, k)) * 0.05).astype(np.float32)
+    up = (rng.standard_normal((i, k)) * 0.05).astype(np.float32)
+    pw = T.PackedGated(ctx, mode, gate, up, k, i)
+    a_d = ctx.upload(a)
+    out = ctx.alloc(m * i * 4)
+    ldq = T.ldq_for(k)
+    qa, rs = ctx.alloc(m * ldq), ctx.alloc(m * 4)
+    T.Linear(ctx, out, a_d, pw, m, act, qa, ldq, rs)
+    ctx.sync()
+    got = out.download(np.float32, (m, i))
+    g = oracle_dense(mode, gate, a)
+    u = oracle_dense(mode, up, a)
+    fn = O.silu if act == _lib.RH_ACT_SWIGLU else O.gelu_tanh
+    want = (fn(g.ravel()).reshape(m, i) * u).astype(np.float32)
+    err = np.abs(got.astype(np.float64) - want) / (1 + np.abs(want))
+    say(f"  max rel err {err.max():.3e}")
+    if mode == _lib.RH_MODE_A8W8:
+        assert err.max() <= 1e-6
+    else:
+        assert err.max() <= 2e-4
+    # the gated weight refuses the plain GEMM entry points and non-gated acts
+    with pytest.raises(_lib.RembedError):
+        T.Linear(ctx, out, a_d, pw, m, _lib.RH_ACT_NONE, qa, ldq, rs)
+
+
+def qwen3_2l():
+    return dataclasses.replace(QWEN3_0_6B, name="qwen3-2l", layers=2, vocab=4000, max_seq=2048)
+
+
+def gemma3_2l():
+    # pattern 2: layer 0 sliding-window (257), layer 1 global
+    return dataclasses.replace(GEMMA3_300M, name="gemma3-2l", layers=2, vocab=4000,
+                               sliding_pattern=2, max_seq=2048)
+
+
+_CACHE = {}
+
+
+def setup(make, bf16):
+    key = (make.__name__, bf16)
+    if key not in _CACHE:
+        shape = make()
+        t = decoder_tensors(shape, seed=0x5EED0011, bf16=bf16)
+        _CACHE[key] = (shape, t)
+    return _CACHE[key]
+
+
+def cos_rows(a, b):
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    return np.sum(a * b, axis=1) / np.linalg.norm(a, axis=1) / np.linalg.norm(b, axis=1)
+
+
+CASES = [(qwen3_2l, True, 6, 5, 300), (gemma3_2l, False, 4, 5, 600)]
+
+
+@pytest.mark.parametrize("make,bf16,batch,lo,hi", CASES, ids=["qwen3", "gemma3"])
+def test_decoder_fp32_max_abs_1e4(gpu_ctx, make, bf16, batch, lo, hi):
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(batch, hi, lo, hi, vocab=shape.vocab, id_lo=0, seed=21)
+    lens[0] = hi  # one text spans the window / several 64-key blocks
+    say(f"{shape.name} fp32 lens {lens.tolist()}")
+    m = Model(gpu_ctx, shape, t, QUANT_NONE)
+    assert not m.quantized()
+    got = m.embed(ids, lens)
+    want = O.DecoderOracle(shape, t, 0).embed_batch(ids, lens, threads=8)
+    err = np.abs(got - want).max()
+    say(f"  max abs err {err:.3e}")
+    assert err <= 1e-4
+
+
+@pytest.mark.parametrize("make,bf16,batch,lo,hi", CASES, ids=["qwen3", "gemma3"])
+def test_decoder_weight_only_int8_cosine(gpu_ctx, make, bf16, batch, lo, hi):
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(batch, hi, lo, hi, vocab=shape.vocab, id_lo=0, seed=22)
+    say(f"{shape.name} weight-only int8 lens {lens.tolist()}")
+    m = Model(gpu_ctx, shape, t, QUANT_WEIGHTS)
+    assert m.quantized() and not m.quantized_activations()
+    got = m.embed(ids, lens)
+    want = O.DecoderOracle(shape, t, 1).embed_batch(ids, lens, threads=8)
+    c = cos_rows(got, want)
+    say(f"  min cos {c.min():.7f}")
+    assert c.min() >= 0.9999
+
+
+@pytest.mark.parametrize("make,bf16,batch,lo,hi", CASES, ids=["qwen3", "gemma3"])
+def test_decoder_full_int8_cosine(gpu_ctx, make, bf16, batch, lo, hi):
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(batch, hi, lo, hi, vocab=shape.vocab, id_lo=0, seed=23)
+    say(f"{shape.name} full int8 lens {lens.tolist()}")
+    m = Model(gpu_ctx, shape, t, QUANT_FULL)
+    assert m.quantized() and m.quantized_activations()
+    got = m.embed(ids, lens)
+    want = O.DecoderOracle(shape, t, 2).embed_batch(ids, lens, threads=8)
+    c = cos_rows(got, want)
+    say(f"  min cos {c.min():.6f}")
+    assert c.min() >= 0.999
+
+
+@pytest.mark.parametrize("make,bf16", [(qwen3_2l, True), (gemma3_2l, False)], ids=["qwen3", "gemma3"])
+def test_decoder_batch_matches_single(gpu_ctx, make, bf16):
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(4, 200, 3, 200, vocab=shape.vocab, id_lo=0, seed=24)
+    m = Model(gpu_ctx, shape, t, QUANT_WEIGHTS)
+    batch = m.embed(ids, lens)
+    for b in range(len(lens)):
+        single = m.embed(ids[b:b + 1, :lens[b]], lens[b:b + 1])
+        assert np.array_equal(single[0], batch[b]), b
+
+
+@pytest.mark.parametrize("make,bf16", [(qwen3_2l, True), (gemma3_2l, False)], ids=["qwen3", "gemma3"])
+def test_decoder_tokens_match_oracle_hidden(gpu_ctx, make, bf16):
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(3, 140, 1, 140, vocab=shape.vocab, id_lo=0, seed=25)
+    m = Model(gpu_ctx, shape, t, QUANT_NONE)
+    toks = m.embed_tokens(ids, lens)
+    orc = O.DecoderOracle(shape, t, 0)
+    for b in range(len(lens)):
+        want = orc.encode(ids[b, :lens[b]])
+        err = np.abs(toks[b] - want).max() / max(1.0, np.abs(want).max())
+        say(f"  text {b} len {lens[b]} rel err {err:.3e}")
+        assert err <= 2e-5
+
+
+def test_decoder_model_errors(gpu_ctx):
+    shape, t = setup(qwen3_2l, True)
+    bad = dict(t)
+    del bad["layers.1.mlp.up_proj.weight"]
+    with pytest.raises(_lib.RembedError) as e:
+        Model(gpu_ctx, shape, bad, QUANT_NONE)
+    assert e.value.code == _lib.RH_ERR_MISSING
+    m = Model(gpu_ctx, shape, t, QUANT_WEIGHTS)
+    with pytest.raises(_lib.RembedError) as e:
+        m.embed(np.array([[shape.vocab]], np.int32), np.array([1], np.int32))
+    assert e.value.code == _lib.RH_ERR_VOCAB
