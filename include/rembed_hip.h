@@ -106,8 +106,9 @@ void rh_weight_destroy(rh_weight *w);
  * stored interleaved (4 gate rows, then the matching 4 up rows) so one GEMM
  * produces both halves and its epilogue writes act(gate) * up. Use it with
  * rh_linear and RH_ACT_SWIGLU / RH_ACT_GEGLU; the output has i columns.
- * i must be a multiple of 8. No counterpart call in the reference, which runs
- * two applyDense calls and a loop. */
+ * gate and up must each pass the packers' shape rule (i % 16 == 0, i >= 16,
+ * k >= 1). No counterpart call in the reference, which runs two applyDense
+ * calls and a loop. */
 int rh_pack_weight_gated(rh_context *ctx, int mode, const float *gate, const float *up,
                          int k, int i, rh_weight **out);
 /* Shape and mode of a packed weight. */

@@ -232,7 +232,10 @@ void ctx_release(Context* ctx) {
 // (a recompute pass credits 0 so the pair counts 2·M·K·N once).
 int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up, int k,
                       int i, rh_weight** out) {
-  if (i <= 0 || i % 8 != 0) return fail(RH_ERR_SHAPE, "gated weight: i must be a multiple of 8");
+  // gate and up are each a PackB*-shaped matrix in the reference (two
+  // newDense calls), so each must pass the packers' shape rule on its own
+  int st0 = check_pack_shape("gated PackB", k, i);
+  if (st0 != RH_OK) return st0;
   std::vector<float> inter((size_t)2 * i * k);
   for (int t = 0; t < i / kGluGroup; t++)
     for (int r = 0; r < kGluGroup; r++) {

@@ -39,8 +39,10 @@ def oracle_dense(mode, bT, a):
         return O.matmul_f32(a, bT)
     if mode == _lib.RH_MODE_W8:
         st, q, sc = O.pack_b8(bT, k, n)
+        assert st == 0
         return O.matmul_w8(a, q, sc)
     st, q, sc, cs = O.pack_b8_vnni(bT, k, n)
+    assert st == 0
     return O.matmul_vnni(a, q, cs, sc)[0]
 
 
@@ -49,7 +51,7 @@ def oracle_dense(mode, bT, a):
 def test_gated_linear_matches_oracle(gpu_ctx, mode, act):
     ctx = gpu_ctx
     rng = np.random.default_rng(10 * mode + act)
-    m, k, i = 301, 384, 520
+    m, k, i = 301, 384, 528
     say(f"gated linear mode={mode} act={act} m={m} k={k} i={i}")
     a = rng.standard_normal((m, k)).astype(np.float32)
     gate = (rng.standard_normal((i, k)) * 0.05).astype(np.float32)
@@ -72,9 +74,13 @@ def test_gated_linear_matches_oracle(gpu_ctx, mode, act):
         assert err.max() <= 1e-6
     else:
         assert err.max() <= 2e-4
-    # the gated weight refuses the plain GEMM entry points and non-gated acts
+    # the gated weight refuses non-gated acts, and each half must pass the
+    # packers' shape rule (pack.go:29-37)
     with pytest.raises(_lib.RembedError):
         T.Linear(ctx, out, a_d, pw, m, _lib.RH_ACT_NONE, qa, ldq, rs)
+    with pytest.raises(_lib.RembedError) as e:
+        T.PackedGated(ctx, mode, gate[:520], up[:520], k, 520)
+    assert e.value.code == _lib.RH_ERR_SHAPE
 
 
 def qwen3_2l():
