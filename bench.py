@@ -149,6 +149,7 @@ def main():
     model.check()
     gemm = ctx.profile_read(gkind)
     attn = ctx.profile_read(3)
+    split = ctx.profile_read(4)  # bf16 split of the W8/fp32 GEMMs' activations
     ctx.profile(False)
 
     ms_per_step = elapsed * 1e3 / args.steps
@@ -157,6 +158,7 @@ def main():
     achieved = gemm["total_ops"] / (gemm["total_ms"] * 1e-3) / 1e12  # TOP/s
     gemm_ms_step = gemm["total_ms"] / args.steps
     attn_ms_step = attn["total_ms"] / args.steps
+    split_ms_step = split["total_ms"] / args.steps
     log(f"{ms_per_step:.3f} ms/step, {value:,.0f} tokens/s; GEMM {gemm_ms_step:.3f} "
         f"ms/step over {gemm['launches'] // args.steps} launches = {achieved:.1f} TOP/s; "
         f"attention {attn_ms_step:.3f} ms/step")
@@ -204,7 +206,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": ("gemm_i8_kernel" if quant == 2 else "gemm_bf16_kernel") +
+            "kernel": ("gemm_i8_kernel" if quant == 2 else "gemm_planes_kernel") +
                       f" (all {gemm['launches'] // args.steps} GEMM launches per step)",
             "achieved": round(achieved, 2),
             "peak": peak,
@@ -216,6 +218,7 @@ def main():
         },
         "gemm_ms_per_step": round(gemm_ms_step, 4),
         "attention_ms_per_step": round(attn_ms_step, 4),
+        "bf16_split_ms_per_step": round(split_ms_step, 4),
         "padded_slots_per_s": round(BATCH * SEQ * args.steps / elapsed, 1),
         "cpu_baseline": baseline,
     }

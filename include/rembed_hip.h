@@ -60,10 +60,15 @@ void *rh_context_stream(rh_context *ctx);
  *   RH_CTX_W8_TERMS  bf16 terms of the fp32 activations in the weight-only
  *                    int8 GEMM: 1 or 2 (default 2)
  *   RH_CTX_I8_TILE   int8 GEMM tile: 0 = automatic, else a fixed
- *                    configuration index (see DESIGN notes of the kernel) */
+ *                    configuration index (see DESIGN notes of the kernel)
+ *   RH_CTX_BF_ALGO   weight-only int8 / fp32 GEMMs: 0 = activations split
+ *                    once into bf16 hi/lo planes and weights stored as bf16
+ *                    planes (default), 1 = split inside the GEMM's main loop */
 #define RH_CTX_F32_ALGO 1
 #define RH_CTX_W8_TERMS 2
 #define RH_CTX_I8_TILE 3
+#define RH_CTX_BF_ALGO 4
+#define RH_CTX_BF_TILE 5
 int rh_context_set_option(rh_context *ctx, int option, int value);
 
 /* Device memory helpers (the Go host has no other allocator for HBM). */
@@ -74,7 +79,8 @@ int rh_memcpy_d2h(rh_context *ctx, void *host_dst, const void *dev_src, size_t b
 
 /* Per-launch GEMM timing with HIP events on the context's stream.
  * kind: 0 = full-int8 GEMM, 1 = weight-only int8 GEMM, 2 = fp32 GEMM,
- * 3 = attention. Reading syncs the stream. */
+ * 3 = attention, 4 = bf16 split of GEMM activations (weight-only int8 and
+ * fp32 GEMMs on bf16 planes). Reading syncs the stream. */
 typedef struct {
   int64_t launches;
   double total_ms;    /* sum of per-launch event durations */

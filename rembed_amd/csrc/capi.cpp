@@ -7,6 +7,7 @@
 // status with a thread-local message instead of aborting.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -54,6 +55,24 @@ hipError_t rh_context::prof_begin(int kind, double ops, double bytes, int* slot)
   recs.push_back(r);
   *slot = (int)recs.size() - 1;
   return hipSuccess;
+}
+
+// Grows only; the old buffer may still be read by queued kernels, so the
+// stream drains before it is freed.
+hipError_t rh_context::ensure_ws(size_t bytes) {
+  if (bytes <= ws_bytes) return hipSuccess;
+  if (ws) {
+    hipError_t e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return e;
+    (void)hipFree(ws);
+    ws = nullptr;
+    ws_bytes = 0;
+  }
+  const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+  hipError_t e = hipMalloc(&ws, want);
+  if (e == hipSuccess) ws_bytes = want;
+  else ws = nullptr;
+  return e;
 }
 
 hipError_t rh_context::prof_end(int slot) {
@@ -150,6 +169,49 @@ static int check_pack_shape(const char* who, int k, int n) {
   return RH_OK;
 }
 
+// bf16 with round-to-nearest-even (the device conversion rounds the same
+// way); NaN stays NaN.
+static uint16_t bf16_rne(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static float bf16_value(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// The bf16 planes of a padded [np][kp] weight image for the bf16-MFMA GEMMs:
+// weight-only int8 gets its integers (exact in bf16), fp32 the split
+// hi = bf16(w), lo = bf16(w - hi). Zero padding stays zero.
+static hipError_t upload_planes(rh_weight* w, const std::vector<uint8_t>& img) {
+  const size_t count = (size_t)w->np * w->kp;
+  std::vector<uint16_t> hi(count), lo;
+  if (w->mode == RH_MODE_W8) {
+    const int8_t* q = reinterpret_cast<const int8_t*>(img.data());
+    for (size_t i = 0; i < count; i++) hi[i] = bf16_rne((float)q[i]);
+  } else {
+    const float* f = reinterpret_cast<const float*>(img.data());
+    lo.resize(count);
+    for (size_t i = 0; i < count; i++) {
+      hi[i] = bf16_rne(f[i]);
+      lo[i] = bf16_rne(f[i] - bf16_value(hi[i]));
+    }
+  }
+  hipError_t e = hipMalloc(&w->d_bf, count * 2);
+  if (e == hipSuccess) e = hipMemcpy(w->d_bf, hi.data(), count * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess && !lo.empty()) {
+    e = hipMalloc(&w->d_bf_lo, count * 2);
+    if (e == hipSuccess) e = hipMemcpy(w->d_bf_lo, lo.data(), count * 2, hipMemcpyHostToDevice);
+  }
+  return e;
+}
+
 int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
                 int n, rh_weight** out) {
   static const char* names[] = {"PackB", "PackB8", "PackB8VNNI"};
@@ -181,6 +243,7 @@ int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int 
   }
   hipError_t e = hipMalloc(&w->d_data, img.size());
   if (e == hipSuccess) e = hipMemcpy(w->d_data, img.data(), img.size(), hipMemcpyHostToDevice);
+  if (e == hipSuccess && mode != RH_MODE_A8W8) e = upload_planes(w, img);
   if (e == hipSuccess && !scales.empty()) {
     e = hipMalloc(&w->d_scales, n * sizeof(float));
     if (e == hipSuccess)
@@ -213,6 +276,8 @@ void destroy_weight(rh_weight* w) {
   if (w->d_scales) (void)hipFree(w->d_scales);
   if (w->d_colsum) (void)hipFree(w->d_colsum);
   if (w->d_bias) (void)hipFree(w->d_bias);
+  if (w->d_bf) (void)hipFree(w->d_bf);
+  if (w->d_bf_lo) (void)hipFree(w->d_bf_lo);
   delete w;
 }
 
@@ -223,6 +288,7 @@ void ctx_release(Context* ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   ctx->prof_clear();
+  if (ctx->ws) (void)hipFree(ctx->ws);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -283,6 +349,57 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
   return RH_OK;
 }
 
+// Weight-only int8 / fp32 linear on bf16 planes: split the activations once
+// into the context workspace, then the planes GEMM. Rows go in chunks that
+// keep the kernel's 32-bit element offsets in range.
+static int run_linear_planes(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
+                             float* dst, int ldc, int act, const float* bias) {
+  hipStream_t s = ctx->stream;
+  const int a_terms = w->mode == RH_MODE_W8 ? ctx->w8_terms : 2;
+  const int b_terms = w->mode == RH_MODE_W8 ? 1 : 2;
+  const int ldk = (int)round_up(w->k, 64);
+  const int chunk = std::min(m, (int)((1u << 30) / (unsigned)ldk));
+  const size_t plane = (size_t)chunk * ldk * 2;
+  hipError_t e = ctx->ensure_ws(plane * a_terms);
+  if (e != hipSuccess) return hip_fail(e, "gemm workspace", __FILE__, __LINE__);
+  __bf16* hi = static_cast<__bf16*>(ctx->ws);
+  __bf16* lo = a_terms == 2 ? reinterpret_cast<__bf16*>(static_cast<uint8_t*>(ctx->ws) + plane)
+                            : nullptr;
+  for (int r0 = 0; r0 < m; r0 += chunk) {
+    const int mc = std::min(chunk, m - r0);
+    const double M = mc, K = w->k, N = w->n;
+    int slot = -1;
+    e = ctx->prof_begin(4, 0.0, M * K * 4 + M * ldk * 2.0 * a_terms, &slot);
+    if (e == hipSuccess) e = launch_split_bf16(a + (size_t)r0 * lda, lda, mc, w->k, hi, lo, ldk, s);
+    if (e == hipSuccess) e = ctx->prof_end(slot);
+    if (e != hipSuccess) return hip_fail(e, "split_bf16", __FILE__, __LINE__);
+    GemmPlArgs g{};
+    g.Ah = hi;
+    g.Al = lo;
+    g.lda = ldk;
+    g.Bh = static_cast<const __bf16*>(w->d_bf);
+    g.Bl = static_cast<const __bf16*>(w->d_bf_lo);
+    g.ldb = w->kp;
+    g.M = mc;
+    g.N = w->n;
+    g.K = w->k;
+    g.col_scales = w->mode == RH_MODE_W8 ? w->d_scales : nullptr;
+    g.bias = bias;
+    g.C = dst + (size_t)r0 * ldc;
+    g.ldc = ldc;
+    g.act = act;
+    // algorithmic bytes: the fp32 activations, the weights as stored for
+    // the mode (int8 / fp32), the fp32 output
+    const double wbytes = w->mode == RH_MODE_W8 ? K * N + 4 * N : 4 * K * N;
+    const double bytes = M * K * 4 + wbytes + M * (w->glu ? N / 2 : N) * 4 + (bias ? 4 * N : 0);
+    e = ctx->prof_begin(w->mode == RH_MODE_W8 ? 1 : 2, 2.0 * M * K * N, bytes, &slot);
+    if (e == hipSuccess) e = launch_gemm_planes(g, a_terms, b_terms, ctx->bf_tile, s);
+    if (e == hipSuccess) e = ctx->prof_end(slot);
+    if (e != hipSuccess) return hip_fail(e, "planes gemm launch", __FILE__, __LINE__);
+  }
+  return RH_OK;
+}
+
 // One linear with fp32 output: the GEMM family dispatch of applyDense
 // (bert.go:282-301) with bias/activation fused. For A8W8 the input must
 // already be quantized into qa/rs (row stride ldq) unless quantize_first,
@@ -302,6 +419,9 @@ int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
     return run_gemm_i8(ctx, w, qa, ldq, rs, m, EPI_F32, dst, ldc, act, bias, nullptr,
                        nullptr, ops);
   }
+  // the planes path serves every mode but the native-f32 MFMA choice
+  if (ctx->bf_algo == 0 && !(w->mode == RH_MODE_F32 && ctx->f32_algo == F32_NATIVE))
+    return run_linear_planes(ctx, w, a, lda, m, dst, ldc, act, bias);
   int slot = -1;
   hipError_t e = hipSuccess;
   GemmBfArgs g{};
@@ -402,6 +522,14 @@ int rh_context_set_option(rh_context* ctx, int option, int value) {
     case RH_CTX_W8_TERMS:
       if (value != 1 && value != 2) return fail(RH_ERR_INVALID, "w8 terms must be 1 or 2");
       ctx->w8_terms = value;
+      return RH_OK;
+    case RH_CTX_BF_ALGO:
+      if (value < 0 || value > 1) return fail(RH_ERR_INVALID, "bf_algo must be 0 or 1");
+      ctx->bf_algo = value;
+      return RH_OK;
+    case RH_CTX_BF_TILE:
+      if (value < 0 || value > kPlanesTileConfigs) return fail(RH_ERR_INVALID, "unknown planes tile");
+      ctx->bf_tile = value;
       return RH_OK;
     case RH_CTX_I8_TILE:
       if (value < 0 || value > kI8TileConfigs) return fail(RH_ERR_INVALID, "unknown int8 tile");

@@ -21,6 +21,13 @@ struct rh_context {
   int f32_algo = rh::F32_SPLIT3;
   int w8_terms = 2;  // bf16 terms of the fp32 activations in weight-only int8
   int i8_tile = 0;   // 0 = automatic int8 GEMM tile choice
+  int bf_algo = 0;   // W8/F32 GEMM: 0 = bf16 planes (pre-split), 1 = in-kernel split
+  int bf_tile = 0;   // 0 = automatic bf16-planes GEMM tile choice
+  // grow-only device workspace (bf16 planes of the activations); the context
+  // serializes its calls, so one buffer serves every GEMM on its stream
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipError_t ensure_ws(size_t bytes);
 
   struct ProfRec {
     hipEvent_t a, b;
@@ -48,6 +55,10 @@ struct rh_weight {
   // gated (SwiGLU/GeGLU) weight: n = 2 * i rows, gate and up interleaved in
   // groups of kGluGroup; rh_linear writes i = n / 2 output columns
   bool glu = false;
+  // bf16 planes [np][kp] for the bf16-MFMA GEMMs: W8 holds the int8 values
+  // (exact in bf16), F32 the hi/lo split of the fp32 weights
+  void* d_bf = nullptr;
+  void* d_bf_lo = nullptr;
 };
 
 namespace rh {

@@ -25,6 +25,30 @@ __device__ __forceinline__ int lds_off(int r, int c) {
   return (r << 7) + ((c ^ ((r ^ (r >> 3)) & 7)) << 4);
 }
 
+// 64-byte rows of 4 chunks. A fragment read has 16 consecutive rows in flight
+// per LDS cycle on gfx950 (64 banks): rows r, r+4, r+8, r+12 share a 256-byte
+// bank window, so their chunks are permuted by ((r>>1) ^ (r>>3)) & 3, which
+// also keeps any 8 consecutive rows distinct for a 32-bank phase.
+__device__ __forceinline__ int i8_slot(int row, int chunk) {
+  return (row << 2) + (chunk ^ (((row >> 1) ^ (row >> 3)) & 3));
+}
+
+// 16-byte global -> LDS copy (global_load_lds_dwordx4). The builtin exists
+// only for the device target; the host pass of the kernel template must
+// still see a valid body to emit its launch stub.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds_dst, 16, 0, 0);
+#endif
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
+// [15:14], expcnt[6:4] and lgkmcnt[11:8] left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 3) << 14));
+}
+
 // erf-GELU with exactly the float32 operation sequence of the reference's
 // geluScalar (internal/tensor/tensor.go:508-538; exp body fastmath.go:93-109).
 // The library is compiled with -ffp-contract=off, so no FMA is formed here.

@@ -26,30 +26,6 @@
 
 namespace rh {
 
-// 64-byte rows of 4 chunks. A fragment read has 16 consecutive rows in flight
-// per LDS cycle on gfx950 (64 banks): rows r, r+4, r+8, r+12 share a 256-byte
-// bank window, so their chunks are permuted by ((r>>1) ^ (r>>3)) & 3, which
-// also keeps any 8 consecutive rows distinct for a 32-bank phase.
-__device__ __forceinline__ int i8_slot(int row, int chunk) {
-  return (row << 2) + (chunk ^ (((row >> 1) ^ (row >> 3)) & 3));
-}
-
-// 16-byte global -> LDS copy (global_load_lds_dwordx4). The builtin exists
-// only for the device target; the host pass of the kernel template must
-// still see a valid body to emit its launch stub.
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds_dst, 16, 0, 0);
-#endif
-}
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
-// [15:14], expcnt[6:4] and lgkmcnt[11:8] left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 3) << 14));
-}
-
 // QuantizeRowU8's per-element step (internal/tensor/pack_vnni.go:103-111).
 __device__ __forceinline__ uint32_t quant_byte(float v, float inv) {
   int q = (int)rintf(v * inv) + 128;
@@ -66,7 +42,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
   constexpr int LA = kA / (256 * 16), LB = kB / (256 * 16);  // loads per thread
   constexpr int kLoads = LA + LB;
   constexpr int kEpiStride = WN + 4;  // ints per row of the epilogue transpose
-  static_assert(NS * kStage >= 4 * 32 * kEpiStride * 4, "epilogue LDS");
+  constexpr int kEpiBytes = 4 * 32 * kEpiStride * 4;
+  static_assert(NS * kStage >= kEpiBytes + 3 * BM * 4, "epilogue LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
 
   const int tid = threadIdx.x;
@@ -169,6 +146,32 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
   // (AddBias), then the activation (bert.go:297-300, 913-915).
   __syncthreads();
   int* ep = reinterpret_cast<int*>(lds) + wave * 32 * kEpiStride;
+  // Per-row operands of the tile (row scale; for EPI_QUANT the output row's
+  // scale and its reciprocal), fetched once per tile by one thread per row
+  // and read from LDS in the store loops: a global load per stored row would
+  // put one memory latency per row pass on the epilogue's critical path.
+  float* rs_l = reinterpret_cast<float*>(lds + kEpiBytes);
+  float* sc_l = rs_l + BM;
+  float* inv_l = sc_l + BM;
+  if constexpr (EPI != EPI_ACC) {
+    for (int r = tid; r < BM; r += 256) {
+      const int gr = row0 + r;
+      float rs = 0.0f, sc = 1.0f;
+      if (gr < p.M) {
+        rs = p.row_scales[gr];
+        if constexpr (EPI == EPI_QUANT) {
+          sc = p.row_absmax[gr] / 127.0f;
+          if (sc == 0.0f) sc = 1.0f;
+        }
+      }
+      rs_l[r] = rs;
+      if constexpr (EPI == EPI_QUANT) {
+        sc_l[r] = sc;
+        inv_l[r] = 1.0f / sc;
+      }
+    }
+    __syncthreads();
+  }
   constexpr int kLanesPerRow = WN / 4;
   constexpr int kRowsPerPass = 64 / kLanesPerRow;
   const int c4 = (lane % kLanesPerRow) * 4;
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
           const v4i ag = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8);
           const v4i au = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8 + 4);
           if (grow < p.M && pk_ok) {
-            const float rs = p.row_scales[grow];
+            const float rs = rs_l[grow - row0];
             v4f o;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
       } else {
         v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
         if (ok) {
-          const float rs = p.row_scales[grow];
+          const float rs = rs_l[grow - row0];
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             float x = (float)a[e] * rs;
@@ -278,9 +281,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
             atomicMax(reinterpret_cast<unsigned int*>(p.row_absmax) + grow, __float_as_uint(m));
         } else {  // EPI_QUANT: QuantizeRowU8 with the row's |max| from pass 1
           if (ok) {
-            float scale = p.row_absmax[grow] / 127.0f;
-            if (scale == 0.0f) scale = 1.0f;
-            const float inv = 1.0f / scale;
+            const float scale = sc_l[grow - row0];
+            const float inv = inv_l[grow - row0];
             const uint32_t w = quant_byte(v[0], inv) | (quant_byte(v[1], inv) << 8) |
                                (quant_byte(v[2], inv) << 16) | (quant_byte(v[3], inv) << 24);
             *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
@@ -309,10 +311,15 @@ static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
   }
 }
 
-// Automatic tile: fewest CU rounds times per-tile cost. Relative costs per
-// unit of work measured on MI355X (the 128x128 tile runs two workgroups per
-// CU but is LDS-bandwidth bound; 256x256 keeps one per CU).
-int pick_i8_tile(int M, int N) {
+// Automatic tile. Epilogues that dequantize (fp32/bf16/u8 out): 128x128,
+// whose two workgroups per CU overlap one tile's epilogue with the other's
+// main loop — the fastest or within 3% at every encoder shape measured
+// (M 10102 and 16384, K x N of the BERT-base linears). Raw int32
+// accumulators: fewest CU rounds times per-tile cost, relative costs per unit
+// of work measured on MI355X (128x128 is LDS-bandwidth bound in the main
+// loop; 256x256 keeps one workgroup per CU).
+int pick_i8_tile(int M, int N, int epi) {
+  if (epi != EPI_ACC) return 3;
   struct Cand { int tile, bm, bn, per_cu; double cost; };
   const Cand cands[] = {{1, 256, 256, 1, 1.0}, {2, 256, 128, 1, 1.25}, {3, 128, 128, 2, 1.8}};
   int best = 1;
@@ -331,7 +338,7 @@ int pick_i8_tile(int M, int N) {
 
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (tile <= 0 || tile > kI8TileConfigs) tile = pick_i8_tile(a.M, a.N);
+  if (tile <= 0 || tile > kI8TileConfigs) tile = pick_i8_tile(a.M, a.N, a.epi);
   switch (a.epi) {
     case EPI_F32: return launch_epi<EPI_F32>(a, tile, s);
     case EPI_BF16: return launch_epi<EPI_BF16>(a, tile, s);

@@ -1,0 +1,329 @@
+// gemm_planes.hip — the weight-only int8 and fp32 GEMMs on bf16 MFMA
+// (v_mfma_f32_32x32x16_bf16, fp32 accumulation) with every operand already
+// in bf16 "planes", so the main loop only moves bytes and multiplies.
+//
+//  * Weight-only int8 (replaces MatMulPacked8, internal/tensor/pack8.go:80-126
+//    and gemm4x16i8, gemm8_amd64.s:14-79): the int8 weights are stored once,
+//    at pack time, as a bf16 plane of the same integers (exact: |q| <= 127
+//    needs 7 significant bits). The fp32 activations are split by one light
+//    pass into hi = bf16(a) and lo = bf16(a - hi), so a·q keeps ~16
+//    significant bits of a; the per-channel scale multiplies the fp32
+//    accumulator in the epilogue, as the reference does.
+//  * fp32 (replaces MatMulPacked, pack.go:123-210 and gemm4x16,
+//    gemm_amd64.s:14-64): weights split into hi/lo planes at pack time,
+//    activations by the same pass; three products hi·hi + hi·lo + lo·hi (the
+//    lo·lo term is ~2^-16 of the others, below the fp32 rounding of the sum
+//    at these magnitudes).
+//
+// Main loop (same scheme as the int8 GEMM): BM x BN tile per 256-thread
+// workgroup, 2x2 waves of 32x32 MFMA tiles, K in stages of 32 bf16 = 64
+// bytes per row and plane. Stages reach LDS by global_load_lds_dwordx4 (no
+// register staging): lane l of a wave instruction writes LDS bytes
+// [16l, 16l+16) of a 1 KiB block, so each lane loads the global 16-byte chunk
+// that belongs at that slot, rows permuted by i8_slot (conflict-free fragment
+// reads). NS stages in flight, one barrier per stage.
+//
+// The epilogue parks each 32-row band of accumulators in LDS and reads rows
+// back 4 columns per lane: scale, bias, activation (or the gated pair) and a
+// 4-wide vector store.
+#include "gemm_common.h"
+
+namespace rh {
+
+template <int BM, int BN, int NS, int AT, int BT, bool GLU>
+__global__ __launch_bounds__(256) void gemm_planes_kernel(GemmPlArgs p) {
+  constexpr int BK = 32;  // bf16 elements per stage and row
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int kA = BM * BK * 2, kB = BN * BK * 2;  // bytes per plane
+  constexpr int kStage = AT * kA + BT * kB;
+  constexpr int LA = kA / (256 * 16), LB = kB / (256 * 16);  // loads per thread and plane
+  constexpr int kLoads = AT * LA + BT * LB;
+  constexpr int kEpiStride = WN + 4;  // floats per row of the epilogue transpose
+  static_assert(NS >= 3, "one barrier per stage needs a ring of >= 3");
+  static_assert(NS * kStage <= 160 * 1024, "LDS");
+  static_assert(NS * kStage >= 4 * 32 * kEpiStride * 4, "epilogue LDS");
+  static_assert((NS - 2) * kLoads < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int row0 = (tile / tiles_n) * BM;
+  const int col0 = (tile % tiles_n) * BN;
+  const int nk = (p.K + BK - 1) / BK;
+
+  // Element offsets of this thread's loads (fixed across stages). Rows past
+  // M read row M-1 (their outputs are never stored); weight rows are
+  // zero-padded to a multiple of 256; both operands are zero past K up to a
+  // multiple of 64, so a stage never masks.
+  int aoff[LA], boff[LB];
+#pragma unroll
+  for (int j = 0; j < LA; j++) {
+    const int slot = (wave * LA + j) * 64 + lane;
+    const int r = slot >> 2;
+    const int chunk = (slot & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);  // inverse of i8_slot
+    const int gr = row0 + r;
+    aoff[j] = (gr < p.M ? gr : p.M - 1) * p.lda + chunk * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < LB; j++) {
+    const int slot = (wave * LB + j) * 64 + lane;
+    const int r = slot >> 2;
+    const int chunk = (slot & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);
+    boff[j] = (col0 + r) * p.ldb + chunk * 8;
+  }
+
+  auto issue = [&](int kt) {
+    uint8_t* s = lds + (kt % NS) * kStage;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int j = 0; j < LA; j++) {
+      lds_dma16(p.Ah + aoff[j] + k0, s + (wave * LA + j) * 1024);
+      if constexpr (AT == 2) lds_dma16(p.Al + aoff[j] + k0, s + kA + (wave * LA + j) * 1024);
+    }
+#pragma unroll
+    for (int j = 0; j < LB; j++) {
+      lds_dma16(p.Bh + boff[j] + k0, s + AT * kA + (wave * LB + j) * 1024);
+      if constexpr (BT == 2)
+        lds_dma16(p.Bl + boff[j] + k0, s + AT * kA + kB + (wave * LB + j) * 1024);
+    }
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+#pragma unroll
+  for (int st = 0; st < NS - 1; st++)
+    if (st < nk) issue(st);
+
+  const int fr = lane & 31, fg = lane >> 5;
+  for (int kt = 0; kt < nk; kt++) {
+    // Stage kt has landed once at most min(NS-2, nk-1-kt) later stages are
+    // still pending for this wave.
+    const int later = nk - 1 - kt;
+    if (later >= NS - 2) wait_vmcnt<(NS - 2) * kLoads>();
+    else if (NS > 3 && later == 1) wait_vmcnt<kLoads>();
+    else wait_vmcnt<0>();
+    // A bare s_barrier (a __syncthreads() fence would drain the whole ring):
+    // every wave's stage-kt data is in LDS and its reads of stage kt-1 are
+    // done, so the slot of stage kt-1 can be refilled.
+    __builtin_amdgcn_s_barrier();
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+    const uint8_t* sA = lds + (kt % NS) * kStage;
+    const uint8_t* sB = sA + AT * kA;
+#pragma unroll
+    for (int s = 0; s < BK / 16; s++) {
+      const int c = 2 * s + fg;
+      v8bf fah[TM], fal[TM], fbh[TN], fbl[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int off = i8_slot(wm * WM + i * 32 + fr, c) * 16;
+        fah[i] = *reinterpret_cast<const v8bf*>(sA + off);
+        if constexpr (AT == 2) fal[i] = *reinterpret_cast<const v8bf*>(sA + kA + off);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int off = i8_slot(wn * WN + j * 32 + fr, c) * 16;
+        fbh[j] = *reinterpret_cast<const v8bf*>(sB + off);
+        if constexpr (BT == 2) fbl[j] = *reinterpret_cast<const v8bf*>(sB + kB + off);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fah[i], fbh[j], acc[i][j], 0, 0, 0);
+          if constexpr (BT == 2)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fah[i], fbl[j], acc[i][j], 0, 0, 0);
+          if constexpr (AT == 2)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fal[i], fbh[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  }
+
+  // ---- epilogue ----------------------------------------------------------
+  // applyDense order (bert.go:282-301, pack8.go:118-122): fp32 sum, ·scale
+  // (weight-only int8), + bias, then the activation.
+  __syncthreads();
+  float* ep = reinterpret_cast<float*>(lds) + wave * 32 * kEpiStride;
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        ep[((r >> 2) * 8 + fg * 4 + (r & 3)) * kEpiStride + j * 32 + fr] = acc[i][j][r];
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    const int grow_base = row0 + wm * WM + i * 32;
+    if constexpr (GLU) {
+      // Gated weight: tile columns 8t..8t+3 are gate rows, 8t+4..8t+7 the
+      // matching up rows. A lane reads both halves of one group of 8 and
+      // writes act(gate) * up at output column (packed column) / 2.
+      constexpr int kL8 = WN / 8, kR8 = 64 / kL8;
+      const int c8 = (lane % kL8) * 8;
+      const int gpk = col0 + wn * WN + c8;
+      const bool pk_ok = gpk < p.N;
+      v4f csg = {1.0f, 1.0f, 1.0f, 1.0f}, csu = csg;
+      v4f bg = {0.0f, 0.0f, 0.0f, 0.0f}, bu = bg;
+      if (pk_ok) {
+        if (p.col_scales) {
+          csg = *reinterpret_cast<const v4f*>(p.col_scales + gpk);
+          csu = *reinterpret_cast<const v4f*>(p.col_scales + gpk + 4);
+        }
+        if (p.bias) {
+          bg = *reinterpret_cast<const v4f*>(p.bias + gpk);
+          bu = *reinterpret_cast<const v4f*>(p.bias + gpk + 4);
+        }
+      }
+      for (int rr = lane / kL8; rr < 32; rr += kR8) {
+        const int grow = grow_base + rr;
+        const v4f ag = *reinterpret_cast<const v4f*>(ep + rr * kEpiStride + c8);
+        const v4f au = *reinterpret_cast<const v4f*>(ep + rr * kEpiStride + c8 + 4);
+        if (grow < p.M && pk_ok) {
+          v4f o;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float g = ag[e], u = au[e];
+            if (p.col_scales) {
+              g = g * csg[e];
+              u = u * csu[e];
+            }
+            if (p.bias) {
+              g = g + bg[e];
+              u = u + bu[e];
+            }
+            o[e] = glu_act(g, u, p.act);
+          }
+          *reinterpret_cast<v4f*>(p.C + (size_t)grow * p.ldc + gpk / 2) = o;
+        }
+      }
+    } else {
+      constexpr int kLanesPerRow = WN / 4;
+      constexpr int kRowsPerPass = 64 / kLanesPerRow;
+      const int c4 = (lane % kLanesPerRow) * 4;
+      const int gcol = col0 + wn * WN + c4;
+      const bool col_ok = gcol < p.N;
+      v4f cs = {1.0f, 1.0f, 1.0f, 1.0f}, bs = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (col_ok) {
+        if (p.col_scales) cs = *reinterpret_cast<const v4f*>(p.col_scales + gcol);
+        if (p.bias) bs = *reinterpret_cast<const v4f*>(p.bias + gcol);
+      }
+#pragma unroll 2
+      for (int rr = lane / kLanesPerRow; rr < 32; rr += kRowsPerPass) {
+        const int grow = grow_base + rr;
+        const v4f a = *reinterpret_cast<const v4f*>(ep + rr * kEpiStride + c4);
+        if (grow < p.M && col_ok) {
+          v4f v;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float x = a[e];
+            if (p.col_scales) x = x * cs[e];
+            if (p.bias) x = x + bs[e];
+            v[e] = apply_act(x, p.act);
+          }
+          *reinterpret_cast<v4f*>(p.C + (size_t)grow * p.ldc + gcol) = v;
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// a [M][lda_f] fp32 -> hi/lo [M][ldk] bf16 planes, zero in [K, ldk). One
+// thread per 4 columns; rows with 16-byte aligned 4-groups load as float4.
+__global__ __launch_bounds__(256) void split_bf16_kernel(const float* __restrict__ a,
+                                                         int lda_f, int M, int K,
+                                                         __bf16* __restrict__ hi,
+                                                         __bf16* __restrict__ lo, int ldk,
+                                                         int vec) {
+  typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+  const int groups = ldk >> 2;
+  const size_t total = (size_t)M * groups;
+  for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+       g += (size_t)gridDim.x * blockDim.x) {
+    const int row = (int)(g / groups);
+    const int c = (int)(g % groups) * 4;
+    const float* src = a + (size_t)row * lda_f + c;
+    v4f x;
+    if (vec && c + 4 <= K) {
+      x = *reinterpret_cast<const v4f*>(src);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) x[e] = c + e < K ? src[e] : 0.0f;
+    }
+    v4bf h, l;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      h[e] = (__bf16)x[e];
+      l[e] = (__bf16)(x[e] - (float)h[e]);
+    }
+    *reinterpret_cast<v4bf*>(hi + (size_t)row * ldk + c) = h;
+    if (lo) *reinterpret_cast<v4bf*>(lo + (size_t)row * ldk + c) = l;
+  }
+}
+
+hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi, __bf16* lo,
+                             int ldk, hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  if (ldk % 64 != 0 || ldk < K) return hipErrorInvalidValue;
+  const int vec = (lda_f % 4 == 0) && ((reinterpret_cast<uintptr_t>(a) & 15) == 0);
+  const size_t total = (size_t)M * (ldk / 4);
+  const size_t blocks = std::min<size_t>((total + 255) / 256, 256 * 16);
+  hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a, lda_f, M, K,
+                     hi, lo, ldk, vec);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int NS, int AT, int BT>
+static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
+  const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
+  if (is_glu(a.act))
+    hipLaunchKernelGGL((gemm_planes_kernel<BM, BN, NS, AT, BT, true>), dim3(tiles), dim3(256), 0,
+                       s, a);
+  else
+    hipLaunchKernelGGL((gemm_planes_kernel<BM, BN, NS, AT, BT, false>), dim3(tiles), dim3(256),
+                       0, s, a);
+  return hipGetLastError();
+}
+
+// Tiles: 1 = 256x256, 2 = 256x128, 3 = 128x128 (stages as many as fit in
+// 160 KiB of LDS; fp32's four planes leave no room for 256x256). Automatic
+// choice: the largest tile that still gives every CU a workgroup.
+int pick_planes_tile(int M, int N, int a_terms, int b_terms) {
+  if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256) return 1;
+  if (ceil_div(M, 256) * ceil_div(N, 128) >= 256) return 2;
+  return 3;
+}
+
+hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int tile,
+                              hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a.lda % 64 != 0 || a.ldb % 64 != 0) return hipErrorInvalidValue;
+  if (tile <= 0 || tile > kPlanesTileConfigs) tile = pick_planes_tile(a.M, a.N, a_terms, b_terms);
+  if (a_terms == 1 && b_terms == 1) {
+    if (tile == 1) return launch_pl<256, 256, 4, 1, 1>(a, s);
+    if (tile == 2) return launch_pl<256, 128, 4, 1, 1>(a, s);
+    return launch_pl<128, 128, 4, 1, 1>(a, s);
+  }
+  if (a_terms == 2 && b_terms == 1) {
+    if (tile == 1) return launch_pl<256, 256, 3, 2, 1>(a, s);
+    if (tile == 2) return launch_pl<256, 128, 4, 2, 1>(a, s);
+    return launch_pl<128, 128, 3, 2, 1>(a, s);
+  }
+  if (a_terms == 2 && b_terms == 2) {
+    if (tile <= 2) return launch_pl<256, 128, 3, 2, 2>(a, s);
+    return launch_pl<128, 128, 3, 2, 2>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace rh

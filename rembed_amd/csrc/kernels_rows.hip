@@ -34,15 +34,17 @@ __device__ __forceinline__ uint8_t quant_u8(float v, float inv) {
 
 // Generic quantizer over rows of any width (two passes over the row; the
 // second pass hits L2). Writes ldq bytes per row: k quantized + zero tail.
+// `act` is applied to each element first (the activation of the GEMM that
+// produced the row, moved here where the kernel has VALU to spare).
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const float* __restrict__ a, int lda, int m, int k, uint8_t* __restrict__ qa,
-    int ldq, float* __restrict__ row_scales, int vec) {
+    int ldq, float* __restrict__ row_scales, int vec, int act) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= m) return;
   const float* src = a + (size_t)row * lda;
   float mx = 0.0f;
-  for (int i = lane; i < k; i += 64) mx = fmaxf(mx, fabsf(src[i]));
+  for (int i = lane; i < k; i += 64) mx = fmaxf(mx, fabsf(apply_act(src[i], act)));
   mx = wave_max(mx);
   float scale = mx / 127.0f;
   if (scale == 0.0f) scale = 1.0f;
@@ -51,13 +53,15 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   if (vec) {
     for (int i = lane * 4; i < k; i += 256) {
       v4f v = *reinterpret_cast<const v4f*>(src + i);
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = apply_act(v[e], act);
       uint32_t w = (uint32_t)quant_u8(v[0], inv) | ((uint32_t)quant_u8(v[1], inv) << 8) |
                    ((uint32_t)quant_u8(v[2], inv) << 16) |
                    ((uint32_t)quant_u8(v[3], inv) << 24);
       *reinterpret_cast<uint32_t*>(dst + i) = w;
     }
   } else {
-    for (int i = lane; i < k; i += 64) dst[i] = quant_u8(src[i], inv);
+    for (int i = lane; i < k; i += 64) dst[i] = quant_u8(apply_act(src[i], act), inv);
   }
   for (int i = k + lane; i < ldq; i += 64) dst[i] = 0;
   if (lane == 0) row_scales[row] = scale;
@@ -66,7 +70,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
 // Single-pass variant for 16-byte aligned rows with k % 4 == 0 and
 // k <= 256 * V: the row stays in registers (V float4 per lane), so HBM sees
 // one read of the row and one write of its bytes.
-template <int V>
+template <int V, bool GELU>
 __global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
     const float* __restrict__ a, int lda, int m, int k, uint8_t* __restrict__ qa,
     int ldq, float* __restrict__ row_scales) {
@@ -80,6 +84,10 @@ __global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
   for (int e = 0; e < V; e++) {
     const int i = (lane + 64 * e) * 4;
     x[e] = i < k ? *reinterpret_cast<const v4f*>(src + i) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (GELU) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) x[e][c] = apply_act(x[e][c], ACT_GELU);
+    }
     mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x[e][0]), fabsf(x[e][1])), fmaxf(fabsf(x[e][2]), fabsf(x[e][3]))));
   }
   mx = wave_max(mx);
@@ -101,33 +109,38 @@ __global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
 
 template <int V>
 static void launch_qvec(const float* a, int lda, int m, int k, uint8_t* qa, int ldq,
-                        float* rs, hipStream_t s) {
-  hipLaunchKernelGGL((quantize_rows_vec_kernel<V>), dim3(ceil_div(m, kRowsPerBlock)),
-                     dim3(256), 0, s, a, lda, m, k, qa, ldq, rs);
+                        float* rs, int act, hipStream_t s) {
+  if (act == ACT_GELU)
+    hipLaunchKernelGGL((quantize_rows_vec_kernel<V, true>), dim3(ceil_div(m, kRowsPerBlock)),
+                       dim3(256), 0, s, a, lda, m, k, qa, ldq, rs);
+  else
+    hipLaunchKernelGGL((quantize_rows_vec_kernel<V, false>), dim3(ceil_div(m, kRowsPerBlock)),
+                       dim3(256), 0, s, a, lda, m, k, qa, ldq, rs);
 }
 
 hipError_t launch_quantize_rows_u8(const float* a, int lda, int m, int k,
                                    uint8_t* qa, int ldq, float* row_scales,
-                                   hipStream_t s) {
+                                   hipStream_t s, int act) {
   if (m <= 0) return hipSuccess;
+  if (act != ACT_NONE && act != ACT_GELU) return hipErrorInvalidValue;
   // 16-byte row loads and 4-byte stores need aligned rows.
   const int vec = (k % 4 == 0) && (lda % 4 == 0) && (ldq % 4 == 0) &&
                   ((reinterpret_cast<uintptr_t>(a) & 15) == 0) &&
                   ((reinterpret_cast<uintptr_t>(qa) & 3) == 0);
   if (vec && k <= 4096) {
     const int v = ceil_div(k, 256);
-    if (v <= 1) launch_qvec<1>(a, lda, m, k, qa, ldq, row_scales, s);
-    else if (v <= 2) launch_qvec<2>(a, lda, m, k, qa, ldq, row_scales, s);
-    else if (v <= 3) launch_qvec<3>(a, lda, m, k, qa, ldq, row_scales, s);
-    else if (v <= 4) launch_qvec<4>(a, lda, m, k, qa, ldq, row_scales, s);
-    else if (v <= 6) launch_qvec<6>(a, lda, m, k, qa, ldq, row_scales, s);
-    else if (v <= 8) launch_qvec<8>(a, lda, m, k, qa, ldq, row_scales, s);
-    else if (v <= 12) launch_qvec<12>(a, lda, m, k, qa, ldq, row_scales, s);
-    else launch_qvec<16>(a, lda, m, k, qa, ldq, row_scales, s);
+    if (v <= 1) launch_qvec<1>(a, lda, m, k, qa, ldq, row_scales, act, s);
+    else if (v <= 2) launch_qvec<2>(a, lda, m, k, qa, ldq, row_scales, act, s);
+    else if (v <= 3) launch_qvec<3>(a, lda, m, k, qa, ldq, row_scales, act, s);
+    else if (v <= 4) launch_qvec<4>(a, lda, m, k, qa, ldq, row_scales, act, s);
+    else if (v <= 6) launch_qvec<6>(a, lda, m, k, qa, ldq, row_scales, act, s);
+    else if (v <= 8) launch_qvec<8>(a, lda, m, k, qa, ldq, row_scales, act, s);
+    else if (v <= 12) launch_qvec<12>(a, lda, m, k, qa, ldq, row_scales, act, s);
+    else launch_qvec<16>(a, lda, m, k, qa, ldq, row_scales, act, s);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(quantize_rows_kernel, dim3(ceil_div(m, kRowsPerBlock)),
-                     dim3(256), 0, s, a, lda, m, k, qa, ldq, row_scales, vec);
+                     dim3(256), 0, s, a, lda, m, k, qa, ldq, row_scales, vec, act);
   return hipGetLastError();
 }
 

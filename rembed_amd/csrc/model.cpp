@@ -370,6 +370,18 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
       st = run_gemm_i8(ctx, L.f2, qa2, ldq_for(I), rs2, M, EPI_F32, y, H, ACT_NONE,
                        L.f2->d_bias, nullptr, nullptr, 2.0 * MH * I * H);
       if (st) return st;
+    } else if (qf1 && needs_q(L.f2)) {
+      // FFN1 writes the fp32 pre-activation (dequant + bias); GELU moves into
+      // FFN2's row quantizer, which has VALU to spare where the GEMM
+      // epilogue does not. Same float32 operations in the same order as
+      // GELU(dense(x)) then QuantizeRowU8 (bert.go:910-916).
+      st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_NONE, L.f1->d_bias, qa, ldq_for(H),
+                      rs, false);
+      if (st) return st;
+      RH_HIP(launch_quantize_rows_u8(hid, I, M, I, qa2, ldq_for(I), rs2, s, ACT_GELU));
+      st = run_linear(ctx, L.f2, hid, I, M, y, H, ACT_NONE, L.f2->d_bias, qa2, ldq_for(I),
+                      rs2, false);
+      if (st) return st;
     } else {
       st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_GELU, L.f1->d_bias, qa, ldq_for(H),
                       rs, false);

@@ -110,6 +110,31 @@ struct GemmBfArgs {
   int act;
 };
 
+// The bf16-planes GEMM (W8 and F32 modes): activations and weights arrive
+// as bf16 planes (hi, optional lo), so the main loop only moves and
+// multiplies. Products: Ah.Bh + [BT=2] Ah.Bl + [AT=2] Al.Bh.
+struct GemmPlArgs {
+  const __bf16* Ah;
+  const __bf16* Al;  // AT == 2
+  int lda;           // elements, >= round_up(K, 64), zero past K
+  const __bf16* Bh;
+  const __bf16* Bl;  // BT == 2
+  int ldb;           // elements (kp)
+  int M, N, K;
+  const float* col_scales;  // W8: [N]; else null
+  const float* bias;
+  float* C;
+  int ldc;
+  int act;
+};
+// a fp32 [M][lda_f] -> hi, lo bf16 [M][ldk] (ldk = round_up(K, 64), zeros
+// past K): hi = bf16(x), lo = bf16(x - float(hi)), both rounded to nearest even
+hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi, __bf16* lo,
+                             int ldk, hipStream_t s);
+constexpr int kPlanesTileConfigs = 3;
+hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int tile,
+                              hipStream_t s);
+
 // fp32 GEMM strategies (selected per model/context; both kept so the
 // choice can be re-measured): three bf16 products or native f32 MFMA.
 enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
@@ -118,7 +143,7 @@ enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 // tile: 0 = automatic, 1 = 256x256, 2 = 256x128, 3 = 128x128.
 constexpr int kI8TileConfigs = 3;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
-int pick_i8_tile(int M, int N);
+int pick_i8_tile(int M, int N, int epi);
 // fills n floats with zero (graph-capture safe, unlike hipMemsetAsync)
 hipError_t launch_fill_zero(float* x, int n, hipStream_t s);
 // a_terms: 1 or 2 bf16 terms for the fp32 activations.
@@ -126,9 +151,10 @@ hipError_t launch_gemm_w8(const GemmBfArgs& a, int a_terms, hipStream_t s);
 hipError_t launch_gemm_f32(const GemmBfArgs& a, int algo, hipStream_t s);
 
 // ---- elementwise / norm / attention launchers (kernels_misc.hip, attention.hip)
+// QuantizeRowU8 of each row, optionally of act(row) (ACT_NONE or ACT_GELU)
 hipError_t launch_quantize_rows_u8(const float* a, int lda, int m, int k,
                                    uint8_t* qa, int ldq, float* row_scales,
-                                   hipStream_t s);
+                                   hipStream_t s, int act = ACT_NONE);
 hipError_t launch_gelu(float* x, size_t n, hipStream_t s);
 hipError_t launch_add_bias(float* x, const float* bias, int m, int n, int ldx,
                            hipStream_t s);

@@ -19,7 +19,7 @@ BERT_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
 PEAK = {"i8": 5000.0, "w8": 2500.0, "f32": 2500.0}  # TOP/s of the MFMA used
 
 
-def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u8=False):
+def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u8=False, bf=0):
     rng = np.random.default_rng(k * 7 + n)
     bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
     bias = rng.standard_normal(n, dtype=np.float32) * 0.02
@@ -32,6 +32,8 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
     rs = ctx.alloc(m * 4)
     kind = {"i8": 0, "w8": 1, "f32": 2}[mode]
     ctx.set_option(_lib.RH_CTX_I8_TILE, tile)
+    ctx.set_option(_lib.RH_CTX_BF_TILE, tile)
+    ctx.set_bf_algo(bf)
     if mode == "i8":
         T.QuantizeRowsU8(ctx, a, m, k, qa, ldq, rs)
 
@@ -59,13 +61,18 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
         run()
     ctx.sync()
     st = ctx.profile_read(kind)
+    sp = ctx.profile_read(4)  # activation split of the planes path
     ctx.profile(False)
     ctx.set_option(_lib.RH_CTX_I8_TILE, 0)
+    ctx.set_option(_lib.RH_CTX_BF_TILE, 0)
+    ctx.set_bf_algo(0)
     per_call = 2 if fused_u8 else 1  # the fused variant launches two GEMM passes
     us = st["total_ms"] * 1e3 / st["launches"] * per_call
     tops = st["total_ops"] / (st["total_ms"] * 1e-3) / 1e12
-    return {"mode": mode, "m": m, "k": k, "n": n, "act": act, "tile": tile,
-            "acc_only": acc_only, "fused_u8": fused_u8, "us": round(us, 2), "tops": round(tops, 1),
+    split_us = sp["total_ms"] * 1e3 / sp["launches"] if sp["launches"] else 0.0
+    return {"mode": mode, "m": m, "k": k, "n": n, "act": act, "tile": tile, "bf": bf,
+            "acc_only": acc_only, "fused_u8": fused_u8, "us": round(us, 2),
+            "split_us": round(split_us, 2), "tops": round(tops, 1),
             "frac": round(tops / PEAK[mode], 4),
             "gbps": round(st["total_bytes"] / (st["total_ms"] * 1e-3) / 1e9, 1)}
 
@@ -94,6 +101,8 @@ def main():
     ap.add_argument("--tiles", default="0")
     ap.add_argument("--shapes", default="", help="k,n;k,n;... (default: BERT-base)")
     ap.add_argument("--variants", default="", help="comma list of acc,fp32,gelu")
+    ap.add_argument("--bf", default="0", help="w8/f32 GEMM algorithms: 0 = bf16 planes, "
+                                              "1 = split in the main loop (comma list)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -114,9 +123,11 @@ def main():
                     table = {"acc": dict(acc_only=True), "fp32": dict(), "gelu": dict(act=1),
                              "u8gelu": dict(act=1, fused_u8=True)}
                     variants = [table[v] for v in args.variants.split(",")]
+                bfs = [0] if mode == "i8" else [int(b) for b in args.bf.split(",")]
                 for v in variants:
-                    r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile, **v)
-                    print(json.dumps(r), flush=True)
+                    for bf in bfs:
+                        r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile, bf=bf, **v)
+                        print(json.dumps(r), flush=True)
     ctx.close()
     return 0
 

@@ -47,6 +47,11 @@ class Context:
     def set_f32_algo(self, algo):
         self.set_option(_lib.RH_CTX_F32_ALGO, algo)
 
+    def set_bf_algo(self, algo):
+        """0: weight-only int8 / fp32 GEMMs on pre-split bf16 planes; 1: the
+        split inside the GEMM's main loop."""
+        self.set_option(_lib.RH_CTX_BF_ALGO, algo)
+
     def alloc(self, nbytes):
         return DeviceBuffer(self, nbytes)
 

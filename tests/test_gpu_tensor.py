@@ -261,10 +261,11 @@ def split_bound(a, b, k, eps, want):
     return eps * mag + f64_tol(k) * (1 + np.abs(want))
 
 
+@pytest.mark.parametrize("bf", [0, 1])
 @pytest.mark.parametrize("shape", KATS["packed_f32_shapes"]["shapes"])
-def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape):
+def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape, bf):
     m, k, n = shape
-    say(f"w8 shape {shape}")
+    say(f"w8 shape {shape} bf_algo {bf}")
     t = T()
     rng = np.random.default_rng(23 + k)
     a = (rng.random((m, k), dtype=np.float32) * 2 - 1).astype(np.float32)
@@ -274,7 +275,11 @@ def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape):
     q, sc, _ = pb.export()
     st, q_o, sc_o = O.pack_b8(bT, k, n)
     assert np.array_equal(q, q_o) and np.array_equal(sc, sc_o)
-    got = t.matmul_host(gpu_ctx, a, pb)
+    gpu_ctx.set_bf_algo(bf)
+    try:
+        got = t.matmul_host(gpu_ctx, a, pb)
+    finally:
+        gpu_ctx.set_bf_algo(0)
     deq = q.astype(np.float64) * sc.astype(np.float64)[:, None]
     want = a.astype(np.float64) @ deq.T
     bound = split_bound(a, deq, k, 2.0 ** -15, want)
@@ -283,21 +288,25 @@ def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape):
     assert np.all(err <= bound)
 
 
-@pytest.mark.parametrize("algo", [0, 1])
+# (f32 algo, bf algo): bf16 split on pre-split planes, split in the main
+# loop, native f32 MFMA
+@pytest.mark.parametrize("algo,bf", [(0, 0), (0, 1), (1, 0)], ids=["planes", "inloop", "native"])
 @pytest.mark.parametrize("shape", KATS["packed_f32_shapes"]["shapes"])
-def test_matmul_packed_f32_against_float64(gpu_ctx, shape, algo):
+def test_matmul_packed_f32_against_float64(gpu_ctx, shape, algo, bf):
     m, k, n = shape
-    say(f"f32 shape {shape} algo {algo}")
+    say(f"f32 shape {shape} algo {algo} bf_algo {bf}")
     t = T()
     rng = np.random.default_rng(11 + k)
     a = (rng.random((m, k), dtype=np.float32) * 2 - 1).astype(np.float32)
     bT = (rng.random((n, k), dtype=np.float32) * 2 - 1).astype(np.float32)
     gpu_ctx.set_f32_algo(algo)
+    gpu_ctx.set_bf_algo(bf)
     try:
         pb = t.PackB(gpu_ctx, bT, k, n)
         got = t.matmul_host(gpu_ctx, a, pb)
     finally:
         gpu_ctx.set_f32_algo(0)
+        gpu_ctx.set_bf_algo(0)
     want = a.astype(np.float64) @ bT.astype(np.float64).T
     err = np.abs(got - want)
     if algo == 1:  # native f32 MFMA: the reference's own tolerance
