@@ -295,45 +295,36 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
   }
 }
 
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int NS, int EPI>
 static hipError_t launch_tile(const GemmI8Args& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
-  hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, 4, EPI>), dim3(tiles), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, NS, EPI>), dim3(tiles), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
+// 1 = 256x256, 2 = 256x128 and 3 = 128x128 with 4 stages; 4 = 256x128 and
+// 5 = 128x256 with 3 stages (72 KiB of LDS and <= 256 registers per lane:
+// two workgroups per CU).
 template <int EPI>
 static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
   switch (tile) {
-    case 1: return launch_tile<256, 256, EPI>(a, s);
-    case 2: return launch_tile<256, 128, EPI>(a, s);
-    default: return launch_tile<128, 128, EPI>(a, s);
+    case 1: return launch_tile<256, 256, 4, EPI>(a, s);
+    case 2: return launch_tile<256, 128, 4, EPI>(a, s);
+    case 4: return launch_tile<256, 128, 3, EPI>(a, s);
+    case 5: return launch_tile<128, 256, 3, EPI>(a, s);
+    default: return launch_tile<128, 128, 4, EPI>(a, s);
   }
 }
 
-// Automatic tile. Epilogues that dequantize (fp32/bf16/u8 out): 128x128,
-// whose two workgroups per CU overlap one tile's epilogue with the other's
-// main loop — the fastest or within 3% at every encoder shape measured
-// (M 10102 and 16384, K x N of the BERT-base linears). Raw int32
-// accumulators: fewest CU rounds times per-tile cost, relative costs per unit
-// of work measured on MI355X (128x128 is LDS-bandwidth bound in the main
-// loop; 256x256 keeps one workgroup per CU).
+// Automatic tile: 128x256 (three stages, two workgroups per CU, one
+// tile's epilogue overlapping the other's main loop) once it yields a full
+// round of workgroups, else 128x128. Measured on MI355X at M 10102 and 16384
+// over the BERT-base linears: the faster of the two, or within 5% of it,
+// for every epilogue; 256x256 (one workgroup per CU) loses whenever the
+// output is dequantized.
 int pick_i8_tile(int M, int N, int epi) {
-  if (epi != EPI_ACC) return 3;
-  struct Cand { int tile, bm, bn, per_cu; double cost; };
-  const Cand cands[] = {{1, 256, 256, 1, 1.0}, {2, 256, 128, 1, 1.25}, {3, 128, 128, 2, 1.8}};
-  int best = 1;
-  double best_t = 1e300;
-  for (const Cand& c : cands) {
-    const int tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn);
-    const double rounds = (double)ceil_div(tiles, 256 * c.per_cu);
-    const double t = rounds * c.per_cu * (double)c.bm * c.bn * c.cost;
-    if (t < best_t) {
-      best_t = t;
-      best = c.tile;
-    }
-  }
-  return best;
+  (void)epi;
+  return ceil_div(M, 128) * ceil_div(N, 256) >= 256 ? 5 : 3;
 }
 
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s) {

@@ -31,8 +31,7 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
     qa = ctx.alloc(m * ldq)
     rs = ctx.alloc(m * 4)
     kind = {"i8": 0, "w8": 1, "f32": 2}[mode]
-    ctx.set_option(_lib.RH_CTX_I8_TILE, tile)
-    ctx.set_option(_lib.RH_CTX_BF_TILE, tile)
+    ctx.set_option(_lib.RH_CTX_I8_TILE if mode == "i8" else _lib.RH_CTX_BF_TILE, tile)
     ctx.set_bf_algo(bf)
     if mode == "i8":
         T.QuantizeRowsU8(ctx, a, m, k, qa, ldq, rs)
