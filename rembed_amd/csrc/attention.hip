@@ -259,11 +259,11 @@ template <int DH>
 static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s) {
   dim3 grid(ceil_div(a.max_len, kAttnQ), a.heads, a.batch);
   if (a.in_bf16)  // bf16 input carries no low half: one-term products
-    hipLaunchKernelGGL((attention_kernel<DH, 1, __bf16>), grid, dim3(256), 0, s, a);
+    timed_launch((attention_kernel<DH, 1, __bf16>), grid, dim3(256), 0, s, a);
   else if (precision == 3)
-    hipLaunchKernelGGL((attention_kernel<DH, 3, float>), grid, dim3(256), 0, s, a);
+    timed_launch((attention_kernel<DH, 3, float>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((attention_kernel<DH, 1, float>), grid, dim3(256), 0, s, a);
+    timed_launch((attention_kernel<DH, 1, float>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

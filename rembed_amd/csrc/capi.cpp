@@ -39,6 +39,13 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line) {
 }  // namespace rh
 
 // ---- profiling ---------------------------------------------------------------
+namespace rh {
+LaunchTiming& launch_timing() {
+  thread_local LaunchTiming t;
+  return t;
+}
+}  // namespace rh
+
 hipError_t rh_context::prof_begin(int kind, double ops, double bytes, int* slot) {
   *slot = -1;
   if (!profiling) return hipSuccess;
@@ -50,10 +57,10 @@ hipError_t rh_context::prof_begin(int kind, double ops, double bytes, int* slot)
   r.kind = kind;
   r.ops = ops;
   r.bytes = bytes;
-  e = hipEventRecord(r.a, stream);
-  if (e != hipSuccess) return e;
   recs.push_back(r);
   *slot = (int)recs.size() - 1;
+  // the next timed launch attaches the pair to its own dispatch packet
+  rh::launch_timing() = rh::LaunchTiming{r.a, r.b};
   return hipSuccess;
 }
 
@@ -77,7 +84,12 @@ hipError_t rh_context::ensure_ws(size_t bytes) {
 
 hipError_t rh_context::prof_end(int slot) {
   if (slot < 0) return hipSuccess;
-  return hipEventRecord(recs[slot].b, stream);
+  rh::LaunchTiming& t = rh::launch_timing();
+  if (t.start == recs[slot].a) {  // nothing was launched (empty problem)
+    t = rh::LaunchTiming{};
+    recs[slot].kind = -1;
+  }
+  return hipSuccess;
 }
 
 void rh_context::prof_clear() {

@@ -406,10 +406,10 @@ template <int BM, int BN, int AT, bool BI8>
 static hipError_t launch_bf(const GemmBfArgs& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
   if (is_glu(a.act))
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, AT, BI8, true>), dim3(tiles), dim3(256),
+    timed_launch((gemm_bf16_kernel<BM, BN, AT, BI8, true>), dim3(tiles), dim3(256),
                        0, s, a, a_vec_ok(a));
   else
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, AT, BI8, false>), dim3(tiles), dim3(256),
+    timed_launch((gemm_bf16_kernel<BM, BN, AT, BI8, false>), dim3(tiles), dim3(256),
                        0, s, a, a_vec_ok(a));
   return hipGetLastError();
 }
@@ -434,10 +434,10 @@ hipError_t launch_gemm_f32(const GemmBfArgs& a, int algo, hipStream_t s) {
   if (algo == F32_NATIVE) {
     const int tiles = ceil_div(a.M, 128) * ceil_div(a.N, 128);
     if (is_glu(a.act))
-      hipLaunchKernelGGL((gemm_f32_native_kernel<128, 128, true>), dim3(tiles), dim3(256),
+      timed_launch((gemm_f32_native_kernel<128, 128, true>), dim3(tiles), dim3(256),
                          0, s, a, a_vec_ok(a));
     else
-      hipLaunchKernelGGL((gemm_f32_native_kernel<128, 128, false>), dim3(tiles), dim3(256),
+      timed_launch((gemm_f32_native_kernel<128, 128, false>), dim3(tiles), dim3(256),
                          0, s, a, a_vec_ok(a));
     return hipGetLastError();
   }

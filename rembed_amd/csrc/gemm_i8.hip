@@ -298,7 +298,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
 template <int BM, int BN, int NS, int EPI>
 static hipError_t launch_tile(const GemmI8Args& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
-  hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, NS, EPI>), dim3(tiles), dim3(256), 0, s, a);
+  timed_launch((gemm_i8_kernel<BM, BN, NS, EPI>), dim3(tiles), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -278,7 +278,7 @@ hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi
   const int vec = (lda_f % 4 == 0) && ((reinterpret_cast<uintptr_t>(a) & 15) == 0);
   const size_t total = (size_t)M * (ldk / 4);
   const size_t blocks = std::min<size_t>((total + 255) / 256, 256 * 16);
-  hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a, lda_f, M, K,
+  timed_launch(split_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a, lda_f, M, K,
                      hi, lo, ldk, vec);
   return hipGetLastError();
 }
@@ -287,10 +287,10 @@ template <int BM, int BN, int NS, int AT, int BT>
 static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
   if (is_glu(a.act))
-    hipLaunchKernelGGL((gemm_planes_kernel<BM, BN, NS, AT, BT, true>), dim3(tiles), dim3(256), 0,
+    timed_launch((gemm_planes_kernel<BM, BN, NS, AT, BT, true>), dim3(tiles), dim3(256), 0,
                        s, a);
   else
-    hipLaunchKernelGGL((gemm_planes_kernel<BM, BN, NS, AT, BT, false>), dim3(tiles), dim3(256),
+    timed_launch((gemm_planes_kernel<BM, BN, NS, AT, BT, false>), dim3(tiles), dim3(256),
                        0, s, a);
   return hipGetLastError();
 }

@@ -5,6 +5,7 @@
 // that the C-ABI layer (capi.cpp) and the model runtime (model.cpp) call.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -14,6 +15,25 @@
 #include "../../include/rembed_hip.h"
 
 namespace rh {
+
+// Per-launch timing without extra stream packets: the profiler parks a
+// start/stop event pair here and the next timed launch on this thread hands
+// them to hipExtLaunchKernel, which stamps them from the kernel's own
+// dispatch. Untimed launches pass null events (a plain launch).
+struct LaunchTiming {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+LaunchTiming& launch_timing();
+
+template <typename F, typename... Args>
+inline void timed_launch(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s,
+                         Args... args) {
+  LaunchTiming& t = launch_timing();
+  const LaunchTiming use = t;
+  t = LaunchTiming{};
+  hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, use.start, use.stop, 0u, args...);
+}
 
 // ---- status ----------------------------------------------------------------
 // A thread-local message backs rh_last_error(); every C entry point returns
