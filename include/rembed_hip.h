@@ -90,6 +90,25 @@ typedef struct {
 int rh_profile_enable(rh_context *ctx, int on); /* also clears the tallies */
 int rh_profile_read(rh_context *ctx, int kind, rh_profile_stat *out);
 
+/* ---- attention (adjacent to the GEMMs; keeps activations on the device) -----
+ * Softmax attention over a packed variable-length batch of fused q|k|v rows,
+ * replacing the per-text, per-head loops of the model forwards: scores =
+ * q·kᵀ·scale, row softmax, ctx = P·v (bert.go:853-902;
+ * flashAttnCausalHead, qwen3.go:319-390; gemma3.go:318-356 with its
+ * sliding window). Text b owns rows cu[b]..cu[b+1]-1 (cu: device int32
+ * [batch+1]); max_len must be >= every text's length. qkv is [M][ldqkv] f32
+ * (in_bf16 = 0) or bf16 (in_bf16 = 1); q head h starts at column
+ * q_off + h*dh, its kv head h / (heads/kv_heads) at k_off / v_off.
+ * causal: key j visible to query i only if j <= i; window > 0: only if
+ * |i - j| < window. precision 1: bf16 MFMA operands; 3: hi/lo bf16 split,
+ * fp32-grade (f32 input only). out is f32 [M][ldout], head h at h*dh.
+ * dh in {32, 64, 128, 256}; ldqkv and the offsets multiples of 8, ldout of 4.
+ * Enqueued on the context's stream. */
+int rh_attention(rh_context *ctx, const void *qkv, int in_bf16, int ldqkv, int q_off,
+                 int k_off, int v_off, const int32_t *cu, int batch, int max_len, int heads,
+                 int kv_heads, int dh, float scale, int causal, int window, int precision,
+                 float *out, int ldout);
+
 /* ---- weights (tensor level) --------------------------------------------------
  * Quantize/pack on the host exactly as the reference does, then upload once
  * to HBM; the handle owns the device copy until rh_weight_destroy.

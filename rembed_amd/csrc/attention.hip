@@ -36,6 +36,69 @@ __device__ __forceinline__ void load8(const __bf16* src, float (&x)[8]) {
   for (int e = 0; e < 8; e++) x[e] = (float)a[e];
 }
 
+// Visible keys of query qi (text-local): [klo, khi]. Keys past the text,
+// after the query (causal, qwen3.go:319-390) or at distance >= window
+// (gemma3.go:339-347) are excluded.
+__device__ __forceinline__ void attn_key_range(const AttnArgs& p, int qi, int len, int& klo,
+                                               int& khi) {
+  khi = len - 1;
+  if (p.causal) khi = min(khi, qi);
+  klo = 0;
+  if (p.window > 0) {
+    khi = min(khi, qi + p.window - 1);
+    klo = qi - p.window + 1;
+  }
+}
+
+// Online-softmax step for one 64-key block held as S^T tiles (lane: query
+// fr, keys key0 + t2*32 + i*8 + fg*4 + j in register t2, i*4 + j). Scores go
+// to log2 units with one multiply (cs = scale·log2 e); `masked` (uniform
+// over the wave) applies the per-key range test. P = 2^(s - mref) against a
+// reference that moves only when a block's max exceeds it by more than 8:
+// P stays <= 256 (no overflow in fp32), and the running output is rescaled
+// (by the returned alpha, when `rescale`) only on those moves. sc becomes P.
+__device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int fg, int klo,
+                                                    int khi, bool masked, float cs,
+                                                    float& mref, float& lrun, bool& rescale) {
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float v = sc[t2][i * 4 + j] * cs;
+        if (masked) {
+          const int key = key0 + t2 * 32 + i * 8 + fg * 4 + j;
+          v = ((key < klo) | (key > khi)) ? -INFINITY : v;
+        }
+        sc[t2][i * 4 + j] = v;
+        mloc = fmaxf(mloc, v);
+      }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  // -inf + 8 = -inf: a lane's first visible key always moves the reference
+  // (alpha = 2^-inf = 0 then); a lane with no visible key keeps -inf.
+  const bool up = mloc > mref + 8.0f;
+  rescale = __any(up);
+  float alpha = 1.0f;
+  if (up) {
+    alpha = __builtin_amdgcn_exp2f(mref - mloc);
+    mref = mloc;
+  }
+  const float m = mref == -INFINITY ? 0.0f : mref;  // all-masked lanes: every p = 0
+  float psum = 0.0f;
+#pragma unroll
+  for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const float pv = __builtin_amdgcn_exp2f(sc[t2][e] - m);
+      sc[t2][e] = pv;
+      psum += pv;
+    }
+  lrun = lrun * alpha + psum;
+  return alpha;
+}
+
 template <int DH, int PREC, typename TIn>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   const TIn* qkv = static_cast<const TIn*>(p.qkv);
@@ -87,7 +150,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
 #pragma unroll
     for (int e = 0; e < 16; e++) o[t][e] = 0.0f;
   float mrun = -INFINITY, lrun = 0.0f;
-  const float l2e = 1.44269504088896341f;
+  const float cs = p.scale * 1.44269504088896341f;  // scores in log2 units
+  int klo, khi;
+  attn_key_range(p, qi, len, klo, khi);
 
   // Key blocks this workgroup's queries can see: causal stops after the
   // last query; a window bounds both ends (|i - j| < window).
@@ -160,43 +225,18 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
         }
       }
     }
-    // Scale, mask keys past the text, running max shared by lanes l, l^32.
-    float mloc = -INFINITY;
+    // Scale, mask, online softmax; the output is rescaled only when some
+    // query's reference max moved.
+    const bool masked = __any(key0 < klo || key0 + kAttnKV - 1 > khi);
+    bool rescale;
+    const float alpha =
+        attn_softmax_block(sc, key0, fg, klo, khi, masked, cs, mrun, lrun, rescale);
+    if (rescale) {
 #pragma unroll
-    for (int t2 = 0; t2 < 2; t2++)
+      for (int t = 0; t < DT; t++)
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const int key = key0 + t2 * 32 + i * 8 + fg * 4 + j;
-          float v = sc[t2][i * 4 + j] * p.scale;
-          if (key >= len || (p.causal && key > qi) ||
-              (p.window > 0 && (key <= qi - p.window || key >= qi + p.window)))
-            v = -INFINITY;
-          sc[t2][i * 4 + j] = v;
-          mloc = fmaxf(mloc, v);
-        }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    // A masked query can see no key of this block yet (mnew = -inf): use a
-    // finite reference so alpha = exp(-inf) = 0 and every p = 0, not NaN.
-    const float mnew = fmaxf(mrun, mloc);
-    const float mref = mnew == -INFINITY ? 0.0f : mnew;
-    const float alpha = exp2f((mrun - mref) * l2e);
-    mrun = mnew;
-    float psum = 0.0f;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const float pv = exp2f((sc[t2][e] - mref) * l2e);
-        sc[t2][e] = pv;
-        psum += pv;
-      }
-    lrun = lrun * alpha + psum;
-#pragma unroll
-    for (int t = 0; t < DT; t++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) o[t][e] *= alpha;
+        for (int e = 0; e < 16; e++) o[t][e] *= alpha;
+    }
 
     // O^T += V^T · P^T over 4 chunks of 16 keys. Chunk kc, lane half g,
     // element e <-> key kc*16 + (e/4)*8 + g*4 + e%4 = register
@@ -255,11 +295,209 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     }
 }
 
+// ---- bf16 operands, pipelined --------------------------------------------------
+// The same algorithm and fragment layouts for bf16 q|k|v rows, with the key
+// blocks double-buffered: while a block is multiplied, the next block's K
+// rows stream into LDS by global_load_lds_dwordx4 and its V rows are loaded
+// into registers, transposed 8x8 there and written as V^T rows.
+//
+// K block: [64 keys][DH] bf16, 16-byte chunk c of row r at slot c ^ kswz(r)
+// (16 consecutive rows of one fragment read land in 16 distinct bank
+// groups). V^T block: [DH][64] bf16, one 128-byte row per d, chunk cc at
+// lds_off(d, cc). Within each 16-key group the keys are stored in the order
+// the P^T registers hold them (see below), so a lane's V^T fragment is one
+// 16-byte read.
+template <int DH>
+__device__ __forceinline__ int attn_kswz(int r) {
+  constexpr int C = DH / 8;                       // chunks per K row
+  constexpr int W = DH * 2 < 256 ? 256 / (DH * 2) : 1;  // rows per 256-B bank window
+  return (r / W) & ((C < 16 ? C : 16) - 1);
+}
+
+template <int DH>
+__global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
+  const __bf16* qkv = static_cast<const __bf16*>(p.qkv);
+  constexpr int KS = DH / 16, DT = DH / 32;
+  constexpr int kRowB = DH * 2;               // bytes of one K row
+  constexpr int kKB = kAttnKV * kRowB;        // K block bytes
+  constexpr int kStage = 2 * kKB;             // K + V^T (same size)
+  constexpr int kKLoads = kKB / (4 * 1024);   // DMA instructions per wave per block
+  static_assert(kKLoads >= 1 && kKB % 4096 == 0, "K block must split into 4 waves x 1 KiB");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage];
+
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int r0 = p.cu[b], len = p.cu[b + 1] - r0;
+  const int q0 = blockIdx.x * kAttnQ;
+  if (q0 >= len) return;
+  const int kvh = h / (p.heads / p.kv_heads);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, fg = lane >> 5;
+  const int qi = q0 + wave * 32 + fr;
+
+  // Q fragments (B operand of S^T), straight from the bf16 rows.
+  v8bf qf[KS];
+  {
+    const __bf16* qrow =
+        qkv + (size_t)(r0 + (qi < len ? qi : len - 1)) * p.ldqkv + p.q_off + h * DH;
+#pragma unroll
+    for (int s = 0; s < KS; s++) qf[s] = *reinterpret_cast<const v8bf*>(qrow + s * 16 + fg * 8);
+  }
+
+  // K DMA: this lane's slot in each of its 1 KiB blocks -> (row, chunk).
+  int k_row[kKLoads], k_chunk[kKLoads];
+#pragma unroll
+  for (int j = 0; j < kKLoads; j++) {
+    const int off = (wave * kKLoads + j) * 1024 + lane * 16;
+    k_row[j] = off / kRowB;
+    k_chunk[j] = ((off % kRowB) >> 4) ^ attn_kswz<DH>(k_row[j]);
+  }
+  const __bf16* kbase = qkv + p.k_off + kvh * DH;
+  const __bf16* vbase = qkv + p.v_off + kvh * DH;
+  auto issue_k = [&](int kb, int buf) {
+    uint8_t* sK = lds + buf * kStage;
+#pragma unroll
+    for (int j = 0; j < kKLoads; j++) {
+      const int kg = kb * kAttnKV + k_row[j];
+      const __bf16* src = kbase + (size_t)(r0 + (kg < len ? kg : len - 1)) * p.ldqkv + k_chunk[j] * 8;
+      lds_dma16(src, sK + (wave * kKLoads + j) * 1024);
+    }
+  };
+  // V: thread t < DH owns key group kgp = t / (DH/8) (16-key chunk kgp/2,
+  // lane half kgp%2) and d block db = t % (DH/8). Its 8 keys, in P^T order:
+  // key(e) = (kgp/2)*16 + (e/4)*8 + (kgp%2)*4 + e%4.
+  const bool vthr = tid < DH;
+  const int kgp = tid / (DH / 8), db = tid % (DH / 8);
+  v4i vx[8];
+  auto load_v = [&](int kb) {
+    if (!vthr) return;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const int key = kb * kAttnKV + (kgp >> 1) * 16 + (e >> 2) * 8 + (kgp & 1) * 4 + (e & 3);
+      vx[e] = *reinterpret_cast<const v4i*>(
+          vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 8);
+    }
+  };
+  auto write_vt = [&](int buf) {
+    if (!vthr) return;
+    uint8_t* sV = lds + buf * kStage + kKB;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {  // d = db*8 + 2j (low halves) and 2j + 1 (high halves)
+      v4i lo, hi;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t a = (uint32_t)vx[2 * i][j], c = (uint32_t)vx[2 * i + 1][j];
+        lo[i] = (int)((a & 0xffffu) | (c << 16));
+        hi[i] = (int)((a >> 16) | (c & 0xffff0000u));
+      }
+      const int d = db * 8 + 2 * j;
+      *reinterpret_cast<v4i*>(sV + lds_off(d, kgp)) = lo;
+      *reinterpret_cast<v4i*>(sV + lds_off(d + 1, kgp)) = hi;
+    }
+  };
+
+  v16f o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; t++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[t][e] = 0.0f;
+  float mrun = -INFINITY, lrun = 0.0f;
+  const float cs = p.scale * 1.44269504088896341f;  // scores in log2 units
+  int klo, khi;
+  attn_key_range(p, qi, len, klo, khi);
+
+  int kb_lo = 0, kb_hi = (len + kAttnKV - 1) / kAttnKV;
+  const int qlast = min(q0 + kAttnQ, len) - 1;
+  if (p.causal) kb_hi = min(kb_hi, qlast / kAttnKV + 1);
+  if (p.window > 0) {
+    kb_lo = max(0, q0 - p.window + 1) / kAttnKV;
+    kb_hi = min(kb_hi, (qlast + p.window - 1) / kAttnKV + 1);
+  }
+
+  issue_k(kb_lo, 0);
+  load_v(kb_lo);
+  write_vt(0);
+  __syncthreads();  // waits for the DMA (vmcnt) and orders the V^T writes
+
+  for (int kb = kb_lo; kb < kb_hi; kb++) {
+    const int buf = (kb - kb_lo) & 1;
+    const bool next = kb + 1 < kb_hi;
+    if (next) {
+      issue_k(kb + 1, buf ^ 1);
+      load_v(kb + 1);
+    }
+    const uint8_t* sK = lds + buf * kStage;
+    const uint8_t* sV = sK + kKB;
+    const int key0 = kb * kAttnKV;
+
+    // S^T for the two 32-key tiles, the two accumulation chains interleaved.
+    v16f sc[2];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) sc[t2][e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; t2++) {
+        const int kr = t2 * 32 + fr;
+        const v8bf kf = *reinterpret_cast<const v8bf*>(
+            sK + kr * kRowB + (((2 * s + fg) ^ attn_kswz<DH>(kr)) << 4));
+        sc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sc[t2], 0, 0, 0);
+      }
+
+    // Scale, mask (only blocks that cross some query's visible range), online
+    // softmax; the output is rescaled only when some query's reference max
+    // moved.
+    const bool masked = __any(key0 < klo || key0 + kAttnKV - 1 > khi);
+    bool rescale;
+    const float alpha =
+        attn_softmax_block(sc, key0, fg, klo, khi, masked, cs, mrun, lrun, rescale);
+    if (rescale) {
+#pragma unroll
+      for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[t][e] *= alpha;
+    }
+
+    // O^T += V^T · P^T over 4 chunks of 16 keys; lane half g, element e of
+    // chunk kc is register sc[kc/2][(kc%2)*8 + e], V^T chunk 2kc + g.
+#pragma unroll
+    for (int kc = 0; kc < 4; kc++) {
+      v8bf ph;
+#pragma unroll
+      for (int e = 0; e < 8; e++) ph[e] = (__bf16)sc[kc >> 1][(kc & 1) * 8 + e];
+#pragma unroll
+      for (int t = 0; t < DT; t++) {
+        const v8bf vf = *reinterpret_cast<const v8bf*>(sV + lds_off(t * 32 + fr, 2 * kc + fg));
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[t], 0, 0, 0);
+      }
+    }
+
+    if (next) write_vt(buf ^ 1);
+    __syncthreads();  // next block landed (vmcnt) and this block's reads are done
+  }
+
+  const float ltot = lrun + __shfl_xor(lrun, 32, 64);
+  if (qi >= len) return;
+  const float inv = 1.0f / ltot;
+  float* orow = p.ctx + (size_t)(r0 + qi) * p.ldctx + h * DH;
+#pragma unroll
+  for (int t = 0; t < DT; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v4f w;
+#pragma unroll
+      for (int j = 0; j < 4; j++) w[j] = o[t][i * 4 + j] * inv;
+      *reinterpret_cast<v4f*>(orow + t * 32 + i * 8 + fg * 4) = w;
+    }
+}
+
 template <int DH>
 static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s) {
   dim3 grid(ceil_div(a.max_len, kAttnQ), a.heads, a.batch);
   if (a.in_bf16)  // bf16 input carries no low half: one-term products
-    timed_launch((attention_kernel<DH, 1, __bf16>), grid, dim3(256), 0, s, a);
+    timed_launch((attention_bf16_kernel<DH>), grid, dim3(256), 0, s, a);
   else if (precision == 3)
     timed_launch((attention_kernel<DH, 3, float>), grid, dim3(256), 0, s, a);
   else

@@ -606,6 +606,47 @@ int rh_profile_read(rh_context* ctx, int kind, rh_profile_stat* out) {
   return RH_OK;
 }
 
+int rh_attention(rh_context* ctx, const void* qkv, int in_bf16, int ldqkv, int q_off,
+                 int k_off, int v_off, const int32_t* cu, int batch, int max_len, int heads,
+                 int kv_heads, int dh, float scale, int causal, int window, int precision,
+                 float* out, int ldout) {
+  if (!qkv || !cu || !out) return fail(RH_ERR_INVALID, "null argument");
+  if (dh != 32 && dh != 64 && dh != 128 && dh != 256)
+    return fail(RH_ERR_SHAPE, "attention head dim must be 32, 64, 128 or 256");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads)
+    return fail(RH_ERR_SHAPE, "heads must be a positive multiple of kv_heads");
+  if (precision != 1 && precision != 3) return fail(RH_ERR_INVALID, "precision must be 1 or 3");
+  if (in_bf16 && precision != 1) return fail(RH_ERR_INVALID, "bf16 input takes precision 1");
+  if (batch < 0 || max_len < 0 || window < 0) return fail(RH_ERR_INVALID, "negative size");
+  if (ldqkv % 8 || q_off % 8 || k_off % 8 || v_off % 8 || ldout % 4 || q_off < 0 ||
+      k_off < 0 || v_off < 0 || ((uintptr_t)qkv & 15) || ((uintptr_t)out & 15))
+    return fail(RH_ERR_SHAPE, "attention rows and offsets must be 16-byte aligned");
+  CTX_GUARD(ctx);
+  AttnArgs a{};
+  a.qkv = qkv;
+  a.in_bf16 = in_bf16 ? 1 : 0;
+  a.ldqkv = ldqkv;
+  a.q_off = q_off;
+  a.k_off = k_off;
+  a.v_off = v_off;
+  a.cu = cu;
+  a.batch = batch;
+  a.max_len = max_len;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.dh = dh;
+  a.scale = scale;
+  a.ctx = out;
+  a.ldctx = ldout;
+  a.causal = causal ? 1 : 0;
+  a.window = window;
+  int slot = -1;
+  RH_HIP(ctx->prof_begin(3, 0.0, 0.0, &slot));
+  RH_HIP(launch_attention(a, precision, ctx->stream));
+  RH_HIP(ctx->prof_end(slot));
+  return RH_OK;
+}
+
 int rh_pack_weight_gated(rh_context* ctx, int mode, const float* gate,
                                     const float* up, int k, int i, rh_weight** out) {
   if (!out || !gate || !up) return fail(RH_ERR_INVALID, "null argument");

@@ -196,18 +196,25 @@ hipError_t launch_rms_residual(float* x, const float* y, const float* post_g,
 // One wave per (row, head) over the q heads then the k heads of a fused
 // q|k|v row: RMSNorm of the head's dh values with its norm weight, then
 // rotate-half RoPE at the row's position (applyRoPE, modernbert.go:130-143:
-// each product rounded to float32 before the add).
+// each product rounded to float32 before the add). With `outh` the results
+// go to bf16 rows of the same layout instead (round to nearest even), and
+// the v heads are converted too: the operands of a bf16 attention.
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     float* __restrict__ qkv, int ldqkv, int m, int nq, int nkv, int dh,
     const float* __restrict__ q_g, const float* __restrict__ k_g, float eps,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    const int32_t* __restrict__ pos) {
+    const int32_t* __restrict__ pos, __bf16* __restrict__ outh) {
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * kRows + (threadIdx.x >> 6);
-  const int nh = nq + nkv;
+  const int nh = nq + nkv + (outh ? nkv : 0);
   if (item >= m * nh) return;
   const int row = item / nh, h = item % nh;
-  float* v = qkv + (size_t)row * ldqkv + h * dh;  // q heads, then k heads
+  float* v = qkv + (size_t)row * ldqkv + h * dh;  // q heads, k heads, [v heads]
+  if (h >= nq + nkv) {  // v head: conversion only
+    __bf16* o = outh + (size_t)row * ldqkv + h * dh;
+    for (int d = lane; d < dh; d += 64) o[d] = (__bf16)v[d];
+    return;
+  }
   const float* g = h < nq ? q_g : k_g;
   const int half = dh >> 1;
   // lane holds pairs (d, d + half) for d = lane, lane + 64 (dh <= 256)
@@ -232,8 +239,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       const float b = x2[e] * inv * g[d + half];
       const float cc = c[d], ssn = sn[d];
       const float t0 = a * cc, t1 = b * ssn, t2 = b * cc, t3 = a * ssn;
-      v[d] = t0 - t1;
-      v[d + half] = t2 + t3;
+      if (outh) {
+        __bf16* o = outh + (size_t)row * ldqkv + h * dh;
+        o[d] = (__bf16)(t0 - t1);
+        o[d + half] = (__bf16)(t2 + t3);
+      } else {
+        v[d] = t0 - t1;
+        v[d + half] = t2 + t3;
+      }
     }
   }
 }
@@ -241,12 +254,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, int dh,
                                const float* q_g, const float* k_g, float eps,
                                const float* cos_t, const float* sin_t,
-                               const int32_t* pos, hipStream_t s) {
+                               const int32_t* pos, __bf16* outh, hipStream_t s) {
   if (m <= 0) return hipSuccess;
   if (dh % 2 || dh > 256) return hipErrorInvalidValue;
-  const int items = m * (nq + nkv);
+  const int items = m * (nq + nkv + (outh ? nkv : 0));
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(ceil_div(items, kRows)), dim3(256), 0, s, qkv,
-                     ldqkv, m, nq, nkv, dh, q_g, k_g, eps, cos_t, sin_t, pos);
+                     ldqkv, m, nq, nkv, dh, q_g, k_g, eps, cos_t, sin_t, pos, outh);
   return hipGetLastError();
 }
 

@@ -180,7 +180,7 @@ struct rh_model {
       const size_t r = newcap;
       RH_HIP(dalloc(&x, r * H));
       RH_HIP(dalloc(&qkv, r * qkv_width()));
-      if (!decoder()) RH_HIP(dalloc(&qkvh, r * qkv_width()));
+      RH_HIP(dalloc(&qkvh, r * qkv_width()));
       RH_HIP(dalloc(&ctxb, r * ctx_width()));
       RH_HIP(dalloc(&y, r * H));
       RH_HIP(dalloc(&hid, r * I));
@@ -439,11 +439,14 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
                     false);
     if (st) return st;
     const bool local = gemma() && !L.global;
+    // bf16 attention reads bf16 q|k|v rows, written by the QK-norm pass
+    const bool hb = attn_precision == 1;
     RH_HIP(launch_qk_norm_rope(qkv, qkvw, M, nq(), nkv(), dh(), L.q_norm, L.k_norm, e,
-                               local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d, s));
+                               local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d,
+                               hb ? qkvh : nullptr, s));
     AttnArgs aa{};
-    aa.qkv = qkv;
-    aa.in_bf16 = 0;
+    aa.qkv = hb ? (const void*)qkvh : (const void*)qkv;
+    aa.in_bf16 = hb ? 1 : 0;
     aa.ldqkv = qkvw;
     aa.q_off = 0;
     aa.k_off = qd;

@@ -255,7 +255,7 @@ hipError_t launch_rms_residual(float* x, const float* y, const float* post_g,
 hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, int dh,
                                const float* q_g, const float* k_g, float eps,
                                const float* cos_t, const float* sin_t,
-                               const int32_t* pos, hipStream_t s);
+                               const int32_t* pos, __bf16* outh, hipStream_t s);
 // EmbeddingGemma Dense head (gemma3.go:174-198) on pooled [batch][H] rows:
 // out = W2 . (W1 . pooled), float32 sequential sums; optional L2.
 hipError_t launch_dense_head(const float* pooled, int batch, int H, int D,

@@ -206,6 +206,15 @@ def GemmU8S8I32(ctx, acc, qa, ldq, pb, m):
     check(lib.rh_gemm_u8s8_i32(ctx.h, acc.ptr, qa.ptr, ldq, pb.h, m))
 
 
+def Attention(ctx, out, ldout, qkv, in_bf16, ldqkv, q_off, k_off, v_off, cu, batch, max_len,
+              heads, kv_heads, dh, scale, causal=False, window=0, precision=1):
+    """Softmax attention over a packed varlen batch (rh_attention): the
+    per-text head loops of bert.go:853-902, qwen3.go:319-390, gemma3.go:318-356."""
+    check(lib.rh_attention(ctx.h, qkv.ptr, int(in_bf16), ldqkv, q_off, k_off, v_off, cu.ptr,
+                           batch, max_len, heads, kv_heads, dh, float(scale), int(causal),
+                           window, precision, out.ptr, ldout))
+
+
 def Linear(ctx, dst, a, pb, m, act=_lib.RH_ACT_NONE, qa=None, ldq=0, row_scales=None):
     """applyDense with fused bias/activation (bert.go:282-301)."""
     check(lib.rh_linear(ctx.h, dst.ptr, a.ptr, pb.h, m, act,
