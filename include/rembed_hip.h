@@ -256,9 +256,14 @@ void rh_model_destroy(rh_model *m);
  * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE).
  * RH_OPT_FUSED_FFN1: 1 = full-int8 FFN1 writes u8 rows directly (two GEMM
  * passes, no fp32 intermediate), 0 = fp32 GELU rows then QuantizeRowU8
- * (default); both give identical bytes. */
+ * (default); both give identical bytes. RH_OPT_PRODUCER_PLANES: 1 = the
+ * kernels that produce a weight-only int8 / fp32 GEMM's input (norms,
+ * attention, the previous GEMM) write its bf16 hi/lo planes directly
+ * (default), 0 = they write fp32 rows and each GEMM splits them; both give
+ * identical values. */
 #define RH_OPT_ATTN_PRECISION 1
 #define RH_OPT_FUSED_FFN1 2
+#define RH_OPT_PRODUCER_PLANES 3
 int rh_model_set_option(rh_model *m, int option, int value);
 /* Model.Quantized / QuantizedActivations (bert.go:526-644). */
 int rh_model_quantized(const rh_model *m);

@@ -283,7 +283,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   const float ltot = lrun + __shfl_xor(lrun, 32, 64);
   if (qi >= len) return;
   const float inv = 1.0f / ltot;
-  float* orow = p.ctx + (size_t)(r0 + qi) * p.ldctx + h * DH;
+  const size_t orow = (size_t)(r0 + qi) * p.ldctx + h * DH;
 #pragma unroll
   for (int t = 0; t < DT; t++)
 #pragma unroll
@@ -291,7 +291,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
       v4f w;
 #pragma unroll
       for (int j = 0; j < 4; j++) w[j] = o[t][i * 4 + j] * inv;
-      *reinterpret_cast<v4f*>(orow + t * 32 + i * 8 + fg * 4) = w;
+      const size_t off = orow + t * 32 + i * 8 + fg * 4;
+      if (p.ctx_hi) store_planes4(p.ctx_hi, p.ctx_lo, off, w);
+      else *reinterpret_cast<v4f*>(p.ctx + off) = w;
     }
 }
 
@@ -481,7 +483,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   const float ltot = lrun + __shfl_xor(lrun, 32, 64);
   if (qi >= len) return;
   const float inv = 1.0f / ltot;
-  float* orow = p.ctx + (size_t)(r0 + qi) * p.ldctx + h * DH;
+  const size_t orow = (size_t)(r0 + qi) * p.ldctx + h * DH;
 #pragma unroll
   for (int t = 0; t < DT; t++)
 #pragma unroll
@@ -489,7 +491,9 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
       v4f w;
 #pragma unroll
       for (int j = 0; j < 4; j++) w[j] = o[t][i * 4 + j] * inv;
-      *reinterpret_cast<v4f*>(orow + t * 32 + i * 8 + fg * 4) = w;
+      const size_t off = orow + t * 32 + i * 8 + fg * 4;
+      if (p.ctx_hi) store_planes4(p.ctx_hi, p.ctx_lo, off, w);
+      else *reinterpret_cast<v4f*>(p.ctx + off) = w;
     }
 }
 

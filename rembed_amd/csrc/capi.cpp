@@ -364,30 +364,54 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
 // Weight-only int8 / fp32 linear on bf16 planes: split the activations once
 // into the context workspace, then the planes GEMM. Rows go in chunks that
 // keep the kernel's 32-bit element offsets in range.
+bool linear_on_planes(const Context* ctx, const rh_weight* w) {
+  return w->mode != RH_MODE_A8W8 && ctx->bf_algo == 0 &&
+         !(w->mode == RH_MODE_F32 && ctx->f32_algo == F32_NATIVE);
+}
+
+int linear_a_terms(const Context* ctx, const rh_weight* w) {
+  return w->mode == RH_MODE_W8 ? ctx->w8_terms : 2;
+}
+
+// Weight-only int8 / fp32 linear on bf16 planes. The activations come as
+// producer-written planes (pin) or are split once here into the context
+// workspace; the output goes to fp32 dst or to planes (pout). Rows go in
+// chunks that keep the kernel's 32-bit element offsets in range.
 static int run_linear_planes(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
-                             float* dst, int ldc, int act, const float* bias) {
+                             float* dst, int ldc, int act, const float* bias,
+                             const Planes* pin, const Planes* pout) {
   hipStream_t s = ctx->stream;
-  const int a_terms = w->mode == RH_MODE_W8 ? ctx->w8_terms : 2;
+  const int a_terms = linear_a_terms(ctx, w);
   const int b_terms = w->mode == RH_MODE_W8 ? 1 : 2;
-  const int ldk = (int)round_up(w->k, 64);
-  const int chunk = std::min(m, (int)((1u << 30) / (unsigned)ldk));
+  const int ldk = pin ? pin->ld : (int)round_up(w->k, 64);
+  const int ldo = pout ? pout->ld : ldc;
+  const long long big = std::max((long long)ldk, (long long)ldo);
+  const int chunk = std::min(m, (int)((1u << 30) / (unsigned long long)big));
   const size_t plane = (size_t)chunk * ldk * 2;
-  hipError_t e = ctx->ensure_ws(plane * a_terms);
-  if (e != hipSuccess) return hip_fail(e, "gemm workspace", __FILE__, __LINE__);
-  __bf16* hi = static_cast<__bf16*>(ctx->ws);
-  __bf16* lo = a_terms == 2 ? reinterpret_cast<__bf16*>(static_cast<uint8_t*>(ctx->ws) + plane)
-                            : nullptr;
+  __bf16* hi = nullptr;
+  __bf16* lo = nullptr;
+  if (!pin) {
+    hipError_t e = ctx->ensure_ws(plane * a_terms);
+    if (e != hipSuccess) return hip_fail(e, "gemm workspace", __FILE__, __LINE__);
+    hi = static_cast<__bf16*>(ctx->ws);
+    lo = a_terms == 2 ? reinterpret_cast<__bf16*>(static_cast<uint8_t*>(ctx->ws) + plane)
+                      : nullptr;
+  }
+  hipError_t e = hipSuccess;
   for (int r0 = 0; r0 < m; r0 += chunk) {
     const int mc = std::min(chunk, m - r0);
     const double M = mc, K = w->k, N = w->n;
     int slot = -1;
-    e = ctx->prof_begin(4, 0.0, M * K * 4 + M * ldk * 2.0 * a_terms, &slot);
-    if (e == hipSuccess) e = launch_split_bf16(a + (size_t)r0 * lda, lda, mc, w->k, hi, lo, ldk, s);
-    if (e == hipSuccess) e = ctx->prof_end(slot);
-    if (e != hipSuccess) return hip_fail(e, "split_bf16", __FILE__, __LINE__);
+    if (!pin) {
+      e = ctx->prof_begin(4, 0.0, M * K * 4 + M * ldk * 2.0 * a_terms, &slot);
+      if (e == hipSuccess)
+        e = launch_split_bf16(a + (size_t)r0 * lda, lda, mc, w->k, hi, lo, ldk, s);
+      if (e == hipSuccess) e = ctx->prof_end(slot);
+      if (e != hipSuccess) return hip_fail(e, "split_bf16", __FILE__, __LINE__);
+    }
     GemmPlArgs g{};
-    g.Ah = hi;
-    g.Al = lo;
+    g.Ah = pin ? pin->hi + (size_t)r0 * ldk : hi;
+    g.Al = pin ? (a_terms == 2 ? pin->lo + (size_t)r0 * ldk : nullptr) : lo;
     g.lda = ldk;
     g.Bh = static_cast<const __bf16*>(w->d_bf);
     g.Bl = static_cast<const __bf16*>(w->d_bf_lo);
@@ -397,13 +421,21 @@ static int run_linear_planes(Context* ctx, const rh_weight* w, const float* a, i
     g.K = w->k;
     g.col_scales = w->mode == RH_MODE_W8 ? w->d_scales : nullptr;
     g.bias = bias;
-    g.C = dst + (size_t)r0 * ldc;
-    g.ldc = ldc;
+    if (pout) {
+      g.Ch = pout->hi + (size_t)r0 * ldo;
+      g.Cl = pout->lo ? pout->lo + (size_t)r0 * ldo : nullptr;
+    } else {
+      g.C = dst + (size_t)r0 * ldc;
+    }
+    g.ldc = ldo;
     g.act = act;
-    // algorithmic bytes: the fp32 activations, the weights as stored for
-    // the mode (int8 / fp32), the fp32 output
+    // algorithmic bytes: the activations (fp32, or the planes a producer
+    // wrote), the weights as stored for the mode (int8 / fp32), the output
+    // (fp32 or planes)
     const double wbytes = w->mode == RH_MODE_W8 ? K * N + 4 * N : 4 * K * N;
-    const double bytes = M * K * 4 + wbytes + M * (w->glu ? N / 2 : N) * 4 + (bias ? 4 * N : 0);
+    const double abytes = pin ? M * K * 2.0 * a_terms : M * K * 4;
+    const double obytes = pout ? (pout->lo ? 4.0 : 2.0) : 4.0;
+    const double bytes = abytes + wbytes + M * (w->glu ? N / 2 : N) * obytes + (bias ? 4 * N : 0);
     e = ctx->prof_begin(w->mode == RH_MODE_W8 ? 1 : 2, 2.0 * M * K * N, bytes, &slot);
     if (e == hipSuccess) e = launch_gemm_planes(g, a_terms, b_terms, ctx->bf_tile, s);
     if (e == hipSuccess) e = ctx->prof_end(slot);
@@ -418,7 +450,8 @@ static int run_linear_planes(Context* ctx, const rh_weight* w, const float* a, i
 // in which case `a` is quantized here first.
 int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
                float* dst, int ldc, int act, const float* bias, uint8_t* qa,
-               int ldq, float* rs, bool quantize_first) {
+               int ldq, float* rs, bool quantize_first, const Planes* pin,
+               const Planes* pout) {
   if (m <= 0) return RH_OK;
   hipStream_t s = ctx->stream;
   const double M = m, K = w->k, N = w->n;
@@ -431,9 +464,9 @@ int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
     return run_gemm_i8(ctx, w, qa, ldq, rs, m, EPI_F32, dst, ldc, act, bias, nullptr,
                        nullptr, ops);
   }
-  // the planes path serves every mode but the native-f32 MFMA choice
-  if (ctx->bf_algo == 0 && !(w->mode == RH_MODE_F32 && ctx->f32_algo == F32_NATIVE))
-    return run_linear_planes(ctx, w, a, lda, m, dst, ldc, act, bias);
+  if (linear_on_planes(ctx, w))
+    return run_linear_planes(ctx, w, a, lda, m, dst, ldc, act, bias, pin, pout);
+  if (pin || pout) return fail(RH_ERR_INVALID, "planes given to a linear that does not use them");
   int slot = -1;
   hipError_t e = hipSuccess;
   GemmBfArgs g{};

@@ -77,9 +77,24 @@ int quantize_b8(const float* bT, int k, int n, std::vector<int8_t>& q,
                 std::vector<float>& scales);
 int quantize_b8_vnni(const float* bT, int k, int n, std::vector<int8_t>& q,
                      std::vector<float>& scales, std::vector<int32_t>& colsum);
+// bf16 planes of GEMM activations exchanged between producers and the
+// planes GEMM: hi/lo [m][ld] (ld a multiple of 64 covering K, zero past K);
+// lo may be null where the consumer takes one term.
+struct Planes {
+  __bf16* hi = nullptr;
+  __bf16* lo = nullptr;
+  int ld = 0;
+};
+// Does the linear of w run on bf16 planes in this context (weight-only int8
+// or fp32, planes algorithm, not native-f32)? Then it can take its input as
+// producer-written planes (`pin`) and write its output as planes (`pout`).
+bool linear_on_planes(const Context* ctx, const rh_weight* w);
+// Number of activation planes (1 or 2) the planes GEMM of w reads.
+int linear_a_terms(const Context* ctx, const rh_weight* w);
 int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
                float* dst, int ldc, int act, const float* bias, uint8_t* qa, int ldq,
-               float* rs, bool quantize_first);
+               float* rs, bool quantize_first, const Planes* pin = nullptr,
+               const Planes* pout = nullptr);
 int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                 const float* rs, int m, int epi, void* out, int ldo, int act,
                 const float* bias, float* row_absmax, float* rs_out, double ops);

@@ -203,7 +203,8 @@ __global__ __launch_bounds__(256) void gemm_planes_kernel(GemmPlArgs p) {
             }
             o[e] = glu_act(g, u, p.act);
           }
-          *reinterpret_cast<v4f*>(p.C + (size_t)grow * p.ldc + gpk / 2) = o;
+          if (p.Ch) store_planes4(p.Ch, p.Cl, (size_t)grow * p.ldc + gpk / 2, o);
+          else *reinterpret_cast<v4f*>(p.C + (size_t)grow * p.ldc + gpk / 2) = o;
         }
       }
     } else {
@@ -230,7 +231,8 @@ __global__ __launch_bounds__(256) void gemm_planes_kernel(GemmPlArgs p) {
             if (p.bias) x = x + bs[e];
             v[e] = apply_act(x, p.act);
           }
-          *reinterpret_cast<v4f*>(p.C + (size_t)grow * p.ldc + gcol) = v;
+          if (p.Ch) store_planes4(p.Ch, p.Cl, (size_t)grow * p.ldc + gcol, v);
+          else *reinterpret_cast<v4f*>(p.C + (size_t)grow * p.ldc + gcol) = v;
         }
       }
     }
@@ -263,8 +265,10 @@ __global__ __launch_bounds__(256) void split_bf16_kernel(const float* __restrict
     v4bf h, l;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      h[e] = (__bf16)x[e];
-      l[e] = (__bf16)(x[e] - (float)h[e]);
+      __bf16 a, b;
+      split_hi_lo(x[e], a, b);
+      h[e] = a;
+      l[e] = b;
     }
     *reinterpret_cast<v4bf*>(hi + (size_t)row * ldk + c) = h;
     if (lo) *reinterpret_cast<v4bf*>(lo + (size_t)row * ldk + c) = l;

@@ -83,24 +83,24 @@ hipError_t launch_embed_gather(const int32_t* ids, int stride, const int32_t* cu
 //   y' = post_g ? RMSNorm(y, post_g) : y   (Gemma post-norms, gemma3.go:357,376)
 //   x += y'                                 (Add, tensor.go:383-387)
 //   out = RMSNorm(x, pre_g)                 (the next sublayer's pre-norm)
-// plus an optional QuantizeRowU8 of out for a full-int8 GEMM. V float4 per lane.
+// out goes to fp32 rows and/or to the bf16 hi/lo planes of the next GEMM's
+// input, plus an optional QuantizeRowU8 of it for a full-int8 GEMM. V float4
+// per lane.
 template <int V>
-__global__ __launch_bounds__(256) void rms_residual_kernel(
-    float* x, const float* __restrict__ y, const float* __restrict__ post_g,
-    const float* __restrict__ pre_g, float* out, int m, int H, float eps,
-    uint8_t* __restrict__ qa, int ldq, float* __restrict__ row_scales) {
+__global__ __launch_bounds__(256) void rms_residual_kernel(RmsArgs p) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRows + (threadIdx.x >> 6);
-  if (row >= m) return;
-  float* xr = x + (size_t)row * H;
+  if (row >= p.m) return;
+  const int H = p.H;
+  float* xr = p.x + (size_t)row * H;
   v4f v[V];
 #pragma unroll
   for (int e = 0; e < V; e++) {
     const int j = (lane + 64 * e) * 4;
     v[e] = j < H ? *reinterpret_cast<const v4f*>(xr + j) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  if (y) {
-    const float* yr = y + (size_t)row * H;
+  if (p.y) {
+    const float* yr = p.y + (size_t)row * H;
     v4f w[V];
     float ss = 0.0f;
 #pragma unroll
@@ -109,13 +109,13 @@ __global__ __launch_bounds__(256) void rms_residual_kernel(
       w[e] = j < H ? *reinterpret_cast<const v4f*>(yr + j) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
       ss += (w[e][0] * w[e][0] + w[e][1] * w[e][1]) + (w[e][2] * w[e][2] + w[e][3] * w[e][3]);
     }
-    if (post_g) {
-      const float inv = rms_inv(wsum(ss), H, eps);
+    if (p.post_g) {
+      const float inv = rms_inv(wsum(ss), H, p.eps);
 #pragma unroll
       for (int e = 0; e < V; e++) {
         const int j = (lane + 64 * e) * 4;
         if (j < H) {
-          const v4f g = *reinterpret_cast<const v4f*>(post_g + j);
+          const v4f g = *reinterpret_cast<const v4f*>(p.post_g + j);
 #pragma unroll
           for (int c = 0; c < 4; c++) w[e][c] = w[e][c] * inv * g[c];
         }
@@ -134,28 +134,28 @@ __global__ __launch_bounds__(256) void rms_residual_kernel(
 #pragma unroll
   for (int e = 0; e < V; e++)
     ss += (v[e][0] * v[e][0] + v[e][1] * v[e][1]) + (v[e][2] * v[e][2] + v[e][3] * v[e][3]);
-  const float inv = rms_inv(wsum(ss), H, eps);
-  float* orow = out + (size_t)row * H;
+  const float inv = rms_inv(wsum(ss), H, p.eps);
   float mx = 0.0f;
 #pragma unroll
   for (int e = 0; e < V; e++) {
     const int j = (lane + 64 * e) * 4;
     if (j < H) {
-      const v4f g = *reinterpret_cast<const v4f*>(pre_g + j);
+      const v4f g = *reinterpret_cast<const v4f*>(p.pre_g + j);
       v4f o;
 #pragma unroll
       for (int c = 0; c < 4; c++) o[c] = v[e][c] * inv * g[c];
       v[e] = o;
-      *reinterpret_cast<v4f*>(orow + j) = o;
+      if (p.out) *reinterpret_cast<v4f*>(p.out + (size_t)row * H + j) = o;
+      if (p.ph) store_planes4(p.ph, p.pl, (size_t)row * p.ldp + j, o);
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
     }
   }
-  if (qa) {  // QuantizeRowU8 (pack_vnni.go:85-117) of the normalized row
+  if (p.qa) {  // QuantizeRowU8 (pack_vnni.go:85-117) of the normalized row
     mx = wmax(mx);
     float scale = mx / 127.0f;
     if (scale == 0.0f) scale = 1.0f;
     const float qinv = 1.0f / scale;
-    uint8_t* q = qa + (size_t)row * ldq;
+    uint8_t* q = p.qa + (size_t)row * p.ldq;
 #pragma unroll
     for (int e = 0; e < V; e++) {
       const int j = (lane + 64 * e) * 4;
@@ -164,88 +164,101 @@ __global__ __launch_bounds__(256) void rms_residual_kernel(
             (uint32_t)qbyte(v[e][0], qinv) | ((uint32_t)qbyte(v[e][1], qinv) << 8) |
             ((uint32_t)qbyte(v[e][2], qinv) << 16) | ((uint32_t)qbyte(v[e][3], qinv) << 24);
     }
-    for (int j = H + lane * 4; j < ldq; j += 256) *reinterpret_cast<uint32_t*>(q + j) = 0u;
-    if (lane == 0) row_scales[row] = scale;
+    for (int j = H + lane * 4; j < p.ldq; j += 256) *reinterpret_cast<uint32_t*>(q + j) = 0u;
+    if (lane == 0) p.row_scales[row] = scale;
   }
 }
 
-template <int V>
-static void launch_rmsv(float* x, const float* y, const float* post_g, const float* pre_g,
-                        float* out, int m, int H, float eps, uint8_t* qa, int ldq, float* rs,
-                        hipStream_t s) {
-  hipLaunchKernelGGL((rms_residual_kernel<V>), dim3(ceil_div(m, kRows)), dim3(256), 0, s, x,
-                     y, post_g, pre_g, out, m, H, eps, qa, ldq, rs);
-}
-
-hipError_t launch_rms_residual(float* x, const float* y, const float* post_g,
-                               const float* pre_g, float* out, int m, int H, float eps,
-                               uint8_t* qa, int ldq, float* row_scales, hipStream_t s) {
-  if (m <= 0) return hipSuccess;
-  if (H % 4 || H > 4096 || (qa && ldq % 4)) return hipErrorInvalidValue;
-  const int v = ceil_div(H, 256);
-  if (v <= 1) launch_rmsv<1>(x, y, post_g, pre_g, out, m, H, eps, qa, ldq, row_scales, s);
-  else if (v <= 2) launch_rmsv<2>(x, y, post_g, pre_g, out, m, H, eps, qa, ldq, row_scales, s);
-  else if (v <= 3) launch_rmsv<3>(x, y, post_g, pre_g, out, m, H, eps, qa, ldq, row_scales, s);
-  else if (v <= 4) launch_rmsv<4>(x, y, post_g, pre_g, out, m, H, eps, qa, ldq, row_scales, s);
-  else if (v <= 8) launch_rmsv<8>(x, y, post_g, pre_g, out, m, H, eps, qa, ldq, row_scales, s);
-  else launch_rmsv<16>(x, y, post_g, pre_g, out, m, H, eps, qa, ldq, row_scales, s);
+hipError_t launch_rms_residual(const RmsArgs& a, hipStream_t s) {
+  if (a.m <= 0) return hipSuccess;
+  if (a.H % 4 || a.H > 4096 || (a.qa && a.ldq % 4) || (a.ph && (a.ldp % 64 || a.ldp < a.H)))
+    return hipErrorInvalidValue;
+  const dim3 grid(ceil_div(a.m, kRows)), block(256);
+  const int v = ceil_div(a.H, 256);
+  if (v <= 1) hipLaunchKernelGGL((rms_residual_kernel<1>), grid, block, 0, s, a);
+  else if (v <= 2) hipLaunchKernelGGL((rms_residual_kernel<2>), grid, block, 0, s, a);
+  else if (v <= 3) hipLaunchKernelGGL((rms_residual_kernel<3>), grid, block, 0, s, a);
+  else if (v <= 4) hipLaunchKernelGGL((rms_residual_kernel<4>), grid, block, 0, s, a);
+  else if (v <= 8) hipLaunchKernelGGL((rms_residual_kernel<8>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((rms_residual_kernel<16>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 
 // ---- QK-norm + RoPE -----------------------------------------------------------------
-// One wave per (row, head) over the q heads then the k heads of a fused
-// q|k|v row: RMSNorm of the head's dh values with its norm weight, then
+// Items are (row, head) over the q heads then the k heads of a fused q|k|v
+// row: RMSNorm of the head's dh values with its norm weight, then
 // rotate-half RoPE at the row's position (applyRoPE, modernbert.go:130-143:
 // each product rounded to float32 before the add). With `outh` the results
 // go to bf16 rows of the same layout instead (round to nearest even), and
 // the v heads are converted too: the operands of a bf16 attention.
+// A wave takes kQkItems consecutive items, loading all of them before it
+// reduces, so their memory latencies overlap.
+constexpr int kQkItems = 4;
+
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     float* __restrict__ qkv, int ldqkv, int m, int nq, int nkv, int dh,
     const float* __restrict__ q_g, const float* __restrict__ k_g, float eps,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
     const int32_t* __restrict__ pos, __bf16* __restrict__ outh) {
   const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * kRows + (threadIdx.x >> 6);
+  const int item0 = (blockIdx.x * kRows + (threadIdx.x >> 6)) * kQkItems;
   const int nh = nq + nkv + (outh ? nkv : 0);
-  if (item >= m * nh) return;
-  const int row = item / nh, h = item % nh;
-  float* v = qkv + (size_t)row * ldqkv + h * dh;  // q heads, k heads, [v heads]
-  if (h >= nq + nkv) {  // v head: conversion only
-    __bf16* o = outh + (size_t)row * ldqkv + h * dh;
-    for (int d = lane; d < dh; d += 64) o[d] = (__bf16)v[d];
-    return;
-  }
-  const float* g = h < nq ? q_g : k_g;
+  const int total = m * nh;
   const int half = dh >> 1;
   // lane holds pairs (d, d + half) for d = lane, lane + 64 (dh <= 256)
-  float x1[2], x2[2];
-  float ss = 0.0f;
+  float x1[kQkItems][2], x2[kQkItems][2];
 #pragma unroll
-  for (int e = 0; e < 2; e++) {
-    const int d = lane + 64 * e;
-    x1[e] = d < half ? v[d] : 0.0f;
-    x2[e] = d < half ? v[d + half] : 0.0f;
-    ss += x1[e] * x1[e] + x2[e] * x2[e];
+  for (int it = 0; it < kQkItems; it++) {
+    const int item = min(item0 + it, total - 1);
+    const float* v = qkv + (size_t)(item / nh) * ldqkv + (item % nh) * dh;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int d = lane + 64 * e;
+      x1[it][e] = d < half ? v[d] : 0.0f;
+      x2[it][e] = d < half ? v[d + half] : 0.0f;
+    }
   }
-  const float inv = rms_inv(wsum(ss), dh, eps);
-  const int p = pos[row];
-  const float* c = cos_t + (size_t)p * half;
-  const float* sn = sin_t + (size_t)p * half;
 #pragma unroll
-  for (int e = 0; e < 2; e++) {
-    const int d = lane + 64 * e;
-    if (d < half) {
-      const float a = x1[e] * inv * g[d];
-      const float b = x2[e] * inv * g[d + half];
-      const float cc = c[d], ssn = sn[d];
-      const float t0 = a * cc, t1 = b * ssn, t2 = b * cc, t3 = a * ssn;
-      if (outh) {
-        __bf16* o = outh + (size_t)row * ldqkv + h * dh;
-        o[d] = (__bf16)(t0 - t1);
-        o[d + half] = (__bf16)(t2 + t3);
-      } else {
-        v[d] = t0 - t1;
-        v[d + half] = t2 + t3;
+  for (int it = 0; it < kQkItems; it++) {
+    const int item = item0 + it;
+    if (item >= total) return;
+    const int row = item / nh, h = item % nh;
+    float* v = qkv + (size_t)row * ldqkv + h * dh;
+    __bf16* o = outh ? outh + (size_t)row * ldqkv + h * dh : nullptr;
+    if (h >= nq + nkv) {  // v head: conversion only
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int d = lane + 64 * e;
+        if (d < half) {
+          o[d] = (__bf16)x1[it][e];
+          o[d + half] = (__bf16)x2[it][e];
+        }
+      }
+      continue;
+    }
+    const float* g = h < nq ? q_g : k_g;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 2; e++) ss += x1[it][e] * x1[it][e] + x2[it][e] * x2[it][e];
+    const float inv = rms_inv(wsum(ss), dh, eps);
+    const int p = pos[row];
+    const float* c = cos_t + (size_t)p * half;
+    const float* sn = sin_t + (size_t)p * half;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int d = lane + 64 * e;
+      if (d < half) {
+        const float a = x1[it][e] * inv * g[d];
+        const float b = x2[it][e] * inv * g[d + half];
+        const float cc = c[d], ssn = sn[d];
+        const float t0 = a * cc, t1 = b * ssn, t2 = b * cc, t3 = a * ssn;
+        if (o) {
+          o[d] = (__bf16)(t0 - t1);
+          o[d + half] = (__bf16)(t2 + t3);
+        } else {
+          v[d] = t0 - t1;
+          v[d + half] = t2 + t3;
+        }
       }
     }
   }
@@ -258,61 +271,53 @@ hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, in
   if (m <= 0) return hipSuccess;
   if (dh % 2 || dh > 256) return hipErrorInvalidValue;
   const int items = m * (nq + nkv + (outh ? nkv : 0));
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(ceil_div(items, kRows)), dim3(256), 0, s, qkv,
-                     ldqkv, m, nq, nkv, dh, q_g, k_g, eps, cos_t, sin_t, pos, outh);
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(ceil_div(items, kRows * kQkItems)), dim3(256), 0,
+                     s, qkv, ldqkv, m, nq, nkv, dh, q_g, k_g, eps, cos_t, sin_t, pos, outh);
   return hipGetLastError();
 }
 
 // ---- EmbeddingGemma Dense head --------------------------------------------------------
 // applyGemmaDenseHead (gemma3.go:174-198): hid[o] = sum_i w1[o][i] * pooled[i],
 // out[o] = sum_i w2[o][i] * hid[i], each a sequential float32 sum in ascending
-// i (no FMA), then L2Normalize (tensor.go:542-554) with a float64 sum.
-// One workgroup per text; hid lives in LDS.
-__global__ __launch_bounds__(256) void dense_head_kernel(const float* __restrict__ pooled,
-                                                         int H, int D,
-                                                         const float* __restrict__ w1,
-                                                         const float* __restrict__ w2,
-                                                         int normalize, float* __restrict__ out) {
-  extern __shared__ float hid[];  // D floats
-  __shared__ double red[256];
-  const int b = blockIdx.x;
-  const float* x = pooled + (size_t)b * H;
-  for (int o = threadIdx.x; o < D; o += 256) {
-    const float* row = w1 + (size_t)o * H;
-    float acc = 0.0f;
-    for (int i = 0; i < H; i++) acc = acc + row[i] * x[i];
-    hid[o] = acc;
-  }
+// i (no FMA). One thread per (text, output) over transposed weights
+// (wT[i][o], so a wave's loads of one i are contiguous); the text's input
+// vector is staged in LDS.
+__global__ __launch_bounds__(256) void dense_matvec_kernel(const float* __restrict__ wT,
+                                                           int in, int outn,
+                                                           const float* __restrict__ x,
+                                                           float* __restrict__ y) {
+  extern __shared__ float xs[];  // in floats
+  const int b = blockIdx.y;
+  for (int i = threadIdx.x; i < in; i += 256) xs[i] = x[(size_t)b * in + i];
   __syncthreads();
-  float* y = out + (size_t)b * H;
-  double ss = 0.0;
-  for (int o = threadIdx.x; o < H; o += 256) {
-    const float* row = w2 + (size_t)o * D;
-    float acc = 0.0f;
-    for (int i = 0; i < D; i++) acc = acc + row[i] * hid[i];
-    y[o] = acc;
-    ss += (double)acc * (double)acc;
+  const int o = blockIdx.x * 256 + threadIdx.x;
+  if (o >= outn) return;
+  const float* w = wT + o;
+  float acc = 0.0f;
+  int i = 0;
+  for (; i + 8 <= in; i += 8) {
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) t[e] = w[(size_t)(i + e) * outn];
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc = acc + t[e] * xs[i + e];
   }
-  if (!normalize) return;
-  red[threadIdx.x] = ss;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
-  }
-  const double sum = red[0];
-  if (sum == 0.0) return;
-  const float inv = (float)(1.0 / sqrt(sum));
-  for (int o = threadIdx.x; o < H; o += 256) y[o] = y[o] * inv;
+  for (; i < in; i++) acc = acc + w[(size_t)i * outn] * xs[i];
+  y[(size_t)b * outn + o] = acc;
 }
 
-hipError_t launch_dense_head(const float* pooled, int batch, int H, int D, const float* w1,
-                             const float* w2, int normalize, float* out, hipStream_t s) {
+hipError_t launch_dense_head(const float* pooled, int batch, int H, int D, const float* w1T,
+                             const float* w2T, int normalize, float* hid, float* out,
+                             hipStream_t s) {
   if (batch <= 0) return hipSuccess;
-  if ((size_t)D * sizeof(float) > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(dense_head_kernel, dim3(batch), dim3(256), D * sizeof(float), s, pooled,
-                     H, D, w1, w2, normalize, out);
-  return hipGetLastError();
+  if ((size_t)std::max(H, D) * sizeof(float) > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dense_matvec_kernel, dim3(ceil_div(D, 256), batch), dim3(256),
+                     H * sizeof(float), s, w1T, H, D, pooled, hid);
+  hipLaunchKernelGGL(dense_matvec_kernel, dim3(ceil_div(H, 256), batch), dim3(256),
+                     D * sizeof(float), s, w2T, D, H, hid, out);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess && normalize) e = launch_l2_rows(out, batch, H, s);
+  return e;
 }
 
 }  // namespace rh

@@ -255,12 +255,15 @@ __global__ __launch_bounds__(256) void add_ln_kernel(
 
 // float4 variant for H % 4 == 0 (every encoder width): lane l holds columns
 // 4(l + 64e) .. +3. Same operation order per element as ln_row_finish.
+// With ph the normalized row also goes to the bf16 hi/lo planes [m][ldp] of
+// the next weight-only int8 / fp32 GEMM's input (pl may be null).
 template <int V>
 __global__ __launch_bounds__(256) void add_ln_vec_kernel(
     float* __restrict__ x, const float* __restrict__ y, int ldy,
     const float* __restrict__ gamma, const float* __restrict__ beta, int m,
     int H, float eps, uint8_t* __restrict__ qa, int ldq,
-    float* __restrict__ row_scales) {
+    float* __restrict__ row_scales, __bf16* __restrict__ ph, __bf16* __restrict__ pl,
+    int ldp) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= m) return;
@@ -303,6 +306,7 @@ __global__ __launch_bounds__(256) void add_ln_vec_kernel(
       for (int c = 0; c < 4; c++) o[c] = (v[e][c] - mean) * inv * g[c] + b[c];
       v[e] = o;
       *reinterpret_cast<v4f*>(xr + j) = o;
+      if (ph) store_planes4(ph, pl, (size_t)row * ldp + j, o);
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
     }
   }
@@ -328,28 +332,30 @@ __global__ __launch_bounds__(256) void add_ln_vec_kernel(
 template <int V>
 static void launch_alnv(float* x, const float* y, int ldy, const float* gamma,
                         const float* beta, int m, int H, float eps, uint8_t* qa, int ldq,
-                        float* rs, hipStream_t s) {
+                        float* rs, __bf16* ph, __bf16* pl, int ldp, hipStream_t s) {
   hipLaunchKernelGGL((add_ln_vec_kernel<V>), dim3(ceil_div(m, kRowsPerBlock)), dim3(256),
-                     0, s, x, y, ldy, gamma, beta, m, H, eps, qa, ldq, rs);
+                     0, s, x, y, ldy, gamma, beta, m, H, eps, qa, ldq, rs, ph, pl, ldp);
 }
 
 hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
                                 const float* gamma, const float* beta, int m,
                                 int H, float eps, uint8_t* qa, int ldq,
-                                float* row_scales, hipStream_t s) {
+                                float* row_scales, hipStream_t s, __bf16* ph, __bf16* pl,
+                                int ldp) {
   if (m <= 0) return hipSuccess;
   if (H > 64 * kMaxPerLane) return hipErrorInvalidValue;
   const bool vec = H % 4 == 0 && (!y || ldy % 4 == 0) && (!qa || ldq % 4 == 0) &&
                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
                      reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) &
                     15) == 0;
+  if (ph && (!vec || ldp % 64 || ldp < H)) return hipErrorInvalidValue;
   if (vec) {
     const int v = ceil_div(H, 256);
-    if (v <= 1) launch_alnv<1>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
-    else if (v <= 2) launch_alnv<2>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
-    else if (v <= 3) launch_alnv<3>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
-    else if (v <= 4) launch_alnv<4>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
-    else launch_alnv<8>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, s);
+    if (v <= 1) launch_alnv<1>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, ph, pl, ldp, s);
+    else if (v <= 2) launch_alnv<2>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, ph, pl, ldp, s);
+    else if (v <= 3) launch_alnv<3>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, ph, pl, ldp, s);
+    else if (v <= 4) launch_alnv<4>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, ph, pl, ldp, s);
+    else launch_alnv<8>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, ph, pl, ldp, s);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(add_ln_kernel, dim3(ceil_div(m, kRowsPerBlock)), dim3(256),
@@ -363,34 +369,46 @@ hipError_t launch_layernorm(float* x, const float* gamma, const float* beta,
                               nullptr, s);
 }
 
-// Pooling per text (bert.go:669-703) + L2Normalize (tensor.go:542-554).
-// Mean pooling sums each column over the text's rows in ascending order —
-// the reference's poolMean order — then multiplies by 1/float32(len).
-__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x,
-                                                   int H,
+// Pooling (bert.go:657-703): one thread per (text, column). CLS / last token
+// copy a row; mean sums the column over the text's rows in ascending order
+// in float32 (poolMean's order), then multiplies by float32(1/len). The
+// column loop is unrolled so the independent row loads overlap.
+__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x, int H,
                                                    const int32_t* __restrict__ cu,
-                                                   int pooling, int normalize,
-                                                   float* __restrict__ out) {
-  __shared__ double red[256];
-  const int b = blockIdx.x;
+                                                   int pooling, float* __restrict__ out) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= H) return;
   const int r0 = cu[b], len = cu[b + 1] - cu[b];
-  float* o = out + (size_t)b * H;
-  double ss = 0.0;
-  for (int j = threadIdx.x; j < H; j += 256) {
-    float v;
-    if (pooling == RH_POOL_CLS) {
-      v = x[(size_t)r0 * H + j];
-    } else if (pooling == RH_POOL_LAST) {
-      v = x[(size_t)(r0 + len - 1) * H + j];
-    } else {
-      float s = 0.0f;
-      for (int i = 0; i < len; i++) s += x[(size_t)(r0 + i) * H + j];
-      v = s * (1.0f / (float)len);
+  float v;
+  if (pooling == RH_POOL_CLS) {
+    v = x[(size_t)r0 * H + j];
+  } else if (pooling == RH_POOL_LAST) {
+    v = x[(size_t)(r0 + len - 1) * H + j];
+  } else {
+    const float* col = x + (size_t)r0 * H + j;
+    float s = 0.0f;
+    int i = 0;
+    for (; i + 8 <= len; i += 8) {
+      float t[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) t[e] = col[(size_t)(i + e) * H];
+#pragma unroll
+      for (int e = 0; e < 8; e++) s += t[e];
     }
-    o[j] = v;
-    ss += (double)v * (double)v;
+    for (; i < len; i++) s += col[(size_t)i * H];
+    v = s * (1.0f / (float)len);
   }
-  if (!normalize) return;
+  out[(size_t)b * H + j] = v;
+}
+
+// L2Normalize (tensor.go:540-554) of each [H] row in place: float64 sum of
+// squares, scale by float32(1/sqrt(sum)); an all-zero row is left as is.
+__global__ __launch_bounds__(256) void l2_rows_kernel(float* __restrict__ y, int H) {
+  __shared__ double red[256];
+  float* o = y + (size_t)blockIdx.x * H;
+  double ss = 0.0;
+  for (int j = threadIdx.x; j < H; j += 256) ss += (double)o[j] * (double)o[j];
   red[threadIdx.x] = ss;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
@@ -403,12 +421,20 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x,
   for (int j = threadIdx.x; j < H; j += 256) o[j] = o[j] * inv;
 }
 
+hipError_t launch_l2_rows(float* y, int rows, int H, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(l2_rows_kernel, dim3(rows), dim3(256), 0, s, y, H);
+  return hipGetLastError();
+}
+
 hipError_t launch_pool(const float* x, int H, const int32_t* cu, int batch,
                        int pooling, int normalize, float* out, hipStream_t s) {
   if (batch <= 0) return hipSuccess;
-  hipLaunchKernelGGL(pool_kernel, dim3(batch), dim3(256), 0, s, x, H, cu, pooling,
-                     normalize, out);
-  return hipGetLastError();
+  hipLaunchKernelGGL(pool_kernel, dim3(ceil_div(H, 256), batch), dim3(256), 0, s, x, H, cu,
+                     pooling, out);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess && normalize) e = launch_l2_rows(out, batch, H, s);
+  return e;
 }
 
 __global__ void fill_zero_kernel(float* x, int n) {

@@ -71,17 +71,25 @@ struct rh_model {
   std::vector<Layer> layers;
   // decoder family
   std::vector<DecLayer> dlayers;
-  float *final_norm = nullptr, *dense1 = nullptr, *dense2 = nullptr;
+  float *final_norm = nullptr;
+  float *dense1 = nullptr, *dense2 = nullptr;  // Gemma Dense head, transposed [in][out]
   float *cos_g = nullptr, *sin_g = nullptr, *cos_l = nullptr, *sin_l = nullptr;
-  float *normed = nullptr, *pooled = nullptr;
+  float *normed = nullptr, *pooled = nullptr, *dense_hid = nullptr;
   int32_t* pos_d = nullptr;
   int attn_precision = 3;
   bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
+  bool producer_planes = true;  // RH_OPT_PRODUCER_PLANES
 
   // workspace, sized for cap rows / cap_batch texts
   int cap = 0, cap_batch = 0, cap_ids = 0;
   float *x = nullptr, *qkv = nullptr, *ctxb = nullptr, *y = nullptr, *hid = nullptr;
-  __bf16* qkvh = nullptr;                 // bf16 QKV rows (full-int8 path)
+  __bf16* qkvh = nullptr;                 // bf16 QKV rows (bf16 attention)
+  // bf16 hi/lo activation planes written by the producers of the
+  // weight-only int8 / fp32 GEMMs: p0 [cap][ld0] holds a width-H or
+  // width-qdim input (normed rows, attention output), p1 [cap][ld1] the
+  // intermediate (the gated / GELU output feeding the down projection).
+  __bf16 *p0h = nullptr, *p0l = nullptr, *p1h = nullptr, *p1l = nullptr;
+  int ld0 = 0, ld1 = 0;
   uint8_t *qa = nullptr, *qa2 = nullptr;  // u8 activations: width H / width I
   float *rs = nullptr, *rs2 = nullptr, *absmax = nullptr;
   int32_t* cu_d = nullptr;
@@ -98,12 +106,13 @@ struct rh_model {
     for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
                     (void*)rs, (void*)cu_d, (void*)ids_d, (void*)out_d, (void*)qkvh,
                     (void*)qa2, (void*)rs2, (void*)absmax, (void*)normed, (void*)pooled,
+                    (void*)dense_hid, (void*)p0h, (void*)p0l, (void*)p1h, (void*)p1l,
                     (void*)pos_d})
       if (p) (void)hipFree(p);
-    x = qkv = ctxb = y = hid = rs = out_d = rs2 = absmax = normed = pooled = nullptr;
+    x = qkv = ctxb = y = hid = rs = out_d = rs2 = absmax = normed = pooled = dense_hid = nullptr;
     pos_d = nullptr;
     qa = qa2 = nullptr;
-    qkvh = nullptr;
+    qkvh = p0h = p0l = p1h = p1l = nullptr;
     cu_d = ids_d = nullptr;
     cap = cap_batch = cap_ids = 0;
   }
@@ -160,6 +169,18 @@ struct rh_model {
   int qkv_width() const { return decoder() ? qdim() + 2 * kvdim() : 3 * cfg.hidden; }
   int ctx_width() const { return decoder() ? qdim() : cfg.hidden; }
   int ldq_for(int k) const { return (int)round_up(k, 16); }
+  // Does w take its input as producer-written planes? (w runs on planes and
+  // K is a multiple of 64, so the producers' K columns fill the planes.)
+  bool planes_in(const rh_weight* w) const {
+    return producer_planes && p0h && linear_on_planes(ctx, w) && w->k % 64 == 0;
+  }
+  Planes plane(int which, const rh_weight* w) const {
+    Planes p;
+    p.hi = which ? p1h : p0h;
+    p.lo = linear_a_terms(ctx, w) == 2 ? (which ? p1l : p0l) : nullptr;
+    p.ld = which ? ld1 : ld0;
+    return p;
+  }
   float eps() const { return cfg.layer_norm_eps == 0.0f ? 1e-12f : cfg.layer_norm_eps; }
   int max_seq() const { return cfg.max_position - cfg.position_offset; }
 
@@ -171,11 +192,12 @@ struct rh_model {
       int newcap = (int)round_up(rows, 256);
       for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
                       (void*)rs, (void*)qkvh, (void*)qa2, (void*)rs2, (void*)absmax,
-                      (void*)normed, (void*)pos_d})
+                      (void*)normed, (void*)pos_d, (void*)p0h, (void*)p0l, (void*)p1h,
+                      (void*)p1l})
         if (p) RH_HIP(hipFree(p));
       x = qkv = ctxb = y = hid = rs = rs2 = absmax = normed = nullptr;
       qa = qa2 = nullptr;
-      qkvh = nullptr;
+      qkvh = p0h = p0l = p1h = p1l = nullptr;
       pos_d = nullptr;
       const size_t r = newcap;
       RH_HIP(dalloc(&x, r * H));
@@ -193,12 +215,22 @@ struct rh_model {
       RH_HIP(dalloc(&rs, r));
       RH_HIP(dalloc(&rs2, r));
       RH_HIP(dalloc(&absmax, r));
+      if (quant != RH_QUANT_FULL) {
+        ld0 = (int)round_up(std::max(H, ctx_width()), 64);
+        ld1 = (int)round_up(I, 64);
+        RH_HIP(dalloc(&p0h, r * ld0));
+        RH_HIP(dalloc(&p0l, r * ld0));
+        RH_HIP(dalloc(&p1h, r * ld1));
+        RH_HIP(dalloc(&p1l, r * ld1));
+      }
       cap = newcap;
     }
     if (batch > cap_batch) {
       if (cu_d) RH_HIP(hipFree(cu_d));
       if (out_d) RH_HIP(hipFree(out_d));
       if (pooled) RH_HIP(hipFree(pooled));
+      if (dense_hid) RH_HIP(hipFree(dense_hid));
+      dense_hid = nullptr;
       cu_d = nullptr;
       out_d = nullptr;
       pooled = nullptr;
@@ -206,6 +238,7 @@ struct rh_model {
       RH_HIP(dalloc(&cu_d, nb + 1));
       RH_HIP(dalloc(&out_d, (size_t)nb * H));
       RH_HIP(dalloc(&pooled, (size_t)nb * H));
+      if (cfg.dense_hidden > 0) RH_HIP(dalloc(&dense_hid, (size_t)nb * cfg.dense_hidden));
       cap_batch = nb;
     }
     if (ids_elems > cap_ids) {
@@ -312,6 +345,9 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
   }
 
   const double MH = M;
+  // p0 holds planes of x for the next QKV when the previous layer's
+  // residual+LN wrote them (layer 0 splits the embeddings' x itself).
+  bool x_planes = false;
   for (size_t li = 0; li < layers.size(); li++) {
     const Layer& L = layers[li];
     // QKV projection. x was quantized into qa/rs by the producer if the
@@ -323,8 +359,9 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
       st = run_gemm_i8(ctx, L.qkv, qa, ldq_for(H), rs, M, EPI_BF16, qkvh, 3 * H, ACT_NONE,
                        L.qkv->d_bias, nullptr, nullptr, 2.0 * MH * H * 3 * H);
     } else {
+      const Planes pq = plane(0, L.qkv);
       st = run_linear(ctx, L.qkv, x, H, M, qkv, 3 * H, ACT_NONE, L.qkv->d_bias, qa,
-                      ldq_for(H), rs, false);
+                      ldq_for(H), rs, false, x_planes ? &pq : nullptr);
     }
     if (st) return st;
     AttnArgs aa{};
@@ -341,18 +378,27 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     aa.kv_heads = heads;
     aa.dh = dh;
     aa.scale = (float)(1.0 / std::sqrt((double)dh));
-    aa.ctx = ctxb;
-    aa.ldctx = H;
+    // the attention output goes straight to the output projection's planes
+    // when it takes them
+    const bool po = planes_in(L.o);
+    const Planes pov = plane(0, L.o);
+    aa.ctx = po ? nullptr : ctxb;
+    aa.ctx_hi = po ? pov.hi : nullptr;
+    aa.ctx_lo = po ? pov.lo : nullptr;
+    aa.ldctx = po ? pov.ld : H;
     int slot = -1;
     RH_HIP(ctx->prof_begin(3, attn_ops, 0.0, &slot));
     RH_HIP(launch_attention(aa, attn_precision, s));
     RH_HIP(ctx->prof_end(slot));
     st = run_linear(ctx, L.o, ctxb, H, M, y, H, ACT_NONE, L.o->d_bias, qa, ldq_for(H),
-                    rs, needs_q(L.o));
+                    rs, needs_q(L.o) && !po, po ? &pov : nullptr);
     if (st) return st;
     const bool qf1 = needs_q(L.f1);
+    const bool pf1 = planes_in(L.f1);
+    const Planes pf1v = plane(0, L.f1);
     RH_HIP(launch_add_layernorm(x, y, H, L.ln1_g, L.ln1_b, M, H, eps(),
-                                qf1 ? qa : nullptr, ldq_for(H), qf1 ? rs : nullptr, s));
+                                qf1 ? qa : nullptr, ldq_for(H), qf1 ? rs : nullptr, s,
+                                pf1 ? pf1v.hi : nullptr, pf1 ? pf1v.lo : nullptr, pf1v.ld));
     if (fused_ffn1 && qf1 && needs_q(L.f2)) {
       // FFN1 + GELU + QuantizeRowU8 without the fp32 intermediate: pass 1
       // finds each row's |max| of the GELU output, pass 2 recomputes the
@@ -383,16 +429,24 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
                       rs2, false);
       if (st) return st;
     } else {
+      // FFN1's GELU output goes to FFN2's planes when FFN2 takes them
+      const bool pf2 = planes_in(L.f2) && linear_on_planes(ctx, L.f1);
+      const Planes pf2v = plane(1, L.f2);
       st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_GELU, L.f1->d_bias, qa, ldq_for(H),
-                      rs, false);
+                      rs, false, pf1 ? &pf1v : nullptr, pf2 ? &pf2v : nullptr);
       if (st) return st;
       st = run_linear(ctx, L.f2, hid, I, M, y, H, ACT_NONE, L.f2->d_bias, qa2, ldq_for(I),
-                      rs2, needs_q(L.f2));
+                      rs2, needs_q(L.f2) && !pf2, pf2 ? &pf2v : nullptr);
       if (st) return st;
     }
-    const bool qn = li + 1 < layers.size() && needs_q(layers[li + 1].qkv);
+    const bool last = li + 1 == layers.size();
+    const bool qn = !last && needs_q(layers[li + 1].qkv);
+    x_planes = !last && planes_in(layers[li + 1].qkv);
+    const Planes pnv = last ? Planes{} : plane(0, layers[li + 1].qkv);
     RH_HIP(launch_add_layernorm(x, y, H, L.ln2_g, L.ln2_b, M, H, eps(),
-                                qn ? qa : nullptr, ldq_for(H), qn ? rs : nullptr, s));
+                                qn ? qa : nullptr, ldq_for(H), qn ? rs : nullptr, s,
+                                x_planes ? pnv.hi : nullptr, x_planes ? pnv.lo : nullptr,
+                                pnv.ld));
   }
   if (pool) {
     RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
@@ -423,9 +477,36 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
                              pos_d, err_d, M, s));
   const float e = eps();
   const int ldqH = ldq_for(std::max(H, qd)), ldqI = ldq_for(I);
-  const bool q0 = needs_q(dlayers[0].qkv);
-  RH_HIP(launch_rms_residual(x, nullptr, nullptr, dlayers[0].in_norm, normed, M, H, e,
-                             q0 ? qa : nullptr, ldqH, q0 ? rs : nullptr, s));
+  // The pre-norms write what the next GEMM reads: fp32 rows, its bf16
+  // planes, or its u8 rows (RmsArgs).
+  auto rms_to = [&](float* xx, const float* yy, const float* post, const float* pre,
+                    const rh_weight* next, bool in_place_out) {
+    RmsArgs ra{};
+    ra.x = xx;
+    ra.y = yy;
+    ra.post_g = post;
+    ra.pre_g = pre;
+    ra.m = M;
+    ra.H = H;
+    ra.eps = e;
+    if (in_place_out) {
+      ra.out = xx;
+    } else if (planes_in(next)) {
+      const Planes p = plane(0, next);
+      ra.ph = p.hi;
+      ra.pl = p.lo;
+      ra.ldp = p.ld;
+    } else {
+      ra.out = normed;
+    }
+    if (next && needs_q(next)) {
+      ra.qa = qa;
+      ra.ldq = ldqH;
+      ra.row_scales = rs;
+    }
+    return launch_rms_residual(ra, s);
+  };
+  RH_HIP(rms_to(x, nullptr, nullptr, dlayers[0].in_norm, dlayers[0].qkv, false));
   double attn_ops = 0;
   for (int b = 0; b < batch; b++) {
     const double L = cu[b + 1] - cu[b];
@@ -435,8 +516,9 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
   for (size_t li = 0; li < dlayers.size(); li++) {
     const DecLayer& L = dlayers[li];
     // attention block: fused q|k|v, QK-norm + RoPE, GQA attention, o_proj
+    const Planes pq = plane(0, L.qkv);
     st = run_linear(ctx, L.qkv, normed, H, M, qkv, qkvw, ACT_NONE, nullptr, qa, ldqH, rs,
-                    false);
+                    false, planes_in(L.qkv) ? &pq : nullptr);
     if (st) return st;
     const bool local = gemma() && !L.global;
     // bf16 attention reads bf16 q|k|v rows, written by the QK-norm pass
@@ -459,40 +541,47 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     aa.dh = dh();
     aa.scale = gemma() ? (float)(1.0 / std::sqrt((double)cfg.query_pre_attn_scalar))
                        : (float)(1.0 / std::sqrt((double)dh()));
-    aa.ctx = ctxb;
-    aa.ldctx = qd;
+    // the attention output goes straight to o_proj's planes when it takes them
+    const bool po = planes_in(L.o);
+    const Planes pov = plane(0, L.o);
+    aa.ctx = po ? nullptr : ctxb;
+    aa.ctx_hi = po ? pov.hi : nullptr;
+    aa.ctx_lo = po ? pov.lo : nullptr;
+    aa.ldctx = po ? pov.ld : qd;
     aa.causal = cfg.arch == RH_ARCH_QWEN3 ? 1 : 0;
     aa.window = local ? cfg.sliding_window : 0;
     int slot = -1;
     RH_HIP(ctx->prof_begin(3, attn_ops, 0.0, &slot));
     RH_HIP(launch_attention(aa, attn_precision, s));
     RH_HIP(ctx->prof_end(slot));
-    st = run_linear(ctx, L.o, ctxb, qd, M, y, H, ACT_NONE, nullptr, qa, ldqH, rs, needs_q(L.o));
+    st = run_linear(ctx, L.o, ctxb, qd, M, y, H, ACT_NONE, nullptr, qa, ldqH, rs,
+                    needs_q(L.o) && !po, po ? &pov : nullptr);
     if (st) return st;
     // x += [RMSNorm(attn, post_attn)]; normed = RMSNorm(x, pre-MLP norm)
-    const bool qg = needs_q(L.gu);
-    RH_HIP(launch_rms_residual(x, y, gemma() ? L.post_attn : nullptr,
-                               gemma() ? L.pre_ffn : L.post_attn, normed, M, H, e,
-                               qg ? qa : nullptr, ldqH, qg ? rs : nullptr, s));
-    // gated MLP: one GEMM over gate|up writes act(gate) * up, then down
-    st = run_linear(ctx, L.gu, normed, H, M, hid, I, glu, nullptr, qa, ldqH, rs, false);
+    RH_HIP(rms_to(x, y, gemma() ? L.post_attn : nullptr, gemma() ? L.pre_ffn : L.post_attn,
+                  L.gu, false));
+    // gated MLP: one GEMM over gate|up writes act(gate) * up (as the down
+    // projection's planes when it takes them), then down
+    const Planes pg = plane(0, L.gu), pd = plane(1, L.down);
+    const bool pdown = planes_in(L.down) && linear_on_planes(ctx, L.gu);
+    st = run_linear(ctx, L.gu, normed, H, M, hid, I, glu, nullptr, qa, ldqH, rs, false,
+                    planes_in(L.gu) ? &pg : nullptr, pdown ? &pd : nullptr);
     if (st) return st;
     st = run_linear(ctx, L.down, hid, I, M, y, H, ACT_NONE, nullptr, qa2, ldqI, rs2,
-                    needs_q(L.down));
+                    needs_q(L.down), pdown ? &pd : nullptr);
     if (st) return st;
     // x += [RMSNorm(mlp, post_ffn)]; then the next layer's input norm, or the
     // final RMSNorm in place (qwen3.go:543, gemma3.go:379)
     const bool last = li + 1 == dlayers.size();
-    const bool qn = !last && needs_q(dlayers[li + 1].qkv);
-    RH_HIP(launch_rms_residual(x, y, gemma() ? L.post_ffn : nullptr,
-                               last ? final_norm : dlayers[li + 1].in_norm, last ? x : normed,
-                               M, H, e, qn ? qa : nullptr, ldqH, qn ? rs : nullptr, s));
+    RH_HIP(rms_to(x, y, gemma() ? L.post_ffn : nullptr,
+                  last ? final_norm : dlayers[li + 1].in_norm,
+                  last ? nullptr : dlayers[li + 1].qkv, last));
   }
   if (pool) {
     if (gemma() && dense1 && dense2) {
       RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, 0, pooled, s));
-      RH_HIP(launch_dense_head(pooled, batch, H, cfg.dense_hidden, dense1, dense2,
-                               cfg.normalize, out_dev, s));
+      RH_HIP(launch_dense_head(pooled, batch, H, cfg.dense_hidden, dense1, dense2, cfg.normalize,
+                               dense_hid, out_dev, s));
     } else {
       RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
     }
@@ -686,8 +775,15 @@ static int finalize_decoder(rh_model* m) {
       return st;
     if ((st = find_tensor(m, "", "3_Dense.linear.weight", {H, m->cfg.dense_hidden}, &d2)))
       return st;
-    if ((st = upload(d1->data.data(), d1->data.size(), &m->dense1))) return st;
-    if ((st = upload(d2->data.data(), d2->data.size(), &m->dense2))) return st;
+    // kept transposed ([in][out]) for the per-output Dense kernels
+    const int D = m->cfg.dense_hidden;
+    std::vector<float> t1((size_t)H * D), t2((size_t)D * H);
+    for (int o = 0; o < D; o++)
+      for (int i = 0; i < H; i++) t1[(size_t)i * D + o] = d1->data[(size_t)o * H + i];
+    for (int o = 0; o < H; o++)
+      for (int i = 0; i < D; i++) t2[(size_t)i * H + o] = d2->data[(size_t)o * D + i];
+    if ((st = upload(t1.data(), t1.size(), &m->dense1))) return st;
+    if ((st = upload(t2.data(), t2.size(), &m->dense2))) return st;
   }
   m->dlayers.resize(m->cfg.layers);
   for (int l = 0; l < m->cfg.layers; l++) {
@@ -810,6 +906,11 @@ int rh_model_set_option(rh_model* m, int option, int value) {
   if (option == RH_OPT_FUSED_FFN1) {
     if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fused FFN1 must be 0 or 1");
     m->fused_ffn1 = value != 0;
+    return RH_OK;
+  }
+  if (option == RH_OPT_PRODUCER_PLANES) {
+    if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "producer planes must be 0 or 1");
+    m->producer_planes = value != 0;
     return RH_OK;
   }
   return fail(RH_ERR_INVALID, "unknown option");

@@ -143,10 +143,33 @@ struct GemmPlArgs {
   int M, N, K;
   const float* col_scales;  // W8: [N]; else null
   const float* bias;
-  float* C;
-  int ldc;
+  float* C;     // fp32 output, or null when the output goes to bf16 planes:
+  __bf16* Ch;   // hi = bf16(c), lo = bf16(c - hi) of the output (the next
+  __bf16* Cl;   // GEMM's activation planes; Cl may be null)
+  int ldc;      // elements, for C or Ch/Cl
   int act;
 };
+
+// The split hi/lo of one value; every producer of activation planes uses
+// exactly this, so planes written by a producer equal launch_split_bf16's.
+__device__ __forceinline__ void split_hi_lo(float x, __bf16& hi, __bf16& lo) {
+  hi = (__bf16)x;
+  lo = (__bf16)(x - (float)hi);
+}
+// Four consecutive values -> four hi and (if lo) four lo bf16, 8-byte stores.
+__device__ __forceinline__ void store_planes4(__bf16* hi, __bf16* lo, size_t off, const v4f& v) {
+  typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+  v4bf h, l;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    __bf16 a, b;
+    split_hi_lo(v[e], a, b);
+    h[e] = a;
+    l[e] = b;
+  }
+  *reinterpret_cast<v4bf*>(hi + off) = h;
+  if (lo) *reinterpret_cast<v4bf*>(lo + off) = l;
+}
 // a fp32 [M][lda_f] -> hi, lo bf16 [M][ldk] (ldk = round_up(K, 64), zeros
 // past K): hi = bf16(x), lo = bf16(x - float(hi)), both rounded to nearest even
 hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi, __bf16* lo,
@@ -203,11 +226,13 @@ hipError_t launch_embed_layernorm(const EmbedArgs& a, int total_rows,
                                   hipStream_t s);
 
 // x = LayerNorm(x + y) (bert.go:906-907,917-918); optional u8 quantization
-// of the result for the next full-int8 GEMM.
+// of the result for the next full-int8 GEMM, or its bf16 hi/lo planes
+// [m][ldp] (ldp % 64 == 0, >= H) for the next weight-only int8 / fp32 GEMM.
 hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
                                 const float* gamma, const float* beta, int m,
                                 int H, float eps, uint8_t* qa, int ldq,
-                                float* row_scales, hipStream_t s);
+                                float* row_scales, hipStream_t s, __bf16* ph = nullptr,
+                                __bf16* pl = nullptr, int ldp = 0);
 // standalone LayerNorm (tests)
 hipError_t launch_layernorm(float* x, const float* gamma, const float* beta,
                             int m, int H, float eps, hipStream_t s);
@@ -228,7 +253,9 @@ struct AttnArgs {
   int max_len;
   int heads, kv_heads, dh;
   float scale;
-  float* ctx;  // [M][ldctx]
+  float* ctx;  // [M][ldctx] fp32, or null when the output goes to planes:
+  __bf16* ctx_hi;  // bf16 hi / lo planes [M][ldctx] of the output (the next
+  __bf16* ctx_lo;  // GEMM's activations; ctx_lo may be null)
   int ldctx;
   int causal;  // key j visible to query i only if j <= i (qwen3.go:307-390)
   int window;  // > 0: key j visible only if |i - j| < window (gemma3.go:339-347)
@@ -247,9 +274,22 @@ hipError_t launch_embed_gather(const int32_t* ids, int stride, const int32_t* cu
 // Residual + RMSNorm sandwich per row (tensor.go:459-471):
 //   y' = post_g ? RMSNorm(y, post_g) : y;  if (y) x += y';
 //   out = RMSNorm(x, pre_g) (out may alias x); optional u8 quantization of out.
-hipError_t launch_rms_residual(float* x, const float* y, const float* post_g,
-                               const float* pre_g, float* out, int m, int H, float eps,
-                               uint8_t* qa, int ldq, float* row_scales, hipStream_t s);
+struct RmsArgs {
+  float* x;              // [m][H] residual stream, updated in place when y
+  const float* y;        // sublayer output to add, or null
+  const float* post_g;   // RMSNorm weight applied to y first, or null
+  const float* pre_g;    // RMSNorm weight of out
+  float* out;            // [m][H] fp32 out (may alias x), or null
+  __bf16* ph;            // bf16 hi / lo planes of out [m][ldp], or null
+  __bf16* pl;            // (pl may be null: one-term consumer)
+  int ldp;               // multiple of 64, >= H (the columns past H are not written)
+  int m, H;
+  float eps;
+  uint8_t* qa;           // QuantizeRowU8 of out [m][ldq], or null
+  int ldq;
+  float* row_scales;
+};
+hipError_t launch_rms_residual(const RmsArgs& a, hipStream_t s);
 // QK-norm (RMSNorm over each head's dh values) then rotate-half RoPE at the
 // row's position, in place on fused q|k rows (qwen3.go:484-516).
 hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, int dh,
@@ -257,9 +297,12 @@ hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, in
                                const float* cos_t, const float* sin_t,
                                const int32_t* pos, __bf16* outh, hipStream_t s);
 // EmbeddingGemma Dense head (gemma3.go:174-198) on pooled [batch][H] rows:
-// out = W2 . (W1 . pooled), float32 sequential sums; optional L2.
-hipError_t launch_dense_head(const float* pooled, int batch, int H, int D,
-                             const float* w1, const float* w2, int normalize,
-                             float* out, hipStream_t s);
+// out = W2 . (W1 . pooled), float32 sequential sums; optional L2. The
+// weights are given transposed: w1T [H][D], w2T [D][H]; hid is [batch][D].
+hipError_t launch_dense_head(const float* pooled, int batch, int H, int D, const float* w1T,
+                             const float* w2T, int normalize, float* hid, float* out,
+                             hipStream_t s);
+// L2Normalize (tensor.go:540-554) of `rows` rows of [H] in place.
+hipError_t launch_l2_rows(float* y, int rows, int H, hipStream_t s);
 
 }  // namespace rh

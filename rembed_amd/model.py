@@ -87,6 +87,11 @@ class Model:
     def set_fused_ffn1(self, on):
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSED_FFN1, 1 if on else 0))
 
+    def set_producer_planes(self, on=True):
+        """Weight-only int8 / fp32 GEMM inputs written as bf16 planes by their
+        producers (True, default) or split by each GEMM (False); same values."""
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_PRODUCER_PLANES, 1 if on else 0))
+
     def quantized(self):
         return bool(lib.rh_model_quantized(self.h))
 

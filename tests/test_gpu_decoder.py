@@ -191,6 +191,20 @@ def test_decoder_tokens_match_oracle_hidden(gpu_ctx, make, bf16):
         assert err <= 2e-5
 
 
+@pytest.mark.parametrize("make,bf16", [(qwen3_2l, True), (gemma3_2l, False)], ids=["qwen3", "gemma3"])
+@pytest.mark.parametrize("quant", [QUANT_NONE, QUANT_WEIGHTS], ids=["fp32", "w8"])
+def test_decoder_producer_planes_identical(gpu_ctx, make, bf16, quant):
+    """RMSNorm, attention and the gated epilogue writing the next GEMM's bf16
+    planes directly match, bit for bit, fp32 rows split by each GEMM."""
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(3, 150, 20, 150, vocab=shape.vocab, id_lo=0, seed=26)
+    m = Model(gpu_ctx, shape, t, quant)
+    direct = m.embed(ids, lens)
+    m.set_producer_planes(False)
+    split = m.embed(ids, lens)
+    assert np.array_equal(direct, split)
+
+
 def test_decoder_model_errors(gpu_ctx):
     shape, t = setup(qwen3_2l, True)
     bad = dict(t)

@@ -122,6 +122,25 @@ def test_fused_ffn1_identical(gpu_ctx, minilm):
     assert np.array_equal(plain, fused)
 
 
+@pytest.mark.parametrize("quant", [0, 1], ids=["fp32", "w8"])
+def test_producer_planes_identical(gpu_ctx, minilm, quant):
+    """Norms, attention and the FFN1 epilogue writing the next GEMM's bf16
+    planes directly give the same embeddings and hidden states, bit for bit,
+    as fp32 rows split by each GEMM (the same hi = bf16(v), lo = bf16(v - hi)
+    of the same values)."""
+    shape, t, ids, lens = minilm
+    from rembed_amd.model import Model
+    m = Model(gpu_ctx, shape, t, quant)
+    direct = m.embed(ids, lens)
+    tok_direct = m.embed_tokens(ids, lens)
+    m.set_producer_planes(False)
+    split = m.embed(ids, lens)
+    tok_split = m.embed_tokens(ids, lens)
+    assert np.array_equal(direct, split)
+    for a, b in zip(tok_direct, tok_split):
+        assert np.array_equal(a, b)
+
+
 def test_embed_tokens_matches_oracle_hidden(gpu_ctx, minilm):
     shape, t, ids, lens = minilm
     from rembed_amd.model import Model
