@@ -58,17 +58,24 @@ void *rh_context_stream(rh_context *ctx);
 /* GEMM strategy switches of a context (kept so choices can be re-measured):
  *   RH_CTX_F32_ALGO  0 = three bf16 MFMA products (default), 1 = native f32
  *   RH_CTX_W8_TERMS  bf16 terms of the fp32 activations in the weight-only
- *                    int8 GEMM: 1 or 2 (default 2)
- *   RH_CTX_I8_TILE   int8 GEMM tile: 0 = automatic, else a fixed
- *                    configuration index (see DESIGN notes of the kernel)
+ *                    int8 GEMM: 1 = bf16(a), the operand a bf16 MFMA takes
+ *                    (default), 2 = bf16 hi + lo split (fp32-grade a)
+ *   RH_CTX_I8_TILE   int8 GEMM tile: 0 = automatic, 1 = 256x256, 2 = 256x128,
+ *                    3 = 128x128 (four stages), 4 = 256x128, 5 = 128x256
+ *                    (three stages, two workgroups per CU)
  *   RH_CTX_BF_ALGO   weight-only int8 / fp32 GEMMs: 0 = activations split
  *                    once into bf16 hi/lo planes and weights stored as bf16
- *                    planes (default), 1 = split inside the GEMM's main loop */
+ *                    planes (default), 1 = split inside the GEMM's main loop
+ *   RH_CTX_BF_TILE   tile of the bf16-planes GEMM: 0 = automatic, 1 = 256x256,
+ *                    2 = 256x128, 3 = 128x128
+ *   RH_CTX_TILE_GROUP  GEMM tile order: consecutive workgroups walk this many
+ *                    row blocks down a column block (1 = row-major; default 4) */
 #define RH_CTX_F32_ALGO 1
 #define RH_CTX_W8_TERMS 2
 #define RH_CTX_I8_TILE 3
 #define RH_CTX_BF_ALGO 4
 #define RH_CTX_BF_TILE 5
+#define RH_CTX_TILE_GROUP 6
 int rh_context_set_option(rh_context *ctx, int option, int value);
 
 /* Device memory helpers (the Go host has no other allocator for HBM). */

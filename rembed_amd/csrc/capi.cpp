@@ -349,6 +349,7 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
   g.epi = epi;
   g.row_absmax = row_absmax;
   g.rs_out = rs_out;
+  g.tile_group = ctx->tile_group;
   const double M = m, K = w->k, N = w->n;
   static const double out_bytes[] = {4, 2, 0, 1, 4};  // per output element
   const double bytes = M * K + K * N + M * N * out_bytes[epi] + 4 * M + 8 * N +
@@ -429,6 +430,7 @@ static int run_linear_planes(Context* ctx, const rh_weight* w, const float* a, i
     }
     g.ldc = ldo;
     g.act = act;
+    g.tile_group = ctx->tile_group;
     // algorithmic bytes: the activations (fp32, or the planes a producer
     // wrote), the weights as stored for the mode (int8 / fp32), the output
     // (fp32 or planes)
@@ -571,6 +573,10 @@ int rh_context_set_option(rh_context* ctx, int option, int value) {
     case RH_CTX_BF_ALGO:
       if (value < 0 || value > 1) return fail(RH_ERR_INVALID, "bf_algo must be 0 or 1");
       ctx->bf_algo = value;
+      return RH_OK;
+    case RH_CTX_TILE_GROUP:
+      if (value < 1 || value > 64) return fail(RH_ERR_INVALID, "tile group must be 1..64");
+      ctx->tile_group = value;
       return RH_OK;
     case RH_CTX_BF_TILE:
       if (value < 0 || value > kPlanesTileConfigs) return fail(RH_ERR_INVALID, "unknown planes tile");

@@ -19,10 +19,11 @@ struct rh_context {
   // AND every object created from it has been destroyed, in any order.
   std::atomic<int> refs{1};
   int f32_algo = rh::F32_SPLIT3;
-  int w8_terms = 2;  // bf16 terms of the fp32 activations in weight-only int8
+  int w8_terms = 1;  // bf16 terms of the fp32 activations in weight-only int8
   int i8_tile = 0;   // 0 = automatic int8 GEMM tile choice
   int bf_algo = 0;   // W8/F32 GEMM: 0 = bf16 planes (pre-split), 1 = in-kernel split
   int bf_tile = 0;   // 0 = automatic bf16-planes GEMM tile choice
+  int tile_group = 4;  // GEMM tile order: row blocks per group (1 = row-major)
   // grow-only device workspace (bf16 planes of the activations); the context
   // serializes its calls, so one buffer serves every GEMM on its stream
   void* ws = nullptr;

@@ -16,6 +16,21 @@ __device__ __forceinline__ int xcd_remap(int b, int nwg) {
   return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
+// Logical tile -> (row block, column block), grouped: consecutive tiles walk
+// `group` row blocks down one column block before moving right. The tiles an
+// XCD runs at once (a contiguous range after xcd_remap) then share both A row
+// blocks and B column blocks in its L2 (group 1 = plain row-major order).
+__device__ __forceinline__ void tile_origin(int t, int tiles_m, int tiles_n, int group,
+                                            int& rb, int& cb) {
+  const int per = group * tiles_n;
+  const int g = t / per;
+  const int first = g * group;
+  const int gm = min(tiles_m - first, group);
+  const int r = t - g * per;
+  rb = first + r % gm;
+  cb = r / gm;
+}
+
 // LDS tiles hold rows of 128 bytes = 8 chunks of 16 bytes. A 16-byte
 // fragment read serves 16 consecutive rows per LDS cycle on gfx950 (64 banks
 // = 256 bytes, i.e. two rows per bank window), so chunk c of row r lives at

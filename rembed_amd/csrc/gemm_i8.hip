@@ -52,8 +52,10 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
   const int wm = wave >> 1, wn = wave & 1;
   const int tiles_n = (p.N + BN - 1) / BN;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int row0 = (tile / tiles_n) * BM;
-  const int col0 = (tile % tiles_n) * BN;
+  int rb, cb;
+  tile_origin(tile, (p.M + BM - 1) / BM, tiles_n, p.tile_group, rb, cb);
+  const int row0 = rb * BM;
+  const int col0 = cb * BN;
   const int nk = (p.K + BK - 1) / BK;
 
   // Per-lane source rows/chunks of this thread's loads (fixed across stages).

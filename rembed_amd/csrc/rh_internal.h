@@ -108,6 +108,7 @@ struct GemmI8Args {
   int epi;
   float* row_absmax;        // EPI_ABSMAX target / EPI_QUANT input
   float* rs_out;            // EPI_QUANT row scales
+  int tile_group;           // row blocks per group of the tile order (tile_origin)
 };
 
 // B formats of the bf16-MFMA GEMM family.
@@ -143,6 +144,7 @@ struct GemmPlArgs {
   int M, N, K;
   const float* col_scales;  // W8: [N]; else null
   const float* bias;
+  int tile_group;  // row blocks per group of the tile order (tile_origin)
   float* C;     // fp32 output, or null when the output goes to bf16 planes:
   __bf16* Ch;   // hi = bf16(c), lo = bf16(c - hi) of the output (the next
   __bf16* Cl;   // GEMM's activation planes; Cl may be null)
@@ -174,7 +176,7 @@ __device__ __forceinline__ void store_planes4(__bf16* hi, __bf16* lo, size_t off
 // past K): hi = bf16(x), lo = bf16(x - float(hi)), both rounded to nearest even
 hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi, __bf16* lo,
                              int ldk, hipStream_t s);
-constexpr int kPlanesTileConfigs = 3;
+constexpr int kPlanesTileConfigs = 5;
 hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int tile,
                               hipStream_t s);
 

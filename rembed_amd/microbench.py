@@ -19,7 +19,8 @@ BERT_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
 PEAK = {"i8": 5000.0, "w8": 2500.0, "f32": 2500.0}  # TOP/s of the MFMA used
 
 
-def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u8=False, bf=0):
+def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u8=False, bf=0,
+               group=4):
     rng = np.random.default_rng(k * 7 + n)
     bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
     bias = rng.standard_normal(n, dtype=np.float32) * 0.02
@@ -33,6 +34,7 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
     kind = {"i8": 0, "w8": 1, "f32": 2}[mode]
     ctx.set_option(_lib.RH_CTX_I8_TILE if mode == "i8" else _lib.RH_CTX_BF_TILE, tile)
     ctx.set_bf_algo(bf)
+    ctx.set_option(_lib.RH_CTX_TILE_GROUP, group)
     if mode == "i8":
         T.QuantizeRowsU8(ctx, a, m, k, qa, ldq, rs)
 
@@ -68,8 +70,10 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
     per_call = 2 if fused_u8 else 1  # the fused variant launches two GEMM passes
     us = st["total_ms"] * 1e3 / st["launches"] * per_call
     tops = st["total_ops"] / (st["total_ms"] * 1e-3) / 1e12
+    ctx.set_option(_lib.RH_CTX_TILE_GROUP, 4)
     split_us = sp["total_ms"] * 1e3 / sp["launches"] if sp["launches"] else 0.0
     return {"mode": mode, "m": m, "k": k, "n": n, "act": act, "tile": tile, "bf": bf,
+            "group": group,
             "acc_only": acc_only, "fused_u8": fused_u8, "us": round(us, 2),
             "split_us": round(split_us, 2), "tops": round(tops, 1),
             "frac": round(tops / PEAK[mode], 4),
@@ -100,6 +104,8 @@ def main():
     ap.add_argument("--tiles", default="0")
     ap.add_argument("--shapes", default="", help="k,n;k,n;... (default: BERT-base)")
     ap.add_argument("--variants", default="", help="comma list of acc,fp32,gelu")
+    ap.add_argument("--groups", default="4", help="tile-order groups (comma list)")
+    ap.add_argument("--w8-terms", type=int, default=1, help="bf16 activation terms of w8 (1 or 2)")
     ap.add_argument("--bf", default="0", help="w8/f32 GEMM algorithms: 0 = bf16 planes, "
                                               "1 = split in the main loop (comma list)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -112,6 +118,7 @@ def main():
     if args.shapes:
         shapes = [tuple(int(x) for x in s.split(",")) for s in args.shapes.split(";")]
     ctx = T.Context(0)
+    ctx.set_option(_lib.RH_CTX_W8_TERMS, args.w8_terms)
     for mode in args.modes.split(","):
         for (k, n) in shapes:
             for tile in [int(t) for t in args.tiles.split(",")]:
@@ -125,8 +132,10 @@ def main():
                 bfs = [0] if mode == "i8" else [int(b) for b in args.bf.split(",")]
                 for v in variants:
                     for bf in bfs:
-                        r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile, bf=bf, **v)
-                        print(json.dumps(r), flush=True)
+                        for grp in [int(g) for g in args.groups.split(",")]:
+                            r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile,
+                                           bf=bf, group=grp, **v)
+                            print(json.dumps(r), flush=True)
     ctx.close()
     return 0
 

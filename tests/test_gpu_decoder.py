@@ -81,6 +81,18 @@ def test_gated_linear_matches_oracle(gpu_ctx, mode, bf, act):
     say(f"  max rel err {err.max():.3e}")
     if mode == _lib.RH_MODE_A8W8:
         assert err.max() <= 1e-6
+    elif mode == _lib.RH_MODE_W8:
+        # one bf16 activation term: |dg| <= 2^-9 sum|a·w| per half (2x
+        # margin); the gated product moves by at most 1.2|dg||u| + |act(g)||du|
+        # (|act'| <= 1.2 for SiLU and GELUTanh)
+        _, qg, sg = O.pack_b8(gate, k, i)
+        _, qu, su = O.pack_b8(up, k, i)
+        aa = np.abs(a.astype(np.float64))
+        dg = 2.0 ** -8 * aa @ (np.abs(qg.astype(np.float64)) * sg[:, None]).T
+        du = 2.0 ** -8 * aa @ (np.abs(qu.astype(np.float64)) * su[:, None]).T
+        fg = np.abs(fn(g.ravel()).reshape(m, i).astype(np.float64))
+        bound = 1.2 * dg * np.abs(u) + fg * du + 2e-4 * (1 + np.abs(want))
+        assert np.all(np.abs(got.astype(np.float64) - want) <= bound)
     else:
         assert err.max() <= 2e-4
     # the gated weight refuses non-gated acts, and each half must pass the
@@ -164,6 +176,28 @@ def test_decoder_full_int8_cosine(gpu_ctx, make, bf16, batch, lo, hi):
     c = cos_rows(got, want)
     say(f"  min cos {c.min():.6f}")
     assert c.min() >= 0.999
+
+
+@pytest.mark.parametrize("shape,bf16", [(QWEN3_0_6B, True), (GEMMA3_300M, False)],
+                         ids=["qwen3-28L", "gemma3-24L"])
+def test_decoder_full_depth_weight_only_cosine(gpu_ctx, shape, bf16):
+    """All 28 / 24 layers (errors compound with depth), weight-only int8 with
+    one bf16 activation term (the default) and with two, against the
+    oracle's int8 path: cosine >= 0.9999 for both."""
+    from rembed_amd._lib import RH_CTX_W8_TERMS
+    t = decoder_tensors(shape, seed=0x5EED0003, bf16=bf16)
+    ids, lens = token_batch(4, 48, 24, 48, vocab=shape.vocab, id_lo=0, seed=7)
+    want = O.DecoderOracle(shape, t, 1).embed_batch(ids, lens, threads=8)
+    for terms in (1, 2):
+        gpu_ctx.set_option(RH_CTX_W8_TERMS, terms)
+        try:
+            m = Model(gpu_ctx, shape, t, QUANT_WEIGHTS)
+            got = m.embed(ids, lens)
+        finally:
+            gpu_ctx.set_option(RH_CTX_W8_TERMS, 1)
+        c = cos_rows(got, want)
+        say(f"{shape.name} {terms}-term min cos {c.min():.7f}")
+        assert c.min() >= 0.9999
 
 
 @pytest.mark.parametrize("make,bf16", [(qwen3_2l, True), (gemma3_2l, False)], ids=["qwen3", "gemma3"])

@@ -6,8 +6,9 @@
   every plane index (rows, ragged K, padding, the gather of the permuted
   column) are pinned bit for bit; any other index picks a different element.
 * Weight-only int8 with a signed permutation of +-127 entries (scale 1/127)
-  gives hi(a)+lo(a) times 127 times float32(1/127), exactly as the float32
-  epilogue multiplies.
+  gives hi(a) (one activation term, the default) or hi(a)+lo(a) (two) times
+  127 times float32(1/127), exactly as the float32 epilogue multiplies.
+* Every tile configuration (4- and 8-wave, 256/128 tiles) on a ragged shape.
 * Planes vs the in-loop split at encoder and decoder shapes (bias, GELU,
   gated SwiGLU): both hold the split's error bound against float64.
 """
@@ -82,11 +83,12 @@ def test_f32_permutation_exact(gpu_ctx, shape, bf):
     assert not np.array_equal(want, a[:, perm]) or k < 4  # the split is visible
 
 
+@pytest.mark.parametrize("terms", [1, 2])
 @pytest.mark.parametrize("bf", [0, 1], ids=["planes", "inloop"])
 @pytest.mark.parametrize("shape", SHAPES[1:])
-def test_w8_signed_permutation_exact(gpu_ctx, shape, bf):
+def test_w8_signed_permutation_exact(gpu_ctx, shape, bf, terms):
     m, k, n = shape
-    say(f"w8 permutation m={m} k={k} n={n} bf_algo {bf}")
+    say(f"w8 permutation m={m} k={k} n={n} bf_algo {bf} terms {terms}")
     rng = np.random.default_rng(3 * m + k + n)
     a = rng.standard_normal((m, k)).astype(np.float32)
     perm = rng.integers(0, k, size=n)
@@ -96,10 +98,46 @@ def test_w8_signed_permutation_exact(gpu_ctx, shape, bf):
     pb = T.PackB8(gpu_ctx, bT, k, n)
     q, sc, _ = pb.export()
     assert np.all(np.abs(q[np.arange(n), perm]) == 127)
-    got = run(gpu_ctx, a, pb, bf)
-    # fp32 accumulator (q·(hi+lo), exact), then the float32 scale multiply
-    acc = (split_sum(a)[:, perm] * (127.0 * sign)).astype(np.float32)
+    gpu_ctx.set_option(_lib.RH_CTX_W8_TERMS, terms)
+    try:
+        got = run(gpu_ctx, a, pb, bf)
+    finally:
+        gpu_ctx.set_option(_lib.RH_CTX_W8_TERMS, 1)
+    # fp32 accumulator (q·hi or q·(hi+lo), exact), then the float32 scale
+    av = bf16_rne(a) if terms == 1 else split_sum(a)
+    acc = (av[:, perm] * (127.0 * sign)).astype(np.float32)
     want = (acc * sc[None, :]).astype(np.float32)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"first mismatch {bad[:3].tolist()}"
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("mode,terms", [(_lib.RH_MODE_F32, 2), (_lib.RH_MODE_W8, 1),
+                                        (_lib.RH_MODE_W8, 2)], ids=["f32", "w8", "w8-2terms"])
+def test_every_planes_tile_exact(gpu_ctx, tile, mode, terms):
+    """Each tile configuration on a ragged shape (partial row and column
+    tiles), exact through a permutation weight."""
+    m, k, n = 700, 1024, 1040
+    say(f"planes tile {tile} mode {mode} terms {terms}")
+    rng = np.random.default_rng(tile * 10 + mode + terms)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    perm = rng.integers(0, k, size=n)
+    bT = np.zeros((n, k), np.float32)
+    bT[np.arange(n), perm] = 1.0
+    pb = T.PackedWeight(gpu_ctx, mode, bT, k, n)
+    gpu_ctx.set_option(_lib.RH_CTX_BF_TILE, tile)
+    gpu_ctx.set_option(_lib.RH_CTX_W8_TERMS, terms)
+    try:
+        got = T.matmul_host(gpu_ctx, a, pb)
+    finally:
+        gpu_ctx.set_option(_lib.RH_CTX_BF_TILE, 0)
+        gpu_ctx.set_option(_lib.RH_CTX_W8_TERMS, 1)
+    av = split_sum(a) if terms == 2 else bf16_rne(a)
+    if mode == _lib.RH_MODE_W8:
+        _, sc, _ = pb.export()
+        want = ((av[:, perm] * 127.0).astype(np.float32) * sc[None, :]).astype(np.float32)
+    else:
+        want = av[:, perm]
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"first mismatch {bad[:3].tolist()}"
 
@@ -122,10 +160,10 @@ def test_planes_vs_inloop_linear_gelu(gpu_ctx, mode, mkn):
     outs = [run(gpu_ctx, a, pb, bf, act=_lib.RH_ACT_GELU) for bf in (0, 1)]
     # float64 reference on a row sample, GELU applied by the oracle
     rows = rng.choice(m, size=64, replace=False)
-    if mode == _lib.RH_MODE_W8:
+    if mode == _lib.RH_MODE_W8:  # one bf16 activation term (the default)
         q, sc, _ = pb.export()
         w = q.astype(np.float64) * sc.astype(np.float64)[:, None]
-        eps = 2.0 ** -15
+        eps = 2.0 ** -8
     else:
         w = bT.astype(np.float64)
         eps = 2.0 ** -14

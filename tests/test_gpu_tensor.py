@@ -248,24 +248,26 @@ def f64_tol(k):
                KATS["packed_f32_shapes"]["tol_sqrtk"] * math.sqrt(k))
 
 
-# Error bounds of the bf16-split MFMA paths. A float x split into bf16 terms
-# hi = rne8(x), lo = rne8(x - hi) keeps |x - hi - lo| <= 2^-16 |x| (each
-# rounding to 8 significant bits loses at most 2^-8 relative). Weight-only
-# int8: q is exact in bf16, so |err| <= 2^-16 sum|a·deq|. fp32 via three
-# products hi·hi + hi·lo + lo·hi: |err| <= ~3·2^-16 sum|a·b|. Both get a
-# factor-2 margin plus the reference's fp32 tolerance for the accumulation.
-# An indexing mistake moves a result by a whole product |a_p·b_p|, far
-# above these bounds.
+# Error bounds of the bf16 MFMA paths. A float x rounded to bf16 (8
+# significant bits) keeps |x - hi| <= 2^-9 |x|; split into hi = rne8(x),
+# lo = rne8(x - hi) it keeps |x - hi - lo| <= 2^-16 |x|. Weight-only int8: q
+# is exact in bf16, so |err| <= 2^-9 sum|a·deq| with one activation term and
+# 2^-16 sum|a·deq| with two. fp32 via three products hi·hi + hi·lo + lo·hi:
+# |err| <= ~3·2^-16 sum|a·b|. Each gets a factor-2 margin plus the
+# reference's fp32 tolerance for the accumulation. An indexing mistake moves
+# a result by a whole product |a_p·b_p|, far above these bounds.
 def split_bound(a, b, k, eps, want):
     mag = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64)).T
     return eps * mag + f64_tol(k) * (1 + np.abs(want))
 
 
+@pytest.mark.parametrize("terms", [1, 2])
 @pytest.mark.parametrize("bf", [0, 1])
 @pytest.mark.parametrize("shape", KATS["packed_f32_shapes"]["shapes"])
-def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape, bf):
+def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape, bf, terms):
+    from rembed_amd._lib import RH_CTX_W8_TERMS
     m, k, n = shape
-    say(f"w8 shape {shape} bf_algo {bf}")
+    say(f"w8 shape {shape} bf_algo {bf} terms {terms}")
     t = T()
     rng = np.random.default_rng(23 + k)
     a = (rng.random((m, k), dtype=np.float32) * 2 - 1).astype(np.float32)
@@ -276,13 +278,15 @@ def test_matmul_packed8_against_dequantized_float64(gpu_ctx, shape, bf):
     st, q_o, sc_o = O.pack_b8(bT, k, n)
     assert np.array_equal(q, q_o) and np.array_equal(sc, sc_o)
     gpu_ctx.set_bf_algo(bf)
+    gpu_ctx.set_option(RH_CTX_W8_TERMS, terms)
     try:
         got = t.matmul_host(gpu_ctx, a, pb)
     finally:
         gpu_ctx.set_bf_algo(0)
+        gpu_ctx.set_option(RH_CTX_W8_TERMS, 1)
     deq = q.astype(np.float64) * sc.astype(np.float64)[:, None]
     want = a.astype(np.float64) @ deq.T
-    bound = split_bound(a, deq, k, 2.0 ** -15, want)
+    bound = split_bound(a, deq, k, 2.0 ** -8 if terms == 1 else 2.0 ** -15, want)
     err = np.abs(got - want)
     say(f"  max err {err.max():.3e}  worst err/bound {(err / bound).max():.3f}")
     assert np.all(err <= bound)
