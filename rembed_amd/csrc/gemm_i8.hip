@@ -9,8 +9,8 @@
 // real = acc_ref − 128·colSum (exact mod 2^32), and acc_ref is recovered as
 // real + 128·colSum when the raw accumulators are requested.
 //
-// Main loop: BM x BN tile per 256-thread workgroup (2x2 waves, each wave a
-// grid of 32x32 MFMA tiles). K advances in 64-byte stages that reach LDS by
+// Main loop: BM x BN tile per workgroup of 2x2 or 2x4 waves, each wave a
+// grid of 32x32 MFMA tiles. K advances in 64-byte stages that reach LDS by
 // global_load_lds_dwordx4 (no register staging): lane l of a wave
 // instruction writes LDS bytes [16l, 16l+16) of a 1 KiB block, so each lane
 // loads the global 16-byte chunk that belongs at that slot. A slot holds
@@ -33,23 +33,28 @@ __device__ __forceinline__ uint32_t quant_byte(float v, float inv) {
   return (uint32_t)q;
 }
 
-template <int BM, int BN, int NS, int EPI>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
+// WGN waves along N: 2 = a 2x2 grid of 4 waves, 4 = a 2x4 grid of 8 (two per
+// SIMD when one workgroup fills a CU).
+template <int BM, int BN, int NS, int EPI, int WGN = 2>
+__global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
+  constexpr int NT = 128 * WGN, NW = 2 * WGN;
   constexpr int BK = 64;
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int kA = BM * BK, kB = BN * BK, kStage = kA + kB;
-  constexpr int LA = kA / (256 * 16), LB = kB / (256 * 16);  // loads per thread
+  constexpr int LA = kA / (NT * 16), LB = kB / (NT * 16);  // loads per thread
   constexpr int kLoads = LA + LB;
   constexpr int kEpiStride = WN + 4;  // ints per row of the epilogue transpose
-  constexpr int kEpiBytes = 4 * 32 * kEpiStride * 4;
+  constexpr int kEpiBytes = NW * 32 * kEpiStride * 4;
+  static_assert(LA >= 1 && LB >= 1 && TN >= 1, "tile too small for the wave grid");
   static_assert(NS * kStage >= kEpiBytes + 3 * BM * 4, "epilogue LDS");
+  static_assert(NS * kStage <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int tiles_n = (p.N + BN - 1) / BN;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
   int rb, cb;
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
   float* sc_l = rs_l + BM;
   float* inv_l = sc_l + BM;
   if constexpr (EPI != EPI_ACC) {
-    for (int r = tid; r < BM; r += 256) {
+    for (int r = tid; r < BM; r += NT) {
       const int gr = row0 + r;
       float rs = 0.0f, sc = 1.0f;
       if (gr < p.M) {
@@ -297,16 +302,17 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
   }
 }
 
-template <int BM, int BN, int NS, int EPI>
+template <int BM, int BN, int NS, int EPI, int WGN = 2>
 static hipError_t launch_tile(const GemmI8Args& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
-  timed_launch((gemm_i8_kernel<BM, BN, NS, EPI>), dim3(tiles), dim3(256), 0, s, a);
+  timed_launch((gemm_i8_kernel<BM, BN, NS, EPI, WGN>), dim3(tiles), dim3(128 * WGN), 0, s, a);
   return hipGetLastError();
 }
 
 // 1 = 256x256, 2 = 256x128 and 3 = 128x128 with 4 stages; 4 = 256x128 and
-// 5 = 128x256 with 3 stages (72 KiB of LDS and <= 256 registers per lane:
-// two workgroups per CU).
+// 5 = 128x256 with 3 stages; 6 = 256x256 (4 stages) and 7 = 128x256 (3
+// stages) on 8 waves. Tiles 4, 5 and 7 take 72 KiB of LDS and <= 256
+// registers per lane, so two workgroups share a CU.
 template <int EPI>
 static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
   switch (tile) {
@@ -314,19 +320,21 @@ static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
     case 2: return launch_tile<256, 128, 4, EPI>(a, s);
     case 4: return launch_tile<256, 128, 3, EPI>(a, s);
     case 5: return launch_tile<128, 256, 3, EPI>(a, s);
+    case 6: return launch_tile<256, 256, 4, EPI, 4>(a, s);
+    case 7: return launch_tile<128, 256, 3, EPI, 4>(a, s);
     default: return launch_tile<128, 128, 4, EPI>(a, s);
   }
 }
 
-// Automatic tile: 128x256 (three stages, two workgroups per CU, one
-// tile's epilogue overlapping the other's main loop) once it yields a full
-// round of workgroups, else 128x128. Measured on MI355X at M 10102 and 16384
-// over the BERT-base linears: the faster of the two, or within 5% of it,
-// for every epilogue; 256x256 (one workgroup per CU) loses whenever the
-// output is dequantized.
+// Automatic tile, measured on MI355X over the BERT-base linears at M = 10102
+// and 16384: 256x256 with 8 waves for the
+// widest outputs (N >= 3072), else 128x256 with 8 waves (two workgroups
+// and four waves per SIMD per CU). Small problems keep 128x128 so the grid
+// still covers the CUs.
 int pick_i8_tile(int M, int N, int epi) {
   (void)epi;
-  return ceil_div(M, 128) * ceil_div(N, 256) >= 256 ? 5 : 3;
+  if (ceil_div(M, 128) * ceil_div(N, 256) < 128) return 3;
+  return N >= 3072 ? 6 : 7;
 }
 
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s) {
