@@ -1,7 +1,7 @@
 /*
  * oracle.c — CPU restatement of rembed's GEMM family and BERT forward.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product). See oracle.h
+ * TEST INFRASTRUCTURE ONLY (the parity reference, never the product). See oracle.h
  * for the pinning map. Every function cites the reference file:line it
  * follows; paths are relative to the rembed source tree.
  *

@@ -2,7 +2,7 @@
  * oracle.h — CPU restatement of rembed's GEMM family and BERT forward pass.
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library (rembed_amd/)
- * links, loads or calls this code: it is the checker that the parity tests,
+ * links, loads or calls this code: it is the reference that the parity tests,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg compare the HIP
  * path against. Each function cites the reference file:line it restates
  * (paths relative to the rembed source tree).

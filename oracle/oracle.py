@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, as the checker. The product never imports it.
+bench.py's cpu_baseline leg, as the parity reference. The product never imports it.
 """
 import ctypes
 import os

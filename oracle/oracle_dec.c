@@ -3,7 +3,7 @@
  * Qwen3 (causal, last-token pooled) and EmbeddingGemma (Gemma 3 run
  * bidirectionally, mean pooled through a Dense head).
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product); see oracle.h.
+ * TEST INFRASTRUCTURE ONLY (the parity reference, never the product); see oracle.h.
  * Every function cites the reference file:line it follows (paths relative
  * to the rembed source tree). Compiled with -ffp-contract=off, so a*b+c
  * rounds twice exactly as Go's float32 arithmetic does.
