@@ -108,8 +108,9 @@ def main():
                          "(two passes, no fp32 intermediate); split = fp32 rows + QuantizeRowU8")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only: this build has no multi-GPU path "
-              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        print(f"bench.py runs on one GPU only: the library has no multi-GPU path; texts "
+              f"shard across GPUs as independent replicas (--gpus {args.gpus} requested)",
+              file=sys.stderr)
         sys.exit(2)
 
     from rembed_amd import tensor as T
