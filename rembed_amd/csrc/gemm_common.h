@@ -133,24 +133,24 @@ __device__ __forceinline__ float gelu_avx2(float v) {
   return (v * 0.5f) * (1.0f + erf);
 }
 
-// SiLU as tensor.SiLU computes it (tensor.go:477-481): the sigmoid's
-// exponential in float64, one float32 rounding of 1 + e, float32 division.
-__device__ __forceinline__ float silu_ref(float v) {
-  return v / (float)(1.0 + exp(-(double)v));
-}
+// SiLU and the tanh-approximation GELU of the gated MLPs. The reference
+// evaluates them in float64 and rounds once (tensor.SiLU: v /
+// float32(1 + exp(-v)), tensor.go:477-481; tensor.GELUTanh: 0.5·x·(1 +
+// tanh(c·(x + 0.044715·x³))), tensor.go:490-497). Here they run in float32
+// on the accurate expf, GELUTanh in the equivalent form x / (1 + e^(-2t))
+// (no cancellation where tanh(t) -> -1): within a few float32 ulp of the
+// reference's values, at a fraction of the epilogue's float64 cost.
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
-// tanh-approximation GELU as tensor.GELUTanh computes it (tensor.go:490-497),
-// all in float64 with one rounding at the end.
-__device__ __forceinline__ float gelu_tanh_ref(float v) {
-  const double x = (double)v;
-  const double inner = 0.7978845608028654 * (x + 0.044715 * x * x * x);
-  return (float)(0.5 * x * (1.0 + tanh(inner)));
+__device__ __forceinline__ float gelu_tanh_f32(float v) {
+  const float t = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+  return v / (1.0f + expf(-2.0f * t));
 }
 
 // Gated activation of one output: act(gate) * up, the float32 product of
 // the model loops (qwen3.go:530-539, gemma3.go:365-374).
 __device__ __forceinline__ float glu_act(float g, float u, int act) {
-  return (act == ACT_SWIGLU ? silu_ref(g) : gelu_tanh_ref(g)) * u;
+  return (act == ACT_SWIGLU ? silu_f32(g) : gelu_tanh_f32(g)) * u;
 }
 
 // GEMM epilogue activation. Output rows always have n % 16 == 0 columns

@@ -264,12 +264,99 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
 }
 
+// Vector form for dh in {64, 128, 256}: one workgroup per row; a head is
+// dh/4 consecutive lanes holding 4 columns each (16-byte loads, 8- or
+// 16-byte stores), so a wave covers 64/(dh/4) heads at once. The head's
+// sum of squares reduces over its lanes; lane l and l ^ (dh/8) hold the
+// RoPE pair (d, d + dh/2). Same per-element operations as the scalar form
+// (only the sum of squares is added in another order).
+template <int DH>
+__global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
+    float* __restrict__ qkv, int ldqkv, int nq, int nkv, const float* __restrict__ q_g,
+    const float* __restrict__ k_g, float eps, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int32_t* __restrict__ pos,
+    __bf16* __restrict__ outh) {
+  typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+  constexpr int LPH = DH / 4;    // lanes per head
+  constexpr int HPW = 64 / LPH;  // heads per wave
+  constexpr int HALF = DH / 2;
+  constexpr int IT = 4;          // passes whose loads are issued together
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = lane % LPH, d = l * 4;
+  const int nh = nq + nkv + (outh ? nkv : 0);
+  float* rowp = qkv + (size_t)row * ldqkv;
+  const int p = pos[row];
+  for (int base = 0; base < nh; base += IT * 4 * HPW) {
+    v4f x[IT];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+      const int h = base + (it * 4 + wave) * HPW + lane / LPH;
+      x[it] = h < nh ? *reinterpret_cast<const v4f*>(rowp + h * DH + d)
+                     : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+      const int h0 = base + (it * 4 + wave) * HPW;  // first head of this wave's pass
+      if (h0 >= nh) break;
+      const int h = h0 + lane / LPH;
+      const size_t off = (size_t)row * ldqkv + h * DH + d;
+      float ss = (x[it][0] * x[it][0] + x[it][1] * x[it][1]) +
+                 (x[it][2] * x[it][2] + x[it][3] * x[it][3]);
+#pragma unroll
+      for (int o = LPH / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      if (h >= nh) continue;
+      if (h >= nq + nkv) {  // v head: conversion only
+        *reinterpret_cast<v4bf*>(outh + off) =
+            v4bf{(__bf16)x[it][0], (__bf16)x[it][1], (__bf16)x[it][2], (__bf16)x[it][3]};
+        continue;
+      }
+      const float inv = rms_inv(ss, DH, eps);
+      const v4f g = *reinterpret_cast<const v4f*>((h < nq ? q_g : k_g) + d);
+      v4f xn, pn;
+#pragma unroll
+      for (int c = 0; c < 4; c++) xn[c] = x[it][c] * inv * g[c];
+#pragma unroll
+      for (int c = 0; c < 4; c++) pn[c] = __shfl_xor(xn[c], LPH / 2, 64);
+      const bool first = l < LPH / 2;  // columns d < dh/2
+      const int dp = first ? d : d - HALF;
+      const v4f cc = *reinterpret_cast<const v4f*>(cos_t + (size_t)p * HALF + dp);
+      const v4f sn = *reinterpret_cast<const v4f*>(sin_t + (size_t)p * HALF + dp);
+      v4f o;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float a = first ? xn[c] : pn[c], b = first ? pn[c] : xn[c];
+        o[c] = first ? a * cc[c] - b * sn[c] : b * cc[c] + a * sn[c];
+      }
+      if (outh)
+        *reinterpret_cast<v4bf*>(outh + off) =
+            v4bf{(__bf16)o[0], (__bf16)o[1], (__bf16)o[2], (__bf16)o[3]};
+      else
+        *reinterpret_cast<v4f*>(qkv + off) = o;
+    }
+  }
+}
+
 hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, int dh,
                                const float* q_g, const float* k_g, float eps,
                                const float* cos_t, const float* sin_t,
                                const int32_t* pos, __bf16* outh, hipStream_t s) {
   if (m <= 0) return hipSuccess;
   if (dh % 2 || dh > 256) return hipErrorInvalidValue;
+  const bool vec = ldqkv % 4 == 0 && ((reinterpret_cast<uintptr_t>(qkv) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(outh) & 7) == 0);
+  if (vec && (dh == 64 || dh == 128 || dh == 256)) {
+    if (dh == 64)
+      hipLaunchKernelGGL((qk_norm_rope_vec_kernel<64>), dim3(m), dim3(256), 0, s, qkv, ldqkv, nq,
+                         nkv, q_g, k_g, eps, cos_t, sin_t, pos, outh);
+    else if (dh == 128)
+      hipLaunchKernelGGL((qk_norm_rope_vec_kernel<128>), dim3(m), dim3(256), 0, s, qkv, ldqkv,
+                         nq, nkv, q_g, k_g, eps, cos_t, sin_t, pos, outh);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_vec_kernel<256>), dim3(m), dim3(256), 0, s, qkv, ldqkv,
+                         nq, nkv, q_g, k_g, eps, cos_t, sin_t, pos, outh);
+    return hipGetLastError();
+  }
   const int items = m * (nq + nkv + (outh ? nkv : 0));
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(ceil_div(items, kRows * kQkItems)), dim3(256), 0,
                      s, qkv, ldqkv, m, nq, nkv, dh, q_g, k_g, eps, cos_t, sin_t, pos, outh);

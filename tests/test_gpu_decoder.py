@@ -4,10 +4,10 @@
   values of gate and up come out of the same epilogue arithmetic as
   MatMulPacked/MatMulPacked8/MatMulPackedVNNI, then act(gate)*up as the model
   loops compute it (qwen3.go:530-539, gemma3.go:365-374). Full int8 is
-  compared element-wise (the int32 accumulators and dequantization are exact;
-  only the float64 exp/tanh of the two libraries may differ in their last
-  bit before the float32 rounding); fp32 and weight-only int8 within the
-  GEMM tolerances.
+  compared element-wise within 1e-6 relative (the int32 accumulators and
+  dequantization are exact; the device evaluates SiLU / GELUTanh in float32,
+  a few ulp from the reference's float64-then-rounded values); fp32 and
+  weight-only int8 within the GEMM tolerances.
 * Qwen3- and EmbeddingGemma-shaped models at full width (hidden 1024 /
   16 Q, 8 KV heads of 128; hidden 768 / 3 Q, 1 KV head of 256, window 257,
   Dense 3072), two layers: fp32 embeddings within 1e-4 of the oracle,
