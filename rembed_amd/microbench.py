@@ -5,6 +5,7 @@ tensor_test.go benchmarks), at the encoder's real shapes.
 Each case is timed with the library's per-launch HIP events on its own
 stream. Usage:
     python -m rembed_amd.microbench [--m 10102] [--iters 20] [--modes i8,w8,f32]
+    python -m rembed_amd.microbench --attention bert-base,qwen3-0.6b,gemma-global
 """
 import argparse
 import json
@@ -80,6 +81,68 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
             "gbps": round(st["total_bytes"] / (st["total_ms"] * 1e-3) / 1e9, 1)}
 
 
+ATTN_CASES = {
+    # name: (dh, heads, kv_heads, causal, window, texts, length)
+    "bert-base": (64, 12, 12, False, 0, 64, None),     # lengths U[64,256]
+    "qwen3-0.6b": (128, 16, 8, True, 0, 32, 512),
+    "gemma-global": (256, 3, 1, False, 0, 16, 2048),
+    "gemma-local": (256, 3, 1, False, 512, 16, 2048),
+}
+
+
+def bench_attention(ctx, name, iters, kernels):
+    """rh_attention at a workload's shape on random bf16-representable
+    q|k|v rows; `kernels`: "bf16" (bf16 rows, the pipelined kernel) and/or
+    "f32" (the same values as fp32 rows at precision 1)."""
+    dh, heads, kv, causal, window, texts, length = ATTN_CASES[name]
+    rng = np.random.default_rng(2)
+    lens = (rng.integers(64, 257, texts) if length is None else np.full(texts, length))
+    lens = lens.astype(np.int32)
+    M, ld = int(lens.sum()), (heads + 2 * kv) * dh
+    x = (rng.standard_normal((M, ld)) * 0.5).astype(np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    bufs = {"bf16": (ctx.upload(bits), 1),
+            "f32": (ctx.upload((bits.astype(np.uint32) << 16).view(np.float32)), 0)}
+    cu = ctx.upload(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32))
+    out = ctx.alloc(M * heads * dh * 4)
+    pairs = 0.0
+    for L in lens.tolist():
+        i = np.arange(L)
+        hi = np.full(L, L - 1)
+        lo = np.zeros(L, np.int64)
+        if causal:
+            hi = np.minimum(hi, i)
+        if window:
+            hi = np.minimum(hi, i + window - 1)
+            lo = np.maximum(lo, i - window + 1)
+        pairs += float(np.sum(hi - lo + 1))
+    flops = 4.0 * pairs * dh * heads
+    res = []
+    for kern in kernels:
+        buf, in_bf16 = bufs[kern]
+
+        def run():
+            T.Attention(ctx, out, heads * dh, buf, in_bf16, ld, 0, heads * dh, (heads + kv) * dh,
+                        cu, texts, int(lens.max()), heads, kv, dh, 1.0 / np.sqrt(dh), causal,
+                        window, 1)
+        for _ in range(3):
+            run()
+        ctx.sync()
+        ctx.profile(True)
+        for _ in range(iters):
+            run()
+        ctx.sync()
+        st = ctx.profile_read(3)
+        ctx.profile(False)
+        us = st["total_ms"] * 1e3 / st["launches"]
+        res.append({"attention": name, "kernel": kern, "dh": dh, "heads": heads, "kv_heads": kv,
+                    "causal": causal, "window": window, "tokens": M, "us": round(us, 1),
+                    "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                    "frac": round(flops / (us * 1e-6) / 1e12 / PEAK["w8"], 4)})
+    return res
+
+
 def copy_calibration(mib, iters):
     """A device-to-device copy of `mib` MiB through torch's elementwise copy
     kernel: each launch reads and writes exactly mib MiB, so a profiler's
@@ -108,12 +171,23 @@ def main():
     ap.add_argument("--w8-terms", type=int, default=1, help="bf16 activation terms of w8 (1 or 2)")
     ap.add_argument("--bf", default="0", help="w8/f32 GEMM algorithms: 0 = bf16 planes, "
                                               "1 = split in the main loop (comma list)")
+    ap.add_argument("--attention", default="",
+                    help="only time rh_attention at these shapes (comma list of "
+                         + ",".join(ATTN_CASES) + ")")
+    ap.add_argument("--attn-kernels", default="bf16", help="bf16 and/or f32 (comma list)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
     args = ap.parse_args()
     if args.copy_mib:
         return copy_calibration(args.copy_mib, args.iters)
+    if args.attention:
+        ctx = T.Context(0)
+        for name in args.attention.split(","):
+            for r in bench_attention(ctx, name, args.iters, args.attn_kernels.split(",")):
+                print(json.dumps(r), flush=True)
+        ctx.close()
+        return 0
     shapes = BERT_SHAPES
     if args.shapes:
         shapes = [tuple(int(x) for x in s.split(",")) for s in args.shapes.split(";")]
