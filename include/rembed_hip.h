@@ -62,12 +62,17 @@ void *rh_context_stream(rh_context *ctx);
  *                    (default), 2 = bf16 hi + lo split (fp32-grade a)
  *   RH_CTX_I8_TILE   int8 GEMM tile: 0 = automatic, 1 = 256x256, 2 = 256x128,
  *                    3 = 128x128 (four stages), 4 = 256x128, 5 = 128x256
- *                    (three stages, two workgroups per CU)
+ *                    (three stages, two workgroups per CU), 6 = 256x256,
+ *                    7 = 128x256 (eight waves), 8 = 256x256, 9 = 128x256
+ *                    (eight waves, two 128-byte k stages)
  *   RH_CTX_BF_ALGO   weight-only int8 / fp32 GEMMs: 0 = activations split
  *                    once into bf16 hi/lo planes and weights stored as bf16
  *                    planes (default), 1 = split inside the GEMM's main loop
  *   RH_CTX_BF_TILE   tile of the bf16-planes GEMM: 0 = automatic, 1 = 256x256,
- *                    2 = 256x128, 3 = 128x128
+ *                    2 = 256x128, 3 = 128x128, 4 = 256x256, 5 = 256x128
+ *                    (eight waves), 6 = 256x256, 7 = 256x128 (eight waves,
+ *                    128-byte k stages; one-term weight-only int8 only, the
+ *                    other products take 3)
  *   RH_CTX_TILE_GROUP  GEMM tile order: consecutive workgroups walk this many
  *                    row blocks down a column block (1 = row-major; default 4) */
 #define RH_CTX_F32_ALGO 1

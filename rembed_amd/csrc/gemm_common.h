@@ -48,6 +48,22 @@ __device__ __forceinline__ int i8_slot(int row, int chunk) {
   return (row << 2) + (chunk ^ (((row >> 1) ^ (row >> 3)) & 3));
 }
 
+// LDS layout of a stage row of RB bytes (64: i8_slot, 128: lds_off): the
+// byte offset of logical 16-byte chunk c of row r, and the inverse the DMA
+// needs (the logical chunk that belongs at physical slot pc of row r). Both
+// permutations are involutions on the chunk index.
+template <int RB>
+__device__ __forceinline__ int stage_frag_off(int r, int c) {
+  static_assert(RB == 64 || RB == 128, "row bytes");
+  if constexpr (RB == 64) return i8_slot(r, c) * 16;
+  else return lds_off(r, c);
+}
+template <int RB>
+__device__ __forceinline__ int stage_slot_chunk(int r, int pc) {
+  if constexpr (RB == 64) return pc ^ (((r >> 1) ^ (r >> 3)) & 3);
+  else return pc ^ ((r ^ (r >> 3)) & 7);
+}
+
 // 16-byte global -> LDS copy (global_load_lds_dwordx4). The builtin exists
 // only for the device target; the host pass of the kernel template must
 // still see a valid body to emit its launch stub.

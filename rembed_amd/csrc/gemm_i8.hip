@@ -35,10 +35,12 @@ __device__ __forceinline__ uint32_t quant_byte(float v, float inv) {
 
 // WGN waves along N: 2 = a 2x2 grid of 4 waves, 4 = a 2x4 grid of 8 (two per
 // SIMD when one workgroup fills a CU).
-template <int BM, int BN, int NS, int EPI, int WGN = 2>
+// BK: k bytes per stage and row, 64 (i8_slot rows) or 128 (lds_off rows;
+// half the barriers, four k-steps per stage).
+template <int BM, int BN, int NS, int EPI, int WGN = 2, int BK = 64>
 __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
   constexpr int NT = 128 * WGN, NW = 2 * WGN;
-  constexpr int BK = 64;
+  constexpr int CPR = BK / 16;  // 16-byte chunks per row
   constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int kA = BM * BK, kB = BN * BK, kStage = kA + kB;
@@ -71,8 +73,8 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
 #pragma unroll
   for (int j = 0; j < LA; j++) {
     const int slot = (wave * LA + j) * 64 + lane;
-    const int r = slot >> 2;
-    achunk[j] = (slot & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);  // inverse of i8_slot
+    const int r = slot / CPR;
+    achunk[j] = stage_slot_chunk<BK>(r, slot % CPR);
     const int gr = row0 + r;
     asrc[j] = p.A + (size_t)(gr < p.M ? gr : p.M - 1) * p.lda;
   }
@@ -81,8 +83,8 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
 #pragma unroll
   for (int j = 0; j < LB; j++) {
     const int slot = (wave * LB + j) * 64 + lane;
-    const int r = slot >> 2;
-    bchunk[j] = (slot & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);
+    const int r = slot / CPR;
+    bchunk[j] = stage_slot_chunk<BK>(r, slot % CPR);
     bsrc[j] = p.B + (size_t)(col0 + r) * p.ldb;
   }
 
@@ -133,12 +135,12 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
 #pragma unroll
       for (int i = 0; i < TM; i++) {
         const int r = wm * WM + i * 32 + fr;
-        fa[i] = *reinterpret_cast<const v4i*>(sA + i8_slot(r, c) * 16) ^ (int)0x80808080;
+        fa[i] = *reinterpret_cast<const v4i*>(sA + stage_frag_off<BK>(r, c)) ^ (int)0x80808080;
       }
 #pragma unroll
       for (int j = 0; j < TN; j++) {
         const int r = wn * WN + j * 32 + fr;
-        fb[j] = *reinterpret_cast<const v4i*>(sB + i8_slot(r, c) * 16);
+        fb[j] = *reinterpret_cast<const v4i*>(sB + stage_frag_off<BK>(r, c));
       }
 #pragma unroll
       for (int i = 0; i < TM; i++)
@@ -302,10 +304,11 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
   }
 }
 
-template <int BM, int BN, int NS, int EPI, int WGN = 2>
+template <int BM, int BN, int NS, int EPI, int WGN = 2, int BK = 64>
 static hipError_t launch_tile(const GemmI8Args& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
-  timed_launch((gemm_i8_kernel<BM, BN, NS, EPI, WGN>), dim3(tiles), dim3(128 * WGN), 0, s, a);
+  timed_launch((gemm_i8_kernel<BM, BN, NS, EPI, WGN, BK>), dim3(tiles), dim3(128 * WGN), 0, s,
+               a);
   return hipGetLastError();
 }
 
@@ -322,24 +325,28 @@ static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
     case 5: return launch_tile<128, 256, 3, EPI>(a, s);
     case 6: return launch_tile<256, 256, 4, EPI, 4>(a, s);
     case 7: return launch_tile<128, 256, 3, EPI, 4>(a, s);
+    case 8: return launch_tile<256, 256, 2, EPI, 4, 128>(a, s);
+    case 9: return launch_tile<128, 256, 2, EPI, 4, 128>(a, s);
     default: return launch_tile<128, 128, 4, EPI>(a, s);
   }
 }
 
 // Automatic tile, measured on MI355X over the BERT-base linears at M = 10102
-// and 16384: 256x256 with 8 waves for the
-// widest outputs (N >= 3072), else 128x256 with 8 waves (two workgroups
-// and four waves per SIMD per CU). Small problems keep 128x128 so the grid
-// still covers the CUs.
-int pick_i8_tile(int M, int N, int epi) {
+// and 16384: 256x256 with 8 waves for the widest outputs (N >= 3072), else
+// 128x256 with 8 waves (two workgroups and four waves per SIMD per CU), or
+// for deep K (3072) its 128-byte-stage form, whose halved barrier count
+// outweighs the single workgroup per CU. Small problems keep 128x128 so the
+// grid still covers the CUs.
+int pick_i8_tile(int M, int N, int K, int epi) {
   (void)epi;
   if (ceil_div(M, 128) * ceil_div(N, 256) < 128) return 3;
-  return N >= 3072 ? 6 : 7;
+  if (N >= 3072) return 6;
+  return K >= 2048 ? 9 : 7;
 }
 
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (tile <= 0 || tile > kI8TileConfigs) tile = pick_i8_tile(a.M, a.N, a.epi);
+  if (tile <= 0 || tile > kI8TileConfigs) tile = pick_i8_tile(a.M, a.N, a.K, a.epi);
   switch (a.epi) {
     case EPI_F32: return launch_epi<EPI_F32>(a, tile, s);
     case EPI_BF16: return launch_epi<EPI_BF16>(a, tile, s);

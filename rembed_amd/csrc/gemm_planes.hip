@@ -32,11 +32,14 @@ namespace rh {
 
 // WGN waves along N (2: a 2x2 grid of 4 waves; 4: a 2x4 grid of 8 waves, two
 // per SIMD, so one wave's LDS waits overlap the other's MFMAs).
-template <int BM, int BN, int NS, int AT, int BT, bool GLU, int WGN = 2>
+// BK: k elements per stage and row, 32 (64-byte rows, i8_slot permutation)
+// or 64 (128-byte rows, lds_off permutation; half the barriers).
+template <int BM, int BN, int NS, int AT, int BT, bool GLU, int WGN = 2, int BK = 32>
 __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
   constexpr int NT = 128 * WGN;  // threads
   constexpr int NW = 2 * WGN;    // waves
-  constexpr int BK = 32;  // bf16 elements per stage and row
+  constexpr int CPR = BK / 8;    // 16-byte chunks per row
+  static_assert(BK == 32 || BK == 64, "stage depth");
   constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int kA = BM * BK * 2, kB = BN * BK * 2;  // bytes per plane
@@ -45,7 +48,9 @@ __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
   constexpr int kLoads = AT * LA + BT * LB;
   constexpr int kEpiStride = WN + 4;  // floats per row of the epilogue transpose
   static_assert(LA >= 1 && LB >= 1 && TN >= 1, "tile too small for the wave grid");
-  static_assert(NS >= 3, "one barrier per stage needs a ring of >= 3");
+  // A stage's slot is refilled right after the barrier that follows the
+  // last reads of it, so two slots suffice (one stage in flight).
+  static_assert(NS >= 2, "ring");
   static_assert(NS * kStage <= 160 * 1024, "LDS");
   static_assert(NS * kStage >= NW * 32 * kEpiStride * 4, "epilogue LDS");
   static_assert((NS - 2) * kLoads < 64, "vmcnt range");
@@ -71,16 +76,16 @@ __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
 #pragma unroll
   for (int j = 0; j < LA; j++) {
     const int slot = (wave * LA + j) * 64 + lane;
-    const int r = slot >> 2;
-    const int chunk = (slot & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);  // inverse of i8_slot
+    const int r = slot / CPR;
+    const int chunk = stage_slot_chunk<BK * 2>(r, slot % CPR);
     const int gr = row0 + r;
     aoff[j] = (gr < p.M ? gr : p.M - 1) * p.lda + chunk * 8;
   }
 #pragma unroll
   for (int j = 0; j < LB; j++) {
     const int slot = (wave * LB + j) * 64 + lane;
-    const int r = slot >> 2;
-    const int chunk = (slot & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);
+    const int r = slot / CPR;
+    const int chunk = stage_slot_chunk<BK * 2>(r, slot % CPR);
     boff[j] = (col0 + r) * p.ldb + chunk * 8;
   }
 
@@ -133,13 +138,13 @@ __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
       v8bf fah[TM], fal[TM], fbh[TN], fbl[TN];
 #pragma unroll
       for (int i = 0; i < TM; i++) {
-        const int off = i8_slot(wm * WM + i * 32 + fr, c) * 16;
+        const int off = stage_frag_off<BK * 2>(wm * WM + i * 32 + fr, c);
         fah[i] = *reinterpret_cast<const v8bf*>(sA + off);
         if constexpr (AT == 2) fal[i] = *reinterpret_cast<const v8bf*>(sA + kA + off);
       }
 #pragma unroll
       for (int j = 0; j < TN; j++) {
-        const int off = i8_slot(wn * WN + j * 32 + fr, c) * 16;
+        const int off = stage_frag_off<BK * 2>(wn * WN + j * 32 + fr, c);
         fbh[j] = *reinterpret_cast<const v8bf*>(sB + off);
         if constexpr (BT == 2) fbl[j] = *reinterpret_cast<const v8bf*>(sB + kB + off);
       }
@@ -294,14 +299,14 @@ hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi
   return hipGetLastError();
 }
 
-template <int BM, int BN, int NS, int AT, int BT, int WGN = 2>
+template <int BM, int BN, int NS, int AT, int BT, int WGN = 2, int BK = 32>
 static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
   const int tiles = ceil_div(a.M, BM) * ceil_div(a.N, BN);
   if (is_glu(a.act))
-    timed_launch((gemm_planes_kernel<BM, BN, NS, AT, BT, true, WGN>), dim3(tiles),
+    timed_launch((gemm_planes_kernel<BM, BN, NS, AT, BT, true, WGN, BK>), dim3(tiles),
                  dim3(128 * WGN), 0, s, a);
   else
-    timed_launch((gemm_planes_kernel<BM, BN, NS, AT, BT, false, WGN>), dim3(tiles),
+    timed_launch((gemm_planes_kernel<BM, BN, NS, AT, BT, false, WGN, BK>), dim3(tiles),
                  dim3(128 * WGN), 0, s, a);
   return hipGetLastError();
 }
@@ -314,7 +319,8 @@ static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
 // MI355X at M = 16384 over the Qwen3/BERT linears: 8 waves 2-15% faster
 // than 4 at the same tile).
 int pick_planes_tile(int M, int N, int a_terms, int b_terms) {
-  if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256) return 4;
+  if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256)
+    return a_terms == 1 && b_terms == 1 ? 6 : 4;
   if (ceil_div(M, 256) * ceil_div(N, 128) >= 256) return 5;
   return 3;
 }
@@ -330,6 +336,8 @@ hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int
       case 2: return launch_pl<256, 128, 4, 1, 1>(a, s);
       case 4: return launch_pl<256, 256, 4, 1, 1, 4>(a, s);
       case 5: return launch_pl<256, 128, 4, 1, 1, 4>(a, s);
+      case 6: return launch_pl<256, 256, 2, 1, 1, 4, 64>(a, s);
+      case 7: return launch_pl<256, 128, 3, 1, 1, 4, 64>(a, s);
       default: return launch_pl<128, 128, 4, 1, 1>(a, s);
     }
   }

@@ -176,7 +176,7 @@ __device__ __forceinline__ void store_planes4(__bf16* hi, __bf16* lo, size_t off
 // past K): hi = bf16(x), lo = bf16(x - float(hi)), both rounded to nearest even
 hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi, __bf16* lo,
                              int ldk, hipStream_t s);
-constexpr int kPlanesTileConfigs = 5;
+constexpr int kPlanesTileConfigs = 7;
 hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int tile,
                               hipStream_t s);
 
@@ -185,10 +185,10 @@ hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int
 enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 
 // Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
-// tile: 0 = automatic, 1 = 256x256, 2 = 256x128, 3 = 128x128.
-constexpr int kI8TileConfigs = 7;
+// tile: 0 = automatic, else one of the configurations RH_CTX_I8_TILE lists.
+constexpr int kI8TileConfigs = 9;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
-int pick_i8_tile(int M, int N, int epi);
+int pick_i8_tile(int M, int N, int K, int epi);
 // fills n floats with zero (graph-capture safe, unlike hipMemsetAsync)
 hipError_t launch_fill_zero(float* x, int n, hipStream_t s);
 // a_terms: 1 or 2 bf16 terms for the fp32 activations.
