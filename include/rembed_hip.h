@@ -64,7 +64,8 @@ void *rh_context_stream(rh_context *ctx);
  *                    3 = 128x128 (four stages), 4 = 256x128, 5 = 128x256
  *                    (three stages, two workgroups per CU), 6 = 256x256,
  *                    7 = 128x256 (eight waves), 8 = 256x256, 9 = 128x256
- *                    (eight waves, two 128-byte k stages)
+ *                    (eight waves, two 128-byte k stages), 10 = 128x256
+ *                    (eight waves, three 128-byte k stages)
  *   RH_CTX_BF_ALGO   weight-only int8 / fp32 GEMMs: 0 = activations split
  *                    once into bf16 hi/lo planes and weights stored as bf16
  *                    planes (default), 1 = split inside the GEMM's main loop

@@ -365,36 +365,70 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
       lds_dma16(src, sK + (wave * kKLoads + j) * 1024);
     }
   };
-  // V: thread t < DH owns key group kgp = t / (DH/8) (16-key chunk kgp/2,
-  // lane half kgp%2) and d block db = t % (DH/8). Its 8 keys, in P^T order:
-  // key(e) = (kgp/2)*16 + (e/4)*8 + (kgp%2)*4 + e%4.
-  const bool vthr = tid < DH;
-  const int kgp = tid / (DH / 8), db = tid % (DH / 8);
-  v4i vx[8];
+  // V, two ways to the V^T block (same bytes):
+  // * DH < 256 (kPairs): work item w (of 32 key pairs x DH/8 d blocks,
+  //   spread over all threads) loads keys 2kp, 2kp+1 of d block db (two
+  //   16-byte row pieces) and writes them as 8 four-byte words of V^T, one
+  //   per d. In P^T order block-local key k sits in chunk 2(k/16) + (k/4)%2
+  //   at element ((k/8)%2)*4 + k%4, so the two keys of a pair share a word.
+  // * DH = 256: thread t owns key group kgp = t / (DH/8) (chunk kgp: 16-key
+  //   group kgp/2, lane half kgp%2) and d block db = t % (DH/8); its 8 keys,
+  //   in P^T order key(e) = (kgp/2)*16 + (e/4)*8 + (kgp%2)*4 + e%4, are
+  //   transposed 8x8 in registers and written as 16-byte V^T pieces (every
+  //   thread busy, a quarter of the LDS write instructions).
+  constexpr bool kPairs = DH < 256;
+  constexpr int kVItems = kPairs ? 32 * (DH / 8) : 256;
+  constexpr int kVPer = (kVItems + 255) / 256;
+  constexpr int kVRegs = kPairs ? 2 : 8;
+  v4i vx[kVPer][kVRegs];
   auto load_v = [&](int kb) {
-    if (!vthr) return;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const int key = kb * kAttnKV + (kgp >> 1) * 16 + (e >> 2) * 8 + (kgp & 1) * 4 + (e & 3);
-      vx[e] = *reinterpret_cast<const v4i*>(
-          vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 8);
+    for (int u = 0; u < kVPer; u++) {
+      const int w = tid + u * 256;
+      if (kVItems % 256 != 0 && w >= kVItems) break;
+      const int kg = w / (DH / 8), db = w % (DH / 8);
+#pragma unroll
+      for (int x = 0; x < kVRegs; x++) {
+        const int key = kb * kAttnKV +
+                        (kPairs ? 2 * kg + x : (kg >> 1) * 16 + (x >> 2) * 8 + (kg & 1) * 4 + (x & 3));
+        vx[u][x] = *reinterpret_cast<const v4i*>(
+            vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 8);
+      }
     }
   };
   auto write_vt = [&](int buf) {
-    if (!vthr) return;
     uint8_t* sV = lds + buf * kStage + kKB;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {  // d = db*8 + 2j (low halves) and 2j + 1 (high halves)
-      v4i lo, hi;
+    for (int u = 0; u < kVPer; u++) {
+      const int w = tid + u * 256;
+      if (kVItems % 256 != 0 && w >= kVItems) break;
+      const int kg = w / (DH / 8), db = w % (DH / 8);
+      if constexpr (kPairs) {
+        const int k = 2 * kg;  // even key of the pair (block-local)
+        const int chunk = 2 * (k >> 4) + ((k >> 2) & 1);
+        const int word = ((k >> 3) & 1) * 2 + ((k & 3) >> 1);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t a = (uint32_t)vx[2 * i][j], c = (uint32_t)vx[2 * i + 1][j];
-        lo[i] = (int)((a & 0xffffu) | (c << 16));
-        hi[i] = (int)((a >> 16) | (c & 0xffff0000u));
+        for (int e = 0; e < 8; e++) {
+          const uint32_t a = (uint32_t)vx[u][0][e >> 1], c = (uint32_t)vx[u][1][e >> 1];
+          const uint32_t pair =
+              (e & 1) ? ((a >> 16) | (c & 0xffff0000u)) : ((a & 0xffffu) | (c << 16));
+          *reinterpret_cast<uint32_t*>(sV + lds_off(db * 8 + e, chunk) + word * 4) = pair;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {  // d = db*8 + 2j (low halves) and 2j + 1 (high halves)
+          v4i lo, hi;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const uint32_t a = (uint32_t)vx[u][2 * i][j], c = (uint32_t)vx[u][2 * i + 1][j];
+            lo[i] = (int)((a & 0xffffu) | (c << 16));
+            hi[i] = (int)((a >> 16) | (c & 0xffff0000u));
+          }
+          const int d = db * 8 + 2 * j;
+          *reinterpret_cast<v4i*>(sV + lds_off(d, kg)) = lo;
+          *reinterpret_cast<v4i*>(sV + lds_off(d + 1, kg)) = hi;
+        }
       }
-      const int d = db * 8 + 2 * j;
-      *reinterpret_cast<v4i*>(sV + lds_off(d, kgp)) = lo;
-      *reinterpret_cast<v4i*>(sV + lds_off(d + 1, kgp)) = hi;
     }
   };
 
@@ -432,6 +466,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     const uint8_t* sV = sK + kKB;
     const int key0 = kb * kAttnKV;
 
+    // A wave whose queries all lie past the text only helps stage blocks.
+    if (q0 + wave * 32 < len) {
     // S^T for the two 32-key tiles, the two accumulation chains interleaved.
     v16f sc[2];
 #pragma unroll
@@ -474,6 +510,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
         const v8bf vf = *reinterpret_cast<const v8bf*>(sV + lds_off(t * 32 + fr, 2 * kc + fg));
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[t], 0, 0, 0);
       }
+    }
     }
 
     if (next) write_vt(buf ^ 1);

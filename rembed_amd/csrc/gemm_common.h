@@ -79,6 +79,18 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 3) << 14));
 }
+// s_waitcnt lgkmcnt(0) alone: this wave's LDS reads have returned.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14));
+}
+// Workgroup barrier that orders no memory by itself: no vmcnt/lgkmcnt wait
+// is attached (callers wait for exactly what they need), and the empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // erf-GELU with exactly the float32 operation sequence of the reference's
 // geluScalar (internal/tensor/tensor.go:508-538; exp body fastmath.go:93-109).

@@ -108,45 +108,71 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = v16i{};
 
-#pragma unroll
-  for (int st = 0; st < NS - 1; st++)
-    if (st < nk) issue(st);
-
+  // Fragments of one 32-byte k-step, double-buffered in registers: the LDS
+  // reads of step s+1 are in flight while the MFMAs of step s run, and at a
+  // stage's end the next stage's first reads go out right after its barrier.
+  constexpr int S = BK / 32;
+  static_assert(S % 2 == 0 && NS <= 4, "k-steps per stage / ring depth");
   const int fr = lane & 31, fg = lane >> 5;
-  for (int kt = 0; kt < nk; kt++) {
-    // Stage kt has landed once at most min(NS-2, nk-1-kt) later stages are
-    // still pending for this wave.
-    const int later = nk - 1 - kt;
+  v4i fa[2][TM], fb[2][TN];
+  auto load = [&](int kt, int s, v4i (&a)[TM], v4i (&b)[TN]) {
+    const uint8_t* sA = lds + (kt % NS) * kStage;
+    const uint8_t* sB = sA + kA;
+    const int c = 2 * s + fg;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+      a[i] = *reinterpret_cast<const v4i*>(sA + stage_frag_off<BK>(wm * WM + i * 32 + fr, c));
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+      b[j] = *reinterpret_cast<const v4i*>(sB + stage_frag_off<BK>(wn * WN + j * 32 + fr, c));
+  };
+  auto mma = [&](const v4i (&a)[TM], const v4i (&b)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const v4i ai = a[i] ^ (int)0x80808080;
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ai, b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  // This wave's DMA of stage `st` has landed once at most min(NS-2, later)
+  // younger stages are pending (later = stages issued after it).
+  auto wait_stage = [&](int later) {
     if (later >= NS - 2) wait_vmcnt<(NS - 2) * kLoads>();
     else if (NS > 3 && later == 1) wait_vmcnt<kLoads>();
     else wait_vmcnt<0>();
-    // A bare s_barrier: __syncthreads() would add a release fence that waits
-    // for every outstanding load (vmcnt(0)), draining the ring each stage.
-    // This wave's stage-kt data is in LDS (vmcnt above); its reads of the
-    // previous stage have completed (their MFMAs consumed them).
-    __builtin_amdgcn_s_barrier();
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
-    const uint8_t* sA = lds + (kt % NS) * kStage;
-    const uint8_t* sB = sA + kA;
+  };
+
 #pragma unroll
-    for (int s = 0; s < BK / 32; s++) {
-      const int c = 2 * s + fg;
-      v4i fa[TM], fb[TN];
+  for (int st = 0; st < NS - 1; st++)
+    if (st < nk) issue(st);
+  wait_stage(nk - 1);
+  stage_barrier();
+  if (NS - 1 < nk) issue(NS - 1);
+  load(0, 0, fa[0], fb[0]);
+
+  for (int kt = 0; kt < nk; kt++) {
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const int r = wm * WM + i * 32 + fr;
-        fa[i] = *reinterpret_cast<const v4i*>(sA + stage_frag_off<BK>(r, c)) ^ (int)0x80808080;
+    for (int s = 0; s < S; s++) {
+      if (s + 1 < S) {
+        load(kt, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+      } else {
+        // The last step's fragments have returned (on every path, so the
+        // MFMAs below need no wait that would also cover the next stage's
+        // reads). Slot kt % NS is refilled after the barrier, which is safe
+        // once every wave is past this point; stage kt+1 must have landed
+        // for every wave.
+        wait_lgkmcnt0();
       }
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int r = wn * WN + j * 32 + fr;
-        fb[j] = *reinterpret_cast<const v4i*>(sB + stage_frag_off<BK>(r, c));
+      if (s + 1 == S && kt + 1 < nk) {
+        wait_stage(nk - 2 - kt);
+        stage_barrier();
+        if (kt + NS < nk) issue(kt + NS);
+        load(kt + 1, 0, fa[0], fb[0]);
       }
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      mma(fa[s & 1], fb[s & 1]);
+      // keep each step's MFMAs ahead of the next step's waits
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -327,21 +353,23 @@ static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
     case 7: return launch_tile<128, 256, 3, EPI, 4>(a, s);
     case 8: return launch_tile<256, 256, 2, EPI, 4, 128>(a, s);
     case 9: return launch_tile<128, 256, 2, EPI, 4, 128>(a, s);
+    case 10: return launch_tile<128, 256, 3, EPI, 4, 128>(a, s);
     default: return launch_tile<128, 128, 4, EPI>(a, s);
   }
 }
 
 // Automatic tile, measured on MI355X over the BERT-base linears at M = 10102
-// and 16384: 256x256 with 8 waves for the widest outputs (N >= 3072), else
-// 128x256 with 8 waves (two workgroups and four waves per SIMD per CU), or
-// for deep K (3072) its 128-byte-stage form, whose halved barrier count
-// outweighs the single workgroup per CU. Small problems keep 128x128 so the
-// grid still covers the CUs.
+// and 16384: 128x256 with 8 waves (two workgroups and four waves per SIMD
+// per CU; ahead of 256x256 by 7-12% at N = 3072), or its 128-byte-stage
+// form where that occupancy cannot be had or does not pay: a grid of at
+// most one workgroup per CU (N = 768 at M = 10102) or deep K (3072), where
+// the halved barrier count wins. Small problems keep 128x128 so the grid
+// still covers the CUs.
 int pick_i8_tile(int M, int N, int K, int epi) {
   (void)epi;
-  if (ceil_div(M, 128) * ceil_div(N, 256) < 128) return 3;
-  if (N >= 3072) return 6;
-  return K >= 2048 ? 9 : 7;
+  const int tiles = ceil_div(M, 128) * ceil_div(N, 256);
+  if (tiles < 128) return 3;
+  return (K >= 2048 || tiles <= 256) ? 9 : 7;
 }
 
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s) {

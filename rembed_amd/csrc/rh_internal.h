@@ -186,7 +186,7 @@ enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 
 // Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
 // tile: 0 = automatic, else one of the configurations RH_CTX_I8_TILE lists.
-constexpr int kI8TileConfigs = 9;
+constexpr int kI8TileConfigs = 10;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
 int pick_i8_tile(int M, int N, int K, int epi);
 // fills n floats with zero (graph-capture safe, unlike hipMemsetAsync)
