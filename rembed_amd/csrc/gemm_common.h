@@ -125,14 +125,29 @@ __device__ __forceinline__ float gelu_ref(float v) {
   return 0.5f * v * (1.0f + erf);
 }
 
+// 1/d rounded to nearest for finite d >= 1: the hardware reciprocal (within
+// 1 ulp) and one Newton step with fused multiply-adds. Over every float
+// input of gelu_avx2 below (all 2^32 bit patterns) this gives the same
+// results as the IEEE division sequence (v_div_scale/fmas/fixup), whose
+// operand scaling and special-case fixups never act for such d; the caller
+// keeps d finite.
+__device__ __forceinline__ float recip_ge1(float d) {
+  const float r = __builtin_amdgcn_rcpf(d);
+  return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+}
+
 // erf-GELU as rembed computes it on amd64 for every whole 8-lane group of a
 // row (geluAVX2, internal/tensor/gelu_amd64.s:37-123): geluScalar's
 // constants with fused multiply-adds exactly where the assembly fuses them,
-// an IEEE division for t and trunc-toward-zero exponent rounding.
+// a correctly rounded reciprocal for t and trunc-toward-zero exponent
+// rounding. |a| enters the reciprocal clamped to FLT_MAX (a = ±inf would
+// make the Newton step NaN); past |a| ~ 4 the product poly·e is below half
+// an ulp of 1, so erf is ±1 either way. 2^n scales by ldexp, which equals
+// the multiplication by the power of two for every n the clamp allows.
 __device__ __forceinline__ float gelu_avx2(float v) {
   const float a = v * 0.7071067811865476f;
   const float aa = fabsf(a);
-  const float t = 1.0f / __builtin_fmaf(0.3275911f, aa, 1.0f);
+  const float t = recip_ge1(__builtin_fmaf(0.3275911f, fminf(aa, 3.40282347e38f), 1.0f));
   float h = 1.061405429f;
   h = __builtin_fmaf(h, t, -1.453152027f);
   h = __builtin_fmaf(h, t, 1.421413741f);
@@ -141,8 +156,7 @@ __device__ __forceinline__ float gelu_avx2(float v) {
   const float poly = h * t;
   float xe = -(aa * aa);
   if (xe < -87.33f) xe = -87.33f;
-  const int nfi = (int)__builtin_fmaf(1.44269504088896341f, xe, -0.5f);
-  const float nf = (float)nfi;
+  const float nf = __builtin_truncf(__builtin_fmaf(1.44269504088896341f, xe, -0.5f));
   xe = __builtin_fmaf(-0.693359375f, nf, xe);
   xe = __builtin_fmaf(2.12194440e-4f, nf, xe);
   const float z = xe * xe;
@@ -154,7 +168,7 @@ __device__ __forceinline__ float gelu_avx2(float v) {
   y = __builtin_fmaf(y, xe, 5.0000001201e-1f);
   y = __builtin_fmaf(y, z, xe);
   y = y + 1.0f;
-  const float e = y * __int_as_float((nfi + 127) << 23);
+  const float e = __builtin_amdgcn_ldexpf(y, (int)nf);
   const float val = __builtin_fmaf(-poly, e, 1.0f);
   // the sign bit of a is xor-ed into val (covers a == -0 as well)
   const float erf = __int_as_float(__float_as_int(val) ^ (__float_as_int(a) & 0x80000000));

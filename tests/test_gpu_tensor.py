@@ -332,6 +332,30 @@ def test_gelu_bit_exact(gpu_ctx):
     assert np.array_equal(d.download(np.float32, xs.shape), O.gelu_ref(xs))
 
 
+def test_gelu_bit_exact_across_float32(gpu_ctx):
+    """erf-GELU over every 61st bit pattern of float32 (70M inputs: both
+    signs, subnormals, the whole exponent range, ±inf and NaNs) equals the
+    oracle's geluAVX2/geluScalar bit for bit (NaN results compare as NaN).
+    The kernel takes t = 1/d from the hardware reciprocal plus one Newton
+    step and 2^n by ldexp; this pins both against the reference's IEEE
+    division and power-of-two product far outside the activations' range."""
+    from rembed_amd._lib import check, lib
+    bits = np.arange(7, 1 << 32, 61, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0x7F800000, 0xFF800000, 0x7FC00000, 0x00000001, 0x80000001,
+                         0x007FFFFF, 0x00800000, 0x7F7FFFFF, 0xFF7FFFFF, 0, 0x80000000],
+                        np.uint32)
+    xs = np.concatenate([specials, bits]).view(np.float32)
+    say(f"gelu over {xs.size} inputs")
+    d = gpu_ctx.upload(xs)
+    check(lib.rh_gelu(gpu_ctx.h, d.ptr, xs.size))
+    gpu_ctx.sync()
+    got = d.download(np.float32, xs.shape)
+    want = O.gelu_ref(xs)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    bad = np.flatnonzero(~same)
+    assert bad.size == 0, f"{bad.size} mismatches, first inputs {xs[bad[:5]].view(np.uint32)}"
+
+
 def test_layernorm_matches_oracle(gpu_ctx):
     from rembed_amd._lib import check, lib
     rng = np.random.default_rng(3)
