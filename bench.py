@@ -106,6 +106,9 @@ def main():
     ap.add_argument("--ffn1", choices=["fused", "split"], default="split",
                     help="full-int8 FFN1: fused = GELU rows re-quantized inside the GEMM "
                          "(two passes, no fp32 intermediate); split = fp32 rows + QuantizeRowU8")
+    ap.add_argument("--streams", type=int, choices=[1, 2, 3, 4], default=2,
+                    help="full-int8 encoders: run a batch as this many parts of whole texts on as many streams "
+                         "(default 2); the roofline pass always runs one stream")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: the library has no multi-GPU path; texts "
@@ -127,6 +130,7 @@ def main():
 
     ctx = T.Context(0)
     model = Model(ctx, shape, tensors, quant)
+    model.set_streams(args.streams)
     if quant == 2:
         assert model.quantized_activations(), "full-int8 path did not take"
         model.set_fused_ffn1(args.ffn1 == "fused")
@@ -154,7 +158,10 @@ def main():
     # The roofline: the same K steps again with a HIP event pair attached to
     # every GEMM / attention / split dispatch (the library's profiler, on
     # the stream the kernels run on). The events cost a few µs per launch,
-    # so these steps are timed apart from `value`.
+    # so these steps are timed apart from `value`, and on one stream: with
+    # two, the parts' kernels overlap and each launch's duration would count
+    # time the GPU spent on the other part.
+    model.set_streams(1)
     ctx.profile(True)
     ctx.sync()
     t1 = time.perf_counter()
@@ -167,6 +174,7 @@ def main():
     attn = ctx.profile_read(3)
     split = ctx.profile_read(4)  # bf16 split of the W8/fp32 GEMMs' activations
     ctx.profile(False)
+    model.set_streams(args.streams)
 
     ms_per_step = elapsed * 1e3 / args.steps
     value = tokens * args.steps / elapsed
@@ -190,7 +198,7 @@ def main():
     vec = out_dev.download(np.float32, (BATCH, shape.hidden))
     assert np.array_equal(vec, host_vec), "host-buffer and device-resident forwards differ"
     if quant == 2:
-        cfg_note = {"ffn1": args.ffn1}
+        cfg_note = {"ffn1": args.ffn1, "streams": args.streams}
     else:
         cfg_note = {}
     norms = np.linalg.norm(vec.astype(np.float64), axis=1)

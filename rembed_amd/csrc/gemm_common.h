@@ -154,8 +154,9 @@ __device__ __forceinline__ float gelu_avx2(float v) {
   h = __builtin_fmaf(h, t, -0.284496736f);
   h = __builtin_fmaf(h, t, 0.254829592f);
   const float poly = h * t;
-  float xe = -(aa * aa);
-  if (xe < -87.33f) xe = -87.33f;
+  // fmaxf instead of the reference's compare-and-set: the same value except
+  // for a NaN input, whose result is NaN either way
+  float xe = fmaxf(-(aa * aa), -87.33f);
   const float nf = __builtin_truncf(__builtin_fmaf(1.44269504088896341f, xe, -0.5f));
   xe = __builtin_fmaf(-0.693359375f, nf, xe);
   xe = __builtin_fmaf(2.12194440e-4f, nf, xe);

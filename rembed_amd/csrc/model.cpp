@@ -79,6 +79,12 @@ struct rh_model {
   int attn_precision = 3;
   bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
   bool producer_planes = true;  // RH_OPT_PRODUCER_PLANES
+  int streams = 2;              // RH_OPT_STREAMS
+  // extra streams (default priority) and the fork/join events of a forward
+  // split into parts
+  static constexpr int kMaxParts = 4;
+  hipStream_t sx[kMaxParts] = {};
+  hipEvent_t ev_fork = nullptr, ev_join[kMaxParts] = {};
 
   // workspace, sized for cap rows / cap_batch texts
   int cap = 0, cap_batch = 0, cap_ids = 0;
@@ -121,6 +127,19 @@ struct rh_model {
       (void)hipSetDevice(ctx->device);
       (void)hipStreamSynchronize(ctx->stream);
     }
+    for (hipStream_t& q : sx)
+      if (q) {
+        (void)hipStreamSynchronize(q);
+        (void)hipStreamDestroy(q);
+        q = nullptr;
+      }
+    if (ev_fork) (void)hipEventDestroy(ev_fork);
+    ev_fork = nullptr;
+    for (hipEvent_t& e : ev_join)
+      if (e) {
+        (void)hipEventDestroy(e);
+        e = nullptr;
+      }
     release_ws();
     for (auto& L : layers) {
       for (rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) {
@@ -338,48 +357,112 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
   ea.err_flag = err_d;
   RH_HIP(launch_embed_layernorm(ea, M, s));
 
-  double attn_ops = 0;
-  for (int b = 0; b < batch; b++) {
-    const double L = cu[b + 1] - cu[b];
-    attn_ops += 4.0 * L * L * dh * heads;
+  // The layer stack runs over one part (all texts) or `streams` parts of
+  // whole texts on as many streams: the parts' kernels share the GPU, so one
+  // part's GEMMs (MFMA/LDS-bound) overlap another's row kernels
+  // (VALU/HBM-bound). Every buffer is indexed by packed row (cu_d by text),
+  // so a part only offsets its pointers; a part's results equal the
+  // one-part forward's rows. Several parts need every linear on the int8
+  // GEMM (the bf16-planes path shares the context's split workspace).
+  struct Part {
+    int row0, rows, b0, nb, max_len;
+    double attn_ops;
+    hipStream_t s;
+  };
+  bool all_i8 = true;
+  for (const Layer& L : layers)
+    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) all_i8 = all_i8 && needs_q(w);
+  auto make_part = [&](int b0, int b1, hipStream_t ps) {
+    Part p{cu[b0], cu[b1] - cu[b0], b0, b1 - b0, 0, 0.0, ps};
+    for (int b = b0; b < b1; b++) {
+      const int L = cu[b + 1] - cu[b];
+      p.max_len = std::max(p.max_len, L);
+      p.attn_ops += 4.0 * L * L * dh * heads;
+    }
+    return p;
+  };
+  // Part boundaries: the text whose start is closest to each k·M/n (whole
+  // texts, at least one per part); at least 1024 rows per part.
+  int np = 1;
+  if (streams > 1 && all_i8) np = std::max(1, std::min({streams, batch, M / 1024}));
+  std::vector<int> bounds{0};
+  for (int k = 1; k < np; k++) {
+    const long target = (long)M * k / np;
+    int best = bounds.back() + 1;
+    for (int b = best; b <= batch - (np - k); b++)
+      if (std::labs(cu[b] - target) < std::labs(cu[best] - target)) best = b;
+    bounds.push_back(best);
+  }
+  bounds.push_back(batch);
+  std::vector<Part> parts;
+  if (np > 1) {
+    if (!ev_fork) RH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+    RH_HIP(hipEventRecord(ev_fork, s));
+  }
+  for (int k = 0; k < np; k++) {
+    hipStream_t ps = s;
+    if (k > 0) {
+      if (!sx[k]) RH_HIP(hipStreamCreate(&sx[k]));
+      if (!ev_join[k]) RH_HIP(hipEventCreateWithFlags(&ev_join[k], hipEventDisableTiming));
+      RH_HIP(hipStreamWaitEvent(sx[k], ev_fork, 0));
+      ps = sx[k];
+    }
+    parts.push_back(make_part(bounds[k], bounds[k + 1], ps));
   }
 
-  const double MH = M;
   // p0 holds planes of x for the next QKV when the previous layer's
   // residual+LN wrote them (layer 0 splits the embeddings' x itself).
   bool x_planes = false;
-  for (size_t li = 0; li < layers.size(); li++) {
+  auto layer = [&](size_t li, const Part& P) -> int {
     const Layer& L = layers[li];
+    const hipStream_t ps = P.s;
+    const int Mp = P.rows;
+    const double MH = Mp;
+    const size_t r0 = P.row0;
+    float* xp = x + r0 * H;
+    float* yp = y + r0 * H;
+    float* hidp = hid + r0 * I;
+    float* ctxp = ctxb + r0 * H;
+    uint8_t* qap = qa + r0 * ldq_for(H);
+    uint8_t* qa2p = qa2 + r0 * ldq_for(I);
+    float* rsp = rs + r0;
+    float* rs2p = rs2 + r0;
+    auto at = [&](Planes p) {  // this part's rows of a planes buffer
+      if (p.hi) p.hi += r0 * p.ld;
+      if (p.lo) p.lo += r0 * p.ld;
+      return p;
+    };
+    int st;
     // QKV projection. x was quantized into qa/rs by the producer if the
     // weight is full-int8. When attention runs on bf16 operands, a full-int8
     // QKV writes bf16 directly (attention would round the fp32 values to the
     // same bf16 on load), halving the write.
     const bool qkv_bf16 = needs_q(L.qkv) && attn_precision == 1;
     if (qkv_bf16) {
-      st = run_gemm_i8(ctx, L.qkv, qa, ldq_for(H), rs, M, EPI_BF16, qkvh, 3 * H, ACT_NONE,
-                       L.qkv->d_bias, nullptr, nullptr, 2.0 * MH * H * 3 * H);
+      st = run_gemm_i8(ctx, L.qkv, qap, ldq_for(H), rsp, Mp, EPI_BF16, qkvh + r0 * 3 * H,
+                       3 * H, ACT_NONE, L.qkv->d_bias, nullptr, nullptr, 2.0 * MH * H * 3 * H);
     } else {
-      const Planes pq = plane(0, L.qkv);
-      st = run_linear(ctx, L.qkv, x, H, M, qkv, 3 * H, ACT_NONE, L.qkv->d_bias, qa,
-                      ldq_for(H), rs, false, x_planes ? &pq : nullptr);
+      const Planes pq = at(plane(0, L.qkv));
+      st = run_linear(ctx, L.qkv, xp, H, Mp, qkv + r0 * 3 * H, 3 * H, ACT_NONE, L.qkv->d_bias,
+                      qap, ldq_for(H), rsp, false, x_planes ? &pq : nullptr);
     }
     if (st) return st;
     AttnArgs aa{};
-    aa.qkv = qkv_bf16 ? (const void*)qkvh : (const void*)qkv;
+    aa.qkv = qkv_bf16 ? (const void*)qkvh : (const void*)qkv;  // rows are absolute (cu)
     aa.in_bf16 = qkv_bf16 ? 1 : 0;
     aa.ldqkv = 3 * H;
     aa.q_off = 0;
     aa.k_off = H;
     aa.v_off = 2 * H;
-    aa.cu = cu_d;
-    aa.batch = batch;
-    aa.max_len = max_len;
+    aa.cu = cu_d + P.b0;
+    aa.batch = P.nb;
+    aa.max_len = P.max_len;
     aa.heads = heads;
     aa.kv_heads = heads;
     aa.dh = dh;
     aa.scale = (float)(1.0 / std::sqrt((double)dh));
     // the attention output goes straight to the output projection's planes
-    // when it takes them
+    // when it takes them (absolute rows, like the q|k|v rows)
     const bool po = planes_in(L.o);
     const Planes pov = plane(0, L.o);
     aa.ctx = po ? nullptr : ctxb;
@@ -387,17 +470,18 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     aa.ctx_lo = po ? pov.lo : nullptr;
     aa.ldctx = po ? pov.ld : H;
     int slot = -1;
-    RH_HIP(ctx->prof_begin(3, attn_ops, 0.0, &slot));
-    RH_HIP(launch_attention(aa, attn_precision, s));
+    RH_HIP(ctx->prof_begin(3, P.attn_ops, 0.0, &slot));
+    RH_HIP(launch_attention(aa, attn_precision, ps));
     RH_HIP(ctx->prof_end(slot));
-    st = run_linear(ctx, L.o, ctxb, H, M, y, H, ACT_NONE, L.o->d_bias, qa, ldq_for(H),
-                    rs, needs_q(L.o) && !po, po ? &pov : nullptr);
+    const Planes povp = at(pov);
+    st = run_linear(ctx, L.o, ctxp, H, Mp, yp, H, ACT_NONE, L.o->d_bias, qap, ldq_for(H),
+                    rsp, needs_q(L.o) && !po, po ? &povp : nullptr);
     if (st) return st;
     const bool qf1 = needs_q(L.f1);
     const bool pf1 = planes_in(L.f1);
-    const Planes pf1v = plane(0, L.f1);
-    RH_HIP(launch_add_layernorm(x, y, H, L.ln1_g, L.ln1_b, M, H, eps(),
-                                qf1 ? qa : nullptr, ldq_for(H), qf1 ? rs : nullptr, s,
+    const Planes pf1v = at(plane(0, L.f1));
+    RH_HIP(launch_add_layernorm(xp, yp, H, L.ln1_g, L.ln1_b, Mp, H, eps(),
+                                qf1 ? qap : nullptr, ldq_for(H), qf1 ? rsp : nullptr, ps,
                                 pf1 ? pf1v.hi : nullptr, pf1 ? pf1v.lo : nullptr, pf1v.ld));
     if (fused_ffn1 && qf1 && needs_q(L.f2)) {
       // FFN1 + GELU + QuantizeRowU8 without the fp32 intermediate: pass 1
@@ -406,14 +490,15 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
       // Both passes see the same int32 accumulators, so the bytes equal
       // QuantizeRowU8 of the fp32 GELU row (bert.go:910-916).
       const double ops1 = 2.0 * MH * H * I;
-      RH_HIP(launch_fill_zero(absmax, M, s));
-      st = run_gemm_i8(ctx, L.f1, qa, ldq_for(H), rs, M, EPI_ABSMAX, nullptr, 0, ACT_GELU,
-                       L.f1->d_bias, absmax, nullptr, ops1);
+      float* amx = absmax + r0;
+      RH_HIP(launch_fill_zero(amx, Mp, ps));
+      st = run_gemm_i8(ctx, L.f1, qap, ldq_for(H), rsp, Mp, EPI_ABSMAX, nullptr, 0, ACT_GELU,
+                       L.f1->d_bias, amx, nullptr, ops1);
       if (st) return st;
-      st = run_gemm_i8(ctx, L.f1, qa, ldq_for(H), rs, M, EPI_QUANT, qa2, ldq_for(I),
-                       ACT_GELU, L.f1->d_bias, absmax, rs2, 0.0);
+      st = run_gemm_i8(ctx, L.f1, qap, ldq_for(H), rsp, Mp, EPI_QUANT, qa2p, ldq_for(I),
+                       ACT_GELU, L.f1->d_bias, amx, rs2p, 0.0);
       if (st) return st;
-      st = run_gemm_i8(ctx, L.f2, qa2, ldq_for(I), rs2, M, EPI_F32, y, H, ACT_NONE,
+      st = run_gemm_i8(ctx, L.f2, qa2p, ldq_for(I), rs2p, Mp, EPI_F32, yp, H, ACT_NONE,
                        L.f2->d_bias, nullptr, nullptr, 2.0 * MH * I * H);
       if (st) return st;
     } else if (qf1 && needs_q(L.f2)) {
@@ -421,32 +506,50 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
       // FFN2's row quantizer, which has VALU to spare where the GEMM
       // epilogue does not. Same float32 operations in the same order as
       // GELU(dense(x)) then QuantizeRowU8 (bert.go:910-916).
-      st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_NONE, L.f1->d_bias, qa, ldq_for(H),
-                      rs, false);
+      st = run_linear(ctx, L.f1, xp, H, Mp, hidp, I, ACT_NONE, L.f1->d_bias, qap, ldq_for(H),
+                      rsp, false);
       if (st) return st;
-      RH_HIP(launch_quantize_rows_u8(hid, I, M, I, qa2, ldq_for(I), rs2, s, ACT_GELU));
-      st = run_linear(ctx, L.f2, hid, I, M, y, H, ACT_NONE, L.f2->d_bias, qa2, ldq_for(I),
-                      rs2, false);
+      RH_HIP(launch_quantize_rows_u8(hidp, I, Mp, I, qa2p, ldq_for(I), rs2p, ps, ACT_GELU));
+      st = run_linear(ctx, L.f2, hidp, I, Mp, yp, H, ACT_NONE, L.f2->d_bias, qa2p,
+                      ldq_for(I), rs2p, false);
       if (st) return st;
     } else {
       // FFN1's GELU output goes to FFN2's planes when FFN2 takes them
       const bool pf2 = planes_in(L.f2) && linear_on_planes(ctx, L.f1);
-      const Planes pf2v = plane(1, L.f2);
-      st = run_linear(ctx, L.f1, x, H, M, hid, I, ACT_GELU, L.f1->d_bias, qa, ldq_for(H),
-                      rs, false, pf1 ? &pf1v : nullptr, pf2 ? &pf2v : nullptr);
+      const Planes pf2v = at(plane(1, L.f2));
+      st = run_linear(ctx, L.f1, xp, H, Mp, hidp, I, ACT_GELU, L.f1->d_bias, qap, ldq_for(H),
+                      rsp, false, pf1 ? &pf1v : nullptr, pf2 ? &pf2v : nullptr);
       if (st) return st;
-      st = run_linear(ctx, L.f2, hid, I, M, y, H, ACT_NONE, L.f2->d_bias, qa2, ldq_for(I),
-                      rs2, needs_q(L.f2) && !pf2, pf2 ? &pf2v : nullptr);
+      st = run_linear(ctx, L.f2, hidp, I, Mp, yp, H, ACT_NONE, L.f2->d_bias, qa2p,
+                      ldq_for(I), rs2p, needs_q(L.f2) && !pf2, pf2 ? &pf2v : nullptr);
       if (st) return st;
     }
     const bool last = li + 1 == layers.size();
     const bool qn = !last && needs_q(layers[li + 1].qkv);
-    x_planes = !last && planes_in(layers[li + 1].qkv);
-    const Planes pnv = last ? Planes{} : plane(0, layers[li + 1].qkv);
-    RH_HIP(launch_add_layernorm(x, y, H, L.ln2_g, L.ln2_b, M, H, eps(),
-                                qn ? qa : nullptr, ldq_for(H), qn ? rs : nullptr, s,
-                                x_planes ? pnv.hi : nullptr, x_planes ? pnv.lo : nullptr,
+    const bool xn_planes = !last && planes_in(layers[li + 1].qkv);
+    const Planes pnv = last ? Planes{} : at(plane(0, layers[li + 1].qkv));
+    RH_HIP(launch_add_layernorm(xp, yp, H, L.ln2_g, L.ln2_b, Mp, H, eps(),
+                                qn ? qap : nullptr, ldq_for(H), qn ? rsp : nullptr, ps,
+                                xn_planes ? pnv.hi : nullptr, xn_planes ? pnv.lo : nullptr,
                                 pnv.ld));
+    return RH_OK;
+  };
+  // run_linear / run_gemm_i8 launch on ctx->stream: point it at each part's
+  // stream while that part's work is enqueued (the context's mutex is held)
+  const hipStream_t s_ctx = ctx->stream;
+  for (size_t li = 0; li < layers.size(); li++) {
+    for (const Part& P : parts) {
+      ctx->stream = P.s;
+      st = layer(li, P);
+      if (st) break;
+    }
+    ctx->stream = s_ctx;
+    if (st) return st;
+    x_planes = li + 1 < layers.size() && planes_in(layers[li + 1].qkv);
+  }
+  for (int k = 1; k < np; k++) {
+    RH_HIP(hipEventRecord(ev_join[k], sx[k]));
+    RH_HIP(hipStreamWaitEvent(s, ev_join[k], 0));
   }
   if (pool) {
     RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
@@ -911,6 +1014,12 @@ int rh_model_set_option(rh_model* m, int option, int value) {
   if (option == RH_OPT_PRODUCER_PLANES) {
     if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "producer planes must be 0 or 1");
     m->producer_planes = value != 0;
+    return RH_OK;
+  }
+  if (option == RH_OPT_STREAMS) {
+    if (value < 1 || value > rh_model::kMaxParts)
+      return fail(RH_ERR_INVALID, "streams must be 1 to 4");
+    m->streams = value;
     return RH_OK;
   }
   return fail(RH_ERR_INVALID, "unknown option");

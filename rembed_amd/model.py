@@ -92,6 +92,12 @@ class Model:
         producers (True, default) or split by each GEMM (False); same values."""
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_PRODUCER_PLANES, 1 if on else 0))
 
+    def set_streams(self, n):
+        """n = 1..4 (default 2): a full-int8 encoder batch runs as up to n
+        parts of whole texts (>= 1024 tokens each) on as many streams; 1: one
+        stream. Same results."""
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_STREAMS, n))
+
     def quantized(self):
         return bool(lib.rh_model_quantized(self.h))
 

@@ -141,6 +141,37 @@ def test_producer_planes_identical(gpu_ctx, minilm, quant):
         assert np.array_equal(a, b)
 
 
+@pytest.fixture(scope="module")
+def minilm_int8_big(gpu_ctx, minilm):
+    from rembed_amd.model import Model
+    from rembed_amd.synthetic import token_batch
+    shape, t, _, _ = minilm
+    ids, lens = token_batch(64, 128, 16, 128, seed=0x5EED0003)
+    m = Model(gpu_ctx, shape, t, 2)
+    m.set_streams(1)
+    return m, ids, lens, m.embed(ids, lens), m.embed_tokens(ids, lens)
+
+
+@pytest.mark.parametrize("streams", [2, 3, 4])
+def test_parts_on_streams_identical(minilm_int8_big, streams):
+    """A full-int8 batch (64 texts, >= 4096 tokens) run as `streams` parts of
+    whole texts on as many streams gives the same embeddings and hidden
+    states, bit for bit, as one stream (every kernel computes each row the
+    same way whichever part it belongs to)."""
+    m, ids, lens, one, tok_one = minilm_int8_big
+    say(f"{streams} streams: {len(lens)} texts, {int(lens.sum())} tokens")
+    assert lens.sum() >= 4096
+    m.set_streams(streams)
+    try:
+        got = m.embed(ids, lens)
+        tok = m.embed_tokens(ids, lens)
+    finally:
+        m.set_streams(1)
+    assert np.array_equal(got, one)
+    for a, b in zip(tok, tok_one):
+        assert np.array_equal(a, b)
+
+
 def test_embed_tokens_matches_oracle_hidden(gpu_ctx, minilm):
     shape, t, ids, lens = minilm
     from rembed_amd.model import Model
