@@ -143,7 +143,10 @@ void rh_weight_destroy(rh_weight *w);
  * per output channel exactly as two separate rh_pack_weight calls would, and
  * stored interleaved (4 gate rows, then the matching 4 up rows) so one GEMM
  * produces both halves and its epilogue writes act(gate) * up. Use it with
- * rh_linear and RH_ACT_SWIGLU / RH_ACT_GEGLU; the output has i columns.
+ * rh_linear and RH_ACT_SWIGLU / RH_ACT_GEGLU / RH_ACT_GEGLU_ERF; the output
+ * has i columns. nomic's fc11 * silu(fc12) is gate = fc12, up = fc11 with
+ * RH_ACT_SWIGLU (nomic.go:232-242); ModernBERT's gelu(Wi[:I]) * Wi[I:] is
+ * gate = Wi[:I], up = Wi[I:] with RH_ACT_GEGLU_ERF (modernbert.go:292-301).
  * gate and up must each pass the packers' shape rule (i % 16 == 0, i >= 16,
  * k >= 1). No counterpart call in the reference, which runs two applyDense
  * calls and a loop. */
@@ -190,6 +193,7 @@ int rh_gemm_u8s8_i32(rh_context *ctx, int32_t *acc, const uint8_t *qa, int ldq,
 #define RH_ACT_GELU 1
 #define RH_ACT_SWIGLU 2 /* silu(gate)*up, tensor.SiLU (tensor.go:477-481)       */
 #define RH_ACT_GEGLU 3  /* gelu_tanh(gate)*up, tensor.GELUTanh (tensor.go:490-497) */
+#define RH_ACT_GEGLU_ERF 4 /* gelu(gate)*up, erf-GELU as tensor.GELU (modernbert.go:292-301) */
 int rh_linear(rh_context *ctx, float *dst, const float *a, const rh_weight *w,
               int m, int act, uint8_t *qa, int ldq, float *row_scales);
 

@@ -815,7 +815,7 @@ int rh_linear(rh_context* ctx, float* dst, const float* a, const rh_weight* w, i
               int act, uint8_t* qa, int ldq, float* row_scales) {
   int st = check_gemm(w, -1, a, dst, m);
   if (st) return st;
-  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU) return fail(RH_ERR_INVALID, "unknown act");
+  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU_ERF) return fail(RH_ERR_INVALID, "unknown act");
   if (w->glu != is_glu(act))
     return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
   if (w->mode == RH_MODE_A8W8) {
@@ -834,7 +834,7 @@ int rh_linear_u8(rh_context* ctx, const uint8_t* qa, int ldq, const float* row_s
   if (!w) return fail(RH_ERR_INVALID, "null weight");
   if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight must be RH_MODE_A8W8");
   if (m < 0) return fail(RH_ERR_INVALID, "negative m");
-  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU) return fail(RH_ERR_INVALID, "unknown act");
+  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU_ERF) return fail(RH_ERR_INVALID, "unknown act");
   if (w->glu != is_glu(act))
     return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
   if (m > 0 && (!qa || !row_scales || !qa_out || !rs_out || !absmax_scratch))

@@ -191,9 +191,15 @@ __device__ __forceinline__ float gelu_tanh_f32(float v) {
 }
 
 // Gated activation of one output: act(gate) * up, the float32 product of
-// the model loops (qwen3.go:530-539, gemma3.go:365-374).
+// the model loops: SiLU (qwen3.go:530-539; nomic.go:232-242 with gate = fc12,
+// up = fc11), GELUTanh (gemma3.go:365-374) or the erf-GELU of tensor.GELU on
+// a row whose length is a multiple of 8, i.e. geluAVX2 (modernbert.go:292-301,
+// gate = Wi[:I], up = Wi[I:]).
 __device__ __forceinline__ float glu_act(float g, float u, int act) {
-  return (act == ACT_SWIGLU ? silu_f32(g) : gelu_tanh_f32(g)) * u;
+  const float a = act == ACT_SWIGLU ? silu_f32(g)
+                  : act == ACT_GEGLU ? gelu_tanh_f32(g)
+                                     : gelu_avx2(g);
+  return a * u;
 }
 
 // GEMM epilogue activation. Output rows always have n % 16 == 0 columns

@@ -77,9 +77,11 @@ constexpr int kWeightKPad = 128;
 // ACT_SWIGLU / ACT_GEGLU apply to a gated weight (rows of gate and up
 // interleaved in groups of 4, see kGluGroup): the epilogue writes
 // act(gate) * up into n/2 output columns (qwen3.go:530-539, gemma3.go:365-374).
-enum Act : int { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2, ACT_GEGLU = 3 };
+enum Act : int { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2, ACT_GEGLU = 3, ACT_GEGLU_ERF = 4 };
 constexpr int kGluGroup = 4;  // packed rows 8t..8t+3 = gate 4t.., 8t+4..8t+7 = up 4t..
-__host__ __device__ inline bool is_glu(int act) { return act == ACT_SWIGLU || act == ACT_GEGLU; }
+__host__ __device__ inline bool is_glu(int act) {
+  return act == ACT_SWIGLU || act == ACT_GEGLU || act == ACT_GEGLU_ERF;
+}
 
 // Epilogue variants of the int8 GEMM. value = act(float32(real)·rs·cs + bias)
 enum I8Epi : int {

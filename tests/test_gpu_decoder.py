@@ -1,12 +1,14 @@
 """Decoder-family parity on the GPU (through the C ABI) against the oracle.
 
-* Gated GEMM (rh_pack_weight_gated + rh_linear with SwiGLU/GeGLU): the fp32
-  values of gate and up come out of the same epilogue arithmetic as
-  MatMulPacked/MatMulPacked8/MatMulPackedVNNI, then act(gate)*up as the model
-  loops compute it (qwen3.go:530-539, gemma3.go:365-374). Full int8 is
-  compared element-wise within 1e-6 relative (the int32 accumulators and
-  dequantization are exact; the device evaluates SiLU / GELUTanh in float32,
-  a few ulp from the reference's float64-then-rounded values); fp32 and
+* Gated GEMM (rh_pack_weight_gated + rh_linear with SwiGLU, tanh-GeGLU or
+  erf-GeGLU): the fp32 values of gate and up come out of the same epilogue
+  arithmetic as MatMulPacked/MatMulPacked8/MatMulPackedVNNI, then
+  act(gate)*up as the model loops compute it (qwen3.go:530-539,
+  gemma3.go:365-374, modernbert.go:292-301). Full int8 is compared
+  element-wise within 1e-6 relative for SiLU / GELUTanh (the int32
+  accumulators and dequantization are exact; the device evaluates them in
+  float32, a few ulp from the reference's float64-then-rounded values) and
+  bit for bit for the erf-GELU (the reference's float32 geluAVX2); fp32 and
   weight-only int8 within the GEMM tolerances.
 * Qwen3- and EmbeddingGemma-shaped models at full width (hidden 1024 /
   16 Q, 8 KV heads of 128; hidden 768 / 3 Q, 1 KV head of 256, window 257,
@@ -52,7 +54,8 @@ def oracle_dense(mode, bT, a):
                                      (_lib.RH_MODE_W8, 0), (_lib.RH_MODE_W8, 1),
                                      (_lib.RH_MODE_A8W8, 0)],
                          ids=["f32", "f32-inloop", "w8", "w8-inloop", "a8w8"])
-@pytest.mark.parametrize("act", [_lib.RH_ACT_SWIGLU, _lib.RH_ACT_GEGLU])
+@pytest.mark.parametrize("act", [_lib.RH_ACT_SWIGLU, _lib.RH_ACT_GEGLU, _lib.RH_ACT_GEGLU_ERF],
+                         ids=["swiglu", "geglu-tanh", "geglu-erf"])
 def test_gated_linear_matches_oracle(gpu_ctx, mode, bf, act):
     ctx = gpu_ctx
     rng = np.random.default_rng(10 * mode + act)
@@ -75,16 +78,22 @@ def test_gated_linear_matches_oracle(gpu_ctx, mode, bf, act):
     got = out.download(np.float32, (m, i))
     g = oracle_dense(mode, gate, a)
     u = oracle_dense(mode, up, a)
-    fn = O.silu if act == _lib.RH_ACT_SWIGLU else O.gelu_tanh
+    # ModernBERT's tensor.GELU runs geluAVX2 over rows of i (a multiple of 8)
+    # values: gelu_ref over the flattened rows takes the same path
+    fn = {_lib.RH_ACT_SWIGLU: O.silu, _lib.RH_ACT_GEGLU: O.gelu_tanh,
+          _lib.RH_ACT_GEGLU_ERF: O.gelu_ref}[act]
     want = (fn(g.ravel()).reshape(m, i) * u).astype(np.float32)
     err = np.abs(got.astype(np.float64) - want) / (1 + np.abs(want))
     say(f"  max rel err {err.max():.3e}")
-    if mode == _lib.RH_MODE_A8W8:
+    if mode == _lib.RH_MODE_A8W8 and act == _lib.RH_ACT_GEGLU_ERF:
+        # exact accumulators, dequantization and erf-GELU: bit for bit
+        assert np.array_equal(got, want)
+    elif mode == _lib.RH_MODE_A8W8:
         assert err.max() <= 1e-6
     elif mode == _lib.RH_MODE_W8:
         # one bf16 activation term: |dg| <= 2^-9 sum|a·w| per half (2x
         # margin); the gated product moves by at most 1.2|dg||u| + |act(g)||du|
-        # (|act'| <= 1.2 for SiLU and GELUTanh)
+        # (|act'| <= 1.2 for SiLU, GELUTanh and erf-GELU)
         _, qg, sg = O.pack_b8(gate, k, i)
         _, qu, su = O.pack_b8(up, k, i)
         aa = np.abs(a.astype(np.float64))
