@@ -227,8 +227,18 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(EmbedArgs p, int total) {
 hipError_t launch_embed_layernorm(const EmbedArgs& a, int total, hipStream_t s) {
   if (total <= 0) return hipSuccess;
   if (a.H > 64 * kMaxPerLane) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(embed_ln_kernel, dim3(ceil_div(total, kRowsPerBlock)),
-                     dim3(256), 0, s, a, total);
+  const bool vec = a.H % 4 == 0 && (!a.qa || a.ldq % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(a.word) | reinterpret_cast<uintptr_t>(a.pos) |
+                     reinterpret_cast<uintptr_t>(a.type0) | reinterpret_cast<uintptr_t>(a.gamma) |
+                     reinterpret_cast<uintptr_t>(a.beta) | reinterpret_cast<uintptr_t>(a.x)) &
+                    15) == 0;
+  const dim3 grid(ceil_div(total, kRowsPerBlock)), block(256);
+  const int v = ceil_div(a.H, 256);
+  if (vec && v <= 1) hipLaunchKernelGGL((embed_ln_vec_kernel<1>), grid, block, 0, s, a, total);
+  else if (vec && v <= 2) hipLaunchKernelGGL((embed_ln_vec_kernel<2>), grid, block, 0, s, a, total);
+  else if (vec && v <= 3) hipLaunchKernelGGL((embed_ln_vec_kernel<3>), grid, block, 0, s, a, total);
+  else if (vec && v <= 4) hipLaunchKernelGGL((embed_ln_vec_kernel<4>), grid, block, 0, s, a, total);
+  else hipLaunchKernelGGL(embed_ln_kernel, grid, block, 0, s, a, total);
   return hipGetLastError();
 }
 
@@ -253,35 +263,23 @@ __global__ __launch_bounds__(256) void add_ln_kernel(
                 row_scales ? row_scales + row : nullptr);
 }
 
-// float4 variant for H % 4 == 0 (every encoder width): lane l holds columns
-// 4(l + 64e) .. +3. Same operation order per element as ln_row_finish.
-// With ph the normalized row also goes to the bf16 hi/lo planes [m][ldp] of
-// the next weight-only int8 / fp32 GEMM's input (pl may be null).
+// LayerNorm of the row held as float4 in v[] (lane l holds columns
+// 4(l + 64e) .. +3; zeros past H), written to xr, optionally to the bf16
+// hi/lo planes [..][ldp] of the next weight-only int8 / fp32 GEMM (pl may be
+// null) and quantized into qa/row_scales (tensor.go:433-452: biased
+// variance, inv = 1/float32(sqrt(var+eps)), out = (v-mean)*inv*g + b; the
+// sums run per lane over its float4 groups, then across the wave).
 template <int V>
-__global__ __launch_bounds__(256) void add_ln_vec_kernel(
-    float* __restrict__ x, const float* __restrict__ y, int ldy,
-    const float* __restrict__ gamma, const float* __restrict__ beta, int m,
-    int H, float eps, uint8_t* __restrict__ qa, int ldq,
-    float* __restrict__ row_scales, __bf16* __restrict__ ph, __bf16* __restrict__ pl,
-    int ldp) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= m) return;
-  float* xr = x + (size_t)row * H;
-  const float* yr = y ? y + (size_t)row * ldy : nullptr;
-  v4f v[V];
+__device__ __forceinline__ void ln_vec_finish(v4f (&v)[V], int lane, int row, int H,
+                                              const float* __restrict__ gamma,
+                                              const float* __restrict__ beta, float eps,
+                                              float* __restrict__ xr, uint8_t* __restrict__ qa,
+                                              int ldq, float* __restrict__ row_scales,
+                                              __bf16* __restrict__ ph, __bf16* __restrict__ pl,
+                                              int ldp) {
   float s = 0.0f;
 #pragma unroll
-  for (int e = 0; e < V; e++) {
-    const int j = (lane + 64 * e) * 4;
-    v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (j < H) {
-      t = *reinterpret_cast<const v4f*>(xr + j);
-      if (yr) t = t + *reinterpret_cast<const v4f*>(yr + j);  // Add, tensor.go:383-387
-    }
-    v[e] = t;
-    s += (t[0] + t[1]) + (t[2] + t[3]);
-  }
+  for (int e = 0; e < V; e++) s += (v[e][0] + v[e][1]) + (v[e][2] + v[e][3]);
   const float mean = wave_sum(s) / (float)H;
   float s2 = 0.0f;
 #pragma unroll
@@ -327,6 +325,73 @@ __global__ __launch_bounds__(256) void add_ln_vec_kernel(
     for (int j = H + lane * 4; j < ldq; j += 256) *reinterpret_cast<uint32_t*>(q + j) = 0u;
     if (lane == 0) row_scales[row] = scale;
   }
+}
+
+// float4 variant for H % 4 == 0 (every encoder width): lane l holds columns
+// 4(l + 64e) .. +3. With ph the normalized row also goes to the bf16 hi/lo
+// planes [m][ldp] of the next weight-only int8 / fp32 GEMM's input (pl may
+// be null).
+template <int V>
+__global__ __launch_bounds__(256) void add_ln_vec_kernel(
+    float* __restrict__ x, const float* __restrict__ y, int ldy,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int m,
+    int H, float eps, uint8_t* __restrict__ qa, int ldq,
+    float* __restrict__ row_scales, __bf16* __restrict__ ph, __bf16* __restrict__ pl,
+    int ldp) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= m) return;
+  float* xr = x + (size_t)row * H;
+  const float* yr = y ? y + (size_t)row * ldy : nullptr;
+  v4f v[V];
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int j = (lane + 64 * e) * 4;
+    v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (j < H) {
+      t = *reinterpret_cast<const v4f*>(xr + j);
+      if (yr) t = t + *reinterpret_cast<const v4f*>(yr + j);  // Add, tensor.go:383-387
+    }
+    v[e] = t;
+  }
+  ln_vec_finish<V>(v, lane, row, H, gamma, beta, eps, xr, qa, ldq, row_scales, ph, pl, ldp);
+}
+
+// Embeddings + LayerNorm, float4 rows (H % 4 == 0, 16-byte aligned tables).
+// The row's text is the number of text starts cu[1..batch-1] at or before
+// it, counted by one ballot per 64 texts (no dependent loads).
+template <int V>
+__global__ __launch_bounds__(256) void embed_ln_vec_kernel(EmbedArgs p, int total) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= total) return;
+  int b = 0;
+  for (int base = 1; base < p.batch; base += 64) {
+    const int i = base + lane;
+    b += __popcll(__ballot(i < p.batch && p.cu[i] <= row));
+  }
+  const int t = row - p.cu[b];
+  int id = p.ids[(size_t)b * p.stride + t];
+  if (id < 0 || id >= p.vocab) {
+    if (lane == 0) *p.err_flag = 1;
+    id = id < 0 ? 0 : p.vocab - 1;  // stay in bounds; the call reports failure
+  }
+  const float* w = p.word + (size_t)id * p.H;
+  const float* ps = p.pos + (size_t)(t + p.pos_off) * p.H;
+  v4f v[V];
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int j = (lane + 64 * e) * 4;
+    v4f r = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (j < p.H) {
+      // bert.go:801-812: row = w + p (+ t)
+      r = *reinterpret_cast<const v4f*>(w + j) + *reinterpret_cast<const v4f*>(ps + j);
+      if (p.type0) r = r + *reinterpret_cast<const v4f*>(p.type0 + j);
+    }
+    v[e] = r;
+  }
+  ln_vec_finish<V>(v, lane, row, p.H, p.gamma, p.beta, p.eps, p.x + (size_t)row * p.H,
+                   p.qa, p.ldq, p.row_scales, nullptr, nullptr, 0);
 }
 
 template <int V>
