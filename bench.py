@@ -107,7 +107,7 @@ def main():
                     help="full-int8 FFN1: fused = GELU rows re-quantized inside the GEMM "
                          "(two passes, no fp32 intermediate); split = fp32 rows + QuantizeRowU8")
     ap.add_argument("--streams", type=int, choices=[1, 2, 3, 4], default=2,
-                    help="full-int8 encoders: run a batch as this many parts of whole texts on as many streams "
+                    help="run a batch as this many parts of whole texts on as many streams "
                          "(default 2); the roofline pass always runs one stream")
     args = ap.parse_args()
     if args.gpus != 1:

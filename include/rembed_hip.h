@@ -277,10 +277,11 @@ void rh_model_destroy(rh_model *m);
  * kernels that produce a weight-only int8 / fp32 GEMM's input (norms,
  * attention, the previous GEMM) write its bf16 hi/lo planes directly
  * (default), 0 = they write fp32 rows and each GEMM splits them; both give
- * identical values. RH_OPT_STREAMS: n = 1..4 (default 2): a full-int8
- * encoder batch runs as up to n parts of whole texts (at least 1024 tokens
- * each) on as many streams, whose kernels overlap; 1 = one stream. Every
- * setting gives identical results. */
+ * identical values. RH_OPT_STREAMS: n = 1..4 (default 2): a batch runs as
+ * up to n parts of whole texts (at least 2048 tokens each) on as many
+ * streams, whose kernels overlap, when no GEMM of the model needs the
+ * context's split workspace (full int8, or producer-written planes);
+ * 1 = one stream. Every setting gives identical results. */
 #define RH_OPT_ATTN_PRECISION 1
 #define RH_OPT_FUSED_FFN1 2
 #define RH_OPT_PRODUCER_PLANES 3

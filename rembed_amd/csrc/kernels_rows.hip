@@ -224,23 +224,6 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(EmbedArgs p, int total) {
                 p.row_scales ? p.row_scales + row : nullptr);
 }
 
-hipError_t launch_embed_layernorm(const EmbedArgs& a, int total, hipStream_t s) {
-  if (total <= 0) return hipSuccess;
-  if (a.H > 64 * kMaxPerLane) return hipErrorInvalidValue;
-  const bool vec = a.H % 4 == 0 && (!a.qa || a.ldq % 4 == 0) &&
-                   ((reinterpret_cast<uintptr_t>(a.word) | reinterpret_cast<uintptr_t>(a.pos) |
-                     reinterpret_cast<uintptr_t>(a.type0) | reinterpret_cast<uintptr_t>(a.gamma) |
-                     reinterpret_cast<uintptr_t>(a.beta) | reinterpret_cast<uintptr_t>(a.x)) &
-                    15) == 0;
-  const dim3 grid(ceil_div(total, kRowsPerBlock)), block(256);
-  const int v = ceil_div(a.H, 256);
-  if (vec && v <= 1) hipLaunchKernelGGL((embed_ln_vec_kernel<1>), grid, block, 0, s, a, total);
-  else if (vec && v <= 2) hipLaunchKernelGGL((embed_ln_vec_kernel<2>), grid, block, 0, s, a, total);
-  else if (vec && v <= 3) hipLaunchKernelGGL((embed_ln_vec_kernel<3>), grid, block, 0, s, a, total);
-  else if (vec && v <= 4) hipLaunchKernelGGL((embed_ln_vec_kernel<4>), grid, block, 0, s, a, total);
-  else hipLaunchKernelGGL(embed_ln_kernel, grid, block, 0, s, a, total);
-  return hipGetLastError();
-}
 
 __global__ __launch_bounds__(256) void add_ln_kernel(
     float* __restrict__ x, const float* __restrict__ y, int ldy,
@@ -391,7 +374,26 @@ __global__ __launch_bounds__(256) void embed_ln_vec_kernel(EmbedArgs p, int tota
     v[e] = r;
   }
   ln_vec_finish<V>(v, lane, row, p.H, p.gamma, p.beta, p.eps, p.x + (size_t)row * p.H,
-                   p.qa, p.ldq, p.row_scales, nullptr, nullptr, 0);
+                   p.qa, p.ldq, p.row_scales, p.ph, p.pl, p.ldp);
+}
+
+hipError_t launch_embed_layernorm(const EmbedArgs& a, int total, hipStream_t s) {
+  if (total <= 0) return hipSuccess;
+  if (a.H > 64 * kMaxPerLane) return hipErrorInvalidValue;
+  const bool vec = a.H % 4 == 0 && (!a.qa || a.ldq % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(a.word) | reinterpret_cast<uintptr_t>(a.pos) |
+                     reinterpret_cast<uintptr_t>(a.type0) | reinterpret_cast<uintptr_t>(a.gamma) |
+                     reinterpret_cast<uintptr_t>(a.beta) | reinterpret_cast<uintptr_t>(a.x)) &
+                    15) == 0;
+  if (a.ph && (!vec || a.ldp % 64 || a.ldp < a.H)) return hipErrorInvalidValue;
+  const dim3 grid(ceil_div(total, kRowsPerBlock)), block(256);
+  const int v = ceil_div(a.H, 256);
+  if (vec && v <= 1) hipLaunchKernelGGL((embed_ln_vec_kernel<1>), grid, block, 0, s, a, total);
+  else if (vec && v <= 2) hipLaunchKernelGGL((embed_ln_vec_kernel<2>), grid, block, 0, s, a, total);
+  else if (vec && v <= 3) hipLaunchKernelGGL((embed_ln_vec_kernel<3>), grid, block, 0, s, a, total);
+  else if (vec && v <= 4) hipLaunchKernelGGL((embed_ln_vec_kernel<4>), grid, block, 0, s, a, total);
+  else hipLaunchKernelGGL(embed_ln_kernel, grid, block, 0, s, a, total);
+  return hipGetLastError();
 }
 
 template <int V>

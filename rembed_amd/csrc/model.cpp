@@ -308,6 +308,25 @@ struct rh_model {
     return RH_OK;
   }
 
+  // A forward runs over one part (all texts) or `streams` parts of whole
+  // texts on as many streams: the parts' kernels share the GPU, so one
+  // part's GEMMs (MFMA/LDS-bound) overlap another's row kernels
+  // (VALU/HBM-bound). Every buffer is indexed by packed row (cu_d by text),
+  // so a part only offsets its pointers; a part's results equal the
+  // one-part forward's rows. Several parts need every linear to run without
+  // the context's split workspace (full int8, or planes written by their
+  // producers), which one buffer serves for all GEMMs of the context.
+  struct Part {
+    int row0, rows, b0, nb, max_len;
+    hipStream_t s;
+  };
+  bool uses_split_ws(const rh_weight* w, bool pin) const {
+    return linear_on_planes(ctx, w) && !pin;
+  }
+  int plan_parts(const std::vector<int32_t>& cu, bool allowed, hipStream_t s,
+                 std::vector<Part>& parts);
+  int join_parts(const std::vector<Part>& parts, hipStream_t s);
+
   // The forward over rows already planned; ids_dev is [batch][stride].
   int forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
               int max_len, bool pool, float* out_dev);
@@ -316,6 +335,56 @@ struct rh_model {
 };
 
 static bool needs_q(const rh_weight* w) { return w->mode == RH_MODE_A8W8; }
+
+// Part boundaries: the text whose start is closest to each k·M/n (whole
+// texts, at least one per part); at least 2048 rows per part (smaller
+// parts' GEMMs lose more than the overlap gains: MiniLM's 2260-row batch
+// ran 8 % slower as two parts). Parts after
+// the first run on extra streams that wait for everything enqueued on s.
+int rh_model::plan_parts(const std::vector<int32_t>& cu, bool allowed, hipStream_t s,
+                         std::vector<Part>& parts) {
+  const int batch = (int)cu.size() - 1;
+  const int M = cu[batch];
+  int np = 1;
+  if (streams > 1 && allowed) np = std::max(1, std::min({streams, batch, M / 2048}));
+  std::vector<int> bounds{0};
+  for (int k = 1; k < np; k++) {
+    const long target = (long)M * k / np;
+    int best = bounds.back() + 1;
+    for (int b = best; b <= batch - (np - k); b++)
+      if (std::labs(cu[b] - target) < std::labs(cu[best] - target)) best = b;
+    bounds.push_back(best);
+  }
+  bounds.push_back(batch);
+  parts.clear();
+  if (np > 1) {
+    if (!ev_fork) RH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+    RH_HIP(hipEventRecord(ev_fork, s));
+  }
+  for (int k = 0; k < np; k++) {
+    hipStream_t ps = s;
+    if (k > 0) {
+      if (!sx[k]) RH_HIP(hipStreamCreate(&sx[k]));
+      if (!ev_join[k]) RH_HIP(hipEventCreateWithFlags(&ev_join[k], hipEventDisableTiming));
+      RH_HIP(hipStreamWaitEvent(sx[k], ev_fork, 0));
+      ps = sx[k];
+    }
+    Part p{cu[bounds[k]], cu[bounds[k + 1]] - cu[bounds[k]], bounds[k],
+           bounds[k + 1] - bounds[k], 0, ps};
+    for (int b = bounds[k]; b < bounds[k + 1]; b++) p.max_len = std::max(p.max_len, cu[b + 1] - cu[b]);
+    parts.push_back(p);
+  }
+  return RH_OK;
+}
+
+// s waits for every part's stream.
+int rh_model::join_parts(const std::vector<Part>& parts, hipStream_t s) {
+  for (size_t k = 1; k < parts.size(); k++) {
+    RH_HIP(hipEventRecord(ev_join[k], parts[k].s));
+    RH_HIP(hipStreamWaitEvent(s, ev_join[k], 0));
+  }
+  return RH_OK;
+}
 
 int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
                       int max_len, bool pool, float* out_dev) {
@@ -355,64 +424,38 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
   ea.ldq = ldq_for(H);
   ea.row_scales = q0 ? rs : nullptr;
   ea.err_flag = err_d;
+  // the first QKV's planes, when it takes them
+  const bool p0 = !layers.empty() && planes_in(layers[0].qkv);
+  if (p0) {
+    const Planes pq = plane(0, layers[0].qkv);
+    ea.ph = pq.hi;
+    ea.pl = pq.lo;
+    ea.ldp = pq.ld;
+  }
   RH_HIP(launch_embed_layernorm(ea, M, s));
 
-  // The layer stack runs over one part (all texts) or `streams` parts of
-  // whole texts on as many streams: the parts' kernels share the GPU, so one
-  // part's GEMMs (MFMA/LDS-bound) overlap another's row kernels
-  // (VALU/HBM-bound). Every buffer is indexed by packed row (cu_d by text),
-  // so a part only offsets its pointers; a part's results equal the
-  // one-part forward's rows. Several parts need every linear on the int8
-  // GEMM (the bf16-planes path shares the context's split workspace).
-  struct Part {
-    int row0, rows, b0, nb, max_len;
-    double attn_ops;
-    hipStream_t s;
-  };
-  bool all_i8 = true;
-  for (const Layer& L : layers)
-    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) all_i8 = all_i8 && needs_q(w);
-  auto make_part = [&](int b0, int b1, hipStream_t ps) {
-    Part p{cu[b0], cu[b1] - cu[b0], b0, b1 - b0, 0, 0.0, ps};
-    for (int b = b0; b < b1; b++) {
-      const int L = cu[b + 1] - cu[b];
-      p.max_len = std::max(p.max_len, L);
-      p.attn_ops += 4.0 * L * L * dh * heads;
-    }
-    return p;
-  };
-  // Part boundaries: the text whose start is closest to each k·M/n (whole
-  // texts, at least one per part); at least 1024 rows per part.
-  int np = 1;
-  if (streams > 1 && all_i8) np = std::max(1, std::min({streams, batch, M / 1024}));
-  std::vector<int> bounds{0};
-  for (int k = 1; k < np; k++) {
-    const long target = (long)M * k / np;
-    int best = bounds.back() + 1;
-    for (int b = best; b <= batch - (np - k); b++)
-      if (std::labs(cu[b] - target) < std::labs(cu[best] - target)) best = b;
-    bounds.push_back(best);
+  // Parts (see plan_parts): allowed when no linear falls back to the
+  // context's split workspace.
+  bool no_ws = true;
+  for (const Layer& L : layers) {
+    no_ws = no_ws && !uses_split_ws(L.qkv, planes_in(L.qkv)) &&
+            !uses_split_ws(L.o, planes_in(L.o)) && !uses_split_ws(L.f1, planes_in(L.f1)) &&
+            !uses_split_ws(L.f2, planes_in(L.f2) && linear_on_planes(ctx, L.f1));
   }
-  bounds.push_back(batch);
   std::vector<Part> parts;
-  if (np > 1) {
-    if (!ev_fork) RH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
-    RH_HIP(hipEventRecord(ev_fork, s));
-  }
-  for (int k = 0; k < np; k++) {
-    hipStream_t ps = s;
-    if (k > 0) {
-      if (!sx[k]) RH_HIP(hipStreamCreate(&sx[k]));
-      if (!ev_join[k]) RH_HIP(hipEventCreateWithFlags(&ev_join[k], hipEventDisableTiming));
-      RH_HIP(hipStreamWaitEvent(sx[k], ev_fork, 0));
-      ps = sx[k];
+  if ((st = plan_parts(cu, no_ws, s, parts))) return st;
+  auto part_attn_ops = [&](const Part& P) {
+    double ops = 0;
+    for (int b = P.b0; b < P.b0 + P.nb; b++) {
+      const double L = cu[b + 1] - cu[b];
+      ops += 4.0 * L * L * dh * heads;
     }
-    parts.push_back(make_part(bounds[k], bounds[k + 1], ps));
-  }
+    return ops;
+  };
 
-  // p0 holds planes of x for the next QKV when the previous layer's
-  // residual+LN wrote them (layer 0 splits the embeddings' x itself).
-  bool x_planes = false;
+  // p0 holds planes of x for the next QKV when its producer (the embedding
+  // LayerNorm, then each layer's residual+LN) wrote them.
+  bool x_planes = p0;
   auto layer = [&](size_t li, const Part& P) -> int {
     const Layer& L = layers[li];
     const hipStream_t ps = P.s;
@@ -470,7 +513,7 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     aa.ctx_lo = po ? pov.lo : nullptr;
     aa.ldctx = po ? pov.ld : H;
     int slot = -1;
-    RH_HIP(ctx->prof_begin(3, P.attn_ops, 0.0, &slot));
+    RH_HIP(ctx->prof_begin(3, part_attn_ops(P), 0.0, &slot));
     RH_HIP(launch_attention(aa, attn_precision, ps));
     RH_HIP(ctx->prof_end(slot));
     const Planes povp = at(pov);
@@ -547,10 +590,7 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     if (st) return st;
     x_planes = li + 1 < layers.size() && planes_in(layers[li + 1].qkv);
   }
-  for (int k = 1; k < np; k++) {
-    RH_HIP(hipEventRecord(ev_join[k], sx[k]));
-    RH_HIP(hipStreamWaitEvent(s, ev_join[k], 0));
-  }
+  if ((st = join_parts(parts, s))) return st;
   if (pool) {
     RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
   }
@@ -580,71 +620,96 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
                              pos_d, err_d, M, s));
   const float e = eps();
   const int ldqH = ldq_for(std::max(H, qd)), ldqI = ldq_for(I);
+  // this part's rows of a planes buffer
+  auto at = [](Planes p, size_t r0) {
+    if (p.hi) p.hi += r0 * p.ld;
+    if (p.lo) p.lo += r0 * p.ld;
+    return p;
+  };
   // The pre-norms write what the next GEMM reads: fp32 rows, its bf16
-  // planes, or its u8 rows (RmsArgs).
-  auto rms_to = [&](float* xx, const float* yy, const float* post, const float* pre,
-                    const rh_weight* next, bool in_place_out) {
+  // planes, or its u8 rows (RmsArgs), for rows [r0, r0 + m).
+  auto rms_to = [&](size_t r0, int m, hipStream_t ps, const float* yy, const float* post,
+                    const float* pre, const rh_weight* next, bool in_place_out) {
     RmsArgs ra{};
-    ra.x = xx;
-    ra.y = yy;
+    ra.x = x + r0 * H;
+    ra.y = yy ? yy + r0 * H : nullptr;
     ra.post_g = post;
     ra.pre_g = pre;
-    ra.m = M;
+    ra.m = m;
     ra.H = H;
     ra.eps = e;
     if (in_place_out) {
-      ra.out = xx;
+      ra.out = ra.x;
     } else if (planes_in(next)) {
-      const Planes p = plane(0, next);
+      const Planes p = at(plane(0, next), r0);
       ra.ph = p.hi;
       ra.pl = p.lo;
       ra.ldp = p.ld;
     } else {
-      ra.out = normed;
+      ra.out = normed + r0 * H;
     }
     if (next && needs_q(next)) {
-      ra.qa = qa;
+      ra.qa = qa + r0 * ldqH;
       ra.ldq = ldqH;
-      ra.row_scales = rs;
+      ra.row_scales = rs + r0;
     }
-    return launch_rms_residual(ra, s);
+    return launch_rms_residual(ra, ps);
   };
-  RH_HIP(rms_to(x, nullptr, nullptr, dlayers[0].in_norm, dlayers[0].qkv, false));
-  double attn_ops = 0;
-  for (int b = 0; b < batch; b++) {
-    const double L = cu[b + 1] - cu[b];
-    attn_ops += 4.0 * L * L * dh() * nq() * (cfg.arch == RH_ARCH_QWEN3 ? 0.5 : 1.0);
+  RH_HIP(rms_to(0, M, s, nullptr, nullptr, dlayers[0].in_norm, dlayers[0].qkv, false));
+
+  // Parts (see plan_parts): allowed when no linear falls back to the
+  // context's split workspace.
+  bool no_ws = true;
+  for (const DecLayer& L : dlayers) {
+    no_ws = no_ws && !uses_split_ws(L.qkv, planes_in(L.qkv)) &&
+            !uses_split_ws(L.o, planes_in(L.o)) && !uses_split_ws(L.gu, planes_in(L.gu)) &&
+            !uses_split_ws(L.down, planes_in(L.down) && linear_on_planes(ctx, L.gu));
   }
+  std::vector<Part> parts;
+  if ((st = plan_parts(cu, no_ws, s, parts))) return st;
   const int glu = gemma() ? ACT_GEGLU : ACT_SWIGLU;
-  for (size_t li = 0; li < dlayers.size(); li++) {
+  auto layer = [&](size_t li, const Part& P) -> int {
     const DecLayer& L = dlayers[li];
+    const hipStream_t ps = P.s;
+    const int Mp = P.rows;
+    const size_t r0 = P.row0;
+    float* normedp = normed + r0 * H;
+    float* qkvp = qkv + r0 * qkvw;
+    float* yp = y + r0 * H;
+    float* hidp = hid + r0 * I;
+    uint8_t* qap = qa + r0 * ldqH;
+    uint8_t* qa2p = qa2 + r0 * ldqI;
+    float* rsp = rs + r0;
+    float* rs2p = rs2 + r0;
+    int st;
     // attention block: fused q|k|v, QK-norm + RoPE, GQA attention, o_proj
-    const Planes pq = plane(0, L.qkv);
-    st = run_linear(ctx, L.qkv, normed, H, M, qkv, qkvw, ACT_NONE, nullptr, qa, ldqH, rs,
+    const Planes pq = at(plane(0, L.qkv), r0);
+    st = run_linear(ctx, L.qkv, normedp, H, Mp, qkvp, qkvw, ACT_NONE, nullptr, qap, ldqH, rsp,
                     false, planes_in(L.qkv) ? &pq : nullptr);
     if (st) return st;
     const bool local = gemma() && !L.global;
     // bf16 attention reads bf16 q|k|v rows, written by the QK-norm pass
     const bool hb = attn_precision == 1;
-    RH_HIP(launch_qk_norm_rope(qkv, qkvw, M, nq(), nkv(), dh(), L.q_norm, L.k_norm, e,
-                               local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d,
-                               hb ? qkvh : nullptr, s));
+    RH_HIP(launch_qk_norm_rope(qkvp, qkvw, Mp, nq(), nkv(), dh(), L.q_norm, L.k_norm, e,
+                               local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d + r0,
+                               hb ? qkvh + r0 * qkvw : nullptr, ps));
     AttnArgs aa{};
-    aa.qkv = hb ? (const void*)qkvh : (const void*)qkv;
+    aa.qkv = hb ? (const void*)qkvh : (const void*)qkv;  // rows are absolute (cu)
     aa.in_bf16 = hb ? 1 : 0;
     aa.ldqkv = qkvw;
     aa.q_off = 0;
     aa.k_off = qd;
     aa.v_off = qd + kvd;
-    aa.cu = cu_d;
-    aa.batch = batch;
-    aa.max_len = max_len;
+    aa.cu = cu_d + P.b0;
+    aa.batch = P.nb;
+    aa.max_len = P.max_len;
     aa.heads = nq();
     aa.kv_heads = nkv();
     aa.dh = dh();
     aa.scale = gemma() ? (float)(1.0 / std::sqrt((double)cfg.query_pre_attn_scalar))
                        : (float)(1.0 / std::sqrt((double)dh()));
-    // the attention output goes straight to o_proj's planes when it takes them
+    // the attention output goes straight to o_proj's planes when it takes
+    // them (absolute rows, like the q|k|v rows)
     const bool po = planes_in(L.o);
     const Planes pov = plane(0, L.o);
     aa.ctx = po ? nullptr : ctxb;
@@ -653,33 +718,53 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     aa.ldctx = po ? pov.ld : qd;
     aa.causal = cfg.arch == RH_ARCH_QWEN3 ? 1 : 0;
     aa.window = local ? cfg.sliding_window : 0;
+    double attn_ops = 0;
+    for (int b = P.b0; b < P.b0 + P.nb; b++) {
+      const double Lb = cu[b + 1] - cu[b];
+      attn_ops += 4.0 * Lb * Lb * dh() * nq() * (cfg.arch == RH_ARCH_QWEN3 ? 0.5 : 1.0);
+    }
     int slot = -1;
     RH_HIP(ctx->prof_begin(3, attn_ops, 0.0, &slot));
-    RH_HIP(launch_attention(aa, attn_precision, s));
+    RH_HIP(launch_attention(aa, attn_precision, ps));
     RH_HIP(ctx->prof_end(slot));
-    st = run_linear(ctx, L.o, ctxb, qd, M, y, H, ACT_NONE, nullptr, qa, ldqH, rs,
-                    needs_q(L.o) && !po, po ? &pov : nullptr);
+    const Planes povp = at(pov, r0);
+    st = run_linear(ctx, L.o, ctxb + r0 * qd, qd, Mp, yp, H, ACT_NONE, nullptr, qap, ldqH, rsp,
+                    needs_q(L.o) && !po, po ? &povp : nullptr);
     if (st) return st;
     // x += [RMSNorm(attn, post_attn)]; normed = RMSNorm(x, pre-MLP norm)
-    RH_HIP(rms_to(x, y, gemma() ? L.post_attn : nullptr, gemma() ? L.pre_ffn : L.post_attn,
-                  L.gu, false));
+    RH_HIP(rms_to(r0, Mp, ps, y, gemma() ? L.post_attn : nullptr,
+                  gemma() ? L.pre_ffn : L.post_attn, L.gu, false));
     // gated MLP: one GEMM over gate|up writes act(gate) * up (as the down
     // projection's planes when it takes them), then down
-    const Planes pg = plane(0, L.gu), pd = plane(1, L.down);
+    const Planes pg = at(plane(0, L.gu), r0), pd = at(plane(1, L.down), r0);
     const bool pdown = planes_in(L.down) && linear_on_planes(ctx, L.gu);
-    st = run_linear(ctx, L.gu, normed, H, M, hid, I, glu, nullptr, qa, ldqH, rs, false,
+    st = run_linear(ctx, L.gu, normedp, H, Mp, hidp, I, glu, nullptr, qap, ldqH, rsp, false,
                     planes_in(L.gu) ? &pg : nullptr, pdown ? &pd : nullptr);
     if (st) return st;
-    st = run_linear(ctx, L.down, hid, I, M, y, H, ACT_NONE, nullptr, qa2, ldqI, rs2,
+    st = run_linear(ctx, L.down, hidp, I, Mp, yp, H, ACT_NONE, nullptr, qa2p, ldqI, rs2p,
                     needs_q(L.down), pdown ? &pd : nullptr);
     if (st) return st;
     // x += [RMSNorm(mlp, post_ffn)]; then the next layer's input norm, or the
     // final RMSNorm in place (qwen3.go:543, gemma3.go:379)
     const bool last = li + 1 == dlayers.size();
-    RH_HIP(rms_to(x, y, gemma() ? L.post_ffn : nullptr,
+    RH_HIP(rms_to(r0, Mp, ps, y, gemma() ? L.post_ffn : nullptr,
                   last ? final_norm : dlayers[li + 1].in_norm,
                   last ? nullptr : dlayers[li + 1].qkv, last));
+    return RH_OK;
+  };
+  // run_linear launches on ctx->stream: point it at each part's stream
+  // while that part's work is enqueued (the context's mutex is held)
+  const hipStream_t s_ctx = ctx->stream;
+  for (size_t li = 0; li < dlayers.size(); li++) {
+    for (const Part& P : parts) {
+      ctx->stream = P.s;
+      st = layer(li, P);
+      if (st) break;
+    }
+    ctx->stream = s_ctx;
+    if (st) return st;
   }
+  if ((st = join_parts(parts, s))) return st;
   if (pool) {
     if (gemma() && dense1 && dense2) {
       RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, 0, pooled, s));

@@ -225,6 +225,9 @@ struct EmbedArgs {
   int ldq;
   float* row_scales;       // optional [M]
   int* err_flag;           // set to 1 on an out-of-range id
+  __bf16* ph = nullptr;    // optional bf16 hi/lo planes [M][ldp] of the first
+  __bf16* pl = nullptr;    // weight-only int8 / fp32 GEMM's input (pl may be
+  int ldp = 0;             // null)
 };
 hipError_t launch_embed_layernorm(const EmbedArgs& a, int total_rows,
                                   hipStream_t s);

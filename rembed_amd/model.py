@@ -93,9 +93,9 @@ class Model:
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_PRODUCER_PLANES, 1 if on else 0))
 
     def set_streams(self, n):
-        """n = 1..4 (default 2): a full-int8 encoder batch runs as up to n
-        parts of whole texts (>= 1024 tokens each) on as many streams; 1: one
-        stream. Same results."""
+        """n = 1..4 (default 2): a batch runs as up to n parts of whole texts
+        (>= 2048 tokens each) on as many streams when no GEMM needs the
+        context's split workspace; 1: one stream. Same results."""
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_STREAMS, n))
 
     def quantized(self):

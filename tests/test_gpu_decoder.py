@@ -248,6 +248,30 @@ def test_decoder_producer_planes_identical(gpu_ctx, make, bf16, quant):
     assert np.array_equal(direct, split)
 
 
+@pytest.mark.parametrize("make,bf16", [(qwen3_2l, True), (gemma3_2l, False)], ids=["qwen3", "gemma3"])
+@pytest.mark.parametrize("quant", [QUANT_NONE, QUANT_WEIGHTS, QUANT_FULL], ids=["fp32", "w8", "a8w8"])
+def test_decoder_parts_on_streams_identical(gpu_ctx, make, bf16, quant):
+    """A batch of >= 6144 tokens run as 2 or 3 parts of whole texts on as
+    many streams gives the same embeddings and hidden states, bit for bit,
+    as one stream (the producers write every GEMM's planes, so no part
+    touches the context's split workspace)."""
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(32, 300, 150, 300, vocab=shape.vocab, id_lo=0, seed=27)
+    say(f"{shape.name} quant={quant}: {len(lens)} texts, {int(lens.sum())} tokens")
+    assert lens.sum() >= 6144
+    m = Model(gpu_ctx, shape, t, quant)
+    m.set_streams(1)
+    one = m.embed(ids, lens)
+    tok_one = m.embed_tokens(ids, lens)
+    for n in (2, 3):
+        m.set_streams(n)
+        got = m.embed(ids, lens)
+        tok = m.embed_tokens(ids, lens)
+        assert np.array_equal(got, one), n
+        for a, b in zip(tok, tok_one):
+            assert np.array_equal(a, b), n
+
+
 def test_decoder_model_errors(gpu_ctx):
     shape, t = setup(qwen3_2l, True)
     bad = dict(t)

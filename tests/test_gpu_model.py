@@ -146,21 +146,38 @@ def minilm_int8_big(gpu_ctx, minilm):
     from rembed_amd.model import Model
     from rembed_amd.synthetic import token_batch
     shape, t, _, _ = minilm
-    ids, lens = token_batch(64, 128, 16, 128, seed=0x5EED0003)
+    ids, lens = token_batch(128, 128, 16, 128, seed=0x5EED0003)
     m = Model(gpu_ctx, shape, t, 2)
     m.set_streams(1)
     return m, ids, lens, m.embed(ids, lens), m.embed_tokens(ids, lens)
 
 
+@pytest.mark.parametrize("quant", [0, 1], ids=["fp32", "w8"])
+def test_parts_on_streams_identical_planes(gpu_ctx, minilm, quant):
+    """The fp32 / weight-only encoder (the embedding LayerNorm writes the
+    first QKV's planes, so no GEMM needs the split workspace) as 2 parts on
+    two streams equals one stream bit for bit."""
+    from rembed_amd.model import Model
+    from rembed_amd.synthetic import token_batch
+    shape, t, _, _ = minilm
+    ids, lens = token_batch(64, 128, 16, 128, seed=0x5EED0004)
+    assert lens.sum() >= 4096
+    m = Model(gpu_ctx, shape, t, quant)
+    m.set_streams(1)
+    one = m.embed(ids, lens)
+    m.set_streams(2)
+    assert np.array_equal(m.embed(ids, lens), one)
+
+
 @pytest.mark.parametrize("streams", [2, 3, 4])
 def test_parts_on_streams_identical(minilm_int8_big, streams):
-    """A full-int8 batch (64 texts, >= 4096 tokens) run as `streams` parts of
-    whole texts on as many streams gives the same embeddings and hidden
-    states, bit for bit, as one stream (every kernel computes each row the
-    same way whichever part it belongs to)."""
+    """A full-int8 batch (128 texts, >= 8192 tokens: parts of >= 2048 rows)
+    run as `streams` parts of whole texts on as many streams gives the same
+    embeddings and hidden states, bit for bit, as one stream (every kernel
+    computes each row the same way whichever part it belongs to)."""
     m, ids, lens, one, tok_one = minilm_int8_big
     say(f"{streams} streams: {len(lens)} texts, {int(lens.sum())} tokens")
-    assert lens.sum() >= 4096
+    assert lens.sum() >= 8192
     m.set_streams(streams)
     try:
         got = m.embed(ids, lens)
