@@ -281,11 +281,16 @@ void rh_model_destroy(rh_model *m);
  * up to n parts of whole texts (at least 2048 tokens each) on as many
  * streams, whose kernels overlap, when no GEMM of the model needs the
  * context's split workspace (full int8, or producer-written planes);
- * 1 = one stream. Every setting gives identical results. */
+ * 1 = one stream. Every setting gives identical results.
+ * RH_OPT_QK_EPILOGUE: 1 = a decoder's weight-only int8 q|k|v projection
+ * applies QK-norm + RoPE in its GEMM epilogue and writes the bf16 rows
+ * attention reads (where the shape allows), 0 = fp32 rows and a separate
+ * pass (default: measured faster); both give identical results. */
 #define RH_OPT_ATTN_PRECISION 1
 #define RH_OPT_FUSED_FFN1 2
 #define RH_OPT_PRODUCER_PLANES 3
 #define RH_OPT_STREAMS 4
+#define RH_OPT_QK_EPILOGUE 5
 int rh_model_set_option(rh_model *m, int option, int value);
 /* Model.Quantized / QuantizedActivations (bert.go:526-644). */
 int rh_model_quantized(const rh_model *m);

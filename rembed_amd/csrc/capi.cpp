@@ -378,6 +378,54 @@ int linear_a_terms(const Context* ctx, const rh_weight* w) {
 // producer-written planes (pin) or are split once here into the context
 // workspace; the output goes to fp32 dst or to planes (pout). Rows go in
 // chunks that keep the kernel's 32-bit element offsets in range.
+int run_linear_qk(Context* ctx, const rh_weight* w, const Planes& pin, int m,
+                  const QkEpilogue& q, __bf16* out, int ldo, bool* applied) {
+  *applied = false;
+  if (!linear_on_planes(ctx, w) || w->mode != RH_MODE_W8 || linear_a_terms(ctx, w) != 1 ||
+      w->glu || ctx->bf_tile != 0 || !pin.hi || m <= 0)
+    return RH_OK;
+  if (w->n % 256 != 0 || !(q.dh == 64 || q.dh == 128 || q.dh == 256) || ldo % 4 != 0)
+    return RH_OK;
+  // the fused tile only where the 256x256 grid keeps the CUs busy, and
+  // without row chunking (32-bit element offsets)
+  if ((long long)ceil_div(m, 256) * (w->n / 256) < 128) return RH_OK;
+  if ((long long)m * std::max(pin.ld, ldo) >= (1LL << 30)) return RH_OK;
+  GemmPlArgs g{};
+  g.Ah = pin.hi;
+  g.Al = nullptr;
+  g.lda = pin.ld;
+  g.Bh = static_cast<const __bf16*>(w->d_bf);
+  g.Bl = nullptr;
+  g.ldb = w->kp;
+  g.M = m;
+  g.N = w->n;
+  g.K = w->k;
+  g.col_scales = w->d_scales;
+  g.bias = w->d_bias;
+  g.ldc = ldo;
+  g.act = ACT_NONE;
+  g.tile_group = ctx->tile_group;
+  g.qk_qg = q.q_g;
+  g.qk_kg = q.k_g;
+  g.qk_cos = q.cos_t;
+  g.qk_sin = q.sin_t;
+  g.qk_pos = q.pos;
+  g.qk_out = out;
+  g.qk_nq = q.nq;
+  g.qk_nkv = q.nkv;
+  g.qk_dh = q.dh;
+  g.qk_eps = q.eps;
+  const double M = m, K = w->k, N = w->n;
+  const double bytes = M * K * 2.0 + K * N + 4 * N + M * N * 2.0;
+  int slot = -1;
+  hipError_t e = ctx->prof_begin(1, 2.0 * M * K * N, bytes, &slot);
+  if (e == hipSuccess) e = launch_gemm_planes_qk(g, ctx->stream);
+  if (e == hipSuccess) e = ctx->prof_end(slot);
+  if (e != hipSuccess) return hip_fail(e, "planes gemm (qk epilogue) launch", __FILE__, __LINE__);
+  *applied = true;
+  return RH_OK;
+}
+
 static int run_linear_planes(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
                              float* dst, int ldc, int act, const float* bias,
                              const Planes* pin, const Planes* pout) {

@@ -96,6 +96,21 @@ int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
                float* dst, int ldc, int act, const float* bias, uint8_t* qa, int ldq,
                float* rs, bool quantize_first, const Planes* pin = nullptr,
                const Planes* pout = nullptr);
+// QK-norm + RoPE applied in the epilogue of the decoders' q|k|v projection
+// (GemmPlArgs::qk_*); pos is per row of the call.
+struct QkEpilogue {
+  const float *q_g, *k_g, *cos_t, *sin_t;
+  const int32_t* pos;
+  int nq, nkv, dh;
+  float eps;
+};
+// The q|k|v linear of w on producer-written planes with the QK-norm + RoPE
+// epilogue, bf16 rows to out [m][ldo]. *applied = false (nothing launched)
+// when this form does not apply (another mode, a forced tile, a shape the
+// fused tile does not cover): the caller then runs run_linear and the
+// separate pass.
+int run_linear_qk(Context* ctx, const rh_weight* w, const Planes& pin, int m,
+                  const QkEpilogue& q, __bf16* out, int ldo, bool* applied);
 int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                 const float* rs, int m, int epi, void* out, int ldo, int act,
                 const float* bias, float* row_absmax, float* rs_out, double ops);

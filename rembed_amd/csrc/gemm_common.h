@@ -125,6 +125,11 @@ __device__ __forceinline__ float gelu_ref(float v) {
   return 0.5f * v * (1.0f + erf);
 }
 
+// RMSNorm's inverse scale (tensor.go:459-471): 1/float32(sqrt(float64(ss/n + eps))).
+__device__ __forceinline__ float rms_inv(float ss, int n, float eps) {
+  return 1.0f / (float)sqrt((double)(ss / (float)n + eps));
+}
+
 // 1/d rounded to nearest for finite d >= 1: the hardware reciprocal (within
 // 1 ulp) and one Newton step with fused multiply-adds. Over every float
 // input of gelu_avx2 below (all 2^32 bit patterns) this gives the same

@@ -34,7 +34,10 @@ namespace rh {
 // per SIMD, so one wave's LDS waits overlap the other's MFMAs).
 // BK: k elements per stage and row, 32 (64-byte rows, i8_slot permutation)
 // or 64 (128-byte rows, lds_off permutation; half the barriers).
-template <int BM, int BN, int NS, int AT, int BT, bool GLU, int WGN = 2, int BK = 32>
+// QKN: the QK-norm + RoPE epilogue of the decoders' q|k|v projection (bf16
+// rows to p.qk_out; see GemmPlArgs).
+template <int BM, int BN, int NS, int AT, int BT, bool GLU, int WGN = 2, int BK = 32,
+          bool QKN = false>
 __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
   constexpr int NT = 128 * WGN;  // threads
   constexpr int NW = 2 * WGN;    // waves
@@ -166,6 +169,25 @@ __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
   // (weight-only int8), + bias, then the activation.
   __syncthreads();
   float* ep = reinterpret_cast<float*>(lds) + wave * 32 * kEpiStride;
+  // QKN: this lane's column scales, bias and norm weights (fixed columns
+  // 4*lane..+3 of the tile for every row)
+  v4f qk_cs = {1.0f, 1.0f, 1.0f, 1.0f}, qk_bs = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4f qk_g = {1.0f, 1.0f, 1.0f, 1.0f};
+  // and the positions of this wave row's WM rows (lane r: rows r, 64 + r),
+  // read per row with readlane: no dependent global load before a row's
+  // cos/sin loads
+  int qk_pos0 = 0, qk_pos1 = 0;
+  if constexpr (QKN) {
+    static_assert(WM == 128, "two position registers cover the wave row");
+    const int r = row0 + wm * WM + lane;
+    qk_pos0 = r < p.M ? p.qk_pos[r] : 0;
+    qk_pos1 = r + 64 < p.M ? p.qk_pos[r + 64] : 0;
+    const int gcol = col0 + lane * 4, h = gcol / p.qk_dh, d = gcol % p.qk_dh;
+    if (p.col_scales) qk_cs = *reinterpret_cast<const v4f*>(p.col_scales + gcol);
+    if (p.bias) qk_bs = *reinterpret_cast<const v4f*>(p.bias + gcol);
+    if (h < p.qk_nq + p.qk_nkv)
+      qk_g = *reinterpret_cast<const v4f*>((h < p.qk_nq ? p.qk_qg : p.qk_kg) + d);
+  }
 #pragma unroll
   for (int i = 0; i < TM; i++) {
 #pragma unroll
@@ -176,7 +198,59 @@ __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     const int grow_base = row0 + wm * WM + i * 32;
-    if constexpr (GLU) {
+    if constexpr (QKN) {
+      // The band's 32 rows x BN columns are parked across the WGN waves of
+      // this wave row (wave wn holds columns [wn*WN, wn*WN + WN)). A pass
+      // takes one tile row: lane l holds columns 4l..4l+3, a head is dh/4
+      // consecutive lanes (the separate QK-norm pass's layout), and wave wn
+      // takes rows wn, wn + WGN, ... of the band. The arithmetic is the
+      // separate pass's, element for element (the sum of squares adds lane
+      // pairs, then a butterfly over the head's lanes).
+      static_assert(BN == 256, "a pass is one 256-column tile row of 64 lanes");
+      __syncthreads();  // every wave of the band row has parked its columns
+      const int dh = p.qk_dh, lph = dh >> 2, half = dh >> 1;
+      const int c = lane * 4, l = lane % lph, d = l * 4;
+      const int gcol = col0 + c, h = gcol / dh;
+      const bool vh = h >= p.qk_nq + p.qk_nkv;  // v head: conversion only
+      const bool first = l < (lph >> 1);        // columns d < dh/2
+      const int dp = first ? d : d - half;
+      const float* src0 = reinterpret_cast<const float*>(lds) +
+                          (wm * WGN + c / WN) * 32 * kEpiStride + c % WN;
+      typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+#pragma unroll 4
+      for (int rr = wn; rr < 32; rr += WGN) {
+        v4f x = *reinterpret_cast<const v4f*>(src0 + rr * kEpiStride);
+        const int grow = grow_base + rr;
+        const bool ok = grow < p.M;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          if (p.col_scales) x[e] = x[e] * qk_cs[e];
+          if (p.bias) x[e] = x[e] + qk_bs[e];
+        }
+        float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
+        for (int o = lph >> 1; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        v4bf* out = reinterpret_cast<v4bf*>(p.qk_out + (size_t)grow * p.ldc + gcol);
+        const int wr = i * 32 + rr;  // row within the wave row (uniform)
+        const int pos = __builtin_amdgcn_readlane(wr < 64 ? qk_pos0 : qk_pos1, wr & 63);
+        const v4f cc = *reinterpret_cast<const v4f*>(p.qk_cos + (size_t)pos * half + dp);
+        const v4f sn = *reinterpret_cast<const v4f*>(p.qk_sin + (size_t)pos * half + dp);
+        const float inv = rms_inv(ss, dh, p.qk_eps);
+        v4f xn, pn;
+#pragma unroll
+        for (int e = 0; e < 4; e++) xn[e] = x[e] * inv * qk_g[e];
+#pragma unroll
+        for (int e = 0; e < 4; e++) pn[e] = __shfl_xor(xn[e], lph >> 1, 64);
+        v4f o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float a = first ? xn[e] : pn[e], b = first ? pn[e] : xn[e];
+          o[e] = first ? a * cc[e] - b * sn[e] : b * cc[e] + a * sn[e];
+        }
+        if (vh) o = x;
+        if (ok) *out = v4bf{(__bf16)o[0], (__bf16)o[1], (__bf16)o[2], (__bf16)o[3]};
+      }
+      __syncthreads();  // the next band overwrites the parked columns
+    } else if constexpr (GLU) {
       // Gated weight: tile columns 8t..8t+3 are gate rows, 8t+4..8t+7 the
       // matching up rows. A lane reads both halves of one group of 8 and
       // writes act(gate) * up at output column (packed column) / 2.
@@ -312,17 +386,30 @@ static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
 }
 
 // Tiles: 1 = 256x256, 2 = 256x128, 3 = 128x128 with 4 waves (2x2); 4 =
-// 256x256 and 5 = 256x128 with 8 waves (2x4, two per SIMD). Stages: as many
-// as fit in 160 KiB of LDS. fp32's four planes leave no room for 256x256
-// (1 and 4 fall back to 2 and 5). Automatic choice: the 8-wave tiles, the
-// largest that still gives every CU a workgroup, else 128x128 (measured on
-// MI355X at M = 16384 over the Qwen3/BERT linears: 8 waves 2-15% faster
-// than 4 at the same tile).
+// 256x256 and 5 = 256x128 with 8 waves (2x4, two per SIMD); for one
+// activation term and int8 weights also 6 = 256x256 and 7 = 256x128 on
+// 128-byte stages (two and three). Stages: as many as fit in 160 KiB of
+// LDS. fp32's four planes leave no room for 256x256 (1 and 4 fall back to 2
+// and 5). Automatic choice (measured on MI355X at M = 16384 over the
+// Qwen3/BERT linears; 8 waves 2-15% faster than 4 at the same tile): tile 6
+// for one-term W8, 4 for the other products when the 256x256 grid gives
+// every CU a workgroup, else 5, else 128x128.
 int pick_planes_tile(int M, int N, int a_terms, int b_terms) {
   if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256)
     return a_terms == 1 && b_terms == 1 ? 6 : 4;
   if (ceil_div(M, 256) * ceil_div(N, 128) >= 256) return 5;
   return 3;
+}
+
+hipError_t launch_gemm_planes_qk(const GemmPlArgs& a, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.N % 256 != 0 || a.lda % 64 != 0 || a.ldb % 64 != 0 || a.ldc % 4 != 0 || !a.qk_out ||
+      !(a.qk_dh == 64 || a.qk_dh == 128 || a.qk_dh == 256) || is_glu(a.act))
+    return hipErrorInvalidValue;
+  const int tiles = ceil_div(a.M, 256) * (a.N / 256);
+  timed_launch((gemm_planes_kernel<256, 256, 2, 1, 1, false, 4, 64, true>), dim3(tiles),
+               dim3(512), 0, s, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int tile,

@@ -29,9 +29,6 @@ __device__ __forceinline__ uint8_t qbyte(float v, float inv) {
 }
 
 // RMSNorm's scale (tensor.go:459-471): 1 / float32(sqrt(float64(ss/n + eps))).
-__device__ __forceinline__ float rms_inv(float ss, int n, float eps) {
-  return 1.0f / (float)sqrt((double)(ss / (float)n + eps));
-}
 
 }  // namespace
 

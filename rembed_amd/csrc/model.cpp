@@ -80,6 +80,11 @@ struct rh_model {
   bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
   bool producer_planes = true;  // RH_OPT_PRODUCER_PLANES
   int streams = 2;              // RH_OPT_STREAMS
+  // RH_OPT_QK_EPILOGUE: off by default; measured slower (Qwen3-0.6B W8
+  // 686K vs 689K tokens/s, EmbeddingGemma 1.59M vs 1.68M): each epilogue
+  // row's cos/sin loads wait behind the previous row's stores (vmcnt counts
+  // both), which costs more than the separate pass's traffic.
+  bool qk_epilogue = false;
   // extra streams (default priority) and the fork/join events of a forward
   // split into parts
   static constexpr int kMaxParts = 4;
@@ -684,15 +689,25 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     int st;
     // attention block: fused q|k|v, QK-norm + RoPE, GQA attention, o_proj
     const Planes pq = at(plane(0, L.qkv), r0);
-    st = run_linear(ctx, L.qkv, normedp, H, Mp, qkvp, qkvw, ACT_NONE, nullptr, qap, ldqH, rsp,
-                    false, planes_in(L.qkv) ? &pq : nullptr);
-    if (st) return st;
     const bool local = gemma() && !L.global;
-    // bf16 attention reads bf16 q|k|v rows, written by the QK-norm pass
+    // bf16 attention reads bf16 q|k|v rows: written by the q|k|v GEMM's
+    // QK-norm + RoPE epilogue where that applies, else by the separate pass
     const bool hb = attn_precision == 1;
-    RH_HIP(launch_qk_norm_rope(qkvp, qkvw, Mp, nq(), nkv(), dh(), L.q_norm, L.k_norm, e,
-                               local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d + r0,
-                               hb ? qkvh + r0 * qkvw : nullptr, ps));
+    bool fused_qk = false;
+    if (qk_epilogue && hb && planes_in(L.qkv)) {
+      const QkEpilogue q{L.q_norm, L.k_norm, local ? cos_l : cos_g, local ? sin_l : sin_g,
+                         pos_d + r0, nq(), nkv(), dh(), e};
+      st = run_linear_qk(ctx, L.qkv, pq, Mp, q, qkvh + r0 * qkvw, qkvw, &fused_qk);
+      if (st) return st;
+    }
+    if (!fused_qk) {
+      st = run_linear(ctx, L.qkv, normedp, H, Mp, qkvp, qkvw, ACT_NONE, nullptr, qap, ldqH,
+                      rsp, false, planes_in(L.qkv) ? &pq : nullptr);
+      if (st) return st;
+      RH_HIP(launch_qk_norm_rope(qkvp, qkvw, Mp, nq(), nkv(), dh(), L.q_norm, L.k_norm, e,
+                                 local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d + r0,
+                                 hb ? qkvh + r0 * qkvw : nullptr, ps));
+    }
     AttnArgs aa{};
     aa.qkv = hb ? (const void*)qkvh : (const void*)qkv;  // rows are absolute (cu)
     aa.in_bf16 = hb ? 1 : 0;
@@ -1099,6 +1114,11 @@ int rh_model_set_option(rh_model* m, int option, int value) {
   if (option == RH_OPT_PRODUCER_PLANES) {
     if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "producer planes must be 0 or 1");
     m->producer_planes = value != 0;
+    return RH_OK;
+  }
+  if (option == RH_OPT_QK_EPILOGUE) {
+    if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "qk epilogue must be 0 or 1");
+    m->qk_epilogue = value != 0;
     return RH_OK;
   }
   if (option == RH_OPT_STREAMS) {

@@ -152,6 +152,19 @@ struct GemmPlArgs {
   __bf16* Cl;   // GEMM's activation planes; Cl may be null)
   int ldc;      // elements, for C or Ch/Cl
   int act;
+  // QK-norm + RoPE epilogue of the decoders' q|k|v projection (qwen3.go /
+  // gemma3.go): bf16 rows to qk_out [M][ldc] instead of C; heads of qk_dh
+  // columns, the first qk_nq RMS-normed by qk_qg, the next qk_nkv by qk_kg,
+  // both rotated by the tables at each row's position qk_pos[row]; the rest
+  // (v) converted only.
+  const float* qk_qg = nullptr;
+  const float* qk_kg = nullptr;
+  const float* qk_cos = nullptr;
+  const float* qk_sin = nullptr;
+  const int32_t* qk_pos = nullptr;
+  __bf16* qk_out = nullptr;
+  int qk_nq = 0, qk_nkv = 0, qk_dh = 0;
+  float qk_eps = 0.0f;
 };
 
 // The split hi/lo of one value; every producer of activation planes uses
@@ -181,6 +194,10 @@ hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi
 constexpr int kPlanesTileConfigs = 7;
 hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int tile,
                               hipStream_t s);
+// The q|k|v projection with the QK-norm + RoPE epilogue (a.qk_out set): one
+// activation term, int8 weights as one bf16 plane, 256x256 tiles of 8 waves
+// on two 128-byte stages; needs N % 256 == 0 and qk_dh in {64, 128, 256}.
+hipError_t launch_gemm_planes_qk(const GemmPlArgs& a, hipStream_t s);
 
 // fp32 GEMM strategies (selected per model/context; both kept so the
 // choice can be re-measured): three bf16 products or native f32 MFMA.

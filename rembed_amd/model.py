@@ -98,6 +98,12 @@ class Model:
         context's split workspace; 1: one stream. Same results."""
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_STREAMS, n))
 
+    def set_qk_epilogue(self, on=True):
+        """Decoders: QK-norm + RoPE in the q|k|v GEMM's epilogue (True,
+        where the shape allows) or a separate pass (False, the default:
+        measured faster); same results."""
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_QK_EPILOGUE, 1 if on else 0))
+
     def quantized(self):
         return bool(lib.rh_model_quantized(self.h))
 

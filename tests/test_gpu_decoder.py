@@ -272,6 +272,31 @@ def test_decoder_parts_on_streams_identical(gpu_ctx, make, bf16, quant):
             assert np.array_equal(a, b), n
 
 
+@pytest.mark.parametrize("make,bf16", [(qwen3_2l, True), (gemma3_2l, False)], ids=["qwen3", "gemma3"])
+def test_decoder_qk_epilogue_identical(gpu_ctx, make, bf16):
+    """Weight-only int8 with QK-norm + RoPE in the q|k|v GEMM's epilogue
+    (bf16 rows straight to attention) equals the GEMM's fp32 rows plus the
+    separate pass, bit for bit: same values, same per-element arithmetic,
+    same sum-of-squares order. The batch (~7000 rows) gives the fused tile
+    at least 128 tiles; texts of one token and ragged row tails are
+    included."""
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(48, 300, 1, 300, vocab=shape.vocab, id_lo=0, seed=28)
+    lens[0], lens[1] = 1, 300
+    say(f"{shape.name} qk epilogue: {len(lens)} texts, {int(lens.sum())} tokens")
+    m = Model(gpu_ctx, shape, t, QUANT_WEIGHTS)
+    m.set_streams(1)
+    m.set_qk_epilogue(True)
+    fused = m.embed(ids, lens)
+    tok_fused = m.embed_tokens(ids, lens)
+    m.set_qk_epilogue(False)
+    sep = m.embed(ids, lens)
+    tok_sep = m.embed_tokens(ids, lens)
+    assert np.array_equal(fused, sep)
+    for a, b in zip(tok_fused, tok_sep):
+        assert np.array_equal(a, b)
+
+
 def test_decoder_model_errors(gpu_ctx):
     shape, t = setup(qwen3_2l, True)
     bad = dict(t)
