@@ -60,21 +60,33 @@ __device__ __forceinline__ void attn_key_range(const AttnArgs& p, int qi, int le
 __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int fg, int klo,
                                                     int khi, bool masked, float cs,
                                                     float& mref, float& lrun, bool& rescale) {
+#pragma unroll
+  for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) sc[t2][e] = sc[t2][e] * cs;
+  // One uniform branch around the whole mask (a per-element condition is
+  // if-converted into selects that every block pays for). key is outside
+  // [klo, khi] iff key - klo, as unsigned, exceeds khi - klo: exact when
+  // klo <= khi, which holds for every query inside its text (the query sees
+  // itself); queries past the text only feed outputs that are not stored.
+  if (masked) {
+    const unsigned span = (unsigned)(khi - klo);
+    const int base = key0 + fg * 4 - klo;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const unsigned off = (unsigned)(base + t2 * 32 + i * 8 + j);
+          sc[t2][i * 4 + j] = off > span ? -INFINITY : sc[t2][i * 4 + j];
+        }
+  }
   float mloc = -INFINITY;
 #pragma unroll
   for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float v = sc[t2][i * 4 + j] * cs;
-        if (masked) {
-          const int key = key0 + t2 * 32 + i * 8 + fg * 4 + j;
-          v = ((key < klo) | (key > khi)) ? -INFINITY : v;
-        }
-        sc[t2][i * 4 + j] = v;
-        mloc = fmaxf(mloc, v);
-      }
+    for (int e = 0; e < 16; e++) mloc = fmaxf(mloc, sc[t2][e]);
   mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
   // -inf + 8 = -inf: a lane's first visible key always moves the reference
   // (alpha = 2^-inf = 0 then); a lane with no visible key keeps -inf.
