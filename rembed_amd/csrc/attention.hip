@@ -51,19 +51,17 @@ __device__ __forceinline__ void attn_key_range(const AttnArgs& p, int qi, int le
 }
 
 // Online-softmax step for one 64-key block held as S^T tiles (lane: query
-// fr, keys key0 + t2*32 + i*8 + fg*4 + j in register t2, i*4 + j). Scores go
-// to log2 units with one multiply (cs = scale·log2 e); `masked` (uniform
-// over the wave) applies the per-key range test. P = 2^(s - mref) against a
-// reference that moves only when a block's max exceeds it by more than 8:
-// P stays <= 256 (no overflow in fp32), and the running output is rescaled
-// (by the returned alpha, when `rescale`) only on those moves. sc becomes P.
+// fr, keys key0 + t2*32 + i*8 + fg*4 + j in register t2, i*4 + j). Scores
+// go to log2 units through cs = scale·log2 e, folded into the exponent:
+// the block max of s·cs is max(s)·cs exactly (rounding is monotonic and
+// cs > 0), and p = 2^fma(s, cs, -m). `masked` (uniform over the wave)
+// applies the per-key range test. P = 2^(s·cs - mref) against a reference
+// that moves only when a block's max exceeds it by more than 8: P stays
+// <= 256 (no overflow in fp32), and the running output is rescaled (by the
+// returned alpha, when `rescale`) only on those moves. sc becomes P.
 __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int fg, int klo,
                                                     int khi, bool masked, float cs,
                                                     float& mref, float& lrun, bool& rescale) {
-#pragma unroll
-  for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-    for (int e = 0; e < 16; e++) sc[t2][e] = sc[t2][e] * cs;
   // One uniform branch around the whole mask (a per-element condition is
   // if-converted into selects that every block pays for). key is outside
   // [klo, khi] iff key - klo, as unsigned, exceeds khi - klo: exact when
@@ -82,12 +80,13 @@ __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int
           sc[t2][i * 4 + j] = off > span ? -INFINITY : sc[t2][i * 4 + j];
         }
   }
-  float mloc = -INFINITY;
+  float smax = -INFINITY;
 #pragma unroll
   for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-    for (int e = 0; e < 16; e++) mloc = fmaxf(mloc, sc[t2][e]);
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    for (int e = 0; e < 16; e++) smax = fmaxf(smax, sc[t2][e]);
+  smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+  const float mloc = smax * cs;
   // -inf + 8 = -inf: a lane's first visible key always moves the reference
   // (alpha = 2^-inf = 0 then); a lane with no visible key keeps -inf.
   const bool up = mloc > mref + 8.0f;
@@ -103,7 +102,7 @@ __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int
   for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
     for (int e = 0; e < 16; e++) {
-      const float pv = __builtin_amdgcn_exp2f(sc[t2][e] - m);
+      const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t2][e], cs, -m));
       sc[t2][e] = pv;
       psum += pv;
     }
