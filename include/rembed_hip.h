@@ -167,6 +167,12 @@ int rh_quantize_rows_u8(rh_context *ctx, const float *a, int m, int k,
                         uint8_t *qa, int ldq, float *row_scales);
 
 /* MatMulPacked (internal/tensor/pack.go:123-176): dst[m][n] = a[m][k]·Wᵀ. */
+/* MatMulFunc / Default (tensor.go:16-70), the unpacked path: dst[m x n] =
+ * a[m x k] · bTᵀ with raw fp32 weights bT [n][k] row-major (device
+ * pointers; any m >= 0, k >= 1, n >= 1). Computed as the packed fp32 path
+ * does, splitting both operands for this call. */
+int rh_matmul(rh_context *ctx, float *dst, const float *a, const float *bT, int m, int k,
+              int n);
 int rh_matmul_packed(rh_context *ctx, float *dst, const float *a,
                      const rh_weight *w, int m);
 /* MatMulPacked8 (internal/tensor/pack8.go:80-111). */

@@ -817,6 +817,66 @@ static int check_gemm(const rh_weight* w, int mode, const float* a, const void* 
   return RH_OK;
 }
 
+// MatMulFunc / Default (tensor.go:16-70): dst[m x n] = a[m x k] · bTᵀ with raw
+// fp32 weights bT [n][k] (no pack). Both operands are split into bf16 hi/lo
+// planes in the context workspace for this call (B padded to 256 rows, zero
+// past n and past k) and multiplied as the packed fp32 path does (three
+// bf16 products). The fp32 epilogue stores 4 columns at a time, so an odd
+// n or an unaligned dst goes through the workspace and a 2-D copy.
+int rh_matmul(rh_context* ctx, float* dst, const float* a, const float* bT, int m, int k,
+              int n) {
+  if (m < 0 || k < 1 || n < 1) return fail(RH_ERR_SHAPE, "bad shape (m >= 0, k >= 1, n >= 1)");
+  if (m > 0 && (!dst || !a || !bT)) return fail(RH_ERR_INVALID, "null argument");
+  CTX_GUARD(ctx);
+  if (m == 0) return RH_OK;
+  const int ldk = (int)round_up(k, 64), np = (int)round_up(n, kWeightRowPad);
+  const bool direct = n % 4 == 0 && aligned16(dst);
+  const int ldc = direct ? n : (int)round_up(n, 4);
+  if ((long long)std::max(m, np) * std::max(ldk, ldc) >= (1LL << 30))
+    return fail(RH_ERR_SHAPE, "matrix too large for one call");
+  const size_t ap = (size_t)m * ldk * 2, bp = (size_t)np * ldk * 2;
+  const size_t cbytes = direct ? 0 : (size_t)m * ldc * 4;
+  hipError_t e = ctx->ensure_ws(2 * ap + 2 * bp + cbytes);
+  if (e != hipSuccess) return hip_fail(e, "matmul workspace", __FILE__, __LINE__);
+  uint8_t* ws = static_cast<uint8_t*>(ctx->ws);
+  __bf16* ah = reinterpret_cast<__bf16*>(ws);
+  __bf16* al = reinterpret_cast<__bf16*>(ws + ap);
+  __bf16* bh = reinterpret_cast<__bf16*>(ws + 2 * ap);
+  __bf16* bl = reinterpret_cast<__bf16*>(ws + 2 * ap + bp);
+  float* ct = direct ? dst : reinterpret_cast<float*>(ws + 2 * ap + 2 * bp);
+  hipStream_t s = ctx->stream;
+  RH_HIP(launch_split_bf16(a, k, m, k, ah, al, ldk, s));
+  RH_HIP(launch_split_bf16(bT, k, n, k, bh, bl, ldk, s));
+  if (np > n) {  // zero rows n..np of both B planes (rows are ldk*2 bytes)
+    const int words = (np - n) * ldk / 2;
+    RH_HIP(launch_fill_zero(reinterpret_cast<float*>(bh + (size_t)n * ldk), words, s));
+    RH_HIP(launch_fill_zero(reinterpret_cast<float*>(bl + (size_t)n * ldk), words, s));
+  }
+  GemmPlArgs g{};
+  g.Ah = ah;
+  g.Al = al;
+  g.lda = ldk;
+  g.Bh = bh;
+  g.Bl = bl;
+  g.ldb = ldk;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  g.C = ct;
+  g.ldc = ldc;
+  g.act = ACT_NONE;
+  g.tile_group = ctx->tile_group;
+  int slot = -1;
+  const double M = m, K = k, N = n;
+  RH_HIP(ctx->prof_begin(2, 2.0 * M * K * N, 4.0 * (M * K + N * K + M * N), &slot));
+  RH_HIP(launch_gemm_planes(g, 2, 2, ctx->bf_tile, s));
+  RH_HIP(ctx->prof_end(slot));
+  if (!direct)
+    RH_HIP(hipMemcpy2DAsync(dst, (size_t)n * 4, ct, (size_t)ldc * 4, (size_t)n * 4, m,
+                            hipMemcpyDeviceToDevice, s));
+  return RH_OK;
+}
+
 int rh_matmul_packed(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m) {
   int st = check_gemm(w, RH_MODE_F32, a, dst, m);
   if (st) return st;

@@ -185,6 +185,11 @@ def QuantizeRowsU8(ctx, a, m, k, qa, ldq, row_scales):
     check(lib.rh_quantize_rows_u8(ctx.h, a.ptr, m, k, qa.ptr, ldq, row_scales.ptr))
 
 
+def MatMul(ctx, dst, a, bT, m, k, n):
+    """tensor.go:16-70 — dst[m][n] = a[m][k]·bTᵀ, raw fp32 weights (no pack)."""
+    check(lib.rh_matmul(ctx.h, dst.ptr, a.ptr, bT.ptr, m, k, n))
+
+
 def MatMulPacked(ctx, dst, a, pb, m):
     """pack.go:123 — dst[m][N] = a[m][K]·Wᵀ."""
     check(lib.rh_matmul_packed(ctx.h, dst.ptr, a.ptr, pb.h, m))

@@ -321,6 +321,32 @@ def test_matmul_packed_f32_against_float64(gpu_ctx, shape, algo, bf):
     assert np.all(err <= bound)
 
 
+@pytest.mark.parametrize("shape", KATS["packed_f32_shapes"]["shapes"] +
+                         [[1, 1, 1], [7, 3, 5], [33, 70, 1030], [300, 129, 250]])
+def test_matmul_unpacked_against_float64(gpu_ctx, shape):
+    """MatMulFunc's unpacked path (tensor.go:16-70): raw fp32 weights, any
+    shape (odd n and k, n not a multiple of 4 or of the 256-row weight
+    padding, unaligned output rows), within the fp32 split's bound."""
+    m, k, n = shape
+    say(f"unpacked f32 shape {shape}")
+    rng = np.random.default_rng(13 + k + n)
+    a = (rng.random((m, k), dtype=np.float32) * 2 - 1).astype(np.float32)
+    bT = (rng.random((n, k), dtype=np.float32) * 2 - 1).astype(np.float32)
+    a_d, b_d = gpu_ctx.upload(a), gpu_ctx.upload(bT)
+    guard = 64
+    out = gpu_ctx.upload(np.full(m * n + guard, 7.0, np.float32))
+    T().MatMul(gpu_ctx, out, a_d, b_d, m, k, n)
+    gpu_ctx.sync()
+    full = out.download(np.float32, (m * n + guard,))
+    assert np.all(full[m * n:] == 7.0)  # nothing written past the output
+    got = full[: m * n].reshape(m, n)
+    want = a.astype(np.float64) @ bT.astype(np.float64).T
+    bound = split_bound(a, bT, k, 2.0 ** -14, want)
+    err = np.abs(got - want)
+    say(f"  max err {err.max():.3e}  worst err/bound {(err / bound).max():.3f}")
+    assert np.all(err <= bound)
+
+
 def test_gelu_bit_exact(gpu_ctx):
     from rembed_amd._lib import check, lib
     xs = np.concatenate([np.arange(-30, 30, 0.2337, dtype=np.float32),
