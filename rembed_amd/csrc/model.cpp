@@ -592,10 +592,15 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
       if (st) break;
     }
     ctx->stream = s_ctx;
-    if (st) return st;
+    if (st) break;
     x_planes = li + 1 < layers.size() && planes_in(layers[li + 1].qkv);
   }
-  if ((st = join_parts(parts, s))) return st;
+  // join even after a failed launch: work already enqueued on the parts'
+  // streams must be ordered before anything the caller does next on s
+  // (buffer reuse, ensure_ws's sync-and-free)
+  const int jst = join_parts(parts, s);
+  if (st) return st;
+  if ((st = jst)) return st;
   if (pool) {
     RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, cfg.normalize, out_dev, s));
   }
@@ -777,9 +782,12 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
       if (st) break;
     }
     ctx->stream = s_ctx;
-    if (st) return st;
+    if (st) break;
   }
-  if ((st = join_parts(parts, s))) return st;
+  // join even after a failed launch (see the encoder's forward)
+  const int jst = join_parts(parts, s);
+  if (st) return st;
+  if ((st = jst)) return st;
   if (pool) {
     if (gemma() && dense1 && dense2) {
       RH_HIP(launch_pool(x, H, cu_d, batch, cfg.pooling, 0, pooled, s));
