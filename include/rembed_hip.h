@@ -165,6 +165,13 @@ int rh_weight_export(const rh_weight *w, int8_t *q, float *scales, int32_t *cols
  * multiple of 16; bytes k..ldq-1 of each row are zeroed. a is [m][k]. */
 int rh_quantize_rows_u8(rh_context *ctx, const float *a, int m, int k,
                         uint8_t *qa, int ldq, float *row_scales);
+/* GELU then QuantizeRowU8: the full-int8 FFN's hand-over from the
+ * intermediate dense to the output dense (internal/model/bert.go:910-916,
+ * GELU as internal/tensor/gelu_amd64.s:37-123 computes it for whole 8-lane
+ * groups). a is the pre-activation [m][k]; k a multiple of 8, qa and ldq as
+ * above. a itself is not modified. */
+int rh_gelu_quantize_rows_u8(rh_context *ctx, const float *a, int m, int k,
+                             uint8_t *qa, int ldq, float *row_scales);
 
 /* MatMulPacked (internal/tensor/pack.go:123-176): dst[m][n] = a[m][k]·Wᵀ. */
 /* MatMulFunc / Default (tensor.go:16-70), the unpacked path: dst[m x n] =

@@ -44,7 +44,7 @@ EXPORTS = [
     "rh_memcpy_d2h", "rh_profile_enable", "rh_profile_read", "rh_pack_weight",
     "rh_pack_weight_gated", "rh_attention",
     "rh_weight_destroy", "rh_weight_info", "rh_weight_export",
-    "rh_quantize_rows_u8", "rh_matmul", "rh_matmul_packed", "rh_matmul_packed8",
+    "rh_quantize_rows_u8", "rh_gelu_quantize_rows_u8", "rh_matmul", "rh_matmul_packed", "rh_matmul_packed8",
     "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_linear_u8", "rh_gelu",
     "rh_layernorm", "rh_model_create", "rh_model_set_tensor",
     "rh_model_finalize", "rh_model_destroy", "rh_model_set_option",
@@ -113,6 +113,7 @@ def _load():
         "rh_weight_info": (I, [P, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)]),
         "rh_weight_export": (I, [P, P, P, P]),
         "rh_quantize_rows_u8": (I, [P, P, I, I, P, I, P]),
+        "rh_gelu_quantize_rows_u8": (I, [P, P, I, I, P, I, P]),
         "rh_matmul": (I, [P, P, P, P, I, I, I]),
         "rh_matmul_packed": (I, [P, P, P, P, I]),
         "rh_matmul_packed8": (I, [P, P, P, P, I]),

@@ -803,6 +803,16 @@ int rh_quantize_rows_u8(rh_context* ctx, const float* a, int m, int k, uint8_t* 
   return RH_OK;
 }
 
+int rh_gelu_quantize_rows_u8(rh_context* ctx, const float* a, int m, int k, uint8_t* qa,
+                             int ldq, float* row_scales) {
+  if (m < 0 || k < 8 || k % 8 != 0) return fail(RH_ERR_INVALID, "k must be a positive multiple of 8");
+  if (ldq < k || ldq % 16 != 0) return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+  if (m > 0 && (!a || !qa || !row_scales)) return fail(RH_ERR_INVALID, "null argument");
+  CTX_GUARD(ctx);
+  RH_HIP(launch_quantize_rows_u8(a, k, m, k, qa, ldq, row_scales, ctx->stream, ACT_GELU));
+  return RH_OK;
+}
+
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 static int check_gemm(const rh_weight* w, int mode, const float* a, const void* dst, int m) {

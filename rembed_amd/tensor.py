@@ -185,6 +185,12 @@ def QuantizeRowsU8(ctx, a, m, k, qa, ldq, row_scales):
     check(lib.rh_quantize_rows_u8(ctx.h, a.ptr, m, k, qa.ptr, ldq, row_scales.ptr))
 
 
+def GELUQuantizeRowsU8(ctx, a, m, k, qa, ldq, row_scales):
+    """GELU then QuantizeRowU8 (bert.go:910-916): the FFN1 -> FFN2 hand-over;
+    k a multiple of 8, a left unmodified."""
+    check(lib.rh_gelu_quantize_rows_u8(ctx.h, a.ptr, m, k, qa.ptr, ldq, row_scales.ptr))
+
+
 def MatMul(ctx, dst, a, bT, m, k, n):
     """tensor.go:16-70 — dst[m][n] = a[m][k]·bTᵀ, raw fp32 weights (no pack)."""
     check(lib.rh_matmul(ctx.h, dst.ptr, a.ptr, bT.ptr, m, k, n))

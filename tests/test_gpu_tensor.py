@@ -189,6 +189,90 @@ def test_quantize_rows_bit_exact(gpu_ctx):
             assert r[i] == so, (k, i)
 
 
+def _gelu_quant_rows_adversarial(rng, k):
+    """Rows that stress a GELU quantizer: scaled GELU values on and next to
+    half-integers (rint's decision points), many near-ties at the row
+    maximum, and rows whose GELU is tiny beside |x|."""
+    rows = []
+    top = np.float32(4.0)
+    mx = O.gelu_ref(np.full(8, top, np.float32))[0]
+    inv = np.float32(1) / (mx / np.float32(127))
+    sweep = np.linspace(-0.3, 3.9, 1 << 20, dtype=np.float32)
+    p = O.gelu_ref(sweep) * inv
+    frac = np.abs(np.abs(p - np.rint(p)) - np.float32(0.5))
+    near = sweep[np.argsort(frac, kind="stable")[: 4 * k]]
+    for r in range(3):
+        row = rng.choice(near, k).astype(np.float32)
+        row[rng.integers(k)] = top
+        rows.append(row)
+    ties = (top + np.float32(2.0 ** -20) * rng.integers(-40, 40, k)).astype(np.float32)
+    rows.append(ties)
+    rows.append((-5 - 15 * rng.random(k)).astype(np.float32))
+    rows.append((-3.5 - rng.random(k)).astype(np.float32))
+    return np.stack(rows)
+
+
+def test_gelu_quantize_rows_bit_exact(gpu_ctx):
+    """GELU then QuantizeRowU8 (bert.go:910-916) in one kernel: bytes and
+    scales equal the oracle's gelu_ref + quantize_row_u8 exactly, random rows
+    at scales 2^-8..2^8 and rows built against the quantizer (scaled GELU
+    values on and next to half-integers, near-ties at the row max, rows of
+    tiny GELU beside large |x|), widths ragged to the 256-element vector
+    loop and past the register-resident range (4096)."""
+    t = T()
+    rng = np.random.default_rng(91)
+    for k in (8, 16, 264, 768, 1000, 1536, 3072, 4096):
+        m = 41
+        a = (rng.standard_normal((m, k), dtype=np.float32) *
+             np.exp2(rng.integers(-8, 9, size=(m, 1))).astype(np.float32)).astype(np.float32)
+        a[3] = 0
+        a = np.concatenate([a, _gelu_quant_rows_adversarial(rng, k)])
+        m = a.shape[0]
+        say(f"gelu quantize k={k} rows={m}")
+        ldq = t.ldq_for(k)
+        da = gpu_ctx.upload(a)
+        qa = gpu_ctx.upload(np.full(m * ldq, 0xCD, np.uint8))
+        rs = gpu_ctx.alloc(m * 4)
+        t.GELUQuantizeRowsU8(gpu_ctx, da, m, k, qa, ldq, rs)
+        gpu_ctx.sync()
+        q = qa.download(np.uint8, (m, ldq))
+        r = rs.download(np.float32, (m,))
+        assert np.array_equal(da.download(np.float32, a.shape), a)
+        for i in range(m):
+            qo, so = O.quantize_row_u8(O.gelu_ref(a[i]), ldq)
+            assert np.array_equal(q[i], qo), (k, i)
+            assert r[i] == so, (k, i)
+
+
+def test_gelu_quantize_rows_nonfinite_and_errors(gpu_ctx):
+    """Rows holding inf or NaN give the same bytes and scales as GELU in
+    place followed by QuantizeRowU8 on the device; k % 8 != 0 is refused."""
+    from rembed_amd._lib import RembedError, check, lib
+    t = T()
+    rng = np.random.default_rng(92)
+    k, m = 768, 6
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    a[0, 5] = np.inf
+    a[1, 9] = -np.inf
+    a[2, 17] = np.nan
+    a[3, :2] = [np.inf, np.nan]
+    ldq = t.ldq_for(k)
+    da = gpu_ctx.upload(a)
+    qa = gpu_ctx.alloc(m * ldq)
+    rs = gpu_ctx.alloc(m * 4)
+    t.GELUQuantizeRowsU8(gpu_ctx, da, m, k, qa, ldq, rs)
+    db = gpu_ctx.upload(a)
+    check(lib.rh_gelu(gpu_ctx.h, db.ptr, a.size))
+    qb = gpu_ctx.alloc(m * ldq)
+    rb = gpu_ctx.alloc(m * 4)
+    t.QuantizeRowsU8(gpu_ctx, db, m, k, qb, ldq, rb)
+    gpu_ctx.sync()
+    assert np.array_equal(qa.download(np.uint8, (m, ldq)), qb.download(np.uint8, (m, ldq)))
+    assert np.array_equal(rs.download(np.uint32, (m,)), rb.download(np.uint32, (m,)))
+    with pytest.raises(RembedError):
+        t.GELUQuantizeRowsU8(gpu_ctx, da, m, 764, qa, ldq, rs)
+
+
 def test_linear_a8w8_bias_gelu_bit_exact(gpu_ctx):
     """Fused bias + erf-GELU epilogue equals AddBias then GELU (bert.go:297-300,913-915)."""
     t = T()
