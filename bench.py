@@ -198,10 +198,9 @@ def main():
 
     vec = out_dev.download(np.float32, (BATCH, shape.hidden))
     assert np.array_equal(vec, host_vec), "host-buffer and device-resident forwards differ"
+    cfg_note = {"streams": args.streams}
     if quant == 2:
-        cfg_note = {"ffn1": args.ffn1, "streams": args.streams}
-    else:
-        cfg_note = {}
+        cfg_note["ffn1"] = args.ffn1
     norms = np.linalg.norm(vec.astype(np.float64), axis=1)
     assert np.all(np.abs(norms - 1) < 1e-4), "embeddings are not unit vectors"
 
