@@ -3,12 +3,15 @@
     python -m rembed_amd.profsummary stats  <kernel_stats.csv> <steps> <title> <command>
     python -m rembed_amd.profsummary traffic <fetch_dir_csv> <write_dir_csv>
                                      <copy_fetch_csv> <copy_write_csv> <copy_mib> <command>
+    python -m rembed_amd.profsummary pmc <counter_collection.csv> <command>
 
 `stats` renders a --kernel-trace --stats table (per-kernel calls, average
 and per-step time). `traffic` turns two --pmc runs (FETCH_SIZE, then
 WRITE_SIZE, KiB per dispatch) into HBM bytes per launch, each counter scaled
 by what it reads for a plain device copy of known size, and prints the JSON
-that bench.py reads for the GEMM's `roofline.traffic`.
+that bench.py reads for the GEMM's `roofline.traffic`. `pmc` renders one
+--pmc pass of SQ instruction and busy counters per kernel: MFMA busy share,
+VALU and LDS instructions per MFMA, LDS bank-conflict share.
 """
 import collections
 import csv
@@ -41,6 +44,41 @@ def stats(path, steps, title, command):
     if gc:
         print(f"\nAll `{GEMM}` launches: {gc} calls, average {gt / gc / 1e3:.2f} µs, "
               f"{gt / 1e3 / steps:.1f} µs per step ({steps} steps incl. warm-up).")
+
+
+# MI355X: 8 XCDs of 32 CUs, 4 SIMDs per CU. GRBM_GUI_ACTIVE sums the XCDs'
+# active cycles; SQ_VALU_MFMA_BUSY_CYCLES sums every SIMD's MFMA-busy cycles.
+XCDS, CUS, SIMDS = 8, 256, 4
+
+
+def pmc(path, command):
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    for r in csv.DictReader(open(path)):
+        per[r["Kernel_Name"]][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    print("# Instruction mix and MFMA busy share per kernel (rocprofv3 --pmc)\n")
+    print(f"Command: `{command}`\n")
+    print("MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x "
+          "4 SIMDs); counters are means per dispatch.\n")
+    print("| kernel | dispatches | waves | MFMA instr | MFMA busy | VALU / MFMA | "
+          "LDS instr / MFMA | LDS bank-conflict cycles / LDS active |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|")
+
+    def mean(c, k):
+        v = c.get(k)
+        return sum(v) / len(v) if v else float("nan")
+
+    rows = sorted(per.items(), key=lambda kv: -mean(kv[1], "GRBM_GUI_ACTIVE") *
+                  len(kv[1].get("GRBM_GUI_ACTIVE", [])))
+    for name, c in rows:
+        n = len(c.get("SQ_WAVES", []))
+        mf = mean(c, "SQ_INSTS_MFMA")
+        active = mean(c, "GRBM_GUI_ACTIVE") / XCDS
+        busy = mean(c, "SQ_VALU_MFMA_BUSY_CYCLES") / (active * CUS * SIMDS) if active else 0.0
+        per_mf = (lambda k: f"{mean(c, k) / mf:.1f}") if mf else (lambda k: "-")
+        lds_act = mean(c, "SQ_ACTIVE_INST_LDS")
+        conf = f"{100 * mean(c, 'SQ_LDS_BANK_CONFLICT') / lds_act:.1f}%" if lds_act else "-"
+        print(f"| `{name[:80]}` | {n} | {mean(c, 'SQ_WAVES'):.0f} | {mf:.0f} | "
+              f"{100 * busy:.1f}% | {per_mf('SQ_INSTS_VALU')} | {per_mf('SQ_INSTS_LDS')} | {conf} |")
 
 
 def traffic(fetch, write, cfetch, cwrite, copy_mib, command):
@@ -78,7 +116,9 @@ def traffic(fetch, write, cfetch, cwrite, copy_mib, command):
 
 
 if __name__ == "__main__":
-    if sys.argv[1] == "stats":
+    if sys.argv[1] == "pmc":
+        pmc(sys.argv[2], sys.argv[3])
+    elif sys.argv[1] == "stats":
         stats(sys.argv[2], int(sys.argv[3]), sys.argv[4], sys.argv[5])
     elif sys.argv[1] == "traffic":
         o = traffic(*sys.argv[2:6], int(sys.argv[6]), sys.argv[7])
