@@ -81,6 +81,52 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
             "gbps": round(st["total_bytes"] / (st["total_ms"] * 1e-3) / 1e9, 1)}
 
 
+def f32_choice(ctx, m, k, n, iters, rows=256):
+    """The fp32 linear's two algorithms at one shape: three bf16 MFMA
+    products on split planes (the default) and native f32 MFMA. Time per
+    launch from HIP events; error on a sample of rows against the float64
+    product, beside numpy's own float32 product (a CPU fp32 GEMM) of the
+    same operands. Inputs: N(0, 1) activations, N(0, 0.02) weights and bias
+    (BERT-like scales)."""
+    rng = np.random.default_rng(k * 11 + n)
+    bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(n, dtype=np.float32) * 0.02).astype(np.float32)
+    a_h = rng.standard_normal((m, k), dtype=np.float32)
+    sample = np.sort(rng.choice(m, size=min(rows, m), replace=False))
+    want = a_h[sample].astype(np.float64) @ bT.T.astype(np.float64) + bias
+    scale = np.abs(a_h[sample]).astype(np.float64) @ np.abs(bT.T).astype(np.float64)
+    cpu = a_h[sample] @ bT.T + bias
+    out = []
+    pb = T.PackB(ctx, bT, k, n, bias=bias)
+    a = ctx.upload(a_h)
+    dst = ctx.alloc(m * n * 4)
+    for algo, name in ((0, "bf16x3 planes"), (1, "native f32")):
+        ctx.set_option(_lib.RH_CTX_F32_ALGO, algo)
+        for _ in range(3):
+            T.Linear(ctx, dst, a, pb, m, 0)
+        ctx.sync()
+        ctx.profile(True)
+        for _ in range(iters):
+            T.Linear(ctx, dst, a, pb, m, 0)
+        ctx.sync()
+        st = ctx.profile_read(2)
+        sp = ctx.profile_read(4)
+        ctx.profile(False)
+        got = dst.download(np.float32, (m, n))[sample].astype(np.float64)
+        us = st["total_ms"] * 1e3 / st["launches"]
+        split_us = sp["total_ms"] * 1e3 / sp["launches"] if sp["launches"] else 0.0
+        out.append({"f32_algo": name, "m": m, "k": k, "n": n, "us": round(us, 2),
+                    "split_us": round(split_us, 2),
+                    "tflops": round(2.0 * m * k * n / ((us + split_us) * 1e-6) / 1e12, 1),
+                    "max_abs_err": float(np.abs(got - want).max()),
+                    "max_err_over_sum_abs": float((np.abs(got - want) / scale).max())})
+    ctx.set_option(_lib.RH_CTX_F32_ALGO, 0)
+    out.append({"f32_algo": "numpy float32 (CPU)", "m": len(sample), "k": k, "n": n,
+                "max_abs_err": float(np.abs(cpu - want).max()),
+                "max_err_over_sum_abs": float((np.abs(cpu - want) / scale).max())})
+    return out
+
+
 ATTN_CASES = {
     # name: (dh, heads, kv_heads, causal, window, texts, length)
     "bert-base": (64, 12, 12, False, 0, 64, None),     # lengths U[64,256]
@@ -175,6 +221,9 @@ def main():
                     help="only time rh_attention at these shapes (comma list of "
                          + ",".join(ATTN_CASES) + ")")
     ap.add_argument("--attn-kernels", default="bf16", help="bf16 and/or f32 (comma list)")
+    ap.add_argument("--f32-choice", action="store_true",
+                    help="only compare the fp32 linear's algorithms (time and error) "
+                         "at the shapes")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -192,6 +241,12 @@ def main():
     if args.shapes:
         shapes = [tuple(int(x) for x in s.split(",")) for s in args.shapes.split(";")]
     ctx = T.Context(0)
+    if args.f32_choice:
+        for (k, n) in shapes:
+            for r in f32_choice(ctx, args.m, k, n, args.iters):
+                print(json.dumps(r), flush=True)
+        ctx.close()
+        return 0
     ctx.set_option(_lib.RH_CTX_W8_TERMS, args.w8_terms)
     for mode in args.modes.split(","):
         for (k, n) in shapes:
