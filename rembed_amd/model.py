@@ -68,6 +68,14 @@ class Model:
             self.close()
             raise
 
+    @classmethod
+    def from_safetensors(cls, ctx, shape, path, quant=QUANT_NONE):
+        """model.Load over one .safetensors file (bert.go:307-524 reading
+        through safetensors.go:122-181): every tensor widened to float32 and
+        handed over by name; the library fuses Q|K|V and packs on finalize."""
+        from .checkpoint import load
+        return cls(ctx, shape, load(path), quant)
+
     def close(self):
         if getattr(self, "h", None):
             lib.rh_model_destroy(self.h)

@@ -249,3 +249,38 @@ def test_bert_base_full_batch_parity(gpu_ctx, bertbase, quant):
         c = cos_rows(got[sample], want)
         say(f"  min cos {c.min():.6f}")
         assert c.min() >= 0.999
+
+
+def _write_safetensors(path, tensors, bf16):
+    """A .safetensors file of the tensors as F32, or as BF16 (top 16 bits)."""
+    import json
+    import struct
+    header, blobs, off = {}, [], 0
+    for name, arr in tensors.items():
+        a = np.ascontiguousarray(arr, np.float32)
+        raw = (a.view(np.uint32) >> 16).astype("<u2").tobytes() if bf16 else a.astype("<f4").tobytes()
+        header[name] = {"dtype": "BF16" if bf16 else "F32", "shape": list(a.shape),
+                        "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    hb = json.dumps(header).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(hb)) + hb + b"".join(blobs))
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_model_from_safetensors_identical(gpu_ctx, minilm, tmp_path, bf16):
+    """Model.from_safetensors (the checkpoint read as safetensors.go:122-181
+    widens it) embeds bit for bit as the model built from the same float32
+    tensors in memory; a BF16 file equals its widened values."""
+    from rembed_amd.model import Model
+    shape, t, ids, lens = minilm
+    path = str(tmp_path / "m.safetensors")
+    _write_safetensors(path, t, bf16)
+    if bf16:
+        t = {k: ((np.ascontiguousarray(v, np.float32).view(np.uint32) >> 16) << 16).view(np.float32)
+             for k, v in t.items()}
+    for quant in (0, 2):
+        want = Model(gpu_ctx, shape, t, quant).embed(ids, lens)
+        got = Model.from_safetensors(gpu_ctx, shape, path, quant).embed(ids, lens)
+        assert np.array_equal(got, want), quant
