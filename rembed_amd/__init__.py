@@ -3,8 +3,9 @@
 The product is librembed_hip.so (C ABI in include/rembed_hip.h: hand-written
 HIP kernels plus the C++ model runtime). This package is its Python binding:
 `tensor` mirrors internal/tensor's GEMM family, `model` mirrors the encoder
-API, `synthetic` generates the benchmark's random-init weights and tokens.
+API, `checkpoint` reads .safetensors weights for it, `synthetic` generates
+the benchmark's random-init weights and tokens.
 Importing `rembed_amd.tensor` or `rembed_amd.model` loads the library and
 raises if it is not built: there is no CPU fallback.
 """
-__all__ = ["tensor", "model", "synthetic"]
+__all__ = ["tensor", "model", "checkpoint", "synthetic"]
