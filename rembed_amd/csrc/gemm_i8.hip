@@ -88,8 +88,8 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
     bsrc[j] = p.B + (size_t)(col0 + r) * p.ldb;
   }
 
-  auto issue = [&](int kt) {
-    uint8_t* s = lds + (kt % NS) * kStage;
+  auto issue = [&](int kt, int slot) {
+    uint8_t* s = lds + slot * kStage;
     const int k0 = kt * BK;
 #pragma unroll
     for (int j = 0; j < LA; j++) {
@@ -115,8 +115,8 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
   static_assert(S % 2 == 0 && NS <= 4, "k-steps per stage / ring depth");
   const int fr = lane & 31, fg = lane >> 5;
   v4i fa[2][TM], fb[2][TN];
-  auto load = [&](int kt, int s, v4i (&a)[TM], v4i (&b)[TN]) {
-    const uint8_t* sA = lds + (kt % NS) * kStage;
+  auto load = [&](int slot, int s, v4i (&a)[TM], v4i (&b)[TN]) {
+    const uint8_t* sA = lds + slot * kStage;
     const uint8_t* sB = sA + kA;
     const int c = 2 * s + fg;
 #pragma unroll
@@ -145,34 +145,40 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
 
 #pragma unroll
   for (int st = 0; st < NS - 1; st++)
-    if (st < nk) issue(st);
+    if (st < nk) issue(st, st);
   wait_stage(nk - 1);
   stage_barrier();
-  if (NS - 1 < nk) issue(NS - 1);
+  if (NS - 1 < nk) issue(NS - 1, NS - 1);
   load(0, 0, fa[0], fb[0]);
 
-  for (int kt = 0; kt < nk; kt++) {
+  // Unrolled by the ring depth, so every slot offset is a constant.
+  for (int kt0 = 0; kt0 < nk; kt0 += NS) {
 #pragma unroll
-    for (int s = 0; s < S; s++) {
-      if (s + 1 < S) {
-        load(kt, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
-      } else {
-        // The last step's fragments have returned (on every path, so the
-        // MFMAs below need no wait that would also cover the next stage's
-        // reads). Slot kt % NS is refilled after the barrier, which is safe
-        // once every wave is past this point; stage kt+1 must have landed
-        // for every wave.
-        wait_lgkmcnt0();
+    for (int u = 0; u < NS; u++) {
+      const int kt = kt0 + u;
+      if (kt >= nk) break;
+#pragma unroll
+      for (int s = 0; s < S; s++) {
+        if (s + 1 < S) {
+          load(u, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+        } else {
+          // The last step's fragments have returned (on every path, so the
+          // MFMAs below need no wait that would also cover the next stage's
+          // reads). Slot u (= kt % NS) is refilled after the barrier, which is safe
+          // once every wave is past this point; stage kt+1 must have landed
+          // for every wave.
+          wait_lgkmcnt0();
+        }
+        if (s + 1 == S && kt + 1 < nk) {
+          wait_stage(nk - 2 - kt);
+          stage_barrier();
+          if (kt + NS < nk) issue(kt + NS, u);
+          load((u + 1) % NS, 0, fa[0], fb[0]);
+        }
+        mma(fa[s & 1], fb[s & 1]);
+        // keep each step's MFMAs ahead of the next step's waits
+        __builtin_amdgcn_sched_barrier(0);
       }
-      if (s + 1 == S && kt + 1 < nk) {
-        wait_stage(nk - 2 - kt);
-        stage_barrier();
-        if (kt + NS < nk) issue(kt + NS);
-        load(kt + 1, 0, fa[0], fb[0]);
-      }
-      mma(fa[s & 1], fb[s & 1]);
-      // keep each step's MFMAs ahead of the next step's waits
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
