@@ -4,7 +4,9 @@
  * Drop-in boundary for rembed's internal/tensor matmul family and the
  * encoder forward that calls it. Every entry point is plain C: opaque
  * handles, plain pointers and sizes, an int status (RH_OK == 0) and a
- * thread-local message from rh_last_error(). No entry point aborts the host.
+ * thread-local message from rh_last_error(). No entry point aborts the host:
+ * no C++ exception crosses the ABI (a failed host allocation returns
+ * RH_ERR_OOM, any other internal exception RH_ERR_INVALID).
  *
  * Pointer conventions
  *   "host"  — ordinary CPU memory, borrowed for the duration of the call.
@@ -129,7 +131,9 @@ int rh_attention(rh_context *ctx, const void *qkv, int in_bf16, int ldqkv, int q
  *   mode RH_MODE_W8   replaces PackB8      (internal/tensor/pack8.go:25-76)
  *   mode RH_MODE_A8W8 replaces PackB8VNNI  (internal/tensor/pack_vnni.go:28-77)
  * bT is the HF [out=n][in=k] row-major matrix; bias (length n) may be NULL
- * and is applied by rh_linear only (newDense's bias, bert.go:263-278). */
+ * and is applied by rh_linear only (newDense's bias, bert.go:263-278).
+ * A weight is used only with the context that packed it: passing it to a
+ * call on another context returns RH_ERR_INVALID. */
 #define RH_MODE_F32 0
 #define RH_MODE_W8 1
 #define RH_MODE_A8W8 2
@@ -216,7 +220,9 @@ int rh_linear(rh_context *ctx, float *dst, const float *a, const rh_weight *w,
  * quantized (qa/row_scales as produced by rh_quantize_rows_u8); output rows
  * go to qa_out [m][ldq_out] (ldq_out >= n, multiple of 16) and rs_out [m].
  * absmax_scratch holds m floats of caller scratch. The weight must be
- * RH_MODE_A8W8. Output bytes equal QuantizeRowU8(act(a·Wᵀ + bias)) exactly. */
+ * RH_MODE_A8W8 and not gated; act is RH_ACT_NONE or RH_ACT_GELU (a gated
+ * weight or act returns RH_ERR_INVALID). Output bytes equal
+ * QuantizeRowU8(act(a·Wᵀ + bias)) exactly. */
 int rh_linear_u8(rh_context *ctx, const uint8_t *qa, int ldq, const float *row_scales,
                  const rh_weight *w, int m, int act, uint8_t *qa_out, int ldq_out,
                  float *rs_out, float *absmax_scratch);
@@ -298,28 +304,39 @@ void rh_model_destroy(rh_model *m);
  * RH_OPT_QK_EPILOGUE: 1 = a decoder's weight-only int8 q|k|v projection
  * applies QK-norm + RoPE in its GEMM epilogue and writes the bf16 rows
  * attention reads (where the shape allows), 0 = fp32 rows and a separate
- * pass (default: measured faster); both give identical results. */
+ * pass (default: measured faster); both give identical results.
+ * RH_OPT_FUSE_PROJECTIONS (set before rh_model_finalize): 1 = a decoder
+ * layer's q, k, v (and gate, up) are packed as one weight where newDense
+ * leaves all of them in one mode (default), 0 = always as separate weights,
+ * as the reference packs them (qwen3.go:479-481,528-529); a group whose
+ * matrices fall back to different modes is always separate. Identical
+ * results either way. */
 #define RH_OPT_ATTN_PRECISION 1
 #define RH_OPT_FUSED_FFN1 2
 #define RH_OPT_PRODUCER_PLANES 3
 #define RH_OPT_STREAMS 4
 #define RH_OPT_QK_EPILOGUE 5
+#define RH_OPT_FUSE_PROJECTIONS 6
 int rh_model_set_option(rh_model *m, int option, int value);
 /* Model.Quantized / QuantizedActivations (bert.go:526-644). */
 int rh_model_quantized(const rh_model *m);
 int rh_model_quantized_activations(const rh_model *m);
 
 /* Embed (rembed.go:287-332 + Forward bert.go:649-689): ids is [batch][stride]
- * host, text b is ids[b*stride .. b*stride+lens[b]); out is [batch][H] host. */
-int rh_model_embed(rh_model *m, const int32_t *ids, const int32_t *lens,
+ * host int64 as the reference's Forward takes them (bert.go:649), text b is
+ * ids[b*stride .. b*stride+lens[b]); out is [batch][H] host. An id outside
+ * [0, vocab) returns RH_ERR_VOCAB (bert.go:797-800); batch*stride must be
+ * below 2^31. Synchronous: the call returns with out filled. */
+int rh_model_embed(rh_model *m, const int64_t *ids, const int32_t *lens,
                    int batch, int stride, float *out);
 /* EmbedTokens / ForwardTokens (rembed.go:370-411, bert.go:705-731): out is
  * [sum(lens)][H] host, texts concatenated in order. */
-int rh_model_embed_tokens(rh_model *m, const int32_t *ids, const int32_t *lens,
+int rh_model_embed_tokens(rh_model *m, const int64_t *ids, const int32_t *lens,
                           int batch, int stride, float *out);
-/* Device-resident variant: ids_dev [batch][stride] and out_dev [batch][H]
- * in HBM, lens on the host; enqueued on the context stream (no sync). Ids
- * out of range are clamped and reported by the next rh_model_check. */
+/* Device-resident variant: ids_dev [batch][stride] int32 and out_dev
+ * [batch][H] in HBM, lens on the host; enqueued on the context stream (no
+ * sync). Ids out of range are clamped and reported by the next
+ * rh_model_check. */
 int rh_model_embed_device(rh_model *m, const int32_t *ids_dev,
                           const int32_t *lens, int batch, int stride,
                           float *out_dev);

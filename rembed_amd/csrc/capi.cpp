@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -19,20 +20,23 @@
 
 namespace rh {
 
-static thread_local std::string g_err;
+static thread_local char g_err[512];
 
-void set_error(const std::string& msg) { g_err = msg; }
+void set_error(const char* msg) noexcept { snprintf(g_err, sizeof g_err, "%s", msg ? msg : ""); }
 
-int fail(int code, const std::string& msg) {
-  g_err = msg;
+int fail(int code, const char* msg) noexcept {
+  set_error(msg);
   return code;
 }
 
-int hip_fail(hipError_t e, const char* what, const char* file, int line) {
-  char buf[512];
-  snprintf(buf, sizeof buf, "%s failed: %s (%s:%d)", what, hipGetErrorString(e),
-           file, line);
-  g_err = buf;
+int fail_exception(int code, const char* what) noexcept {
+  snprintf(g_err, sizeof g_err, "internal error: %s", what ? what : "exception");
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what, const char* file, int line) noexcept {
+  snprintf(g_err, sizeof g_err, "%s failed: %s (%s:%d)", what, hipGetErrorString(e), file,
+           line);
   return e == hipErrorOutOfMemory ? RH_ERR_OOM : RH_ERR_HIP;
 }
 
@@ -224,12 +228,41 @@ static hipError_t upload_planes(rh_weight* w, const std::vector<uint8_t>& img) {
   return e;
 }
 
-int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
-                int n, rh_weight** out) {
+// The unpacked fp32 fallback (MatMulFunc's raw weights, tensor.go:16-70)
+// takes any shape the device epilogue can store: k >= 1 and n a positive
+// multiple of 4 (4-column vector stores).
+static int check_raw_shape(int k, int n) {
+  char buf[160];
+  if (n < 4 || n % 4 != 0 || k < 1) {
+    snprintf(buf, sizeof buf, "unpacked fp32 weight needs k>=1 and n%%4==0, got k=%d n=%d", k, n);
+    return fail(RH_ERR_SHAPE, buf);
+  }
+  return RH_OK;
+}
+
+int pack_check(int mode, const float* bT, int k, int n, bool raw_ok) {
   static const char* names[] = {"PackB", "PackB8", "PackB8VNNI"};
-  int st = check_pack_shape(names[mode], k, n);
+  int st = raw_ok && mode == RH_MODE_F32 ? check_raw_shape(k, n)
+                                         : check_pack_shape(names[mode], k, n);
+  if (st != RH_OK || mode == RH_MODE_F32) return st;
+  const size_t count = (size_t)n * k;
+  for (size_t i = 0; i < count; i++)
+    if (!std::isfinite(bT[i])) {
+      char buf[160];
+      snprintf(buf, sizeof buf, "%s: weight [%zu,%zu] is not finite", names[mode], i / k, i % k);
+      return fail(RH_ERR_NONFINITE, buf);
+    }
+  return RH_OK;
+}
+
+int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
+                int n, rh_weight** out, bool raw_ok) {
+  static const char* names[] = {"PackB", "PackB8", "PackB8VNNI"};
+  int st = raw_ok && mode == RH_MODE_F32 ? check_raw_shape(k, n)
+                                         : check_pack_shape(names[mode], k, n);
   if (st != RH_OK) return st;
-  auto* w = new rh_weight();
+  // owned here until the upload succeeds (a throw or a failed upload frees it)
+  std::unique_ptr<rh_weight, void (*)(rh_weight*)> w(new rh_weight(), destroy_weight);
   w->ctx = ctx;
   w->mode = mode;
   w->k = k;
@@ -242,10 +275,7 @@ int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int 
   size_t elem = mode == RH_MODE_F32 ? 4 : 1;
   if (mode == RH_MODE_W8) st = quantize_b8(bT, k, n, q, scales);
   else if (mode == RH_MODE_A8W8) st = quantize_b8_vnni(bT, k, n, q, scales, colsum);
-  if (st != RH_OK) {
-    delete w;
-    return st;
-  }
+  if (st != RH_OK) return st;
   // Padded [np][kp] image, zero outside [n][k].
   std::vector<uint8_t> img((size_t)w->np * w->kp * elem, 0);
   for (int j = 0; j < n; j++) {
@@ -255,7 +285,7 @@ int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int 
   }
   hipError_t e = hipMalloc(&w->d_data, img.size());
   if (e == hipSuccess) e = hipMemcpy(w->d_data, img.data(), img.size(), hipMemcpyHostToDevice);
-  if (e == hipSuccess && mode != RH_MODE_A8W8) e = upload_planes(w, img);
+  if (e == hipSuccess && mode != RH_MODE_A8W8) e = upload_planes(w.get(), img);
   if (e == hipSuccess && !scales.empty()) {
     e = hipMalloc(&w->d_scales, n * sizeof(float));
     if (e == hipSuccess)
@@ -271,12 +301,9 @@ int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int 
     if (e == hipSuccess)
       e = hipMemcpy(w->d_bias, bias, n * sizeof(float), hipMemcpyHostToDevice);
   }
-  if (e != hipSuccess) {
-    destroy_weight(w);
-    return hip_fail(e, "weight upload", __FILE__, __LINE__);
-  }
+  if (e != hipSuccess) return hip_fail(e, "weight upload", __FILE__, __LINE__);
   ctx_retain(ctx);
-  *out = w;
+  *out = w.release();
   return RH_OK;
 }
 
@@ -309,10 +336,12 @@ void ctx_release(Context* ctx) {
 // Profiled as kind 0; `ops` is the algorithmic work credited to the launch
 // (a recompute pass credits 0 so the pair counts 2·M·K·N once).
 int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up, int k,
-                      int i, rh_weight** out) {
+                      int i, rh_weight** out, bool raw_ok) {
   // gate and up are each a PackB*-shaped matrix in the reference (two
   // newDense calls), so each must pass the packers' shape rule on its own
-  int st0 = check_pack_shape("gated PackB", k, i);
+  // (the unpacked fp32 fallback: whole groups of kGluGroup rows)
+  int st0 = raw_ok && mode == RH_MODE_F32 ? check_raw_shape(k, i)
+                                          : check_pack_shape("gated PackB", k, i);
   if (st0 != RH_OK) return st0;
   std::vector<float> inter((size_t)2 * i * k);
   for (int t = 0; t < i / kGluGroup; t++)
@@ -322,7 +351,7 @@ int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up
       memcpy(&inter[((size_t)2 * kGluGroup * t + kGluGroup + r) * k],
              up + ((size_t)kGluGroup * t + r) * k, sizeof(float) * k);
     }
-  int st = pack_weight(ctx, mode, inter.data(), nullptr, k, 2 * i, out);
+  int st = pack_weight(ctx, mode, inter.data(), nullptr, k, 2 * i, out, raw_ok);
   if (st == RH_OK) (*out)->glu = true;
   return st;
 }
@@ -559,9 +588,9 @@ using namespace rh;
 
 extern "C" {
 
-const char* rh_last_error(void) { return g_err.c_str(); }
+const char* rh_last_error(void) { return g_err; }
 
-int rh_version(void) { return 200; }
+int rh_version(void) { return 300; }
 
 int rh_device_count(int* count) {
   if (!count) return fail(RH_ERR_INVALID, "null count");
@@ -576,247 +605,294 @@ int rh_device_count(int* count) {
 }
 
 int rh_context_create(int device, rh_context** out) {
-  if (!out) return fail(RH_ERR_INVALID, "null out");
-  int n = 0;
-  if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
-    return fail(RH_ERR_NO_DEVICE, "no HIP device available");
-  if (device < 0 || device >= n) return fail(RH_ERR_INVALID, "device index out of range");
-  RH_HIP(hipSetDevice(device));
-  auto* c = new rh_context();
-  c->device = device;
-  hipError_t e = hipStreamCreate(&c->stream);
-  if (e != hipSuccess) {
-    delete c;
-    return hip_fail(e, "hipStreamCreate", __FILE__, __LINE__);
-  }
-  *out = c;
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (!out) return fail(RH_ERR_INVALID, "null out");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+      return fail(RH_ERR_NO_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n) return fail(RH_ERR_INVALID, "device index out of range");
+    RH_HIP(hipSetDevice(device));
+    auto* c = new rh_context();
+    c->device = device;
+    hipError_t e = hipStreamCreate(&c->stream);
+    if (e != hipSuccess) {
+      delete c;
+      return hip_fail(e, "hipStreamCreate", __FILE__, __LINE__);
+    }
+    *out = c;
+    return RH_OK;
+  });
 }
 
 void rh_context_destroy(rh_context* ctx) {
-  if (!ctx) return;
-  ctx_release(ctx);
+  api_void([&] {
+    if (!ctx) return;
+    ctx_release(ctx);
+  });
 }
 
 int rh_context_sync(rh_context* ctx) {
-  CTX_GUARD(ctx);
-  RH_HIP(hipStreamSynchronize(ctx->stream));
-  return RH_OK;
+  return api_call([&]() -> int {
+    CTX_GUARD(ctx);
+    RH_HIP(hipStreamSynchronize(ctx->stream));
+    return RH_OK;
+  });
 }
 
 void* rh_context_stream(rh_context* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
 
 int rh_context_set_option(rh_context* ctx, int option, int value) {
-  if (!ctx) return fail(RH_ERR_INVALID, "null context");
-  std::lock_guard<std::mutex> lk(ctx->mu);
-  switch (option) {
-    case RH_CTX_F32_ALGO:
-      if (value != F32_SPLIT3 && value != F32_NATIVE) return fail(RH_ERR_INVALID, "unknown fp32 algo");
-      ctx->f32_algo = value;
-      return RH_OK;
-    case RH_CTX_W8_TERMS:
-      if (value != 1 && value != 2) return fail(RH_ERR_INVALID, "w8 terms must be 1 or 2");
-      ctx->w8_terms = value;
-      return RH_OK;
-    case RH_CTX_BF_ALGO:
-      if (value < 0 || value > 1) return fail(RH_ERR_INVALID, "bf_algo must be 0 or 1");
-      ctx->bf_algo = value;
-      return RH_OK;
-    case RH_CTX_TILE_GROUP:
-      if (value < 1 || value > 64) return fail(RH_ERR_INVALID, "tile group must be 1..64");
-      ctx->tile_group = value;
-      return RH_OK;
-    case RH_CTX_BF_TILE:
-      if (value < 0 || value > kPlanesTileConfigs) return fail(RH_ERR_INVALID, "unknown planes tile");
-      ctx->bf_tile = value;
-      return RH_OK;
-    case RH_CTX_I8_TILE:
-      if (value < 0 || value > kI8TileConfigs) return fail(RH_ERR_INVALID, "unknown int8 tile");
-      ctx->i8_tile = value;
-      return RH_OK;
-    default:
-      return fail(RH_ERR_INVALID, "unknown context option");
-  }
+  return api_call([&]() -> int {
+    if (!ctx) return fail(RH_ERR_INVALID, "null context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    switch (option) {
+      case RH_CTX_F32_ALGO:
+        if (value != F32_SPLIT3 && value != F32_NATIVE) return fail(RH_ERR_INVALID, "unknown fp32 algo");
+        ctx->f32_algo = value;
+        return RH_OK;
+      case RH_CTX_W8_TERMS:
+        if (value != 1 && value != 2) return fail(RH_ERR_INVALID, "w8 terms must be 1 or 2");
+        ctx->w8_terms = value;
+        return RH_OK;
+      case RH_CTX_BF_ALGO:
+        if (value < 0 || value > 1) return fail(RH_ERR_INVALID, "bf_algo must be 0 or 1");
+        ctx->bf_algo = value;
+        return RH_OK;
+      case RH_CTX_TILE_GROUP:
+        if (value < 1 || value > 64) return fail(RH_ERR_INVALID, "tile group must be 1..64");
+        ctx->tile_group = value;
+        return RH_OK;
+      case RH_CTX_BF_TILE:
+        if (value < 0 || value > kPlanesTileConfigs) return fail(RH_ERR_INVALID, "unknown planes tile");
+        ctx->bf_tile = value;
+        return RH_OK;
+      case RH_CTX_I8_TILE:
+        if (value < 0 || value > kI8TileConfigs) return fail(RH_ERR_INVALID, "unknown int8 tile");
+        ctx->i8_tile = value;
+        return RH_OK;
+      default:
+        return fail(RH_ERR_INVALID, "unknown context option");
+    }
+  });
 }
 
 int rh_malloc(rh_context* ctx, size_t bytes, void** dev) {
-  if (!dev) return fail(RH_ERR_INVALID, "null out");
-  CTX_GUARD(ctx);
-  RH_HIP(hipMalloc(dev, bytes ? bytes : 1));
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (!dev) return fail(RH_ERR_INVALID, "null out");
+    CTX_GUARD(ctx);
+    RH_HIP(hipMalloc(dev, bytes ? bytes : 1));
+    return RH_OK;
+  });
 }
 
 int rh_free(rh_context* ctx, void* dev) {
-  CTX_GUARD(ctx);
-  RH_HIP(hipStreamSynchronize(ctx->stream));
-  RH_HIP(hipFree(dev));
-  return RH_OK;
+  return api_call([&]() -> int {
+    CTX_GUARD(ctx);
+    RH_HIP(hipStreamSynchronize(ctx->stream));
+    RH_HIP(hipFree(dev));
+    return RH_OK;
+  });
 }
 
 int rh_memcpy_h2d(rh_context* ctx, void* dst, const void* src, size_t bytes) {
-  CTX_GUARD(ctx);
-  RH_HIP(hipStreamSynchronize(ctx->stream));
-  RH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
-  return RH_OK;
+  return api_call([&]() -> int {
+    CTX_GUARD(ctx);
+    RH_HIP(hipStreamSynchronize(ctx->stream));
+    RH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return RH_OK;
+  });
 }
 
 int rh_memcpy_d2h(rh_context* ctx, void* dst, const void* src, size_t bytes) {
-  CTX_GUARD(ctx);
-  RH_HIP(hipStreamSynchronize(ctx->stream));
-  RH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
-  return RH_OK;
+  return api_call([&]() -> int {
+    CTX_GUARD(ctx);
+    RH_HIP(hipStreamSynchronize(ctx->stream));
+    RH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return RH_OK;
+  });
 }
 
 int rh_profile_enable(rh_context* ctx, int on) {
-  CTX_GUARD(ctx);
-  RH_HIP(hipStreamSynchronize(ctx->stream));
-  ctx->prof_clear();
-  ctx->profiling = on != 0;
-  return RH_OK;
+  return api_call([&]() -> int {
+    CTX_GUARD(ctx);
+    RH_HIP(hipStreamSynchronize(ctx->stream));
+    ctx->prof_clear();
+    ctx->profiling = on != 0;
+    return RH_OK;
+  });
 }
 
 int rh_profile_read(rh_context* ctx, int kind, rh_profile_stat* out) {
-  if (!out) return fail(RH_ERR_INVALID, "null out");
-  CTX_GUARD(ctx);
-  RH_HIP(hipStreamSynchronize(ctx->stream));
-  rh_profile_stat st{};
-  for (auto& r : ctx->recs) {
-    if (r.kind != kind) continue;
-    float ms = 0.0f;
-    RH_HIP(hipEventElapsedTime(&ms, r.a, r.b));
-    st.launches++;
-    st.total_ms += ms;
-    st.total_ops += r.ops;
-    st.total_bytes += r.bytes;
-  }
-  *out = st;
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (!out) return fail(RH_ERR_INVALID, "null out");
+    CTX_GUARD(ctx);
+    RH_HIP(hipStreamSynchronize(ctx->stream));
+    rh_profile_stat st{};
+    for (auto& r : ctx->recs) {
+      if (r.kind != kind) continue;
+      float ms = 0.0f;
+      RH_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+      st.launches++;
+      st.total_ms += ms;
+      st.total_ops += r.ops;
+      st.total_bytes += r.bytes;
+    }
+    *out = st;
+    return RH_OK;
+  });
 }
 
 int rh_attention(rh_context* ctx, const void* qkv, int in_bf16, int ldqkv, int q_off,
                  int k_off, int v_off, const int32_t* cu, int batch, int max_len, int heads,
                  int kv_heads, int dh, float scale, int causal, int window, int precision,
                  float* out, int ldout) {
-  if (!qkv || !cu || !out) return fail(RH_ERR_INVALID, "null argument");
-  if (dh != 32 && dh != 64 && dh != 128 && dh != 256)
-    return fail(RH_ERR_SHAPE, "attention head dim must be 32, 64, 128 or 256");
-  if (heads < 1 || kv_heads < 1 || heads % kv_heads)
-    return fail(RH_ERR_SHAPE, "heads must be a positive multiple of kv_heads");
-  if (precision != 1 && precision != 3) return fail(RH_ERR_INVALID, "precision must be 1 or 3");
-  if (in_bf16 && precision != 1) return fail(RH_ERR_INVALID, "bf16 input takes precision 1");
-  if (batch < 0 || max_len < 0 || window < 0) return fail(RH_ERR_INVALID, "negative size");
-  if (ldqkv % 8 || q_off % 8 || k_off % 8 || v_off % 8 || ldout % 4 || q_off < 0 ||
-      k_off < 0 || v_off < 0 || ((uintptr_t)qkv & 15) || ((uintptr_t)out & 15))
-    return fail(RH_ERR_SHAPE, "attention rows and offsets must be 16-byte aligned");
-  CTX_GUARD(ctx);
-  AttnArgs a{};
-  a.qkv = qkv;
-  a.in_bf16 = in_bf16 ? 1 : 0;
-  a.ldqkv = ldqkv;
-  a.q_off = q_off;
-  a.k_off = k_off;
-  a.v_off = v_off;
-  a.cu = cu;
-  a.batch = batch;
-  a.max_len = max_len;
-  a.heads = heads;
-  a.kv_heads = kv_heads;
-  a.dh = dh;
-  a.scale = scale;
-  a.ctx = out;
-  a.ldctx = ldout;
-  a.causal = causal ? 1 : 0;
-  a.window = window;
-  int slot = -1;
-  RH_HIP(ctx->prof_begin(3, 0.0, 0.0, &slot));
-  RH_HIP(launch_attention(a, precision, ctx->stream));
-  RH_HIP(ctx->prof_end(slot));
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (!qkv || !cu || !out) return fail(RH_ERR_INVALID, "null argument");
+    if (dh != 32 && dh != 64 && dh != 128 && dh != 256)
+      return fail(RH_ERR_SHAPE, "attention head dim must be 32, 64, 128 or 256");
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads)
+      return fail(RH_ERR_SHAPE, "heads must be a positive multiple of kv_heads");
+    if (precision != 1 && precision != 3) return fail(RH_ERR_INVALID, "precision must be 1 or 3");
+    if (in_bf16 && precision != 1) return fail(RH_ERR_INVALID, "bf16 input takes precision 1");
+    if (batch < 0 || max_len < 0 || window < 0) return fail(RH_ERR_INVALID, "negative size");
+    if (ldqkv % 8 || q_off % 8 || k_off % 8 || v_off % 8 || ldout % 4 || q_off < 0 ||
+        k_off < 0 || v_off < 0 || ((uintptr_t)qkv & 15) || ((uintptr_t)out & 15))
+      return fail(RH_ERR_SHAPE, "attention rows and offsets must be 16-byte aligned");
+    CTX_GUARD(ctx);
+    AttnArgs a{};
+    a.qkv = qkv;
+    a.in_bf16 = in_bf16 ? 1 : 0;
+    a.ldqkv = ldqkv;
+    a.q_off = q_off;
+    a.k_off = k_off;
+    a.v_off = v_off;
+    a.cu = cu;
+    a.batch = batch;
+    a.max_len = max_len;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.dh = dh;
+    a.scale = scale;
+    a.ctx = out;
+    a.ldctx = ldout;
+    a.causal = causal ? 1 : 0;
+    a.window = window;
+    int slot = -1;
+    RH_HIP(ctx->prof_begin(3, 0.0, 0.0, &slot));
+    RH_HIP(launch_attention(a, precision, ctx->stream));
+    RH_HIP(ctx->prof_end(slot));
+    return RH_OK;
+  });
 }
 
 int rh_pack_weight_gated(rh_context* ctx, int mode, const float* gate,
                                     const float* up, int k, int i, rh_weight** out) {
-  if (!out || !gate || !up) return fail(RH_ERR_INVALID, "null argument");
-  if (mode < RH_MODE_F32 || mode > RH_MODE_A8W8) return fail(RH_ERR_INVALID, "unknown mode");
-  CTX_GUARD(ctx);
-  return pack_weight_gated(ctx, mode, gate, up, k, i, out);
+  return api_call([&]() -> int {
+    if (!out || !gate || !up) return fail(RH_ERR_INVALID, "null argument");
+    if (mode < RH_MODE_F32 || mode > RH_MODE_A8W8) return fail(RH_ERR_INVALID, "unknown mode");
+    CTX_GUARD(ctx);
+    return pack_weight_gated(ctx, mode, gate, up, k, i, out);
+  });
 }
 
 int rh_pack_weight(rh_context* ctx, int mode, const float* bT, const float* bias,
                    int k, int n, rh_weight** out) {
-  if (!out || !bT) return fail(RH_ERR_INVALID, "null argument");
-  if (mode < RH_MODE_F32 || mode > RH_MODE_A8W8) return fail(RH_ERR_INVALID, "unknown mode");
-  CTX_GUARD(ctx);
-  return pack_weight(ctx, mode, bT, bias, k, n, out);
+  return api_call([&]() -> int {
+    if (!out || !bT) return fail(RH_ERR_INVALID, "null argument");
+    if (mode < RH_MODE_F32 || mode > RH_MODE_A8W8) return fail(RH_ERR_INVALID, "unknown mode");
+    CTX_GUARD(ctx);
+    return pack_weight(ctx, mode, bT, bias, k, n, out);
+  });
 }
 
 void rh_weight_destroy(rh_weight* w) {
-  if (!w) return;
-  Context* ctx = w->ctx;
-  {
-    std::lock_guard<std::mutex> lk(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
-    destroy_weight(w);
-  }
-  ctx_release(ctx);
+  api_void([&] {
+    if (!w) return;
+    Context* ctx = w->ctx;
+    {
+      std::lock_guard<std::mutex> lk(ctx->mu);
+      (void)hipSetDevice(ctx->device);
+      (void)hipStreamSynchronize(ctx->stream);
+      destroy_weight(w);
+    }
+    ctx_release(ctx);
+  });
 }
 
 int rh_weight_info(const rh_weight* w, int* mode, int* k, int* n) {
-  if (!w) return fail(RH_ERR_INVALID, "null weight");
-  if (mode) *mode = w->mode;
-  if (k) *k = w->k;
-  if (n) *n = w->n;
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (!w) return fail(RH_ERR_INVALID, "null weight");
+    if (mode) *mode = w->mode;
+    if (k) *k = w->k;
+    if (n) *n = w->n;
+    return RH_OK;
+  });
 }
 
 int rh_weight_export(const rh_weight* w, int8_t* q, float* scales, int32_t* colsum) {
-  if (!w) return fail(RH_ERR_INVALID, "null weight");
-  Context* ctx = w->ctx;
-  CTX_GUARD(ctx);
-  RH_HIP(hipStreamSynchronize(ctx->stream));
-  if (q) {
-    if (w->mode == RH_MODE_F32) return fail(RH_ERR_INVALID, "fp32 weight has no int8 image");
-    std::vector<int8_t> img((size_t)w->np * w->kp);
-    RH_HIP(hipMemcpy(img.data(), w->d_data, img.size(), hipMemcpyDeviceToHost));
-    for (int j = 0; j < w->n; j++)
-      memcpy(q + (size_t)j * w->k, img.data() + (size_t)j * w->kp, w->k);
-  }
-  if (scales) {
-    if (!w->d_scales) return fail(RH_ERR_INVALID, "weight has no scales");
-    RH_HIP(hipMemcpy(scales, w->d_scales, w->n * sizeof(float), hipMemcpyDeviceToHost));
-  }
-  if (colsum) {
-    if (!w->d_colsum) return fail(RH_ERR_INVALID, "weight has no colsum");
-    RH_HIP(hipMemcpy(colsum, w->d_colsum, w->n * sizeof(int32_t), hipMemcpyDeviceToHost));
-  }
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (!w) return fail(RH_ERR_INVALID, "null weight");
+    Context* ctx = w->ctx;
+    CTX_GUARD(ctx);
+    RH_HIP(hipStreamSynchronize(ctx->stream));
+    if (q) {
+      if (w->mode == RH_MODE_F32) return fail(RH_ERR_INVALID, "fp32 weight has no int8 image");
+      std::vector<int8_t> img((size_t)w->np * w->kp);
+      RH_HIP(hipMemcpy(img.data(), w->d_data, img.size(), hipMemcpyDeviceToHost));
+      for (int j = 0; j < w->n; j++)
+        memcpy(q + (size_t)j * w->k, img.data() + (size_t)j * w->kp, w->k);
+    }
+    if (scales) {
+      if (!w->d_scales) return fail(RH_ERR_INVALID, "weight has no scales");
+      RH_HIP(hipMemcpy(scales, w->d_scales, w->n * sizeof(float), hipMemcpyDeviceToHost));
+    }
+    if (colsum) {
+      if (!w->d_colsum) return fail(RH_ERR_INVALID, "weight has no colsum");
+      RH_HIP(hipMemcpy(colsum, w->d_colsum, w->n * sizeof(int32_t), hipMemcpyDeviceToHost));
+    }
+    return RH_OK;
+  });
 }
 
 int rh_quantize_rows_u8(rh_context* ctx, const float* a, int m, int k, uint8_t* qa,
                         int ldq, float* row_scales) {
-  if (m < 0 || k < 1) return fail(RH_ERR_INVALID, "bad m/k");
-  if (ldq < k || ldq % 16 != 0) return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
-  if (m > 0 && (!a || !qa || !row_scales)) return fail(RH_ERR_INVALID, "null argument");
-  CTX_GUARD(ctx);
-  RH_HIP(launch_quantize_rows_u8(a, k, m, k, qa, ldq, row_scales, ctx->stream));
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (m < 0 || k < 1) return fail(RH_ERR_INVALID, "bad m/k");
+    if (ldq < k || ldq % 16 != 0) return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+    if (m > 0 && (!a || !qa || !row_scales)) return fail(RH_ERR_INVALID, "null argument");
+    CTX_GUARD(ctx);
+    RH_HIP(launch_quantize_rows_u8(a, k, m, k, qa, ldq, row_scales, ctx->stream));
+    return RH_OK;
+  });
 }
 
 int rh_gelu_quantize_rows_u8(rh_context* ctx, const float* a, int m, int k, uint8_t* qa,
                              int ldq, float* row_scales) {
-  if (m < 0 || k < 8 || k % 8 != 0) return fail(RH_ERR_INVALID, "k must be a positive multiple of 8");
-  if (ldq < k || ldq % 16 != 0) return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
-  if (m > 0 && (!a || !qa || !row_scales)) return fail(RH_ERR_INVALID, "null argument");
-  CTX_GUARD(ctx);
-  RH_HIP(launch_quantize_rows_u8(a, k, m, k, qa, ldq, row_scales, ctx->stream, ACT_GELU));
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (m < 0 || k < 8 || k % 8 != 0) return fail(RH_ERR_INVALID, "k must be a positive multiple of 8");
+    if (ldq < k || ldq % 16 != 0) return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+    if (m > 0 && (!a || !qa || !row_scales)) return fail(RH_ERR_INVALID, "null argument");
+    CTX_GUARD(ctx);
+    RH_HIP(launch_quantize_rows_u8(a, k, m, k, qa, ldq, row_scales, ctx->stream, ACT_GELU));
+    return RH_OK;
+  });
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-static int check_gemm(const rh_weight* w, int mode, const float* a, const void* dst, int m) {
+// A weight is used only on the context that packed it: its device copy lives
+// on that context's device, and the context's mutex orders its use against
+// rh_weight_destroy.
+static int check_owner(const rh_context* ctx, const rh_weight* w) {
+  if (!ctx) return fail(RH_ERR_INVALID, "null context");
   if (!w) return fail(RH_ERR_INVALID, "null weight");
+  if (w->ctx != ctx) return fail(RH_ERR_INVALID, "weight belongs to another context");
+  return RH_OK;
+}
+
+static int check_gemm(const rh_context* ctx, const rh_weight* w, int mode, const float* a,
+                      const void* dst, int m) {
+  if (int st = check_owner(ctx, w)) return st;
   if (mode >= 0 && w->mode != mode) return fail(RH_ERR_INVALID, "weight packed for another mode");
   if (mode >= 0 && w->glu) return fail(RH_ERR_INVALID, "gated weight: use rh_linear with a gated act");
   if (m < 0) return fail(RH_ERR_INVALID, "negative m");
@@ -835,157 +911,177 @@ static int check_gemm(const rh_weight* w, int mode, const float* a, const void* 
 // n or an unaligned dst goes through the workspace and a 2-D copy.
 int rh_matmul(rh_context* ctx, float* dst, const float* a, const float* bT, int m, int k,
               int n) {
-  if (m < 0 || k < 1 || n < 1) return fail(RH_ERR_SHAPE, "bad shape (m >= 0, k >= 1, n >= 1)");
-  if (m > 0 && (!dst || !a || !bT)) return fail(RH_ERR_INVALID, "null argument");
-  CTX_GUARD(ctx);
-  if (m == 0) return RH_OK;
-  const int ldk = (int)round_up(k, 64), np = (int)round_up(n, kWeightRowPad);
-  const bool direct = n % 4 == 0 && aligned16(dst);
-  const int ldc = direct ? n : (int)round_up(n, 4);
-  if ((long long)std::max(m, np) * std::max(ldk, ldc) >= (1LL << 30))
-    return fail(RH_ERR_SHAPE, "matrix too large for one call");
-  const size_t ap = (size_t)m * ldk * 2, bp = (size_t)np * ldk * 2;
-  const size_t cbytes = direct ? 0 : (size_t)m * ldc * 4;
-  hipError_t e = ctx->ensure_ws(2 * ap + 2 * bp + cbytes);
-  if (e != hipSuccess) return hip_fail(e, "matmul workspace", __FILE__, __LINE__);
-  uint8_t* ws = static_cast<uint8_t*>(ctx->ws);
-  __bf16* ah = reinterpret_cast<__bf16*>(ws);
-  __bf16* al = reinterpret_cast<__bf16*>(ws + ap);
-  __bf16* bh = reinterpret_cast<__bf16*>(ws + 2 * ap);
-  __bf16* bl = reinterpret_cast<__bf16*>(ws + 2 * ap + bp);
-  float* ct = direct ? dst : reinterpret_cast<float*>(ws + 2 * ap + 2 * bp);
-  hipStream_t s = ctx->stream;
-  RH_HIP(launch_split_bf16(a, k, m, k, ah, al, ldk, s));
-  RH_HIP(launch_split_bf16(bT, k, n, k, bh, bl, ldk, s));
-  if (np > n) {  // zero rows n..np of both B planes (rows are ldk*2 bytes)
-    const int words = (np - n) * ldk / 2;
-    RH_HIP(launch_fill_zero(reinterpret_cast<float*>(bh + (size_t)n * ldk), words, s));
-    RH_HIP(launch_fill_zero(reinterpret_cast<float*>(bl + (size_t)n * ldk), words, s));
-  }
-  GemmPlArgs g{};
-  g.Ah = ah;
-  g.Al = al;
-  g.lda = ldk;
-  g.Bh = bh;
-  g.Bl = bl;
-  g.ldb = ldk;
-  g.M = m;
-  g.N = n;
-  g.K = k;
-  g.C = ct;
-  g.ldc = ldc;
-  g.act = ACT_NONE;
-  g.tile_group = ctx->tile_group;
-  int slot = -1;
-  const double M = m, K = k, N = n;
-  RH_HIP(ctx->prof_begin(2, 2.0 * M * K * N, 4.0 * (M * K + N * K + M * N), &slot));
-  RH_HIP(launch_gemm_planes(g, 2, 2, ctx->bf_tile, s));
-  RH_HIP(ctx->prof_end(slot));
-  if (!direct)
-    RH_HIP(hipMemcpy2DAsync(dst, (size_t)n * 4, ct, (size_t)ldc * 4, (size_t)n * 4, m,
-                            hipMemcpyDeviceToDevice, s));
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (m < 0 || k < 1 || n < 1) return fail(RH_ERR_SHAPE, "bad shape (m >= 0, k >= 1, n >= 1)");
+    if (m > 0 && (!dst || !a || !bT)) return fail(RH_ERR_INVALID, "null argument");
+    CTX_GUARD(ctx);
+    if (m == 0) return RH_OK;
+    const int ldk = (int)round_up(k, 64), np = (int)round_up(n, kWeightRowPad);
+    const bool direct = n % 4 == 0 && aligned16(dst);
+    const int ldc = direct ? n : (int)round_up(n, 4);
+    if ((long long)std::max(m, np) * std::max(ldk, ldc) >= (1LL << 30))
+      return fail(RH_ERR_SHAPE, "matrix too large for one call");
+    const size_t ap = (size_t)m * ldk * 2, bp = (size_t)np * ldk * 2;
+    const size_t cbytes = direct ? 0 : (size_t)m * ldc * 4;
+    hipError_t e = ctx->ensure_ws(2 * ap + 2 * bp + cbytes);
+    if (e != hipSuccess) return hip_fail(e, "matmul workspace", __FILE__, __LINE__);
+    uint8_t* ws = static_cast<uint8_t*>(ctx->ws);
+    __bf16* ah = reinterpret_cast<__bf16*>(ws);
+    __bf16* al = reinterpret_cast<__bf16*>(ws + ap);
+    __bf16* bh = reinterpret_cast<__bf16*>(ws + 2 * ap);
+    __bf16* bl = reinterpret_cast<__bf16*>(ws + 2 * ap + bp);
+    float* ct = direct ? dst : reinterpret_cast<float*>(ws + 2 * ap + 2 * bp);
+    hipStream_t s = ctx->stream;
+    RH_HIP(launch_split_bf16(a, k, m, k, ah, al, ldk, s));
+    RH_HIP(launch_split_bf16(bT, k, n, k, bh, bl, ldk, s));
+    if (np > n) {  // zero rows n..np of both B planes (rows are ldk*2 bytes)
+      const int words = (np - n) * ldk / 2;
+      RH_HIP(launch_fill_zero(reinterpret_cast<float*>(bh + (size_t)n * ldk), words, s));
+      RH_HIP(launch_fill_zero(reinterpret_cast<float*>(bl + (size_t)n * ldk), words, s));
+    }
+    GemmPlArgs g{};
+    g.Ah = ah;
+    g.Al = al;
+    g.lda = ldk;
+    g.Bh = bh;
+    g.Bl = bl;
+    g.ldb = ldk;
+    g.M = m;
+    g.N = n;
+    g.K = k;
+    g.C = ct;
+    g.ldc = ldc;
+    g.act = ACT_NONE;
+    g.tile_group = ctx->tile_group;
+    int slot = -1;
+    const double M = m, K = k, N = n;
+    RH_HIP(ctx->prof_begin(2, 2.0 * M * K * N, 4.0 * (M * K + N * K + M * N), &slot));
+    RH_HIP(launch_gemm_planes(g, 2, 2, ctx->bf_tile, s));
+    RH_HIP(ctx->prof_end(slot));
+    if (!direct)
+      RH_HIP(hipMemcpy2DAsync(dst, (size_t)n * 4, ct, (size_t)ldc * 4, (size_t)n * 4, m,
+                              hipMemcpyDeviceToDevice, s));
+    return RH_OK;
+  });
 }
 
 int rh_matmul_packed(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m) {
-  int st = check_gemm(w, RH_MODE_F32, a, dst, m);
-  if (st) return st;
-  CTX_GUARD(ctx);
-  return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
-                    nullptr, false);
+  return api_call([&]() -> int {
+    int st = check_gemm(ctx, w, RH_MODE_F32, a, dst, m);
+    if (st) return st;
+    CTX_GUARD(ctx);
+    return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
+                      nullptr, false);
+  });
 }
 
 int rh_matmul_packed8(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m) {
-  int st = check_gemm(w, RH_MODE_W8, a, dst, m);
-  if (st) return st;
-  CTX_GUARD(ctx);
-  return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
-                    nullptr, false);
+  return api_call([&]() -> int {
+    int st = check_gemm(ctx, w, RH_MODE_W8, a, dst, m);
+    if (st) return st;
+    CTX_GUARD(ctx);
+    return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, nullptr, 0,
+                      nullptr, false);
+  });
 }
 
 int rh_matmul_packed_vnni(rh_context* ctx, float* dst, const float* a, const rh_weight* w,
                           int m, uint8_t* qa, int ldq, float* row_scales) {
-  int st = check_gemm(w, RH_MODE_A8W8, a, dst, m);
-  if (st) return st;
-  if (m > 0 && (!qa || !row_scales)) return fail(RH_ERR_INVALID, "null scratch");
-  if (ldq < w->k || ldq % 16 != 0)
-    return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
-  CTX_GUARD(ctx);
-  return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, qa, ldq,
-                    row_scales, true);
+  return api_call([&]() -> int {
+    int st = check_gemm(ctx, w, RH_MODE_A8W8, a, dst, m);
+    if (st) return st;
+    if (m > 0 && (!qa || !row_scales)) return fail(RH_ERR_INVALID, "null scratch");
+    if (ldq < w->k || ldq % 16 != 0)
+      return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+    CTX_GUARD(ctx);
+    return run_linear(ctx, w, a, w->k, m, dst, w->n, ACT_NONE, nullptr, qa, ldq,
+                      row_scales, true);
+  });
 }
 
 int rh_gemm_u8s8_i32(rh_context* ctx, int32_t* acc, const uint8_t* qa, int ldq,
                      const rh_weight* w, int m) {
-  if (!w) return fail(RH_ERR_INVALID, "null weight");
-  if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight packed for another mode");
-  if (m < 0) return fail(RH_ERR_INVALID, "negative m");
-  if (m > 0 && (!acc || !qa)) return fail(RH_ERR_INVALID, "null argument");
-  if (ldq < w->k || ldq % 16 != 0)
-    return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
-  if (!aligned16(acc) || !aligned16(qa)) return fail(RH_ERR_INVALID, "buffers must be 16-byte aligned");
-  CTX_GUARD(ctx);
-  return run_gemm_i8(ctx, w, qa, ldq, nullptr, m, EPI_ACC, acc, w->n, ACT_NONE, nullptr,
-                     nullptr, nullptr, 2.0 * m * w->k * w->n);
+  return api_call([&]() -> int {
+    if (int st = check_owner(ctx, w)) return st;
+    if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight packed for another mode");
+    if (m < 0) return fail(RH_ERR_INVALID, "negative m");
+    if (m > 0 && (!acc || !qa)) return fail(RH_ERR_INVALID, "null argument");
+    if (ldq < w->k || ldq % 16 != 0)
+      return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+    if (!aligned16(acc) || !aligned16(qa)) return fail(RH_ERR_INVALID, "buffers must be 16-byte aligned");
+    CTX_GUARD(ctx);
+    return run_gemm_i8(ctx, w, qa, ldq, nullptr, m, EPI_ACC, acc, w->n, ACT_NONE, nullptr,
+                       nullptr, nullptr, 2.0 * m * w->k * w->n);
+  });
 }
 
 int rh_linear(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m,
               int act, uint8_t* qa, int ldq, float* row_scales) {
-  int st = check_gemm(w, -1, a, dst, m);
-  if (st) return st;
-  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU_ERF) return fail(RH_ERR_INVALID, "unknown act");
-  if (w->glu != is_glu(act))
-    return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
-  if (w->mode == RH_MODE_A8W8) {
-    if (m > 0 && (!qa || !row_scales)) return fail(RH_ERR_INVALID, "null scratch");
-    if (ldq < w->k || ldq % 16 != 0)
-      return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
-  }
-  CTX_GUARD(ctx);
-  return run_linear(ctx, w, a, w->k, m, dst, w->glu ? w->n / 2 : w->n, act, w->d_bias, qa,
-                    ldq, row_scales, true);
+  return api_call([&]() -> int {
+    int st = check_gemm(ctx, w, -1, a, dst, m);
+    if (st) return st;
+    if (act < RH_ACT_NONE || act > RH_ACT_GEGLU_ERF) return fail(RH_ERR_INVALID, "unknown act");
+    if (w->glu != is_glu(act))
+      return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
+    if (w->mode == RH_MODE_A8W8) {
+      if (m > 0 && (!qa || !row_scales)) return fail(RH_ERR_INVALID, "null scratch");
+      if (ldq < w->k || ldq % 16 != 0)
+        return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+    }
+    CTX_GUARD(ctx);
+    return run_linear(ctx, w, a, w->k, m, dst, w->glu ? w->n / 2 : w->n, act, w->d_bias, qa,
+                      ldq, row_scales, true);
+  });
 }
 
 int rh_linear_u8(rh_context* ctx, const uint8_t* qa, int ldq, const float* row_scales,
                  const rh_weight* w, int m, int act, uint8_t* qa_out, int ldq_out,
                  float* rs_out, float* absmax_scratch) {
-  if (!w) return fail(RH_ERR_INVALID, "null weight");
-  if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight must be RH_MODE_A8W8");
-  if (m < 0) return fail(RH_ERR_INVALID, "negative m");
-  if (act < RH_ACT_NONE || act > RH_ACT_GEGLU_ERF) return fail(RH_ERR_INVALID, "unknown act");
-  if (w->glu != is_glu(act))
-    return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
-  if (m > 0 && (!qa || !row_scales || !qa_out || !rs_out || !absmax_scratch))
-    return fail(RH_ERR_INVALID, "null argument");
-  if (ldq < w->k || ldq % 16 != 0)
-    return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
-  if (ldq_out < w->n || ldq_out % 16 != 0)
-    return fail(RH_ERR_INVALID, "ldq_out must be >= n and a multiple of 16");
-  if (!aligned16(qa) || !aligned16(qa_out)) return fail(RH_ERR_INVALID, "buffers must be 16-byte aligned");
-  CTX_GUARD(ctx);
-  if (m == 0) return RH_OK;
-  RH_HIP(launch_fill_zero(absmax_scratch, m, ctx->stream));
-  int st = run_gemm_i8(ctx, w, qa, ldq, row_scales, m, EPI_ABSMAX, nullptr, 0, act, w->d_bias,
-                       absmax_scratch, nullptr, 2.0 * m * w->k * w->n);
-  if (st) return st;
-  return run_gemm_i8(ctx, w, qa, ldq, row_scales, m, EPI_QUANT, qa_out, ldq_out, act,
-                     w->d_bias, absmax_scratch, rs_out, 0.0);
+  return api_call([&]() -> int {
+    if (int st = check_owner(ctx, w)) return st;
+    if (w->mode != RH_MODE_A8W8) return fail(RH_ERR_INVALID, "weight must be RH_MODE_A8W8");
+    if (m < 0) return fail(RH_ERR_INVALID, "negative m");
+    // the re-quantizing epilogue has no gate/up pairing: gated weights go
+    // through rh_linear (fp32 act(gate)*up rows) and rh_quantize_rows_u8
+    if (w->glu || is_glu(act))
+      return fail(RH_ERR_INVALID, "rh_linear_u8 takes no gated weight or gated act");
+    if (act != RH_ACT_NONE && act != RH_ACT_GELU) return fail(RH_ERR_INVALID, "unknown act");
+    if (m > 0 && (!qa || !row_scales || !qa_out || !rs_out || !absmax_scratch))
+      return fail(RH_ERR_INVALID, "null argument");
+    if (ldq < w->k || ldq % 16 != 0)
+      return fail(RH_ERR_INVALID, "ldq must be >= k and a multiple of 16");
+    if (ldq_out < w->n || ldq_out % 16 != 0)
+      return fail(RH_ERR_INVALID, "ldq_out must be >= n and a multiple of 16");
+    if (!aligned16(qa) || !aligned16(qa_out)) return fail(RH_ERR_INVALID, "buffers must be 16-byte aligned");
+    CTX_GUARD(ctx);
+    if (m == 0) return RH_OK;
+    RH_HIP(launch_fill_zero(absmax_scratch, m, ctx->stream));
+    int st = run_gemm_i8(ctx, w, qa, ldq, row_scales, m, EPI_ABSMAX, nullptr, 0, act, w->d_bias,
+                         absmax_scratch, nullptr, 2.0 * m * w->k * w->n);
+    if (st) return st;
+    return run_gemm_i8(ctx, w, qa, ldq, row_scales, m, EPI_QUANT, qa_out, ldq_out, act,
+                       w->d_bias, absmax_scratch, rs_out, 0.0);
+  });
 }
 
 int rh_gelu(rh_context* ctx, float* x, size_t n) {
-  if (n > 0 && !x) return fail(RH_ERR_INVALID, "null x");
-  CTX_GUARD(ctx);
-  RH_HIP(launch_gelu(x, n, ctx->stream));
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (n > 0 && !x) return fail(RH_ERR_INVALID, "null x");
+    CTX_GUARD(ctx);
+    RH_HIP(launch_gelu(x, n, ctx->stream));
+    return RH_OK;
+  });
 }
 
 int rh_layernorm(rh_context* ctx, float* x, const float* gamma, const float* beta, int m,
                  int n, float eps) {
-  if (m < 0 || n < 1 || n > 2048) return fail(RH_ERR_INVALID, "bad shape (n <= 2048)");
-  if (m > 0 && (!x || !gamma || !beta)) return fail(RH_ERR_INVALID, "null argument");
-  CTX_GUARD(ctx);
-  RH_HIP(launch_layernorm(x, gamma, beta, m, n, eps, ctx->stream));
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (m < 0 || n < 1 || n > 2048) return fail(RH_ERR_INVALID, "bad shape (n <= 2048)");
+    if (m > 0 && (!x || !gamma || !beta)) return fail(RH_ERR_INVALID, "null argument");
+    CTX_GUARD(ctx);
+    RH_HIP(launch_layernorm(x, gamma, beta, m, n, eps, ctx->stream));
+    return RH_OK;
+  });
 }
 
 }  // extern "C"

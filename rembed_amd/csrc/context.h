@@ -67,13 +67,20 @@ using Context = rh_context;
 
 void ctx_retain(Context* ctx);
 void ctx_release(Context* ctx);  // frees the context on the last reference
+// raw_ok: mode RH_MODE_F32 as newDense's last resort, the unpacked MatMulFunc
+// weights (any k >= 1 and n % 4 == 0) rather than PackB's n % 16 rule.
 int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int k,
-                int n, rh_weight** out);
+                int n, rh_weight** out, bool raw_ok = false);
+// The packers' refusal rules without packing: RH_OK when pack_weight(mode)
+// would accept bT [n][k], else the status it would return (RH_ERR_SHAPE:
+// PackB*'s n % 16 rule, or the unpacked rule with raw_ok; RH_ERR_NONFINITE:
+// a NaN/Inf weight, pack8.go:43-48 / pack_vnni.go:48-56).
+int pack_check(int mode, const float* bT, int k, int n, bool raw_ok = false);
 void destroy_weight(rh_weight* w);
 // gate/up [i][k] -> one interleaved [2i][k] weight (rows 8t..8t+3 = gate
 // 4t..4t+3, rows 8t+4..8t+7 = up 4t..4t+3), packed in `mode`, glu = true
 int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up, int k,
-                      int i, rh_weight** out);
+                      int i, rh_weight** out, bool raw_ok = false);
 int quantize_b8(const float* bT, int k, int n, std::vector<int8_t>& q,
                 std::vector<float>& scales);
 int quantize_b8_vnni(const float* bT, int k, int n, std::vector<int8_t>& q,

@@ -404,4 +404,25 @@ hipError_t launch_dense_head(const float* pooled, int batch, int H, int D, const
   return e;
 }
 
+// Gated-MLP glue over separate gate and up rows (qwen3.go:530-539,
+// gemma3.go:365-374): out = act(gate) * up element by element, with the same
+// float32 glu_act the fused gated epilogues apply, so the result equals the
+// fused form bit for bit. Used when newDense packed gate and up in different
+// modes. out may alias gate.
+__global__ void glu_rows_kernel(const float* gate, const float* up, float* out, size_t n,
+                                int act) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = glu_act(gate[i], up[i], act);
+}
+
+hipError_t launch_glu_rows(const float* gate, const float* up, float* out, size_t n, int act,
+                           hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  if (!is_glu(act)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(glu_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gate,
+                     up, out, n, act);
+  return hipGetLastError();
+}
+
 }  // namespace rh

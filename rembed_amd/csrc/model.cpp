@@ -42,10 +42,15 @@ struct Layer {
 // and gate|up into one gated weight; norm weights are uploaded as the
 // reference uses them (Gemma's with the unit offset folded in).
 struct DecLayer {
-  rh_weight* qkv = nullptr;  // [qdim + 2 kvdim][H]
+  rh_weight* qkv = nullptr;  // [qdim + 2 kvdim][H], or null when q, k, v are separate
   rh_weight* o = nullptr;    // [H][qdim]
-  rh_weight* gu = nullptr;   // gated [2I][H]
+  rh_weight* gu = nullptr;   // gated [2I][H], or null when gate, up are separate
   rh_weight* down = nullptr; // [H][I]
+  // The reference packs q, k, v, gate and up one matrix at a time
+  // (qwen3.go:479-481,528-529; gemma3.go:297-299,363-364), so newDense can
+  // leave them in different modes; a group whose modes differ stays as
+  // separate weights (each [out][H]) and runs as separate GEMMs.
+  rh_weight *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *up = nullptr;
   float *in_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr,
         *pre_ffn = nullptr, *post_ffn = nullptr;
   bool global = true;
@@ -85,6 +90,11 @@ struct rh_model {
   // row's cos/sin loads wait behind the previous row's stores (vmcnt counts
   // both), which costs more than the separate pass's traffic.
   bool qk_epilogue = false;
+  // RH_OPT_FUSE_PROJECTIONS: decoder q|k|v and gate|up packed as one weight
+  // each where newDense leaves the group in one mode (default), or always
+  // as separate weights like the reference; set before finalize.
+  bool fuse_projections = true;
+  bool split_gu_any = false;  // some layer runs gate and up as separate GEMMs
   // extra streams (default priority) and the fork/join events of a forward
   // split into parts
   static constexpr int kMaxParts = 4;
@@ -92,8 +102,10 @@ struct rh_model {
   hipEvent_t ev_fork = nullptr, ev_join[kMaxParts] = {};
 
   // workspace, sized for cap rows / cap_batch texts
-  int cap = 0, cap_batch = 0, cap_ids = 0;
+  int cap = 0, cap_batch = 0;
+  size_t cap_ids = 0;
   float *x = nullptr, *qkv = nullptr, *ctxb = nullptr, *y = nullptr, *hid = nullptr;
+  float* hid2 = nullptr;  // [cap][I] up rows of a layer whose gate and up are separate
   __bf16* qkvh = nullptr;                 // bf16 QKV rows (bf16 attention)
   // bf16 hi/lo activation planes written by the producers of the
   // weight-only int8 / fp32 GEMMs: p0 [cap][ld0] holds a width-H or
@@ -110,6 +122,11 @@ struct rh_model {
   int32_t* cu_pinned = nullptr;
   hipEvent_t cu_evt = nullptr;
   int cu_pinned_cap = 0;
+  // pinned int32 staging rows of the host-buffer embed calls (ids narrowed
+  // from the caller's int64); reused once the previous call has synced
+  int32_t* ids_pinned = nullptr;
+  size_t ids_pinned_cap = 0;
+  std::vector<int32_t> cu_host;  // packed row offsets of the current call
 
   ~rh_model() { release(); }
 
@@ -118,9 +135,10 @@ struct rh_model {
                     (void*)rs, (void*)cu_d, (void*)ids_d, (void*)out_d, (void*)qkvh,
                     (void*)qa2, (void*)rs2, (void*)absmax, (void*)normed, (void*)pooled,
                     (void*)dense_hid, (void*)p0h, (void*)p0l, (void*)p1h, (void*)p1l,
-                    (void*)pos_d})
+                    (void*)pos_d, (void*)hid2})
       if (p) (void)hipFree(p);
     x = qkv = ctxb = y = hid = rs = out_d = rs2 = absmax = normed = pooled = dense_hid = nullptr;
+    hid2 = nullptr;
     pos_d = nullptr;
     qa = qa2 = nullptr;
     qkvh = p0h = p0l = p1h = p1l = nullptr;
@@ -157,7 +175,7 @@ struct rh_model {
     }
     layers.clear();
     for (auto& L : dlayers) {
-      for (rh_weight* w : {L.qkv, L.o, L.gu, L.down}) {
+      for (rh_weight* w : {L.qkv, L.o, L.gu, L.down, L.q, L.k, L.v, L.gate, L.up}) {
         if (!w) continue;
         destroy_weight(w);
         ctx_release(ctx);
@@ -175,6 +193,9 @@ struct rh_model {
     err_d = nullptr;
     if (cu_pinned) (void)hipHostFree(cu_pinned);
     cu_pinned = nullptr;
+    if (ids_pinned) (void)hipHostFree(ids_pinned);
+    ids_pinned = nullptr;
+    ids_pinned_cap = 0;
     if (cu_evt) (void)hipEventDestroy(cu_evt);
     cu_evt = nullptr;
   }
@@ -196,7 +217,7 @@ struct rh_model {
   // Does w take its input as producer-written planes? (w runs on planes and
   // K is a multiple of 64, so the producers' K columns fill the planes.)
   bool planes_in(const rh_weight* w) const {
-    return producer_planes && p0h && linear_on_planes(ctx, w) && w->k % 64 == 0;
+    return w && producer_planes && p0h && linear_on_planes(ctx, w) && w->k % 64 == 0;
   }
   Planes plane(int which, const rh_weight* w) const {
     Planes p;
@@ -208,7 +229,7 @@ struct rh_model {
   float eps() const { return cfg.layer_norm_eps == 0.0f ? 1e-12f : cfg.layer_norm_eps; }
   int max_seq() const { return cfg.max_position - cfg.position_offset; }
 
-  int ensure_ws(int rows, int batch, int ids_elems) {
+  int ensure_ws(int rows, int batch, size_t ids_elems) {
     const int H = this->H(), I = this->I();
     if (rows > cap || batch > cap_batch || ids_elems > cap_ids)
       RH_HIP(hipStreamSynchronize(ctx->stream));  // buffers may be in flight
@@ -217,9 +238,9 @@ struct rh_model {
       for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
                       (void*)rs, (void*)qkvh, (void*)qa2, (void*)rs2, (void*)absmax,
                       (void*)normed, (void*)pos_d, (void*)p0h, (void*)p0l, (void*)p1h,
-                      (void*)p1l})
+                      (void*)p1l, (void*)hid2})
         if (p) RH_HIP(hipFree(p));
-      x = qkv = ctxb = y = hid = rs = rs2 = absmax = normed = nullptr;
+      x = qkv = ctxb = y = hid = rs = rs2 = absmax = normed = hid2 = nullptr;
       qa = qa2 = nullptr;
       qkvh = p0h = p0l = p1h = p1l = nullptr;
       pos_d = nullptr;
@@ -230,6 +251,7 @@ struct rh_model {
       RH_HIP(dalloc(&ctxb, r * ctx_width()));
       RH_HIP(dalloc(&y, r * H));
       RH_HIP(dalloc(&hid, r * I));
+      if (split_gu_any) RH_HIP(dalloc(&hid2, r * I));
       RH_HIP(dalloc(&qa, r * ldq_for(std::max(H, ctx_width()))));
       RH_HIP(dalloc(&qa2, r * ldq_for(I)));
       if (decoder()) {
@@ -268,7 +290,7 @@ struct rh_model {
     if (ids_elems > cap_ids) {
       if (ids_d) RH_HIP(hipFree(ids_d));
       ids_d = nullptr;
-      const int n = (int)round_up(ids_elems, 4096);
+      const size_t n = round_up(ids_elems, 4096);
       RH_HIP(dalloc(&ids_d, n));
       cap_ids = n;
     }
@@ -290,6 +312,19 @@ struct rh_model {
     return RH_OK;
   }
 
+  // Pinned staging for `elems` int32 ids (grow-only; the previous call has
+  // synchronized its stream before returning, so the old buffer is idle).
+  int ensure_ids_staging(size_t elems) {
+    if (elems <= ids_pinned_cap) return RH_OK;
+    if (ids_pinned) RH_HIP(hipHostFree(ids_pinned));
+    ids_pinned = nullptr;
+    ids_pinned_cap = 0;
+    const size_t n = round_up(elems, 4096);
+    RH_HIP(hipHostMalloc((void**)&ids_pinned, n * sizeof(int32_t)));
+    ids_pinned_cap = n;
+    return RH_OK;
+  }
+
   // Validate lengths (bert.go:741-747) and build packed row offsets.
   int plan(const int32_t* lens, int batch, std::vector<int32_t>& cu, int* max_len) {
     cu.assign(batch + 1, 0);
@@ -306,6 +341,8 @@ struct rh_model {
                  lens[b], max_seq());
         return fail(RH_ERR_SEQ, buf);
       }
+      if ((long long)cu[b] + lens[b] > (long long)INT32_MAX)
+        return fail(RH_ERR_INVALID, "total tokens of the batch exceed 2^31 - 1");
       cu[b + 1] = cu[b] + lens[b];
       mx = std::max(mx, (int)lens[b]);
     }
@@ -670,10 +707,13 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
   // Parts (see plan_parts): allowed when no linear falls back to the
   // context's split workspace.
   bool no_ws = true;
+  auto ws = [&](const rh_weight* w, bool pin) { return w && uses_split_ws(w, pin); };
   for (const DecLayer& L : dlayers) {
-    no_ws = no_ws && !uses_split_ws(L.qkv, planes_in(L.qkv)) &&
-            !uses_split_ws(L.o, planes_in(L.o)) && !uses_split_ws(L.gu, planes_in(L.gu)) &&
-            !uses_split_ws(L.down, planes_in(L.down) && linear_on_planes(ctx, L.gu));
+    // separate q/k/v/gate/up weights take fp32 rows (no producer planes)
+    no_ws = no_ws && !ws(L.qkv, planes_in(L.qkv)) && !ws(L.q, false) && !ws(L.k, false) &&
+            !ws(L.v, false) && !ws(L.o, planes_in(L.o)) && !ws(L.gu, planes_in(L.gu)) &&
+            !ws(L.gate, false) && !ws(L.up, false) &&
+            !ws(L.down, L.gu && planes_in(L.down) && linear_on_planes(ctx, L.gu));
   }
   std::vector<Part> parts;
   if ((st = plan_parts(cu, no_ws, s, parts))) return st;
@@ -699,16 +739,28 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     // QK-norm + RoPE epilogue where that applies, else by the separate pass
     const bool hb = attn_precision == 1;
     bool fused_qk = false;
-    if (qk_epilogue && hb && planes_in(L.qkv)) {
+    if (qk_epilogue && hb && L.qkv && planes_in(L.qkv)) {
       const QkEpilogue q{L.q_norm, L.k_norm, local ? cos_l : cos_g, local ? sin_l : sin_g,
                          pos_d + r0, nq(), nkv(), dh(), e};
       st = run_linear_qk(ctx, L.qkv, pq, Mp, q, qkvh + r0 * qkvw, qkvw, &fused_qk);
       if (st) return st;
     }
-    if (!fused_qk) {
+    if (!fused_qk && L.qkv) {
       st = run_linear(ctx, L.qkv, normedp, H, Mp, qkvp, qkvw, ACT_NONE, nullptr, qap, ldqH,
                       rsp, false, planes_in(L.qkv) ? &pq : nullptr);
       if (st) return st;
+    } else if (!fused_qk) {
+      // q, k, v in different modes: three GEMMs over the fp32 normed rows,
+      // each writing its columns of the q|k|v rows
+      const rh_weight* sep[3] = {L.q, L.k, L.v};
+      const int col[3] = {0, qd, qd + kvd};
+      for (int j = 0; j < 3; j++) {
+        st = run_linear(ctx, sep[j], normedp, H, Mp, qkvp + col[j], qkvw, ACT_NONE, nullptr,
+                        qap, ldqH, rsp, needs_q(sep[j]));
+        if (st) return st;
+      }
+    }
+    if (!fused_qk) {
       RH_HIP(launch_qk_norm_rope(qkvp, qkvw, Mp, nq(), nkv(), dh(), L.q_norm, L.k_norm, e,
                                  local ? cos_l : cos_g, local ? sin_l : sin_g, pos_d + r0,
                                  hb ? qkvh + r0 * qkvw : nullptr, ps));
@@ -756,14 +808,29 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
                   gemma() ? L.pre_ffn : L.post_attn, L.gu, false));
     // gated MLP: one GEMM over gate|up writes act(gate) * up (as the down
     // projection's planes when it takes them), then down
-    const Planes pg = at(plane(0, L.gu), r0), pd = at(plane(1, L.down), r0);
-    const bool pdown = planes_in(L.down) && linear_on_planes(ctx, L.gu);
-    st = run_linear(ctx, L.gu, normedp, H, Mp, hidp, I, glu, nullptr, qap, ldqH, rsp, false,
-                    planes_in(L.gu) ? &pg : nullptr, pdown ? &pd : nullptr);
-    if (st) return st;
-    st = run_linear(ctx, L.down, hidp, I, Mp, yp, H, ACT_NONE, nullptr, qa2p, ldqI, rs2p,
-                    needs_q(L.down), pdown ? &pd : nullptr);
-    if (st) return st;
+    if (L.gu) {
+      const Planes pg = at(plane(0, L.gu), r0), pd = at(plane(1, L.down), r0);
+      const bool pdown = planes_in(L.down) && linear_on_planes(ctx, L.gu);
+      st = run_linear(ctx, L.gu, normedp, H, Mp, hidp, I, glu, nullptr, qap, ldqH, rsp, false,
+                      planes_in(L.gu) ? &pg : nullptr, pdown ? &pd : nullptr);
+      if (st) return st;
+      st = run_linear(ctx, L.down, hidp, I, Mp, yp, H, ACT_NONE, nullptr, qa2p, ldqI, rs2p,
+                      needs_q(L.down), pdown ? &pd : nullptr);
+      if (st) return st;
+    } else {
+      // gate and up in different modes: two GEMMs, the glue, then down
+      float* hid2p = hid2 + r0 * I;
+      st = run_linear(ctx, L.gate, normedp, H, Mp, hidp, I, ACT_NONE, nullptr, qap, ldqH, rsp,
+                      needs_q(L.gate));
+      if (st) return st;
+      st = run_linear(ctx, L.up, normedp, H, Mp, hid2p, I, ACT_NONE, nullptr, qap, ldqH, rsp,
+                      needs_q(L.up));
+      if (st) return st;
+      RH_HIP(launch_glu_rows(hidp, hid2p, hidp, (size_t)Mp * I, glu, ps));
+      st = run_linear(ctx, L.down, hidp, I, Mp, yp, H, ACT_NONE, nullptr, qa2p, ldqI, rs2p,
+                      needs_q(L.down));
+      if (st) return st;
+    }
     // x += [RMSNorm(mlp, post_ffn)]; then the next layer's input norm, or the
     // final RMSNorm in place (qwen3.go:543, gemma3.go:379)
     const bool last = li + 1 == dlayers.size();
@@ -834,17 +901,36 @@ static int upload(const float* src, size_t n, float** dst) {
   return RH_OK;
 }
 
+// A packer's refusal (bad shape, non-finite weight) sends newDense to the
+// next mode; anything else (device allocation, HIP, host memory) is the
+// caller's error and ends the load.
+static bool pack_refused(int st) { return st == RH_ERR_SHAPE || st == RH_ERR_NONFINITE; }
+
 // newDense (bert.go:263-278): requested mode, then the fallback chain
-// A8W8 -> W8 -> F32 on a pack error.
+// A8W8 -> W8 -> F32 when the packer refuses the matrix.
 static int new_dense(rh_model* m, const float* raw, const float* bias, int in, int out,
                      rh_weight** w) {
-  if (m->quant == RH_QUANT_FULL &&
-      pack_weight(m->ctx, RH_MODE_A8W8, raw, bias, in, out, w) == RH_OK)
-    return RH_OK;
-  if (m->quant >= RH_QUANT_WEIGHTS &&
-      pack_weight(m->ctx, RH_MODE_W8, raw, bias, in, out, w) == RH_OK)
-    return RH_OK;
-  return pack_weight(m->ctx, RH_MODE_F32, raw, bias, in, out, w);
+  int st;
+  if (m->quant == RH_QUANT_FULL) {
+    st = pack_weight(m->ctx, RH_MODE_A8W8, raw, bias, in, out, w);
+    if (!pack_refused(st)) return st;
+  }
+  if (m->quant >= RH_QUANT_WEIGHTS) {
+    st = pack_weight(m->ctx, RH_MODE_W8, raw, bias, in, out, w);
+    if (!pack_refused(st)) return st;
+  }
+  // PackB, then the unpacked weights (bert.go:274-277)
+  return pack_weight(m->ctx, RH_MODE_F32, raw, bias, in, out, w, true);
+}
+
+// The mode newDense ends at for one matrix: the requested one unless its
+// packer refuses the matrix, then the next (bert.go:263-278).
+static int dense_mode(const rh_model* m, const float* raw, int in, int out) {
+  if (m->quant == RH_QUANT_FULL && pack_check(RH_MODE_A8W8, raw, in, out) == RH_OK)
+    return RH_MODE_A8W8;
+  if (m->quant >= RH_QUANT_WEIGHTS && pack_check(RH_MODE_W8, raw, in, out) == RH_OK)
+    return RH_MODE_W8;
+  return RH_MODE_F32;
 }
 
 static int finalize_bert(rh_model* m) {
@@ -924,16 +1010,43 @@ static int finalize_bert(rh_model* m) {
 }
 
 
-// newDense for the gated gate|up pair: the same A8W8 -> W8 -> F32 chain.
+// newDense for the gate and up projections (qwen3.go:528-529,
+// gemma3.go:363-364): each matrix goes through the chain on its own. When both
+// end in the same mode they are packed as one gated weight (the GEMM's
+// epilogue then writes act(gate) * up), else as two weights.
 static int new_dense_gated(rh_model* m, const float* gate, const float* up, int in, int i,
-                           rh_weight** w) {
-  if (m->quant == RH_QUANT_FULL &&
-      pack_weight_gated(m->ctx, RH_MODE_A8W8, gate, up, in, i, w) == RH_OK)
-    return RH_OK;
-  if (m->quant >= RH_QUANT_WEIGHTS &&
-      pack_weight_gated(m->ctx, RH_MODE_W8, gate, up, in, i, w) == RH_OK)
-    return RH_OK;
-  return pack_weight_gated(m->ctx, RH_MODE_F32, gate, up, in, i, w);
+                           DecLayer& L) {
+  const int mg = dense_mode(m, gate, in, i), mu = dense_mode(m, up, in, i);
+  if (m->fuse_projections && mg == mu) {
+    int st = pack_weight_gated(m->ctx, mg, gate, up, in, i, &L.gu, true);
+    if (st == RH_OK || !pack_refused(st)) return st;
+  }
+  m->split_gu_any = true;
+  int st = new_dense(m, gate, nullptr, in, i, &L.gate);
+  if (st) return st;
+  return new_dense(m, up, nullptr, in, i, &L.up);
+}
+
+// newDense for q, k and v (qwen3.go:479-481, gemma3.go:297-299): one fused
+// [qdim + 2 kvdim][H] weight when all three end in the same mode, else three.
+static int new_dense_qkv(rh_model* m, const float* qw, const float* kw, const float* vw, int H,
+                         int qd, int kvd, DecLayer& L) {
+  const int mq = dense_mode(m, qw, H, qd), mk = dense_mode(m, kw, H, kvd),
+            mv = dense_mode(m, vw, H, kvd);
+  if (m->fuse_projections && mq == mk && mk == mv) {
+    // rows fused: each output column is the same dot product as in the
+    // reference's three separate applyDense calls
+    std::vector<float> qkvw((size_t)(qd + 2 * kvd) * H);
+    memcpy(qkvw.data(), qw, sizeof(float) * (size_t)qd * H);
+    memcpy(qkvw.data() + (size_t)qd * H, kw, sizeof(float) * (size_t)kvd * H);
+    memcpy(qkvw.data() + (size_t)(qd + kvd) * H, vw, sizeof(float) * (size_t)kvd * H);
+    int st = pack_weight(m->ctx, mq, qkvw.data(), nullptr, H, qd + 2 * kvd, &L.qkv, true);
+    if (st == RH_OK || !pack_refused(st)) return st;
+  }
+  int st = new_dense(m, qw, nullptr, H, qd, &L.q);
+  if (st) return st;
+  if ((st = new_dense(m, kw, nullptr, H, kvd, &L.k))) return st;
+  return new_dense(m, vw, nullptr, H, kvd, &L.v);
 }
 
 // Upload a norm weight, adding Gemma's unit offset (gemma3.go:40-50).
@@ -1031,16 +1144,11 @@ static int finalize_decoder(rh_model* m) {
     }
     DecLayer& L = m->dlayers[l];
     L.global = !gemma || (l + 1) % m->cfg.sliding_pattern == 0;  // gemma3.go:87
-    // q|k|v rows fused: each output column is the same dot product as in the
-    // reference's three separate applyDense calls.
-    std::vector<float> qkvw((size_t)(qd + 2 * kvd) * H);
-    memcpy(qkvw.data(), qw->data.data(), sizeof(float) * (size_t)qd * H);
-    memcpy(qkvw.data() + (size_t)qd * H, kw->data.data(), sizeof(float) * (size_t)kvd * H);
-    memcpy(qkvw.data() + (size_t)(qd + kvd) * H, vw->data.data(),
-           sizeof(float) * (size_t)kvd * H);
-    if ((st = new_dense(m, qkvw.data(), nullptr, H, qd + 2 * kvd, &L.qkv))) return st;
+    if ((st = new_dense_qkv(m, qw->data.data(), kw->data.data(), vw->data.data(), H, qd, kvd,
+                            L)))
+      return st;
     if ((st = new_dense(m, ow->data.data(), nullptr, qd, H, &L.o))) return st;
-    if ((st = new_dense_gated(m, gw->data.data(), uw->data.data(), H, I, &L.gu))) return st;
+    if ((st = new_dense_gated(m, gw->data.data(), uw->data.data(), H, I, L))) return st;
     if ((st = new_dense(m, dw->data.data(), nullptr, I, H, &L.down))) return st;
     if ((st = upload_norm(in_n, H, gemma, &L.in_norm))) return st;
     if ((st = upload_norm(qn, dh, gemma, &L.q_norm))) return st;
@@ -1065,176 +1173,219 @@ static int finalize_decoder(rh_model* m) {
 extern "C" {
 
 int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_model** out) {
-  if (!ctx || !cfg || !out) return fail(RH_ERR_INVALID, "null argument");
-  if (cfg->arch != RH_ARCH_BERT && cfg->arch != RH_ARCH_QWEN3 && cfg->arch != RH_ARCH_GEMMA3)
-    return fail(RH_ERR_INVALID, "unsupported arch");
-  if (cfg->hidden <= 0 || cfg->heads <= 0) return fail(RH_ERR_INVALID, "bad hidden/heads");
-  if (cfg->intermediate <= 0 || cfg->layers <= 0 || cfg->vocab <= 0 || cfg->max_position <= 0)
-    return fail(RH_ERR_INVALID, "bad config sizes");
-  if (cfg->hidden % 64 != 0 || cfg->hidden > 4096)
-    return fail(RH_ERR_INVALID, "hidden must be a multiple of 64 and <= 4096");
-  if (quant < RH_QUANT_NONE || quant > RH_QUANT_FULL) return fail(RH_ERR_INVALID, "bad quant");
-  if (cfg->arch == RH_ARCH_BERT) {
-    if (cfg->hidden % cfg->heads != 0 || cfg->hidden > 2048)
-      return fail(RH_ERR_INVALID, "hidden must divide by heads and be <= 2048");
-    const int dh = cfg->hidden / cfg->heads;
-    if (dh != 32 && dh != 64 && dh != 128)
-      return fail(RH_ERR_INVALID, "head dim must be 32, 64 or 128");
-  } else {
-    const int nkv = cfg->kv_heads > 0 ? cfg->kv_heads : cfg->heads;
-    const int dh = cfg->head_dim > 0 ? cfg->head_dim : cfg->hidden / cfg->heads;
-    if (cfg->heads % nkv != 0) return fail(RH_ERR_INVALID, "heads must be a multiple of kv_heads");
-    if (dh != 64 && dh != 128 && dh != 256)
-      return fail(RH_ERR_INVALID, "head dim must be 64, 128 or 256");
-    if (cfg->intermediate % 8 != 0) return fail(RH_ERR_INVALID, "intermediate must divide by 8");
-    if (cfg->rope_theta <= 0) return fail(RH_ERR_INVALID, "rope_theta must be positive");
-    if (cfg->arch == RH_ARCH_GEMMA3) {
-      if (cfg->rope_local_theta <= 0 || cfg->sliding_pattern <= 0 || cfg->sliding_window <= 0 ||
-          cfg->query_pre_attn_scalar <= 0)
-        return fail(RH_ERR_INVALID, "gemma needs local theta, window, pattern, attn scalar");
-      if (cfg->dense_hidden < 0 || cfg->dense_hidden > 16384)
-        return fail(RH_ERR_INVALID, "bad dense_hidden");
+  return api_call([&]() -> int {
+    if (!ctx || !cfg || !out) return fail(RH_ERR_INVALID, "null argument");
+    if (cfg->arch != RH_ARCH_BERT && cfg->arch != RH_ARCH_QWEN3 && cfg->arch != RH_ARCH_GEMMA3)
+      return fail(RH_ERR_INVALID, "unsupported arch");
+    if (cfg->hidden <= 0 || cfg->heads <= 0) return fail(RH_ERR_INVALID, "bad hidden/heads");
+    if (cfg->intermediate <= 0 || cfg->layers <= 0 || cfg->vocab <= 0 || cfg->max_position <= 0)
+      return fail(RH_ERR_INVALID, "bad config sizes");
+    if (cfg->hidden % 64 != 0 || cfg->hidden > 4096)
+      return fail(RH_ERR_INVALID, "hidden must be a multiple of 64 and <= 4096");
+    if (quant < RH_QUANT_NONE || quant > RH_QUANT_FULL) return fail(RH_ERR_INVALID, "bad quant");
+    if (cfg->arch == RH_ARCH_BERT) {
+      if (cfg->intermediate % 4 != 0)
+        return fail(RH_ERR_INVALID, "intermediate must divide by 4");
+      if (cfg->hidden % cfg->heads != 0 || cfg->hidden > 2048)
+        return fail(RH_ERR_INVALID, "hidden must divide by heads and be <= 2048");
+      const int dh = cfg->hidden / cfg->heads;
+      if (dh != 32 && dh != 64 && dh != 128)
+        return fail(RH_ERR_INVALID, "head dim must be 32, 64 or 128");
+    } else {
+      const int nkv = cfg->kv_heads > 0 ? cfg->kv_heads : cfg->heads;
+      const int dh = cfg->head_dim > 0 ? cfg->head_dim : cfg->hidden / cfg->heads;
+      if (cfg->heads % nkv != 0) return fail(RH_ERR_INVALID, "heads must be a multiple of kv_heads");
+      if (dh != 64 && dh != 128 && dh != 256)
+        return fail(RH_ERR_INVALID, "head dim must be 64, 128 or 256");
+      if (cfg->intermediate % 8 != 0) return fail(RH_ERR_INVALID, "intermediate must divide by 8");
+      if (cfg->rope_theta <= 0) return fail(RH_ERR_INVALID, "rope_theta must be positive");
+      if (cfg->arch == RH_ARCH_GEMMA3) {
+        if (cfg->rope_local_theta <= 0 || cfg->sliding_pattern <= 0 || cfg->sliding_window <= 0 ||
+            cfg->query_pre_attn_scalar <= 0)
+          return fail(RH_ERR_INVALID, "gemma needs local theta, window, pattern, attn scalar");
+        if (cfg->dense_hidden < 0 || cfg->dense_hidden > 16384)
+          return fail(RH_ERR_INVALID, "bad dense_hidden");
+      }
     }
-  }
-  auto* m = new rh_model();
-  m->ctx = ctx;
-  ctx_retain(ctx);
-  m->cfg = *cfg;
-  m->quant = quant;
-  m->attn_precision = quant == RH_QUANT_NONE ? 3 : 1;
-  *out = m;
-  return RH_OK;
+    auto* m = new rh_model();
+    m->ctx = ctx;
+    ctx_retain(ctx);
+    m->cfg = *cfg;
+    m->quant = quant;
+    m->attn_precision = quant == RH_QUANT_NONE ? 3 : 1;
+    *out = m;
+    return RH_OK;
+  });
 }
 
 int rh_model_set_option(rh_model* m, int option, int value) {
-  if (!m) return fail(RH_ERR_INVALID, "null model");
-  std::lock_guard<std::mutex> lk(m->mu);
-  if (option == RH_OPT_ATTN_PRECISION) {
-    if (value != 1 && value != 3) return fail(RH_ERR_INVALID, "attn precision must be 1 or 3");
-    m->attn_precision = value;
-    return RH_OK;
-  }
-  if (option == RH_OPT_FUSED_FFN1) {
-    if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fused FFN1 must be 0 or 1");
-    m->fused_ffn1 = value != 0;
-    return RH_OK;
-  }
-  if (option == RH_OPT_PRODUCER_PLANES) {
-    if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "producer planes must be 0 or 1");
-    m->producer_planes = value != 0;
-    return RH_OK;
-  }
-  if (option == RH_OPT_QK_EPILOGUE) {
-    if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "qk epilogue must be 0 or 1");
-    m->qk_epilogue = value != 0;
+  return api_call([&]() -> int {
+    if (!m) return fail(RH_ERR_INVALID, "null model");
+    std::lock_guard<std::mutex> lk(m->mu);
+    if (option == RH_OPT_ATTN_PRECISION) {
+      if (value != 1 && value != 3) return fail(RH_ERR_INVALID, "attn precision must be 1 or 3");
+      m->attn_precision = value;
+      return RH_OK;
+    }
+    if (option == RH_OPT_FUSED_FFN1) {
+      if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fused FFN1 must be 0 or 1");
+      m->fused_ffn1 = value != 0;
+      return RH_OK;
+    }
+    if (option == RH_OPT_PRODUCER_PLANES) {
+      if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "producer planes must be 0 or 1");
+      m->producer_planes = value != 0;
+      return RH_OK;
+    }
+    if (option == RH_OPT_QK_EPILOGUE) {
+      if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "qk epilogue must be 0 or 1");
+      m->qk_epilogue = value != 0;
+      return RH_OK;
+    }
+    if (option == RH_OPT_FUSE_PROJECTIONS) {
+    if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fuse projections must be 0 or 1");
+    if (m->finalized) return fail(RH_ERR_INVALID, "fuse projections is set before finalize");
+    m->fuse_projections = value != 0;
     return RH_OK;
   }
   if (option == RH_OPT_STREAMS) {
-    if (value < 1 || value > rh_model::kMaxParts)
-      return fail(RH_ERR_INVALID, "streams must be 1 to 4");
-    m->streams = value;
-    return RH_OK;
-  }
-  return fail(RH_ERR_INVALID, "unknown option");
+      if (value < 1 || value > rh_model::kMaxParts)
+        return fail(RH_ERR_INVALID, "streams must be 1 to 4");
+      m->streams = value;
+      return RH_OK;
+    }
+    return fail(RH_ERR_INVALID, "unknown option");
+  });
 }
 
 int rh_model_set_tensor(rh_model* m, const char* name, const float* host,
                         const int64_t* shape, int ndim) {
-  if (!m || !name || !host || (ndim > 0 && !shape) || ndim < 0 || ndim > 4)
-    return fail(RH_ERR_INVALID, "bad argument");
-  std::lock_guard<std::mutex> lk(m->mu);
-  if (m->finalized) return fail(RH_ERR_INVALID, "model already finalized");
-  HostTensor t;
-  size_t n = 1;
-  for (int i = 0; i < ndim; i++) {
-    if (shape[i] < 0) return fail(RH_ERR_INVALID, "negative dim");
-    t.shape.push_back(shape[i]);
-    n *= (size_t)shape[i];
-  }
-  t.data.assign(host, host + n);
-  m->pending[name] = std::move(t);
-  return RH_OK;
+  return api_call([&]() -> int {
+    if (!m || !name || !host || (ndim > 0 && !shape) || ndim < 0 || ndim > 4)
+      return fail(RH_ERR_INVALID, "bad argument");
+    std::lock_guard<std::mutex> lk(m->mu);
+    if (m->finalized) return fail(RH_ERR_INVALID, "model already finalized");
+    HostTensor t;
+    size_t n = 1;
+    for (int i = 0; i < ndim; i++) {
+      if (shape[i] < 0) return fail(RH_ERR_INVALID, "negative dim");
+      t.shape.push_back(shape[i]);
+      n *= (size_t)shape[i];
+    }
+    t.data.assign(host, host + n);
+    m->pending[name] = std::move(t);
+    return RH_OK;
+  });
 }
 
 int rh_model_finalize(rh_model* m) {
-  MODEL_GUARD(m);
-  if (m->finalized) return fail(RH_ERR_INVALID, "model already finalized");
-  int st = m->decoder() ? finalize_decoder(m) : finalize_bert(m);
-  if (st) {
-    std::string msg = rh_last_error();
-    m->release();
-    set_error(msg);
-    return st;
-  }
-  m->pending.clear();
-  m->finalized = true;
-  return RH_OK;
+  return api_call([&]() -> int {
+    MODEL_GUARD(m);
+    if (m->finalized) return fail(RH_ERR_INVALID, "model already finalized");
+    // A failed finalize (a status or an exception) releases every device
+    // object made so far, so the model is left empty rather than half built.
+    int st;
+    try {
+      st = m->decoder() ? finalize_decoder(m) : finalize_bert(m);
+    } catch (...) {
+      m->release();
+      throw;
+    }
+    if (st) {
+      char msg[512];
+      snprintf(msg, sizeof msg, "%s", rh_last_error());
+      m->release();
+      set_error(msg);
+      return st;
+    }
+    m->pending.clear();
+    m->finalized = true;
+    return RH_OK;
+  });
 }
 
 void rh_model_destroy(rh_model* m) {
-  if (!m) return;
-  rh_context* ctx = m->ctx;
-  {
-    std::lock_guard<std::mutex> lk(ctx->mu);
-    m->release();
-  }
-  m->ctx = nullptr;
-  delete m;
-  ctx_release(ctx);
+  api_void([&] {
+    if (!m) return;
+    rh_context* ctx = m->ctx;
+    {
+      std::lock_guard<std::mutex> lk(ctx->mu);
+      m->release();
+    }
+    m->ctx = nullptr;
+    delete m;
+    ctx_release(ctx);
+  });
 }
 
-// Per-layer weight handles in load order (the same set for every arch).
-static std::vector<const rh_weight*> all_weights(const rh_model* m) {
-  std::vector<const rh_weight*> v;
+// Does every per-layer weight satisfy pred? (Walks the handles in place:
+// the introspection calls allocate nothing.)
+static bool all_weights(const rh_model* m, bool (*pred)(const rh_weight*)) {
   for (const Layer& L : m->layers)
-    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) v.push_back(w);
+    for (const rh_weight* w : {L.qkv, L.o, L.f1, L.f2})
+      if (!pred(w)) return false;
   for (const DecLayer& L : m->dlayers)
-    for (const rh_weight* w : {L.qkv, L.o, L.gu, L.down}) v.push_back(w);
-  return v;
+    for (const rh_weight* w : {L.qkv, L.o, L.gu, L.down, L.q, L.k, L.v, L.gate, L.up})
+      if (w && !pred(w)) return false;
+  return true;
 }
 
 int rh_model_quantized(const rh_model* m) {
   if (!m || !m->finalized) return 0;
-  for (const rh_weight* w : all_weights(m))
-    if (w->mode == RH_MODE_F32) return 0;
-  return 1;
+  return all_weights(m, [](const rh_weight* w) { return w->mode != RH_MODE_F32; }) ? 1 : 0;
 }
 
 int rh_model_quantized_activations(const rh_model* m) {
   if (!m || !m->finalized) return 0;
-  for (const rh_weight* w : all_weights(m))
-    if (w->mode != RH_MODE_A8W8) return 0;
-  return 1;
+  return all_weights(m, [](const rh_weight* w) { return w->mode == RH_MODE_A8W8; }) ? 1 : 0;
 }
 
-static int embed_common(rh_model* m, const int32_t* ids, const int32_t* lens, int batch,
+// The host-buffer forward of Embed / EmbedTokens. ids are int64 as the
+// reference passes them (bert.go:649, rembed.go:416); each one is checked
+// against the vocabulary (bert.go:797-800) while it is narrowed into the
+// model's pinned int32 staging rows, which go to HBM in one copy.
+static int embed_common(rh_model* m, const int64_t* ids, const int32_t* lens, int batch,
                         int stride, float* out, bool pool) {
   if (!ids || !lens || !out || batch < 0 || stride < 1)
     return fail(RH_ERR_INVALID, "bad argument");
   if (!m->finalized) return fail(RH_ERR_INVALID, "model not finalized");
   if (batch == 0) return RH_OK;
-  std::vector<int32_t> cu;
+  const size_t elems = (size_t)batch * (size_t)stride;
+  if (elems > (size_t)INT32_MAX)
+    return fail(RH_ERR_INVALID, "batch * stride exceeds 2^31 - 1 token slots");
+  for (int b = 0; b < batch; b++)
+    if (lens[b] > stride) return fail(RH_ERR_INVALID, "length exceeds row stride");
+  std::vector<int32_t>& cu = m->cu_host;
   int max_len = 0;
   int st = m->plan(lens, batch, cu, &max_len);
   if (st) return st;
+  const int M = cu[batch], H = m->cfg.hidden;
+  if ((st = m->ensure_ws(M, batch, elems))) return st;
+  if ((st = m->ensure_ids_staging(elems))) return st;
+  int32_t* stage = m->ids_pinned;
   for (int b = 0; b < batch; b++) {
-    if (lens[b] > stride) return fail(RH_ERR_INVALID, "length exceeds row stride");
+    const int64_t* row = ids + (size_t)b * stride;
+    int32_t* srow = stage + (size_t)b * stride;
     for (int t = 0; t < lens[b]; t++) {
-      const int32_t id = ids[(size_t)b * stride + t];
+      const int64_t id = row[t];
       if (id < 0 || id >= m->cfg.vocab) {
         char buf[160];
-        snprintf(buf, sizeof buf, "text %d: token id %d out of vocab range %d", b, id,
-                 m->cfg.vocab);
+        snprintf(buf, sizeof buf, "text %d: token id %lld out of vocab range %d", b,
+                 (long long)id, m->cfg.vocab);
         return fail(RH_ERR_VOCAB, buf);
       }
+      srow[t] = (int32_t)id;
     }
+    for (int t = lens[b]; t < stride; t++) srow[t] = 0;  // never read
   }
-  const int M = cu[batch], H = m->cfg.hidden;
-  if ((st = m->ensure_ws(M, batch, batch * stride))) return st;
   hipStream_t s = m->ctx->stream;
-  RH_HIP(hipMemcpyAsync(m->ids_d, ids, (size_t)batch * stride * sizeof(int32_t),
-                        hipMemcpyHostToDevice, s));
-  if ((st = m->forward(m->ids_d, stride, cu, max_len, pool, m->out_d))) return st;
+  RH_HIP(hipMemcpyAsync(m->ids_d, stage, elems * sizeof(int32_t), hipMemcpyHostToDevice, s));
+  // the staging rows are reused by the next call only after this one's sync
+  st = m->forward(m->ids_d, stride, cu, max_len, pool, m->out_d);
+  if (st) {
+    (void)hipStreamSynchronize(s);
+    return st;
+  }
   if (pool)
     RH_HIP(hipMemcpyAsync(out, m->out_d, (size_t)batch * H * sizeof(float),
                           hipMemcpyDeviceToHost, s));
@@ -1245,45 +1396,54 @@ static int embed_common(rh_model* m, const int32_t* ids, const int32_t* lens, in
   return RH_OK;
 }
 
-int rh_model_embed(rh_model* m, const int32_t* ids, const int32_t* lens, int batch,
+int rh_model_embed(rh_model* m, const int64_t* ids, const int32_t* lens, int batch,
                    int stride, float* out) {
-  MODEL_GUARD(m);
-  return embed_common(m, ids, lens, batch, stride, out, true);
+  return api_call([&]() -> int {
+    MODEL_GUARD(m);
+    return embed_common(m, ids, lens, batch, stride, out, true);
+  });
 }
 
-int rh_model_embed_tokens(rh_model* m, const int32_t* ids, const int32_t* lens, int batch,
+int rh_model_embed_tokens(rh_model* m, const int64_t* ids, const int32_t* lens, int batch,
                           int stride, float* out) {
-  MODEL_GUARD(m);
-  return embed_common(m, ids, lens, batch, stride, out, false);
+  return api_call([&]() -> int {
+    MODEL_GUARD(m);
+    return embed_common(m, ids, lens, batch, stride, out, false);
+  });
 }
 
 int rh_model_embed_device(rh_model* m, const int32_t* ids_dev, const int32_t* lens,
                           int batch, int stride, float* out_dev) {
-  MODEL_GUARD(m);
-  if (!ids_dev || !lens || !out_dev || batch < 0 || stride < 1)
-    return fail(RH_ERR_INVALID, "bad argument");
-  if (!m->finalized) return fail(RH_ERR_INVALID, "model not finalized");
-  if (batch == 0) return RH_OK;
-  std::vector<int32_t> cu;
-  int max_len = 0;
-  int st = m->plan(lens, batch, cu, &max_len);
-  if (st) return st;
-  for (int b = 0; b < batch; b++)
-    if (lens[b] > stride) return fail(RH_ERR_INVALID, "length exceeds row stride");
-  return m->forward(ids_dev, stride, cu, max_len, true, out_dev);
+  return api_call([&]() -> int {
+    MODEL_GUARD(m);
+    if (!ids_dev || !lens || !out_dev || batch < 0 || stride < 1)
+      return fail(RH_ERR_INVALID, "bad argument");
+    if (!m->finalized) return fail(RH_ERR_INVALID, "model not finalized");
+    if (batch == 0) return RH_OK;
+    if ((size_t)batch * (size_t)stride > (size_t)INT32_MAX)
+      return fail(RH_ERR_INVALID, "batch * stride exceeds 2^31 - 1 token slots");
+    for (int b = 0; b < batch; b++)
+      if (lens[b] > stride) return fail(RH_ERR_INVALID, "length exceeds row stride");
+    int max_len = 0;
+    int st = m->plan(lens, batch, m->cu_host, &max_len);
+    if (st) return st;
+    return m->forward(ids_dev, stride, m->cu_host, max_len, true, out_dev);
+  });
 }
 
 int rh_model_check(rh_model* m) {
-  MODEL_GUARD(m);
-  RH_HIP(hipStreamSynchronize(m->ctx->stream));
-  if (!m->err_d) return RH_OK;
-  int flag = 0;
-  RH_HIP(hipMemcpy(&flag, m->err_d, sizeof(int), hipMemcpyDeviceToHost));
-  if (flag) {
-    RH_HIP(hipMemset(m->err_d, 0, sizeof(int)));
-    return fail(RH_ERR_VOCAB, "a token id was out of vocab range (clamped on device)");
-  }
-  return RH_OK;
+  return api_call([&]() -> int {
+    MODEL_GUARD(m);
+    RH_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (!m->err_d) return RH_OK;
+    int flag = 0;
+    RH_HIP(hipMemcpy(&flag, m->err_d, sizeof(int), hipMemcpyDeviceToHost));
+    if (flag) {
+      RH_HIP(hipMemset(m->err_d, 0, sizeof(int)));
+      return fail(RH_ERR_VOCAB, "a token id was out of vocab range (clamped on device)");
+    }
+    return RH_OK;
+  });
 }
 
 }  // extern "C"

@@ -10,6 +10,8 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <exception>
+#include <new>
 #include <string>
 
 #include "../../include/rembed_hip.h"
@@ -37,10 +39,38 @@ inline void timed_launch(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStr
 
 // ---- status ----------------------------------------------------------------
 // A thread-local message backs rh_last_error(); every C entry point returns
-// one of the RH_* codes and never aborts the host.
-void set_error(const std::string& msg);
-int fail(int code, const std::string& msg);
-int hip_fail(hipError_t e, const char* what, const char* file, int line);
+// one of the RH_* codes and never aborts the host. The message lives in a
+// fixed thread-local buffer, so recording it never allocates or throws.
+void set_error(const char* msg) noexcept;
+int fail(int code, const char* msg) noexcept;
+inline int fail(int code, const std::string& msg) noexcept { return fail(code, msg.c_str()); }
+int hip_fail(hipError_t e, const char* what, const char* file, int line) noexcept;
+
+// Exception barrier of the C ABI: every extern "C" body runs inside it, so no
+// C++ exception unwinds into the (cgo) caller. A failed host allocation
+// becomes RH_ERR_OOM, any other exception RH_ERR_INVALID, with a message.
+int fail_exception(int code, const char* what) noexcept;
+template <class F>
+inline int api_call(F&& body) noexcept {
+  try {
+    return body();
+  } catch (const std::bad_alloc&) {
+    return fail(RH_ERR_OOM, "host memory allocation failed");
+  } catch (const std::exception& e) {
+    return fail_exception(RH_ERR_INVALID, e.what());
+  } catch (...) {
+    return fail(RH_ERR_INVALID, "internal error: unknown exception");
+  }
+}
+// The same for entry points without a status (destroy calls): an exception
+// is recorded for rh_last_error() and dropped.
+template <class F>
+inline void api_void(F&& body) noexcept {
+  (void)api_call([&]() -> int {
+    body();
+    return 0;
+  });
+}
 
 #define RH_HIP(call)                                                   \
   do {                                                                 \
@@ -326,6 +356,10 @@ hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, in
 hipError_t launch_dense_head(const float* pooled, int batch, int H, int D, const float* w1T,
                              const float* w2T, int normalize, float* hid, float* out,
                              hipStream_t s);
+// out[i] = act(gate[i]) * up[i] over n floats (act a gated ACT_*): the
+// gated-MLP glue for gate and up packed as separate weights.
+hipError_t launch_glu_rows(const float* gate, const float* up, float* out, size_t n, int act,
+                           hipStream_t s);
 // L2Normalize (tensor.go:540-554) of `rows` rows of [H] in place.
 hipError_t launch_l2_rows(float* y, int rows, int H, hipStream_t s);
 

@@ -50,7 +50,7 @@ def make_config(shape):
 class Model:
     """A loaded encoder resident in HBM (rh_model)."""
 
-    def __init__(self, ctx, shape, tensors, quant=QUANT_NONE):
+    def __init__(self, ctx, shape, tensors, quant=QUANT_NONE, fuse_projections=True):
         self.ctx = ctx
         self.shape = shape
         cfg = make_config(shape)
@@ -58,6 +58,8 @@ class Model:
         check(lib.rh_model_create(ctx.h, ctypes.byref(cfg), quant, ctypes.byref(h)))
         self.h = h
         try:
+            if not fuse_projections:
+                self.set_fuse_projections(False)
             for name, arr in tensors.items():
                 arr = np.ascontiguousarray(arr, dtype=np.float32)
                 dims = (ctypes.c_int64 * arr.ndim)(*arr.shape)
@@ -69,12 +71,12 @@ class Model:
             raise
 
     @classmethod
-    def from_safetensors(cls, ctx, shape, path, quant=QUANT_NONE):
+    def from_safetensors(cls, ctx, shape, path, quant=QUANT_NONE, **kw):
         """model.Load over one .safetensors file (bert.go:307-524 reading
         through safetensors.go:122-181): every tensor widened to float32 and
         handed over by name; the library fuses Q|K|V and packs on finalize."""
         from .checkpoint import load
-        return cls(ctx, shape, load(path), quant)
+        return cls(ctx, shape, load(path), quant, **kw)
 
     def close(self):
         if getattr(self, "h", None):
@@ -106,6 +108,12 @@ class Model:
         context's split workspace; 1: one stream. Same results."""
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_STREAMS, n))
 
+    def set_fuse_projections(self, on=True):
+        """Decoders, before finalize: q|k|v and gate|up packed as one weight
+        each where their modes agree (True, default), or as separate weights
+        like the reference (False); same results."""
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSE_PROJECTIONS, 1 if on else 0))
+
     def set_qk_epilogue(self, on=True):
         """Decoders: QK-norm + RoPE in the q|k|v GEMM's epilogue (True,
         where the shape allows) or a separate pass (False, the default:
@@ -120,16 +128,24 @@ class Model:
 
     @staticmethod
     def _pack(ids, lens):
+        """int64 id rows [batch][stride] and int32 lengths, as the C ABI takes
+        them (the reference's ids are []int64, bert.go:649)."""
         if lens is None:  # list of sequences
-            seqs = [np.asarray(s, np.int32) for s in ids]
+            seqs = [np.asarray(s, np.int64) for s in ids]
             lens = np.array([len(s) for s in seqs], np.int32)
             stride = max(1, int(lens.max())) if len(seqs) else 1
-            arr = np.zeros((len(seqs), stride), np.int32)
+            arr = np.zeros((len(seqs), stride), np.int64)
             for i, s in enumerate(seqs):
                 arr[i, : len(s)] = s
             return arr, lens
-        return (np.ascontiguousarray(ids, np.int32),
-                np.ascontiguousarray(lens, np.int32))
+        ids = np.ascontiguousarray(ids, np.int64)
+        lens = np.ascontiguousarray(lens, np.int32)
+        if ids.ndim != 2:
+            raise ValueError(f"ids must be [batch][stride], got shape {ids.shape}")
+        if lens.ndim != 1 or lens.shape[0] != ids.shape[0]:
+            raise ValueError(f"lens must hold one length per row of ids "
+                             f"({ids.shape[0]}), got shape {lens.shape}")
+        return ids, lens
 
     def embed(self, ids, lens=None):
         """Pooled (and L2-normalized per config) vectors, [batch][H]."""

@@ -13,7 +13,8 @@ window |i-j| < w, grouped kv heads).
   to bf16 before P·V: relative 2^-9 per weight), and precision 3 (hi/lo
   split) within 1e-4 of the output scale.
 * Texts of length 1, block edges (63/64/65, 127/128/129), windows shorter
-  and longer than the text, GQA groups of 1, 2 and 3.
+  and longer than the text, GQA groups of 1, 2 and 3, and EmbeddingGemma's
+  window of 512 at lengths 511, 512, 513 and 2048.
 """
 import sys
 
@@ -77,12 +78,15 @@ CASES = [
     (256, 3, 1, False, 257, [5, 300, 600, 1000]),
     (256, 3, 1, False, 0, [70, 333, 700]),
     (128, 4, 4, False, 40, [200, 90]),
+    # EmbeddingGemma's local layers at the benchmark's window and length:
+    # texts just under, at and over the window, and one of 2048 tokens
+    (256, 3, 1, False, 512, [511, 512, 513, 2048]),
 ]
 
 
 @pytest.mark.parametrize("case", CASES,
                          ids=["bert64", "dh32-gqa2", "qwen3-causal", "gemma-window",
-                              "gemma-global", "dh128-window40"])
+                              "gemma-global", "dh128-window40", "gemma-window512-2048"])
 def test_attention_kernels(gpu_ctx, case):
     dh, heads, kv_heads, causal, window, lens = case
     say(f"attention dh={dh} heads={heads}/{kv_heads} causal={causal} window={window} lens={lens}")

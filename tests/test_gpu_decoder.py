@@ -15,6 +15,8 @@
   Dense 3072), two layers: fp32 embeddings within 1e-4 of the oracle,
   weight-only int8 cosine >= 0.9999 against the oracle's int8 path, full
   int8 cosine >= 0.999, batch == single, per-token hidden states.
+* The same at the configurations' full length: Qwen3 one 512-token text,
+  EmbeddingGemma one 2048-token text with window 512 / pattern 2.
 """
 import dataclasses
 
@@ -295,6 +297,48 @@ def test_decoder_qk_epilogue_identical(gpu_ctx, make, bf16):
     assert np.array_equal(fused, sep)
     for a, b in zip(tok_fused, tok_sep):
         assert np.array_equal(a, b)
+
+
+def gemma3_2l_w512():
+    # the benchmark's attention: layer 0 sliding window 512, layer 1 global
+    return dataclasses.replace(GEMMA3_300M, name="gemma3-2l-w512", layers=2, vocab=4000,
+                               sliding_window=512, sliding_pattern=2, max_seq=2048)
+
+
+# Qwen3 at the benchmark's 512 tokens, EmbeddingGemma at 2048 with window 512:
+# one full-length text each, two layers, against the oracle's forward
+FULL_LENGTH = [(qwen3_2l, True, 512), (gemma3_2l_w512, False, 2048)]
+
+
+@pytest.mark.parametrize("make,bf16,length", FULL_LENGTH, ids=["qwen3-512", "gemma3-2048-w512"])
+@pytest.mark.parametrize("quant", [QUANT_NONE, QUANT_WEIGHTS], ids=["fp32", "w8"])
+def test_decoder_full_config_length(gpu_ctx, make, bf16, length, quant):
+    """The configurations' full text length: every key block of the causal
+    mask (qwen3.go:319-390) and of the |i-j| < 512 window (gemma3.go:339-347)
+    is crossed. fp32 embeddings within 1e-4 of the oracle, weight-only int8
+    cosine >= 0.9999 against the oracle's int8 path; per-token hidden states
+    checked too."""
+    shape, t = setup(make, bf16)
+    ids, lens = token_batch(1, length, length, length, vocab=shape.vocab, id_lo=0, seed=29)
+    say(f"{shape.name} quant={quant} one text of {length} tokens, window {shape.sliding_window}")
+    m = Model(gpu_ctx, shape, t, quant)
+    got = m.embed(ids, lens)
+    toks = m.embed_tokens(ids, lens)[0]
+    orc = O.DecoderOracle(shape, t, quant)
+    want = orc.embed_batch(ids, lens)
+    want_tok = orc.encode(ids[0, :length])
+    if quant == QUANT_NONE:
+        err = np.abs(got - want).max()
+        terr = np.abs(toks - want_tok).max() / max(1.0, np.abs(want_tok).max())
+        say(f"  max abs err {err:.3e}, hidden rel err {terr:.3e}")
+        assert err <= 1e-4
+        assert terr <= 2e-5
+    else:
+        c = cos_rows(got, want)
+        ct = cos_rows(toks, want_tok)
+        say(f"  cos {c.min():.7f}, per-token min cos {ct.min():.7f}")
+        assert c.min() >= 0.9999
+        assert ct.min() >= 0.9999
 
 
 def test_decoder_model_errors(gpu_ctx):
