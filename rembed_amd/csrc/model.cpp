@@ -221,6 +221,7 @@ struct rh_model {
   }
   Planes plane(int which, const rh_weight* w) const {
     Planes p;
+    if (!w) return p;  // a group run as separate weights takes fp32 rows
     p.hi = which ? p1h : p0h;
     p.lo = linear_a_terms(ctx, w) == 2 ? (which ? p1l : p0l) : nullptr;
     p.ld = which ? ld1 : ld0;
