@@ -227,6 +227,22 @@ int rh_linear_u8(rh_context *ctx, const uint8_t *qa, int ldq, const float *row_s
                  const rh_weight *w, int m, int act, uint8_t *qa_out, int ldq_out,
                  float *rs_out, float *absmax_scratch);
 
+/* rh_linear for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. It computes exactly what rh_linear computes, with the same
+ * kernels, but stages its intermediate data (full int8: the u8 rows and row
+ * scales; weight-only int8 / fp32: the bf16 planes of a) in a fixed device
+ * array of RH_NOALLOC_SCRATCH_BYTES per GPU, held from library load until
+ * the process ends, instead of caller scratch or a workspace it allocates.
+ * It calls no hipMalloc/hipFree and times no launches. Sizes whose staging
+ * exceeds the array (full int8: m*round_up(k,16) + 4m bytes; planes:
+ * m*round_up(k,64)*2 bytes per plane) return RH_ERR_INVALID. Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (from
+ * different contexts or threads) race and must be ordered by the caller. */
+#define RH_NOALLOC_SCRATCH_BYTES (64u * 1024u * 1024u)
+int rh_linear_noalloc(rh_context *ctx, float *dst, const float *a, const rh_weight *w,
+                      int m, int act);
+
 /* Elementwise entry points used by parity tests (dev pointers). */
 int rh_gelu(rh_context *ctx, float *x, size_t n);          /* tensor.go:508-538 */
 int rh_layernorm(rh_context *ctx, float *x, const float *gamma,

@@ -36,6 +36,7 @@ RH_OPT_QK_EPILOGUE = 5
 RH_OPT_FUSE_PROJECTIONS = 6
 RH_CTX_F32_ALGO, RH_CTX_W8_TERMS, RH_CTX_I8_TILE, RH_CTX_BF_ALGO, RH_CTX_BF_TILE = 1, 2, 3, 4, 5
 RH_CTX_TILE_GROUP = 6
+RH_NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024
 
 # Symbols the header declares (checked by the CPU test suite).
 EXPORTS = [
@@ -46,7 +47,8 @@ EXPORTS = [
     "rh_pack_weight_gated", "rh_attention",
     "rh_weight_destroy", "rh_weight_info", "rh_weight_export",
     "rh_quantize_rows_u8", "rh_gelu_quantize_rows_u8", "rh_matmul", "rh_matmul_packed", "rh_matmul_packed8",
-    "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_linear_u8", "rh_gelu",
+    "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_linear_u8",
+    "rh_linear_noalloc", "rh_gelu",
     "rh_layernorm", "rh_model_create", "rh_model_set_tensor",
     "rh_model_finalize", "rh_model_destroy", "rh_model_set_option",
     "rh_model_quantized", "rh_model_quantized_activations", "rh_model_embed",
@@ -122,6 +124,7 @@ def _load():
         "rh_gemm_u8s8_i32": (I, [P, P, P, I, P, I]),
         "rh_linear": (I, [P, P, P, P, I, I, P, I, P]),
         "rh_linear_u8": (I, [P, P, I, P, P, I, I, P, I, P, P]),
+        "rh_linear_noalloc": (I, [P, P, P, P, I, I]),
         "rh_gelu": (I, [P, P, S]),
         "rh_layernorm": (I, [P, P, P, P, I, I, F]),
         "rh_model_create": (I, [P, ctypes.POINTER(ModelConfig), I, ctypes.POINTER(P)]),

@@ -577,6 +577,40 @@ int run_linear(Context* ctx, const rh_weight* w, const float* a, int lda, int m,
 
 }  // namespace rh
 
+// ---- scratch of the allocation-free linear -------------------------------------
+// rh_linear_noalloc stages its activations (u8 rows and row scales, or bf16
+// planes) in this file-scope device array instead of a workspace it would
+// have to allocate. Every GPU the library runs on holds its own copy for the
+// life of the process. In host code the array's name is not a device
+// address: each device's address is looked up once, with that device
+// current, when the first context on it is created, and only that address
+// is handed to kernels.
+static __device__ __align__(256) uint8_t scratch[RH_NOALLOC_SCRATCH_BYTES];
+
+namespace rh {
+constexpr int kMaxScratchDevices = 64;
+static void* g_scratch_addr[kMaxScratchDevices] = {};
+static std::mutex g_scratch_mu;
+
+// Resolve this device's copy of `scratch` (the device is current).
+static int resolve_scratch(int device) {
+  if (device >= kMaxScratchDevices)
+    return fail(RH_ERR_INVALID, "device index beyond the scratch address table");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_addr[device]) return RH_OK;
+  void* addr = nullptr;
+  RH_HIP(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+  if (!addr) return fail(RH_ERR_HIP, "hipGetSymbolAddress returned a null scratch address");
+  g_scratch_addr[device] = addr;
+  return RH_OK;
+}
+
+static void* scratch_addr(int device) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return device >= 0 && device < kMaxScratchDevices ? g_scratch_addr[device] : nullptr;
+}
+}  // namespace rh
+
 using namespace rh;
 
 // ---- C ABI ---------------------------------------------------------------------
@@ -612,6 +646,7 @@ int rh_context_create(int device, rh_context** out) {
       return fail(RH_ERR_NO_DEVICE, "no HIP device available");
     if (device < 0 || device >= n) return fail(RH_ERR_INVALID, "device index out of range");
     RH_HIP(hipSetDevice(device));
+    if (int st = resolve_scratch(device)) return st;
     auto* c = new rh_context();
     c->device = device;
     hipError_t e = hipStreamCreate(&c->stream);
@@ -1061,6 +1096,67 @@ int rh_linear_u8(rh_context* ctx, const uint8_t* qa, int ldq, const float* row_s
     if (st) return st;
     return run_gemm_i8(ctx, w, qa, ldq, row_scales, m, EPI_QUANT, qa_out, ldq_out, act,
                        w->d_bias, absmax_scratch, rs_out, 0.0);
+  });
+}
+
+// Scratch bytes rh_linear_noalloc stages for m rows through w (256-byte
+// aligned pieces): full int8 u8 rows [m][ldq] and row scales [m]; the bf16
+// planes GEMM one or two planes [m][round_up(k, 64)]; the other weight-only
+// int8 / fp32 algorithms read the fp32 rows directly and stage nothing.
+static size_t noalloc_bytes(const rh_context* ctx, const rh_weight* w, int m) {
+  if (w->mode == RH_MODE_A8W8)
+    return round_up((size_t)m * round_up(w->k, 16), 256) + (size_t)m * 4;
+  if (linear_on_planes(ctx, w))
+    return round_up((size_t)m * round_up(w->k, 64) * 2, 256) * linear_a_terms(ctx, w);
+  return 0;
+}
+
+int rh_linear_noalloc(rh_context* ctx, float* dst, const float* a, const rh_weight* w, int m,
+                      int act) {
+  return api_call([&]() -> int {
+    int st = check_gemm(ctx, w, -1, a, dst, m);
+    if (st) return st;
+    if (act < RH_ACT_NONE || act > RH_ACT_GEGLU_ERF) return fail(RH_ERR_INVALID, "unknown act");
+    if (w->glu != is_glu(act))
+      return fail(RH_ERR_INVALID, "gated acts need a gated weight and vice versa");
+    CTX_GUARD(ctx);
+    if (m == 0) return RH_OK;
+    const size_t need = noalloc_bytes(ctx, w, m);
+    if (need > (size_t)RH_NOALLOC_SCRATCH_BYTES) {
+      char buf[200];
+      snprintf(buf, sizeof buf,
+               "rh_linear_noalloc: %d rows of k=%d need %zu scratch bytes, the maximum is %zu",
+               m, w->k, need, (size_t)RH_NOALLOC_SCRATCH_BYTES);
+      return fail(RH_ERR_INVALID, buf);
+    }
+    uint8_t* base = static_cast<uint8_t*>(scratch_addr(ctx->device));
+    if (!base) return fail(RH_ERR_INVALID, "scratch address of the device was not resolved");
+    // per-launch event timing creates events: off for this call
+    struct ProfOff {
+      rh_context* c;
+      bool was;
+      ~ProfOff() { c->profiling = was; }
+    } prof_off{ctx, ctx->profiling};
+    ctx->profiling = false;
+    const int ldc = w->glu ? w->n / 2 : w->n;
+    if (w->mode == RH_MODE_A8W8) {
+      const int ldq = (int)round_up(w->k, 16);
+      uint8_t* qa = base;
+      float* rs = reinterpret_cast<float*>(base + round_up((size_t)m * ldq, 256));
+      return run_linear(ctx, w, a, w->k, m, dst, ldc, act, w->d_bias, qa, ldq, rs, true);
+    }
+    if (linear_on_planes(ctx, w)) {
+      const int ldk = (int)round_up(w->k, 64);
+      const size_t plane = round_up((size_t)m * ldk * 2, 256);
+      Planes pin;
+      pin.hi = reinterpret_cast<__bf16*>(base);
+      pin.lo = linear_a_terms(ctx, w) == 2 ? reinterpret_cast<__bf16*>(base + plane) : nullptr;
+      pin.ld = ldk;
+      RH_HIP(launch_split_bf16(a, w->k, m, w->k, pin.hi, pin.lo, ldk, ctx->stream));
+      return run_linear(ctx, w, a, w->k, m, dst, ldc, act, w->d_bias, nullptr, 0, nullptr,
+                        false, &pin);
+    }
+    return run_linear(ctx, w, a, w->k, m, dst, ldc, act, w->d_bias, nullptr, 0, nullptr, false);
   });
 }
 

@@ -233,6 +233,12 @@ def Linear(ctx, dst, a, pb, m, act=_lib.RH_ACT_NONE, qa=None, ldq=0, row_scales=
                         None if row_scales is None else row_scales.ptr))
 
 
+def LinearNoAlloc(ctx, dst, a, pb, m, act=_lib.RH_ACT_NONE):
+    """rh_linear without allocating: staging in the library's fixed device
+    scratch (rh_linear_noalloc)."""
+    check(lib.rh_linear_noalloc(ctx.h, dst.ptr, a.ptr, pb.h, m, act))
+
+
 def LinearU8(ctx, qa, ldq, row_scales, pb, m, act, qa_out, ldq_out, rs_out, absmax):
     """applyDense + QuantizeRowU8 of the output rows (rh_linear_u8)."""
     check(lib.rh_linear_u8(ctx.h, qa.ptr, ldq, row_scales.ptr, pb.h, m, act, qa_out.ptr,
