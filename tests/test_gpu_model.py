@@ -169,6 +169,26 @@ def test_parts_on_streams_identical_planes(gpu_ctx, minilm, quant):
     assert np.array_equal(m.embed(ids, lens), one)
 
 
+@pytest.mark.parametrize("tile", [3, 7, 9, 10])
+def test_full_int8_forward_identical_on_every_tile(gpu_ctx, minilm_int8_big, tile):
+    """The full-int8 forward (bf16 q|k|v rows, fp32 O / FFN rows, every
+    epilogue the model uses) gives the same embeddings and hidden states, bit
+    for bit, whichever int8 GEMM tile runs: the accumulators and the
+    dequantization are the same."""
+    from rembed_amd._lib import RH_CTX_I8_TILE
+    m, ids, lens, one, tok_one = minilm_int8_big
+    say(f"tile {tile}: {len(lens)} texts, {int(lens.sum())} tokens")
+    gpu_ctx.set_option(RH_CTX_I8_TILE, tile)
+    try:
+        got = m.embed(ids, lens)
+        tok = m.embed_tokens(ids, lens)
+    finally:
+        gpu_ctx.set_option(RH_CTX_I8_TILE, 0)
+    assert np.array_equal(got, one)
+    for a, b in zip(tok, tok_one):
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("streams", [2, 3, 4])
 def test_parts_on_streams_identical(minilm_int8_big, streams):
     """A full-int8 batch (128 texts, >= 8192 tokens: parts of >= 2048 rows)
