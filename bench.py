@@ -10,8 +10,13 @@ few µs per launch, so that pass is timed apart). The CPU baseline is the
 oracle's restatement of the reference algorithm on the host cores over a
 bounded sample of texts. --workload selects the other configurations.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+Each timed step is bracketed by HIP events on the library's stream, so the
+line also reports the median / p10 / p90 step time over the K steps (K = 30
+by default); `value` is the wall-clock rate over all K.
+
+Usage: python bench.py [--gpus 1] [--steps 30] [--warmup 5]
 """
+import ctypes
 import argparse
 import json
 import os
@@ -53,30 +58,150 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+class StepEvents:
+    """HIP events recorded on a stream between steps (hipEventRecord through
+    the HIP runtime the library already uses): per-step device times without
+    a host synchronization inside the timed loop."""
+
+    def __init__(self, stream, n):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.stream = ctypes.c_void_p(stream)
+        self.ev = []
+        for _ in range(n + 1):
+            e = ctypes.c_void_p()
+            assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
+            self.ev.append(e)
+        self.i = 0
+
+    def mark(self):
+        assert self.hip.hipEventRecord(self.ev[self.i], self.stream) == 0
+        self.i += 1
+
+    def step_ms(self):
+        assert self.hip.hipEventSynchronize(self.ev[self.i - 1]) == 0
+        out = []
+        for a, b in zip(self.ev[: self.i - 1], self.ev[1: self.i]):
+            ms = ctypes.c_float()
+            assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+            out.append(ms.value)
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+        return np.array(out)
+
+
+def pct(x, q):
+    return float(np.percentile(np.asarray(x, np.float64), q))
+
+
 def cpu_baseline(shape, tensors, ids, lens, quant, max_len=None):
-    """Oracle (port of the reference algorithm) on the host cores: one serial
-    forward per text, texts fanned out across threads (rembed.go:309-330).
-    `max_len` truncates the sample's texts (the decoders' full texts would
-    take minutes per text on one core)."""
+    """The reference algorithm restated in C (the oracle) on the host cores,
+    with the reference's batch policy (rembed.go:309-330): one serial
+    forward per text, texts across all cores (across = min(cores, texts),
+    within = 1 here). Full int8 runs on the reference's own kernel shape:
+    PackB8VNNI panels and 4x16 VPDPBUSD tiles (vnni_amd64.s /
+    vnni512_amd64.s). The whole batch is timed on every core (each text's
+    forward timed too: p10/p50/p90 of the per-text rates), and a sample of
+    texts on one core. `max_len` truncates the decoders' texts (a full
+    28-layer 512-token text takes ~30 s on one core)."""
     from oracle import oracle as O
-    threads = min(16, os.cpu_count() or 1)
-    n = min(len(lens), threads)
-    lens = np.minimum(lens[:n], max_len) if max_len else lens[:n]
+    cores = os.cpu_count() or 1
     dec = hasattr(shape, "arch")
+    if max_len:
+        lens = np.minimum(lens, max_len)
     orc = O.DecoderOracle(shape, tensors, quant) if dec else O.BertOracle(shape, tensors, quant)
-    orc.embed_batch(ids[:1], np.minimum(lens[:1], 32), threads=1)  # warm-up
-    t0 = time.perf_counter()
-    orc.embed_batch(ids[:n], lens, threads=threads)
-    dt = time.perf_counter() - t0
-    orc.close()
-    kind = {0: "fp32 FMA-chain", 1: "fp32 x int8 FMA-chain",
-            2: f"u8xs8 {'AVX-512-VNNI' if O.lib.or_vnni_kind() == 2 else 'portable'}"}[quant]
-    trunc = f", truncated to {max_len} tokens" if max_len else ""
-    return {"value": float(lens.sum()) / dt, "unit": "tokens/s", "cores": threads,
+    O.lib.or_set_gemm_impl(1 if quant == 2 else 0)
+    try:
+        orc.embed_batch(ids[:1], np.minimum(lens[:1], 32), threads=1)  # warm-up
+        secs = np.zeros(len(lens))
+        t0 = time.perf_counter()
+        orc.embed_batch(ids, lens, threads=cores, secs=secs)
+        dt = time.perf_counter() - t0
+        n1 = min(8, len(lens))
+        t1 = time.perf_counter()
+        orc.embed_batch(ids[:n1], lens[:n1], threads=1)
+        dt1 = time.perf_counter() - t1
+    finally:
+        O.lib.or_set_gemm_impl(0)
+        orc.close()
+    per_text = lens.astype(np.float64) / secs
+    if quant == 2:
+        pk = O.lib.or_vnni_panel_kind()
+        kind = ("u8xs8 " + {1: "AVX-VNNI (VEX)", 2: "AVX-512-VNNI (EVEX ymm)",
+                            0: "portable"}[pk] + " 4x16 VPDPBUSD tiles on PackB8VNNI panels")
+    else:
+        kind = {0: "fp32 FMA-chain", 1: "fp32 x int8 FMA-chain"}[quant]
+    trunc = f", texts truncated to {max_len} tokens" if max_len else ""
+    return {"value": float(lens.sum()) / dt, "unit": "tokens/s", "cores": cores,
             "kind": "port",
-            "sample": f"{n} texts of the same batch ({int(lens.sum())} tokens{trunc}), "
-                      f"one serial forward per text across {threads} threads, "
-                      f"{kind} dot products, {dt:.2f} s"}
+            "label": "rembed-algorithm C++ restatement (not the Go binary: no Go toolchain here)",
+            "per_text_tokens_per_s": {"p10": pct(per_text, 10), "median": pct(per_text, 50),
+                                      "p90": pct(per_text, 90), "texts": len(lens)},
+            "single_core": {"value": float(lens[:n1].sum()) / dt1, "cores": 1,
+                            "sample": f"first {n1} texts ({int(lens[:n1].sum())} tokens), "
+                                      f"{dt1:.2f} s"},
+            "sample": f"the whole batch: {len(lens)} texts, {int(lens.sum())} tokens{trunc}, "
+                      f"one serial forward per text across {cores} threads, {kind}, "
+                      f"{dt:.2f} s"}
+
+
+def _u8_rows(h):
+    """QuantizeRowU8 of every row (pack_vnni.go:85-117), by the oracle."""
+    from oracle import oracle as O
+    return np.stack([O.quantize_row_u8(r)[0] for r in h])
+
+
+def oracle_u8_sensitivity(shape, tensors, ids, lens, texts=4):
+    """The count of u8_byte_diffs between the oracle and the oracle itself
+    with every word-embedding weight moved by one float32 ulp
+    (np.nextafter toward +inf): how far a rounding-level change to the input
+    carries through the quantized network, layer by layer."""
+    from oracle import oracle as O
+    nudged = dict(tensors)
+    w = np.asarray(tensors["embeddings.word_embeddings.weight"], np.float32)
+    nudged["embeddings.word_embeddings.weight"] = np.nextafter(w, np.float32(np.inf))
+    a, b = O.BertOracle(shape, tensors, 2), O.BertOracle(shape, nudged, 2)
+    rows = []
+    for L in range(1, shape.layers + 1):
+        diff = 0
+        for t in range(texts):
+            x = ids[t, :lens[t]]
+            diff += int(np.count_nonzero(_u8_rows(a.encode(x, L)) != _u8_rows(b.encode(x, L))))
+        rows.append(diff)
+    a.close()
+    b.close()
+    return rows
+
+
+def u8_byte_diffs(ctx, shape, tensors, ids, lens, texts=4, precisions=(1, 3)):
+    """Per layer, the u8 bytes of the next layer's activation rows
+    (QuantizeRowU8 of the hidden states after layer L, pack_vnni.go:85-117)
+    that differ between the device's full-int8 forward and the oracle's, over
+    the first `texts` texts, for each attention precision: device models of
+    1..L layers, the oracle stopped after L layers, both sides quantized by
+    the oracle's quantizer."""
+    import dataclasses
+
+    from oracle import oracle as O
+    from rembed_amd.model import Model
+    orc = O.BertOracle(shape, tensors, 2)
+    rows = {p: [] for p in precisions}
+    total = 0
+    for L in range(1, shape.layers + 1):
+        m = Model(ctx, dataclasses.replace(shape, layers=L), tensors, 2)
+        want = [_u8_rows(orc.encode(ids[t, :lens[t]], L)) for t in range(texts)]
+        total = sum(w.size for w in want)
+        for p in precisions:
+            m.set_attention_precision(p)
+            toks = m.embed_tokens(ids[:texts], lens[:texts])
+            rows[p].append(sum(int(np.count_nonzero(_u8_rows(toks[t]) != want[t]))
+                               for t in range(texts)))
+        m.close()
+    orc.close()
+    return {"per_layer_bytes_differing": {f"attention_precision_{p}": rows[p]
+                                          for p in precisions},
+            "bytes_per_layer": total, "texts": texts,
+            "what": "QuantizeRowU8 of the hidden states after each layer (the next "
+                    "layer's u8 q|k|v input), device full-int8 forward vs the oracle's"}
 
 
 def make_workload(name):
@@ -98,7 +223,7 @@ def make_workload(name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="bert-base-int8",
@@ -106,6 +231,8 @@ def main():
     ap.add_argument("--ffn1", choices=["fused", "split"], default="split",
                     help="full-int8 FFN1: fused = GELU rows re-quantized inside the GEMM "
                          "(two passes, no fp32 intermediate); split = fp32 rows + QuantizeRowU8")
+    ap.add_argument("--no-u8-diff", action="store_true",
+                    help="skip the per-layer u8 comparison with the oracle (full int8)")
     ap.add_argument("--streams", type=int, choices=[1, 2, 3, 4], default=2,
                     help="run a batch as this many parts of whole texts on as many streams "
                          "(default 2); the roofline pass always runs one stream")
@@ -146,14 +273,35 @@ def main():
     model.check()
     ctx.sync()
 
-    # `value`: K steps with nothing but the forward on the stream.
+    # `value`: K steps with nothing but the forward on the stream (plus an
+    # event between steps for the per-step distribution).
     ctx.sync()
+    ev = StepEvents(ctx.stream, args.steps)
     t0 = time.perf_counter()
+    ev.mark()
     for _ in range(args.steps):
         model.embed_device(ids_dev, lens, BATCH, SEQ, out_dev)
+        ev.mark()
     ctx.sync()
     elapsed = time.perf_counter() - t0
+    step_ms = ev.step_ms()
     model.check()
+
+    # The same K steps with fp32-grade attention (three-term bf16 split),
+    # the reference's float32 attention arithmetic class, reported beside
+    # `value` (the default for the quantized modes is bf16 operands).
+    attn3_rate = None
+    if quant != 0:
+        model.set_attention_precision(3)
+        model.embed_device(ids_dev, lens, BATCH, SEQ, out_dev)
+        ctx.sync()
+        t2 = time.perf_counter()
+        for _ in range(args.steps):
+            model.embed_device(ids_dev, lens, BATCH, SEQ, out_dev)
+        ctx.sync()
+        attn3_rate = tokens * args.steps / (time.perf_counter() - t2)
+        model.set_attention_precision(1)
+        model.check()
 
     # The roofline: the same K steps again with a HIP event pair attached to
     # every GEMM / attention / split dispatch (the library's profiler, on
@@ -187,20 +335,31 @@ def main():
         f"ms/step over {gemm['launches'] // args.steps} launches = {achieved:.1f} TOP/s; "
         f"attention {attn_ms_step:.3f} ms/step")
 
-    # The same forward through the host-buffer boundary (ids up, vectors
-    # back over PCIe each batch), reported beside `value`, never as it.
-    host_steps = max(1, min(args.steps, 20))
+    # The same forward through the host-buffer boundary (int64 ids up,
+    # vectors back over PCIe each batch, one synchronous call per batch),
+    # reported beside `value`, never as it.
+    host_steps = max(1, args.steps)
     model.embed(ids, lens)
-    t0 = time.perf_counter()
+    host_ms = []
     for _ in range(host_steps):
+        t0 = time.perf_counter()
         host_vec = model.embed(ids, lens)
-    host_rate = tokens * host_steps / (time.perf_counter() - t0)
+        host_ms.append((time.perf_counter() - t0) * 1e3)
+    host_rate = tokens * host_steps / (sum(host_ms) * 1e-3)
 
     vec = out_dev.download(np.float32, (BATCH, shape.hidden))
     assert np.array_equal(vec, host_vec), "host-buffer and device-resident forwards differ"
     cfg_note = {"streams": args.streams}
     if quant == 2:
         cfg_note["ffn1"] = args.ffn1
+    if quant != 0:
+        # what the quantized forward computes besides its int8 GEMMs
+        cfg_note["attention"] = ("bf16 MFMA operands, fp32 softmax and accumulation "
+                                 "(RH_OPT_ATTN_PRECISION 1)")
+        if quant == 2:
+            cfg_note["qkv_rows"] = "bf16 (the q|k|v GEMM's epilogue rounds to the attention operands)"
+    else:
+        cfg_note["attention"] = "three-term bf16 split, fp32-grade (RH_OPT_ATTN_PRECISION 3)"
     norms = np.linalg.norm(vec.astype(np.float64), axis=1)
     assert np.all(np.abs(norms - 1) < 1e-4), "embeddings are not unit vectors"
 
@@ -209,9 +368,19 @@ def main():
     if quant == 2 and os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("bytes_per_launch")
 
+    u8diff = None
+    if quant == 2 and not args.no_cpu_baseline and not args.no_u8_diff:
+        log("comparing u8 activations with the oracle, layer by layer")
+        u8diff = u8_byte_diffs(ctx, shape, tensors, ids, lens)
+        u8diff["oracle_vs_oracle_1ulp_embeddings"] = oracle_u8_sensitivity(
+            shape, tensors, ids, lens)
+        log(f"u8 bytes differing per layer of {u8diff['bytes_per_layer']}: "
+            f"{u8diff['per_layer_bytes_differing']}; oracle vs itself with 1-ulp word "
+            f"embeddings {u8diff['oracle_vs_oracle_1ulp_embeddings']}")
+
     baseline = None
     if not args.no_cpu_baseline:
-        log("timing the CPU baseline sample")
+        log("timing the CPU baseline")
         trunc = {"qwen3-0.6b-w8": 48, "gemma-300m-w8": 64}.get(args.workload)
         baseline = cpu_baseline(shape, tensors, ids, lens, quant, max_len=trunc)
         log(f"cpu baseline {baseline['value']:,.1f} tokens/s")
@@ -227,7 +396,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {2: "int8", 1: "int8 weights x bf16-split activations", 0: "fp32 (3xbf16 split)"}[quant],
+        "dtype": {2: "int8", 1: "int8 weights x bf16(a) activations (one bf16 term)",
+                  0: "fp32 (3xbf16 split)"}[quant],
         "data": "synthetic (random-init N(0,0.02) weights, uniform token ids)",
         "config": {
             "workload": desc + ", texts packed varlen (M = sum of lengths)",
@@ -253,7 +423,16 @@ def main():
         "gemm_ms_per_step": round(gemm_ms_step, 4),
         "attention_ms_per_step": round(attn_ms_step, 4),
         "bf16_split_ms_per_step": round(split_ms_step, 4),
+        "step_ms": {"median": round(pct(step_ms, 50), 4), "p10": round(pct(step_ms, 10), 4),
+                    "p90": round(pct(step_ms, 90), 4), "steps": int(step_ms.size),
+                    "clock": "HIP events between steps on the library stream"},
+        "median_tokens_per_s": round(tokens / (pct(step_ms, 50) * 1e-3), 1),
+        "fp32_attention_tokens_per_s": None if attn3_rate is None else round(attn3_rate, 1),
         "pcie_inclusive_tokens_per_s": round(host_rate, 1),
+        "pcie_inclusive_step_ms": {"median": round(pct(host_ms, 50), 4),
+                                   "p10": round(pct(host_ms, 10), 4),
+                                   "p90": round(pct(host_ms, 90), 4)},
+        "u8_vs_oracle": u8diff,
         "padded_slots_per_s": round(BATCH * SEQ * args.steps / elapsed, 1),
         "cpu_baseline": baseline,
     }

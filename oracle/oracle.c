@@ -15,6 +15,7 @@
 #include "oracle_int.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -232,6 +233,159 @@ gemm_u8s8_vnni512(int32_t *acc, const uint8_t *qa, int lda, const int8_t *q,
   }
 }
 #endif
+
+/* ------------------------------------------------------------------------ */
+/* The reference's own full-int8 kernel shape (the CPU baseline's path)      */
+/* ------------------------------------------------------------------------ */
+
+/* PackB8VNNI's weight layout, internal/tensor/pack_vnni.go:44-72: panels of
+ * 16 columns, per k-group of 4 the 16 columns' 4 bytes, zero past k:
+ * pb[(c/16)*kg*64 + (p/4)*64 + (c%16)*4 + p%4] = q[c][p]. */
+void or_pack_vnni_panels(const int8_t *q, int k, int n, int8_t *pb) {
+  int kg = (k + 3) / 4;
+  memset(pb, 0, (size_t)(n / 16) * kg * 64);
+  for (int c = 0; c < n; c++) {
+    size_t base = (size_t)(c / 16) * kg * 64 + (size_t)(c % 16) * 4;
+    for (int p = 0; p < k; p++) pb[base + (size_t)(p / 4) * 64 + p % 4] = q[(size_t)c * k + p];
+  }
+}
+
+/* gemm4x16vnni / gemm4x16vnni512 (vnni_amd64.s:22-82, vnni512_amd64.s:16-76):
+ * a 4x16 int32 tile; per k-group the 64-byte panel slice is two 8-dword
+ * vectors, each row's 4 activation bytes are broadcast, and eight VPDPBUSD
+ * accumulate (u8 x s8, wrapping). a0..a3 are the four rows (kg*4 bytes). */
+#if defined(__x86_64__)
+__attribute__((target("avxvnni"))) static void tile4x16_avxvnni(
+    int32_t *dst, int n, const uint8_t *const a[4], const int8_t *pb, int kg) {
+  __m256i c0 = _mm256_setzero_si256(), c1 = c0, c2 = c0, c3 = c0, c4 = c0, c5 = c0,
+          c6 = c0, c7 = c0;
+  for (int g = 0; g < kg; g++) {
+    __m256i b0 = _mm256_loadu_si256((const __m256i *)(pb + (size_t)g * 64));
+    __m256i b1 = _mm256_loadu_si256((const __m256i *)(pb + (size_t)g * 64 + 32));
+    int32_t w0, w1, w2, w3;
+    memcpy(&w0, a[0] + 4 * g, 4);
+    memcpy(&w1, a[1] + 4 * g, 4);
+    memcpy(&w2, a[2] + 4 * g, 4);
+    memcpy(&w3, a[3] + 4 * g, 4);
+    __m256i r0 = _mm256_set1_epi32(w0), r1 = _mm256_set1_epi32(w1),
+            r2 = _mm256_set1_epi32(w2), r3 = _mm256_set1_epi32(w3);
+    c0 = _mm256_dpbusd_avx_epi32(c0, r0, b0);
+    c1 = _mm256_dpbusd_avx_epi32(c1, r0, b1);
+    c2 = _mm256_dpbusd_avx_epi32(c2, r1, b0);
+    c3 = _mm256_dpbusd_avx_epi32(c3, r1, b1);
+    c4 = _mm256_dpbusd_avx_epi32(c4, r2, b0);
+    c5 = _mm256_dpbusd_avx_epi32(c5, r2, b1);
+    c6 = _mm256_dpbusd_avx_epi32(c6, r3, b0);
+    c7 = _mm256_dpbusd_avx_epi32(c7, r3, b1);
+  }
+  _mm256_storeu_si256((__m256i *)(dst), c0);
+  _mm256_storeu_si256((__m256i *)(dst + 8), c1);
+  _mm256_storeu_si256((__m256i *)(dst + n), c2);
+  _mm256_storeu_si256((__m256i *)(dst + n + 8), c3);
+  _mm256_storeu_si256((__m256i *)(dst + 2 * n), c4);
+  _mm256_storeu_si256((__m256i *)(dst + 2 * n + 8), c5);
+  _mm256_storeu_si256((__m256i *)(dst + 3 * n), c6);
+  _mm256_storeu_si256((__m256i *)(dst + 3 * n + 8), c7);
+}
+
+__attribute__((target("avx512f,avx512vl,avx512vnni"))) static void tile4x16_avx512vnni(
+    int32_t *dst, int n, const uint8_t *const a[4], const int8_t *pb, int kg) {
+  __m256i c0 = _mm256_setzero_si256(), c1 = c0, c2 = c0, c3 = c0, c4 = c0, c5 = c0,
+          c6 = c0, c7 = c0;
+  for (int g = 0; g < kg; g++) {
+    __m256i b0 = _mm256_loadu_si256((const __m256i *)(pb + (size_t)g * 64));
+    __m256i b1 = _mm256_loadu_si256((const __m256i *)(pb + (size_t)g * 64 + 32));
+    int32_t w0, w1, w2, w3;
+    memcpy(&w0, a[0] + 4 * g, 4);
+    memcpy(&w1, a[1] + 4 * g, 4);
+    memcpy(&w2, a[2] + 4 * g, 4);
+    memcpy(&w3, a[3] + 4 * g, 4);
+    __m256i r0 = _mm256_set1_epi32(w0), r1 = _mm256_set1_epi32(w1),
+            r2 = _mm256_set1_epi32(w2), r3 = _mm256_set1_epi32(w3);
+    c0 = _mm256_dpbusd_epi32(c0, r0, b0);
+    c1 = _mm256_dpbusd_epi32(c1, r0, b1);
+    c2 = _mm256_dpbusd_epi32(c2, r1, b0);
+    c3 = _mm256_dpbusd_epi32(c3, r1, b1);
+    c4 = _mm256_dpbusd_epi32(c4, r2, b0);
+    c5 = _mm256_dpbusd_epi32(c5, r2, b1);
+    c6 = _mm256_dpbusd_epi32(c6, r3, b0);
+    c7 = _mm256_dpbusd_epi32(c7, r3, b1);
+  }
+  _mm256_storeu_si256((__m256i *)(dst), c0);
+  _mm256_storeu_si256((__m256i *)(dst + 8), c1);
+  _mm256_storeu_si256((__m256i *)(dst + n), c2);
+  _mm256_storeu_si256((__m256i *)(dst + n + 8), c3);
+  _mm256_storeu_si256((__m256i *)(dst + 2 * n), c4);
+  _mm256_storeu_si256((__m256i *)(dst + 2 * n + 8), c5);
+  _mm256_storeu_si256((__m256i *)(dst + 3 * n), c6);
+  _mm256_storeu_si256((__m256i *)(dst + 3 * n + 8), c7);
+}
+#endif
+
+/* The same tile with scalar integer arithmetic (no VNNI on the host). */
+static void tile4x16_portable(int32_t *dst, int n, const uint8_t *const a[4],
+                              const int8_t *pb, int kg) {
+  uint32_t c[4][16] = {{0}};
+  for (int g = 0; g < kg; g++)
+    for (int r = 0; r < 4; r++)
+      for (int col = 0; col < 16; col++)
+        for (int e = 0; e < 4; e++)
+          c[r][col] += (uint32_t)((int32_t)a[r][4 * g + e] *
+                                  (int32_t)pb[(size_t)g * 64 + col * 4 + e]);
+  for (int r = 0; r < 4; r++)
+    for (int col = 0; col < 16; col++) dst[(size_t)r * n + col] = (int32_t)c[r][col];
+}
+
+static int panel_kind_cached = -1;
+
+int or_vnni_panel_kind(void) {
+  if (panel_kind_cached < 0) {
+    int kind = 0;
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    if (getenv("OR_FORCE_PORTABLE") == 0) {
+      /* the reference prefers the VEX form where it exists (pack_vnni.go:152-156) */
+      if (__builtin_cpu_supports("avxvnni")) kind = 1;
+      else if (__builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512vl"))
+        kind = 2;
+    }
+#endif
+    panel_kind_cached = kind;
+  }
+  return panel_kind_cached;
+}
+
+/* MatMulPackedVNNI's unit loop (pack_vnni.go:142-151): one unit per 4-row x
+ * 16-column tile over the row panels of qa (rows of lda >= kg*4 bytes, zero
+ * past k) and the panels of pb; a partial last row panel reads zero rows, as
+ * the reference's PackAPad rows are. acc[m][n] is the u8 x s8 sum. */
+void or_gemm_u8s8_panels(int32_t *acc, const uint8_t *qa, int lda, const int8_t *pb, int m,
+                         int k, int n) {
+  int kg = (k + 3) / 4;
+  int kind = or_vnni_panel_kind();
+  uint8_t *zero = (uint8_t *)calloc((size_t)kg * 4, 1);
+  int32_t tile[4 * 16];
+  for (int rp = 0; rp < (m + 3) / 4; rp++) {
+    const uint8_t *a[4];
+    for (int r = 0; r < 4; r++) a[r] = rp * 4 + r < m ? qa + (size_t)(rp * 4 + r) * lda : zero;
+    for (int cp = 0; cp < n / 16; cp++) {
+      const int8_t *panel = pb + (size_t)cp * kg * 64;
+#if defined(__x86_64__)
+      if (kind == 1) tile4x16_avxvnni(tile, 16, a, panel, kg);
+      else if (kind == 2) tile4x16_avx512vnni(tile, 16, a, panel, kg);
+      else
+#endif
+        tile4x16_portable(tile, 16, a, panel, kg);
+      for (int r = 0; r < 4 && rp * 4 + r < m; r++)
+        memcpy(acc + (size_t)(rp * 4 + r) * n + (size_t)cp * 16, tile + r * 16, 64);
+    }
+  }
+  free(zero);
+}
+
+static int gemm_impl = 0; /* 0: row-major dot products, 1: the reference's panels */
+
+void or_set_gemm_impl(int impl) { gemm_impl = impl; }
 
 static int vnni_kind_cached = -1;
 
@@ -579,6 +733,8 @@ void or__dense_init(or_dense *d, const float *raw, int owned_raw,
     d->colsum = (int32_t *)malloc(sizeof(int32_t) * out);
     if (or_pack_b8_vnni(raw, in, out, d->q, d->colsum, d->scales) == OR_OK) {
       d->kind = 2;
+      d->panels = (int8_t *)malloc((size_t)(out / 16) * ((in + 3) / 4) * 64);
+      or_pack_vnni_panels(d->q, in, out, d->panels);
       if (owned_raw) free((void *)raw);
       return;
     }
@@ -613,13 +769,42 @@ void or__dense_free(or_dense *d) {
   free(d->colsum);
   free(d->rawcopy);
   free(d->bias);
+  free(d->panels);
+}
+
+/* MatMulPackedVNNI as the reference runs it (pack_vnni.go:124-176): rows
+ * quantized into kg*4-byte rows (QuantizeRowU8 zeroes the tail), the 4x16
+ * panel kernel, then the same dequantization as or_matmul_vnni. */
+static void matmul_vnni_panels(const or_dense *d, float *dst, const float *x, int seq) {
+  if (seq <= 0) return;
+  int k = d->in, n = d->out, lda = ((k + 3) / 4) * 4;
+  uint8_t *qa = (uint8_t *)malloc((size_t)seq * lda + 4);
+  float *rs = (float *)malloc(sizeof(float) * (size_t)seq + 4);
+  int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)seq * n + 4);
+  for (int i = 0; i < seq; i++)
+    rs[i] = or_quantize_row_u8(qa + (size_t)i * lda, lda, x + (size_t)i * k, k);
+  or_gemm_u8s8_panels(acc, qa, lda, d->panels, seq, k, n);
+  for (int i = 0; i < seq; i++) {
+    float r = rs[i];
+    for (int j = 0; j < n; j++) {
+      int32_t real =
+          (int32_t)((uint32_t)acc[(size_t)i * n + j] - 128u * (uint32_t)d->colsum[j]);
+      float t = (float)real * r;
+      dst[(size_t)i * n + j] = t * d->scales[j];
+    }
+  }
+  free(qa);
+  free(rs);
+  free(acc);
 }
 
 /* applyDense, bert.go:282-301: GEMM by the mode the weight took, then a
  * separate AddBias pass. */
 void or__dense_apply(const or_dense *d, float *dst, const float *x,
                         int seq) {
-  if (d->kind == 2)
+  if (d->kind == 2 && gemm_impl == 1 && d->panels)
+    matmul_vnni_panels(d, dst, x, seq);
+  else if (d->kind == 2)
     or_matmul_vnni(dst, x, d->q, d->colsum, d->scales, seq, d->in, d->out,
                    NULL, NULL, NULL);
   else if (d->kind == 1)
@@ -684,7 +869,15 @@ void or_bert_free(or_bert_model *m) {
 /* encodeWorkers, bert.go:740-923 (BERT branch; no MPNet relative bias). */
 int or_bert_encode(const or_bert_model *m, const int32_t *ids, int seq,
                    float *x) {
+  return or_bert_encode_layers(m, ids, seq, x, m->cfg.layers);
+}
+
+/* The same forward stopped after the first `layers` layers (the hidden
+ * states that enter layer `layers`). */
+int or_bert_encode_layers(const or_bert_model *m, const int32_t *ids, int seq,
+                          float *x, int layers) {
   const or_bert_config *c = &m->cfg;
+  if (layers < 0 || layers > c->layers) return OR_ERR_SEQ;
   int H = c->hidden, I = c->inter, heads = c->heads, dh = H / heads;
   if (seq <= 0) return OR_ERR_SEQ;
   if (seq > c->max_pos) return OR_ERR_SEQ;
@@ -716,7 +909,7 @@ int or_bert_encode(const or_bert_model *m, const int32_t *ids, int seq,
   or_layernorm(x, m->emb_ln_g, m->emb_ln_b, seq, H, c->eps);
 
   float scale = (float)(1.0 / sqrt((double)dh));
-  for (int li = 0; li < c->layers; li++) {
+  for (int li = 0; li < layers; li++) {
     const or_layer *L = &m->layers[li];
     or__dense_apply(&L->qkv, qkv, x, seq);
     /* Per-head attention, bert.go:853-902. */
@@ -787,13 +980,21 @@ int or_bert_forward(const or_bert_model *m, const int32_t *ids, int seq,
 int or_bert_embed_batch(const or_bert_model *m, const int32_t *ids,
                         const int32_t *lens, int batch, int stride,
                         float *out, int threads) {
+  return or_bert_embed_batch_timed(m, ids, lens, batch, stride, out, threads, NULL);
+}
+
+/* The same with each text's forward timed (wall seconds; secs may be NULL). */
+int or_bert_embed_batch_timed(const or_bert_model *m, const int32_t *ids,
+                        const int32_t *lens, int batch, int stride,
+                        float *out, int threads, double *secs) {
   int H = m->cfg.hidden;
   int err = OR_OK;
   if (threads < 1) threads = 1;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
   for (int b = 0; b < batch; b++) {
-    int st = or_bert_forward(m, ids + (size_t)b * stride, lens[b],
-                             out + (size_t)b * H);
+    double t0 = omp_get_wtime();
+    int st = or_bert_forward(m, ids + (size_t)b * stride, lens[b], out + (size_t)b * H);
+    if (secs) secs[b] = omp_get_wtime() - t0;
     if (st != OR_OK) {
 #pragma omp critical
       if (err == OR_OK) err = st;

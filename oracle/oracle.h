@@ -131,6 +131,9 @@ void or_bert_free(or_bert_model *m);
  * writing the final hidden states [seq][H]. */
 int or_bert_encode(const or_bert_model *m, const int32_t *ids, int seq,
                    float *hidden);
+/* ...stopped after the first `layers` layers (0 <= layers <= cfg.layers). */
+int or_bert_encode_layers(const or_bert_model *m, const int32_t *ids, int seq,
+                          float *x, int layers);
 /* Forward (bert.go:649-703): encode, pool, optional L2. out is [H]. */
 int or_bert_forward(const or_bert_model *m, const int32_t *ids, int seq,
                     float *out);
@@ -140,6 +143,11 @@ int or_bert_forward(const or_bert_model *m, const int32_t *ids, int seq,
 int or_bert_embed_batch(const or_bert_model *m, const int32_t *ids,
                         const int32_t *lens, int batch, int stride,
                         float *out, int threads);
+/* ...with each text's forward timed into secs[batch] (wall seconds). */
+int or_bert_embed_batch_timed(const or_bert_model *m, const int32_t *ids,
+                        const int32_t *lens, int batch, int stride,
+                        float *out, int threads,
+                        double *secs);
 
 /* ---- decoder-family embedders (internal/model/qwen3.go, gemma3.go) ---- */
 #define OR_ARCH_QWEN3 1
@@ -181,6 +189,11 @@ int or_dec_forward(const or_dec_model *m, const int32_t *ids, int seq, float *ou
 int or_dec_embed_batch(const or_dec_model *m, const int32_t *ids,
                        const int32_t *lens, int batch, int stride, float *out,
                        int threads);
+/* ...with each text's forward timed into secs[batch] (wall seconds). */
+int or_dec_embed_batch_timed(const or_dec_model *m, const int32_t *ids,
+                       const int32_t *lens, int batch, int stride, float *out,
+                       int threads,
+                        double *secs);
 
 /* building blocks (exported for the unit tests) */
 void or_rope_table(float *cos_t, float *sin_t, int seq, int dh, double theta);
@@ -192,6 +205,17 @@ void or_flash_causal_head(const float *qh, const float *kh, const float *vh,
  * 2 = AVX-512-VNNI intrinsics, 0 = portable C. Both produce identical
  * integers. */
 int or_vnni_kind(void);
+/* The reference's full-int8 kernel shape: PackB8VNNI's panel layout
+ * (pack_vnni.go:44-72) and gemm4x16vnni / gemm4x16vnni512's 4x16 tiles
+ * (vnni_amd64.s:22-82, vnni512_amd64.s:16-76) over qa rows of lda >=
+ * kg*4 bytes; same integers as or_gemm_u8s8_i32. or_vnni_panel_kind: 1 VEX
+ * AVX-VNNI, 2 EVEX AVX-512-VNNI, 0 portable. or_set_gemm_impl(1) makes the
+ * models' full-int8 denses run this path (the CPU baseline), 0 the default. */
+void or_pack_vnni_panels(const int8_t *q, int k, int n, int8_t *pb);
+void or_gemm_u8s8_panels(int32_t *acc, const uint8_t *qa, int lda, const int8_t *pb, int m,
+                         int k, int n);
+int or_vnni_panel_kind(void);
+void or_set_gemm_impl(int impl);
 
 #ifdef __cplusplus
 }

@@ -49,15 +49,22 @@ def _load():
         "or_bert_create": (P, [P, I, P, P, P, P, P, P]),
         "or_bert_free": (None, [P]),
         "or_bert_encode": (I, [P, P, I, P]),
+        "or_bert_encode_layers": (I, [P, P, I, P, I]),
         "or_bert_forward": (I, [P, P, I, P]),
         "or_bert_embed_batch": (I, [P, P, P, I, I, P, I]),
+        "or_bert_embed_batch_timed": (I, [P, P, P, I, I, P, I, P]),
         "or_vnni_kind": (I, []),
+        "or_pack_vnni_panels": (None, [P, I, I, P]),
+        "or_gemm_u8s8_panels": (None, [P, P, I, P, I, I, I]),
+        "or_vnni_panel_kind": (I, []),
+        "or_set_gemm_impl": (None, [I]),
         "or_dec_create": (P, [P, I, P, P, P, P, P]),
         "or_dec_free": (None, [P]),
         "or_dec_quantized_kind": (I, [P]),
         "or_dec_encode": (I, [P, P, I, P]),
         "or_dec_forward": (I, [P, P, I, P]),
         "or_dec_embed_batch": (I, [P, P, P, I, I, P, I]),
+        "or_dec_embed_batch_timed": (I, [P, P, P, I, I, P, I, P]),
         "or_rope_table": (None, [P, P, I, I, ctypes.c_double]),
         "or_apply_rope": (None, [P, I, I, P, P]),
         "or_flash_causal_head": (None, [P, P, P, P, I, I, F]),
@@ -97,6 +104,25 @@ def pack_b8_vnni(bT, k, n):
     bT = f32(bT)
     st = lib.or_pack_b8_vnni(_p(bT), k, n, _p(q), _p(cs), _p(sc))
     return st, q, sc, cs
+
+
+def pack_vnni_panels(q):
+    """PackB8VNNI's panel layout of int8 q [n][k] (pack_vnni.go:44-72)."""
+    q = np.ascontiguousarray(q, np.int8)
+    n, k = q.shape
+    kg = (k + 3) // 4
+    pb = np.empty((n // 16) * kg * 64, np.int8)
+    lib.or_pack_vnni_panels(_p(q), k, n, _p(pb))
+    return pb
+
+
+def gemm_u8s8_panels(qa, pb, k, n):
+    """The 4x16 VPDPBUSD tiles of the reference over qa rows [m][lda]."""
+    qa = np.ascontiguousarray(qa, np.uint8)
+    m, lda = qa.shape
+    acc = np.empty((m, n), np.int32)
+    lib.or_gemm_u8s8_panels(_p(acc), _p(qa), lda, _p(pb), m, k, n)
+    return acc
 
 
 def quantize_row_u8(a, dstlen=None):
@@ -258,10 +284,13 @@ class BertOracle:
     def __del__(self):
         self.close()
 
-    def encode(self, ids):
+    def encode(self, ids, layers=None):
+        """Final hidden states [len][H]; with `layers`, the hidden states
+        after that many layers."""
         ids = np.ascontiguousarray(ids, np.int32)
         out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
-        st = lib.or_bert_encode(self.h, _p(ids), ids.shape[0], _p(out))
+        n = self.shape.layers if layers is None else layers
+        st = lib.or_bert_encode_layers(self.h, _p(ids), ids.shape[0], _p(out), n)
         if st:
             raise RuntimeError(f"oracle encode status {st}")
         return out
@@ -274,12 +303,15 @@ class BertOracle:
             raise RuntimeError(f"oracle forward status {st}")
         return out
 
-    def embed_batch(self, ids, lens, threads=1):
+    def embed_batch(self, ids, lens, threads=1, secs=None):
+        """One forward per text across `threads`; `secs` (float64 [batch])
+        receives each text's forward time."""
         ids = np.ascontiguousarray(ids, np.int32)
         lens = np.ascontiguousarray(lens, np.int32)
         out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
-        st = lib.or_bert_embed_batch(self.h, _p(ids), _p(lens), ids.shape[0],
-                                     ids.shape[1], _p(out), threads)
+        st = lib.or_bert_embed_batch_timed(self.h, _p(ids), _p(lens), ids.shape[0],
+                                           ids.shape[1], _p(out), threads,
+                                           None if secs is None else _p(secs))
         if st:
             raise RuntimeError(f"oracle embed status {st}")
         return out
@@ -367,12 +399,15 @@ class DecoderOracle:
             raise RuntimeError(f"oracle forward status {st}")
         return out
 
-    def embed_batch(self, ids, lens, threads=1):
+    def embed_batch(self, ids, lens, threads=1, secs=None):
+        """One forward per text across `threads`; `secs` (float64 [batch])
+        receives each text's forward time."""
         ids = np.ascontiguousarray(ids, np.int32)
         lens = np.ascontiguousarray(lens, np.int32)
         out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
-        st = lib.or_dec_embed_batch(self.h, _p(ids), _p(lens), ids.shape[0], ids.shape[1],
-                                    _p(out), threads)
+        st = lib.or_dec_embed_batch_timed(self.h, _p(ids), _p(lens), ids.shape[0],
+                                          ids.shape[1], _p(out), threads,
+                                          None if secs is None else _p(secs))
         if st:
             raise RuntimeError(f"oracle embed status {st}")
         return out

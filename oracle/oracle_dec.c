@@ -9,6 +9,7 @@
  * rounds twice exactly as Go's float32 arithmetic does.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -394,13 +395,23 @@ int or_dec_forward(const or_dec_model *m, const int32_t *ids, int seq, float *ou
 }
 
 int or_dec_embed_batch(const or_dec_model *m, const int32_t *ids,
-                       const int32_t *lens, int batch, int stride, float *out,
-                       int threads) {
-  int H = m->cfg.hidden, err = OR_OK;
+                        const int32_t *lens, int batch, int stride,
+                        float *out, int threads) {
+  return or_dec_embed_batch_timed(m, ids, lens, batch, stride, out, threads, NULL);
+}
+
+/* The same with each text's forward timed (wall seconds; secs may be NULL). */
+int or_dec_embed_batch_timed(const or_dec_model *m, const int32_t *ids,
+                        const int32_t *lens, int batch, int stride,
+                        float *out, int threads, double *secs) {
+  int H = m->cfg.hidden;
+  int err = OR_OK;
   if (threads < 1) threads = 1;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
   for (int b = 0; b < batch; b++) {
+    double t0 = omp_get_wtime();
     int st = or_dec_forward(m, ids + (size_t)b * stride, lens[b], out + (size_t)b * H);
+    if (secs) secs[b] = omp_get_wtime() - t0;
     if (st != OR_OK) {
 #pragma omp critical
       if (err == OR_OK) err = st;

@@ -19,6 +19,7 @@ typedef struct {
   int32_t *colsum;
   float *bias; /* owned (fused QKV) or NULL */
   const float *bias_ref;
+  int8_t *panels; /* full int8: the same q in PackB8VNNI's panel layout */
 } or_dense;
 
 /* newDense (bert.go:263-278): full int8 -> weight-only int8 -> fp32 fallback. */

@@ -126,6 +126,52 @@ def test_gemm_u8s8_vnni_body_matches_portable():
         assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("m,k,n", [(13, 129, 64), (7, 384, 384), (64, 768, 2304),
+                                   (5, 3, 16), (33, 1000, 32), (1, 3072, 768)])
+def test_vnni_panel_kernel_matches_brute_force(m, k, n):
+    """The reference's kernel shape (PackB8VNNI panels, 4x16 VPDPBUSD tiles
+    with broadcast activation groups, zero past k and past m) gives the
+    wrapping int64-brute-force sums and the default oracle body's integers;
+    the portable tile agrees. A transposed panel index, a dropped k-group or
+    a wrong row panel breaks the first check."""
+    rng = np.random.default_rng(m * 7 + k + n)
+    q = rng.integers(-128, 128, size=(n, k)).astype(np.int8)
+    kg = (k + 3) // 4
+    qa = np.zeros((m, kg * 4), np.uint8)
+    qa[:, :k] = rng.integers(0, 256, size=(m, k))
+    pb = O.pack_vnni_panels(q)
+    # the layout itself: column c, k index p at (c//16)*kg*64 + (p//4)*64 + (c%16)*4 + p%4
+    c, pk = rng.integers(0, n), rng.integers(0, k)
+    assert pb[(c // 16) * kg * 64 + (pk // 4) * 64 + (c % 16) * 4 + pk % 4] == q[c, pk]
+    got = O.gemm_u8s8_panels(qa, pb, k, n)
+    ref = qa[:, :k].astype(np.int64) @ q.astype(np.int64).T
+    ref = ((ref + 2**31) % 2**32 - 2**31).astype(np.int32)
+    assert np.array_equal(got, ref)
+    assert np.array_equal(got, O.gemm_u8s8_i32(np.ascontiguousarray(qa[:, :k]), q))
+
+
+def test_vnni_panel_kernel_portable_body():
+    """The scalar 4x16 tile (hosts without VNNI) gives the same integers,
+    run in a fresh process so the CPU dispatch is decided again."""
+    import subprocess
+    import sys
+    code = (
+        "import numpy as np\n"
+        "from oracle import oracle as O\n"
+        "assert O.lib.or_vnni_panel_kind() == 0\n"
+        "rng = np.random.default_rng(3)\n"
+        "q = rng.integers(-128, 128, size=(48, 200)).astype(np.int8)\n"
+        "qa = rng.integers(0, 256, size=(9, 200)).astype(np.uint8)\n"
+        "got = O.gemm_u8s8_panels(qa, O.pack_vnni_panels(q), 200, 48)\n"
+        "ref = qa.astype(np.int64) @ q.astype(np.int64).T\n"
+        "ref = ((ref + 2**31) % 2**32 - 2**31).astype(np.int32)\n"
+        "assert np.array_equal(got, ref)\n")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, OR_FORCE_PORTABLE="1", PYTHONPATH=root)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
 def test_pack_b8_error_bound_and_zero_channel():
     kk = KATS["pack_b8_error"]
     k, n = kk["k"], kk["n"]
@@ -403,11 +449,36 @@ def test_bert_oracle_modes_and_batch_policy():
         single = np.stack([orc.forward(ids[b, :lens[b]]) for b in range(len(lens))])
         assert np.array_equal(batch1, single)
         outs[quant] = batch1
+    # the full-int8 denses on the reference's panel kernel give the same bits
+    orc = O.BertOracle(shape, t, 2)
+    O.lib.or_set_gemm_impl(1)
+    try:
+        secs = np.zeros(len(lens))
+        panels = orc.embed_batch(ids, lens, threads=3, secs=secs)
+    finally:
+        O.lib.or_set_gemm_impl(0)
+    assert np.array_equal(panels, outs[2])
+    assert np.all(secs > 0)
     for quant, floor in ((1, 0.999), (2, 0.99)):
         cos = np.sum(outs[quant] * outs[0], axis=1)
         assert np.all(cos >= floor), (quant, cos.min())
         # the quantized path must actually be active (rembed_test.go:176-237)
         assert np.max(np.abs(outs[quant] - outs[0])) >= 1e-4
+
+
+def test_bert_oracle_encode_stops_after_layers():
+    """encode(ids, L) of a model equals the full encode of the same model
+    built with its first L layers."""
+    import dataclasses
+
+    from rembed_amd.synthetic import bert_tensors
+    shape = tiny_shape()
+    t = bert_tensors(shape, seed=12)
+    ids = np.arange(5, 40, dtype=np.int32) % shape.vocab
+    full = O.BertOracle(shape, t, 2)
+    for L in range(1, shape.layers + 1):
+        part = O.BertOracle(dataclasses.replace(shape, layers=L), t, 2)
+        assert np.array_equal(full.encode(ids, L), part.encode(ids)), L
 
 
 def test_bert_oracle_rejects_bad_input():
