@@ -5,6 +5,7 @@ QuantizedActivations); embed()/embed_tokens() take token ids the way
 Embedder.Embed/EmbedTokens feed them (rembed.go:287-411), batched.
 """
 import ctypes
+import os
 import sys
 
 import numpy as np
@@ -72,11 +73,19 @@ class Model:
 
     @classmethod
     def from_safetensors(cls, ctx, shape, path, quant=QUANT_NONE, **kw):
-        """model.Load over one .safetensors file (bert.go:307-524 reading
-        through safetensors.go:122-181): every tensor widened to float32 and
-        handed over by name; the library fuses Q|K|V and packs on finalize."""
-        from .checkpoint import load
-        return cls(ctx, shape, load(path), quant, **kw)
+        """model.Load (bert.go:307-524) over `path`: a model directory
+        (model.safetensors, or the shards its model.safetensors.index.json
+        names, safetensors.go:54-121; for Gemma also 2_Dense/ and 3_Dense/,
+        gemma3.go:144-172) or one .safetensors file. Every tensor is widened
+        to float32 and handed over by name; the library fuses projections and
+        packs on finalize."""
+        from . import checkpoint
+        if os.path.isdir(path):
+            dense = getattr(shape, "dense_hidden", 0)
+            t = checkpoint.load_model_dir(path, dense, shape.hidden)
+        else:
+            t = checkpoint.load_any(path)
+        return cls(ctx, shape, t, quant, **kw)
 
     def close(self):
         if getattr(self, "h", None):
