@@ -252,7 +252,7 @@ int rh_layernorm(rh_context *ctx, float *x, const float *gamma,
  * Replaces model.Load + Model.Forward/ForwardTokens + the Embed batch loop
  * (internal/model/bert.go:307-524,649-731; rembed.go:287-411) with one
  * device-resident forward over a packed variable-length batch. */
-#define RH_ARCH_BERT 0   /* BERT / RoBERTa / DistilBERT-style post-LN encoder */
+#define RH_ARCH_BERT 0   /* BERT / RoBERTa post-LN encoder (encoder.layer.N.* names) */
 #define RH_ARCH_QWEN3 1  /* Qwen3 causal decoder embedder (qwen3.go:395-548) */
 #define RH_ARCH_GEMMA3 2 /* EmbeddingGemma: Gemma 3 run bidirectionally (gemma3.go:206-384) */
 #define RH_POOL_MEAN 0
@@ -294,7 +294,7 @@ typedef struct rh_model rh_model;
 int rh_model_create(rh_context *ctx, const rh_model_config *cfg, int quant,
                     rh_model **out);
 /* Hand one HF tensor (by its safetensors name, with or without the
- * "bert."/"roberta."/"distilbert." prefix; decoders: embed_tokens.weight,
+ * "bert."/"roberta." prefix; decoders: embed_tokens.weight,
  * norm.weight, layers.N.*, with or without "model.", and Gemma's Dense head
  * as "2_Dense.linear.weight" / "3_Dense.linear.weight") to the model; data
  * is copied. */
@@ -303,6 +303,17 @@ int rh_model_set_tensor(rh_model *m, const char *name, const float *host,
 /* Check every tensor is present, fuse Q|K|V (decoders: also gate|up into
  * one gated weight), quantize/pack and upload. */
 int rh_model_finalize(rh_model *m);
+/* A second handle on a finalized model's weights, bound to another context
+ * on the same device. The weights stay in HBM once; each handle has its own
+ * stream, workspace and lock, so calls on different handles run
+ * concurrently (calls on one handle, or on handles sharing a context,
+ * serialize). Options are copied from src and may then be set per handle
+ * (not RH_OPT_FUSE_PROJECTIONS). Handles are destroyed in any order; the
+ * weights go with the last. RH_ERR_INVALID for an unfinalized src or a
+ * context on another device. Replaces: the reference Model's safety for
+ * concurrent use with its weights held once (bert.go:52-56,
+ * rembed.go:36-41), which a context-bound device model cannot give alone. */
+int rh_model_share(rh_model *src, rh_context *ctx, rh_model **out);
 void rh_model_destroy(rh_model *m);
 /* Per-model switches. RH_OPT_ATTN_PRECISION: 1 = bf16 attention operands,
  * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE).

@@ -50,7 +50,7 @@ EXPORTS = [
     "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_linear_u8",
     "rh_linear_noalloc", "rh_gelu",
     "rh_layernorm", "rh_model_create", "rh_model_set_tensor",
-    "rh_model_finalize", "rh_model_destroy", "rh_model_set_option",
+    "rh_model_finalize", "rh_model_share", "rh_model_destroy", "rh_model_set_option",
     "rh_model_quantized", "rh_model_quantized_activations", "rh_model_embed",
     "rh_model_embed_tokens", "rh_model_embed_device", "rh_model_check",
 ]
@@ -130,6 +130,7 @@ def _load():
         "rh_model_create": (I, [P, ctypes.POINTER(ModelConfig), I, ctypes.POINTER(P)]),
         "rh_model_set_tensor": (I, [P, ctypes.c_char_p, P, P, I]),
         "rh_model_finalize": (I, [P]),
+        "rh_model_share": (I, [P, P, ctypes.POINTER(P)]),
         "rh_model_destroy": (None, [P]),
         "rh_model_set_option": (I, [P, I, I]),
         "rh_model_quantized": (I, [P]),

@@ -61,6 +61,52 @@ hipError_t dalloc(T** p, size_t count) {
   return hipMalloc((void**)p, count * sizeof(T) + 16);
 }
 
+// A model's device weights: packed linears, norms, embedding tables, RoPE
+// tables, the Dense head. Every rh_model handle over them (the one that
+// finalized them and each made by rh_model_share) holds a reference, and
+// the last one to go frees them. They are immutable once finalized, so
+// handles on different streams read them concurrently.
+struct WeightSet {
+  rh_context* ctx = nullptr;  // the context they were packed on (a reference)
+  std::vector<Layer> layers;
+  std::vector<DecLayer> dlayers;
+  std::vector<float*> bufs;
+
+  WeightSet(rh_context* c, std::vector<Layer> l, std::vector<DecLayer> d,
+            std::vector<float*> b)
+      : ctx(c), layers(std::move(l)), dlayers(std::move(d)), bufs(std::move(b)) {
+    ctx_retain(ctx);
+  }
+  WeightSet(const WeightSet&) = delete;
+  WeightSet& operator=(const WeightSet&) = delete;
+  // Each handle has synchronized its own streams before dropping its
+  // reference, so no kernel still reads these.
+  ~WeightSet() {
+    (void)hipSetDevice(ctx->device);
+    for (auto& L : layers) {
+      for (rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) {
+        if (!w) continue;
+        destroy_weight(w);
+        ctx_release(ctx);  // never the last reference: this set holds one
+      }
+      for (float* p : {L.ln1_g, L.ln1_b, L.ln2_g, L.ln2_b})
+        if (p) (void)hipFree(p);
+    }
+    for (auto& L : dlayers) {
+      for (rh_weight* w : {L.qkv, L.o, L.gu, L.down, L.q, L.k, L.v, L.gate, L.up}) {
+        if (!w) continue;
+        destroy_weight(w);
+        ctx_release(ctx);
+      }
+      for (float* p : {L.in_norm, L.q_norm, L.k_norm, L.post_attn, L.pre_ffn, L.post_ffn})
+        if (p) (void)hipFree(p);
+    }
+    for (float* p : bufs)
+      if (p) (void)hipFree(p);
+    ctx_release(ctx);
+  }
+};
+
 }  // namespace
 
 struct rh_model {
@@ -127,8 +173,19 @@ struct rh_model {
   int32_t* ids_pinned = nullptr;
   size_t ids_pinned_cap = 0;
   std::vector<int32_t> cu_host;  // packed row offsets of the current call
+  // Owner of the weights above once finalized, shared with every handle
+  // made by rh_model_share; null while the model is being built.
+  std::shared_ptr<WeightSet> weights;
 
   ~rh_model() { release(); }
+
+  // The weight set of the pointers above, which it then owns.
+  std::shared_ptr<WeightSet> own_weights() {
+    return std::make_shared<WeightSet>(
+        ctx, layers, dlayers,
+        std::vector<float*>{word, pos, type0, emb_g, emb_b, final_norm, dense1, dense2, cos_g,
+                            sin_g, cos_l, sin_l});
+  }
 
   void release_ws() {
     for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
@@ -164,29 +221,15 @@ struct rh_model {
         e = nullptr;
       }
     release_ws();
-    for (auto& L : layers) {
-      for (rh_weight* w : {L.qkv, L.o, L.f1, L.f2}) {
-        if (!w) continue;
-        destroy_weight(w);
-        ctx_release(ctx);  // never the last reference: the model holds one
-      }
-      for (float* p : {L.ln1_g, L.ln1_b, L.ln2_g, L.ln2_b})
-        if (p) (void)hipFree(p);
-    }
+    // Drop this handle's reference to the weights; a model that never
+    // finalized (or failed to) owns what it built so far and frees it here.
+    try {
+      if (ctx && !weights) weights = own_weights();
+    } catch (...) {
+    }  // out of host memory: the device weights leak rather than abort
+    weights.reset();
     layers.clear();
-    for (auto& L : dlayers) {
-      for (rh_weight* w : {L.qkv, L.o, L.gu, L.down, L.q, L.k, L.v, L.gate, L.up}) {
-        if (!w) continue;
-        destroy_weight(w);
-        ctx_release(ctx);
-      }
-      for (float* p : {L.in_norm, L.q_norm, L.k_norm, L.post_attn, L.pre_ffn, L.post_ffn})
-        if (p) (void)hipFree(p);
-    }
     dlayers.clear();
-    for (float* p : {word, pos, type0, emb_g, emb_b, final_norm, dense1, dense2, cos_g, sin_g,
-                     cos_l, sin_l})
-      if (p) (void)hipFree(p);
     word = pos = type0 = emb_g = emb_b = nullptr;
     final_norm = dense1 = dense2 = cos_g = sin_g = cos_l = sin_l = nullptr;
     if (err_d) (void)hipFree(err_d);
@@ -1299,8 +1342,49 @@ int rh_model_finalize(rh_model* m) {
       set_error(msg);
       return st;
     }
+    m->weights = m->own_weights();
     m->pending.clear();
     m->finalized = true;
+    return RH_OK;
+  });
+}
+
+int rh_model_share(rh_model* src, rh_context* ctx, rh_model** out) {
+  return api_call([&]() -> int {
+    if (!src || !ctx || !out) return fail(RH_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lk(src->mu);
+    if (!src->finalized || !src->weights) return fail(RH_ERR_INVALID, "model not finalized");
+    if (ctx->device != src->ctx->device)
+      return fail(RH_ERR_INVALID, "the context is on another device than the model's weights");
+    std::unique_ptr<rh_model> m(new rh_model());
+    m->cfg = src->cfg;
+    m->quant = src->quant;
+    m->layers = src->layers;
+    m->dlayers = src->dlayers;
+    m->word = src->word;
+    m->pos = src->pos;
+    m->type0 = src->type0;
+    m->emb_g = src->emb_g;
+    m->emb_b = src->emb_b;
+    m->final_norm = src->final_norm;
+    m->dense1 = src->dense1;
+    m->dense2 = src->dense2;
+    m->cos_g = src->cos_g;
+    m->sin_g = src->sin_g;
+    m->cos_l = src->cos_l;
+    m->sin_l = src->sin_l;
+    m->attn_precision = src->attn_precision;
+    m->fused_ffn1 = src->fused_ffn1;
+    m->producer_planes = src->producer_planes;
+    m->streams = src->streams;
+    m->qk_epilogue = src->qk_epilogue;
+    m->fuse_projections = src->fuse_projections;
+    m->split_gu_any = src->split_gu_any;
+    m->weights = src->weights;
+    m->finalized = true;
+    m->ctx = ctx;
+    ctx_retain(ctx);
+    *out = m.release();
     return RH_OK;
   });
 }

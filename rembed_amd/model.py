@@ -87,6 +87,16 @@ class Model:
             t = checkpoint.load_any(path)
         return cls(ctx, shape, t, quant, **kw)
 
+    def share(self, ctx):
+        """Another Model over these weights, bound to `ctx` (same device):
+        the weights stay in HBM once and the two run concurrently on their
+        own streams (rh_model_share). Close them in any order."""
+        h = ctypes.c_void_p()
+        check(lib.rh_model_share(self.h, ctx.h, ctypes.byref(h)))
+        other = Model.__new__(Model)
+        other.ctx, other.shape, other.h = ctx, self.shape, h
+        return other
+
     def close(self):
         if getattr(self, "h", None):
             lib.rh_model_destroy(self.h)

@@ -9,6 +9,10 @@
  *   rh_model_finalize                 (quantize, pack, upload; raw weights may go)
  *   rh_model_quantized[_activations]  (Quantized / QuantizedActivations)
  *   rh_model_embed(int64 ids)         (Embed's batch forward)
+ *   rh_context_create + rh_model_share (a second handle on the same weights,
+ *                                       as a concurrent server's pool holds)
+ *   rh_model_destroy, rh_context_destroy of the first handle, then an
+ *   rh_model_embed on the second that must give the same bytes
  *   rh_model_destroy, rh_context_destroy  (Close)
  *
  * Usage: abi_driver <bundle> <out>
@@ -24,7 +28,8 @@
  * quantized_activations, int32 batch, int32 hidden, float32 vectors
  * [batch][hidden]. The exit code is the first failing status (0 = ok), with
  * rh_last_error() on stderr; no device is RH_ERR_NO_DEVICE, as a Go host
- * would see before falling back to its CPU path.
+ * would see before falling back to its CPU path; 70 = the shared handle's
+ * vectors differ from the first handle's.
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -48,9 +53,9 @@ int main(int argc, char **argv) {
   int32_t ci[22], quant = 0, ntensors = 0, batch = 0, stride = 0;
   int32_t *lens = NULL;
   int64_t *ids = NULL;
-  float *vecs = NULL;
-  rh_context *ctx = NULL;
-  rh_model *model = NULL;
+  float *vecs = NULL, *vecs2 = NULL;
+  rh_context *ctx = NULL, *ctx2 = NULL;
+  rh_model *model = NULL, *model2 = NULL;
   int st = RH_OK, ndev = 0, i;
   int32_t header[5];
   FILE *out;
@@ -164,6 +169,42 @@ int main(int argc, char **argv) {
     goto done;
   }
 
+  /* A second handle on the same weights, on its own context; the first
+   * handle and its context go before the second is used. */
+  st = rh_context_create(0, &ctx2);
+  if (st != RH_OK) {
+    fail_status("rh_context_create (second)", st);
+    goto done;
+  }
+  st = rh_model_share(model, ctx2, &model2);
+  if (st != RH_OK) {
+    fail_status("rh_model_share", st);
+    goto done;
+  }
+  header[1] = rh_model_quantized(model);
+  header[2] = rh_model_quantized_activations(model);
+  rh_model_destroy(model);
+  rh_context_destroy(ctx);
+  model = NULL;
+  ctx = NULL;
+  vecs2 = (float *)malloc((size_t)batch * (size_t)cfg.hidden * 4 + 4);
+  if (!vecs2) {
+    st = RH_ERR_INVALID;
+    goto done;
+  }
+  st = rh_model_embed(model2, ids, lens, batch, stride, vecs2);
+  if (st != RH_OK) {
+    fail_status("rh_model_embed (shared handle)", st);
+    goto done;
+  }
+  if (rh_model_quantized(model2) != header[1] ||
+      rh_model_quantized_activations(model2) != header[2] ||
+      memcmp(vecs, vecs2, (size_t)batch * (size_t)cfg.hidden * 4) != 0) {
+    fprintf(stderr, "the shared handle's vectors differ\n");
+    st = 70;
+    goto done;
+  }
+
   out = fopen(argv[2], "wb");
   if (!out) {
     perror(argv[2]);
@@ -171,8 +212,6 @@ int main(int argc, char **argv) {
     goto done;
   }
   header[0] = st;
-  header[1] = rh_model_quantized(model);
-  header[2] = rh_model_quantized_activations(model);
   header[3] = batch;
   header[4] = cfg.hidden;
   if (fwrite(header, 4, 5, out) != 5 ||
@@ -184,9 +223,12 @@ int main(int argc, char **argv) {
 done:
   rh_model_destroy(model);
   rh_context_destroy(ctx);
+  rh_model_destroy(model2);
+  rh_context_destroy(ctx2);
   free(lens);
   free(ids);
   free(vecs);
+  free(vecs2);
   fclose(g_in);
   return st;
 }

@@ -59,3 +59,4 @@ def test_null_arguments_are_rejected_without_a_device():
     assert L.rh_weight_info(None, None, None, None) == _lib.RH_ERR_INVALID
     assert L.rh_model_create(None, None, 0, None) == _lib.RH_ERR_INVALID
     assert L.rh_model_embed(None, None, None, 0, 1, None) == _lib.RH_ERR_INVALID
+    assert L.rh_model_share(None, None, None) == _lib.RH_ERR_INVALID
