@@ -64,7 +64,8 @@ class StepEvents:
     a host synchronization inside the timed loop."""
 
     def __init__(self, stream, n):
-        self.hip = ctypes.CDLL("libamdhip64.so")
+        from rembed_amd import _lib
+        self.hip = _lib.hip_runtime()
         self.stream = ctypes.c_void_p(stream)
         self.ev = []
         for _ in range(n + 1):

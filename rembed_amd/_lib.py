@@ -150,6 +150,16 @@ def _load():
 lib = _load()
 
 
+def hip_runtime():
+    """The HIP runtime instance this library is linked against, for host
+    calls beside it (events on its stream, memory queries). Opened by its
+    soname, so the dynamic loader returns the copy already mapped for the
+    library; a lookup by file name could map a second runtime (another
+    package may ship a libamdhip64.so of its own) that shares no state with
+    the library's streams or devices."""
+    return ctypes.CDLL("libamdhip64.so.7")
+
+
 def check(code):
     """Raise RembedError for a non-zero status."""
     if code != RH_OK:

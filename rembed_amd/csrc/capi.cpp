@@ -228,6 +228,20 @@ static hipError_t upload_planes(rh_weight* w, const std::vector<uint8_t>& img) {
   return e;
 }
 
+// The s8 image [np][kp] rearranged into B-fragment order (rh_weight::d_frag).
+static hipError_t upload_frag(rh_weight* w, const std::vector<uint8_t>& img) {
+  const int ks_n = w->kp / 32;
+  std::vector<uint8_t> frag(img.size());
+  for (int nb = 0; nb < w->np / 32; nb++)
+    for (int ks = 0; ks < ks_n; ks++)
+      for (int l = 0; l < 64; l++)
+        memcpy(&frag[(((size_t)nb * ks_n + ks) * 64 + l) * 16],
+               &img[(size_t)(nb * 32 + l % 32) * w->kp + ks * 32 + (l / 32) * 16], 16);
+  hipError_t e = hipMalloc(&w->d_frag, frag.size());
+  if (e == hipSuccess) e = hipMemcpy(w->d_frag, frag.data(), frag.size(), hipMemcpyHostToDevice);
+  return e;
+}
+
 // The unpacked fp32 fallback (MatMulFunc's raw weights, tensor.go:16-70)
 // takes any shape the device epilogue can store: k >= 1 and n a positive
 // multiple of 4 (4-column vector stores).
@@ -286,6 +300,7 @@ int pack_weight(Context* ctx, int mode, const float* bT, const float* bias, int 
   hipError_t e = hipMalloc(&w->d_data, img.size());
   if (e == hipSuccess) e = hipMemcpy(w->d_data, img.data(), img.size(), hipMemcpyHostToDevice);
   if (e == hipSuccess && mode != RH_MODE_A8W8) e = upload_planes(w.get(), img);
+  if (e == hipSuccess && mode == RH_MODE_A8W8) e = upload_frag(w.get(), img);
   if (e == hipSuccess && !scales.empty()) {
     e = hipMalloc(&w->d_scales, n * sizeof(float));
     if (e == hipSuccess)
@@ -317,6 +332,7 @@ void destroy_weight(rh_weight* w) {
   if (w->d_bias) (void)hipFree(w->d_bias);
   if (w->d_bf) (void)hipFree(w->d_bf);
   if (w->d_bf_lo) (void)hipFree(w->d_bf_lo);
+  if (w->d_frag) (void)hipFree(w->d_frag);
   delete w;
 }
 
@@ -365,6 +381,7 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
   g.lda = ldq;
   g.B = static_cast<const int8_t*>(w->d_data);
   g.ldb = w->kp;
+  g.Bf = static_cast<const int8_t*>(w->d_frag);
   g.M = m;
   g.N = w->n;
   g.K = w->k;

@@ -60,6 +60,12 @@ struct rh_weight {
   // (exact in bf16), F32 the hi/lo split of the fp32 weights
   void* d_bf = nullptr;
   void* d_bf_lo = nullptr;
+  // A8W8: the s8 image again in v_mfma_i32_32x32x32_i8 B-fragment order
+  // (kp % 128 == 0, np % 256 == 0): the 1 KiB for column block nb (32
+  // columns) and k-step ks (32 bytes) sits at (nb * kp/32 + ks) * 1024, lane
+  // l's 16 bytes (column nb*32 + l%32, k bytes ks*32 + (l/32)*16 ..) at l*16,
+  // so a wave's fragment is one coalesced 16-byte load per lane
+  void* d_frag = nullptr;
 };
 
 namespace rh {

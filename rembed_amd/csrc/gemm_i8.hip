@@ -33,6 +33,172 @@ __device__ __forceinline__ uint32_t quant_byte(float v, float inv) {
   return (uint32_t)q;
 }
 
+// Epilogue shared by the int8 kernels: per 32-row band each wave parks its
+// accumulators in LDS and reads rows back 4 columns per lane, so every output
+// is a 4-wide vector store. Dequant order matches the reference:
+// float32(real)·rs, ·cs, then + bias (AddBias), then the activation
+// (bert.go:297-300, 913-915). `lds` must hold NW·32·(WN+4) ints plus 3·BM
+// floats; the caller has finished every LDS read and DMA of its main loop.
+template <int BM, int WM, int WN, int TM, int TN, int NW, int NT, int EPI>
+__device__ __forceinline__ void i8_epilogue(const GemmI8Args& p, v16i (&acc)[TM][TN],
+                                            uint8_t* lds, int row0, int col0, int wave,
+                                            int wm, int wn, int tid) {
+  constexpr int kEpiStride = WN + 4;  // ints per row of the epilogue transpose
+  constexpr int kEpiBytes = NW * 32 * kEpiStride * 4;
+  const int lane = tid & 63;
+  const int fr = lane & 31, fg = lane >> 5;
+  __syncthreads();
+  int* ep = reinterpret_cast<int*>(lds) + wave * 32 * kEpiStride;
+  // Per-row operands of the tile (row scale; for EPI_QUANT the output row's
+  // scale and its reciprocal), fetched once per tile by one thread per row
+  // and read from LDS in the store loops: a global load per stored row would
+  // put one memory latency per row pass on the epilogue's critical path.
+  float* rs_l = reinterpret_cast<float*>(lds + kEpiBytes);
+  float* sc_l = rs_l + BM;
+  float* inv_l = sc_l + BM;
+  if constexpr (EPI != EPI_ACC) {
+    for (int r = tid; r < BM; r += NT) {
+      const int gr = row0 + r;
+      float rs = 0.0f, sc = 1.0f;
+      if (gr < p.M) {
+        rs = p.row_scales[gr];
+        if constexpr (EPI == EPI_QUANT) {
+          sc = p.row_absmax[gr] / 127.0f;
+          if (sc == 0.0f) sc = 1.0f;
+        }
+      }
+      rs_l[r] = rs;
+      if constexpr (EPI == EPI_QUANT) {
+        sc_l[r] = sc;
+        inv_l[r] = 1.0f / sc;
+      }
+    }
+    __syncthreads();
+  }
+  constexpr int kLanesPerRow = WN / 4;
+  constexpr int kRowsPerPass = 64 / kLanesPerRow;
+  const int c4 = (lane % kLanesPerRow) * 4;
+  const int gcol = col0 + wn * WN + c4;
+  const bool col_ok = gcol < p.N;
+  v4f cs = {1.0f, 1.0f, 1.0f, 1.0f}, bs = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4i corr = {0, 0, 0, 0};
+  if (col_ok) {
+    if (p.col_scales) cs = *reinterpret_cast<const v4f*>(p.col_scales + gcol);
+    if (p.bias) bs = *reinterpret_cast<const v4f*>(p.bias + gcol);
+    if (EPI == EPI_ACC && p.colsum) corr = *reinterpret_cast<const v4i*>(p.colsum + gcol) * 128;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        ep[((r >> 2) * 8 + fg * 4 + (r & 3)) * kEpiStride + j * 32 + fr] = acc[i][j][r];
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    const int grow_base = row0 + wm * WM + i * 32;
+    if constexpr (EPI == EPI_F32) {
+      if (is_glu(p.act)) {
+        // Gated weight: tile columns 8t..8t+3 are gate rows, 8t+4..8t+7 the
+        // matching up rows. A lane reads both halves of one group of 8 and
+        // writes 4 outputs act(gate) * up at column (packed column) / 2.
+        constexpr int kL8 = WN / 8, kR8 = 64 / kL8;
+        const int c8 = (lane % kL8) * 8;
+        const int gpk = col0 + wn * WN + c8;
+        const bool pk_ok = gpk < p.N;
+        v4f csg = {1.0f, 1.0f, 1.0f, 1.0f}, csu = csg;
+        v4f bg = {0.0f, 0.0f, 0.0f, 0.0f}, bu = bg;
+        if (pk_ok) {
+          csg = *reinterpret_cast<const v4f*>(p.col_scales + gpk);
+          csu = *reinterpret_cast<const v4f*>(p.col_scales + gpk + 4);
+          if (p.bias) {
+            bg = *reinterpret_cast<const v4f*>(p.bias + gpk);
+            bu = *reinterpret_cast<const v4f*>(p.bias + gpk + 4);
+          }
+        }
+        for (int rr = lane / kL8; rr < 32; rr += kR8) {
+          const int grow = grow_base + rr;
+          const v4i ag = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8);
+          const v4i au = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8 + 4);
+          if (grow < p.M && pk_ok) {
+            const float rs = rs_l[grow - row0];
+            v4f o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              float g = (float)ag[e] * rs;
+              g = g * csg[e];
+              float u = (float)au[e] * rs;
+              u = u * csu[e];
+              if (p.bias) {
+                g = g + bg[e];
+                u = u + bu[e];
+              }
+              o[e] = glu_act(g, u, p.act);
+            }
+            *reinterpret_cast<v4f*>(static_cast<float*>(p.out) + (size_t)grow * p.ldo + gpk / 2) = o;
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+        continue;
+      }
+    }
+#pragma unroll 2
+    for (int it = 0; it < 32 / kRowsPerPass; it++) {
+      const int rr = lane / kLanesPerRow + it * kRowsPerPass;
+      const int grow = grow_base + rr;
+      const bool ok = grow < p.M && col_ok;
+      const v4i a = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c4);
+      if constexpr (EPI == EPI_ACC) {
+        if (ok) {
+          v4i w;
+#pragma unroll
+          for (int e = 0; e < 4; e++) w[e] = (int)((uint32_t)a[e] + (uint32_t)corr[e]);
+          *reinterpret_cast<v4i*>(static_cast<int32_t*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
+        }
+      } else {
+        v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (ok) {
+          const float rs = rs_l[grow - row0];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float x = (float)a[e] * rs;
+            x = x * cs[e];
+            if (p.bias) x = x + bs[e];
+            v[e] = apply_act(x, p.act);
+          }
+        }
+        if constexpr (EPI == EPI_F32) {
+          if (ok) *reinterpret_cast<v4f*>(static_cast<float*>(p.out) + (size_t)grow * p.ldo + gcol) = v;
+        } else if constexpr (EPI == EPI_BF16) {
+          if (ok) {
+            typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+            v4bf w = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+            *reinterpret_cast<v4bf*>(static_cast<__bf16*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
+          }
+        } else if constexpr (EPI == EPI_ABSMAX) {
+          // |value| max over this row's columns of the tile; every lane takes
+          // part in the shuffles (invalid lanes contribute 0).
+          float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+          for (int o = kLanesPerRow / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+          if (grow < p.M && (lane % kLanesPerRow) == 0)
+            atomicMax(reinterpret_cast<unsigned int*>(p.row_absmax) + grow, __float_as_uint(m));
+        } else {  // EPI_QUANT: QuantizeRowU8 with the row's |max| from pass 1
+          if (ok) {
+            const float scale = sc_l[grow - row0];
+            const float inv = inv_l[grow - row0];
+            const uint32_t w = quant_byte(v[0], inv) | (quant_byte(v[1], inv) << 8) |
+                               (quant_byte(v[2], inv) << 16) | (quant_byte(v[3], inv) << 24);
+            *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
+            if (gcol == 0) p.rs_out[grow] = scale;
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // WGN waves along N: 2 = a 2x2 grid of 4 waves, 4 = a 2x4 grid of 8 (two per
 // SIMD when one workgroup fills a CU).
 // BK: k bytes per stage and row, 64 (i8_slot rows) or 128 (lds_off rows;
@@ -182,158 +348,176 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
     }
   }
 
-  // ---- epilogue ----------------------------------------------------------
-  // Dequant order matches the reference: float32(real)·rs, ·cs, then + bias
-  // (AddBias), then the activation (bert.go:297-300, 913-915).
-  __syncthreads();
-  int* ep = reinterpret_cast<int*>(lds) + wave * 32 * kEpiStride;
-  // Per-row operands of the tile (row scale; for EPI_QUANT the output row's
-  // scale and its reciprocal), fetched once per tile by one thread per row
-  // and read from LDS in the store loops: a global load per stored row would
-  // put one memory latency per row pass on the epilogue's critical path.
-  float* rs_l = reinterpret_cast<float*>(lds + kEpiBytes);
-  float* sc_l = rs_l + BM;
-  float* inv_l = sc_l + BM;
-  if constexpr (EPI != EPI_ACC) {
-    for (int r = tid; r < BM; r += NT) {
-      const int gr = row0 + r;
-      float rs = 0.0f, sc = 1.0f;
-      if (gr < p.M) {
-        rs = p.row_scales[gr];
-        if constexpr (EPI == EPI_QUANT) {
-          sc = p.row_absmax[gr] / 127.0f;
-          if (sc == 0.0f) sc = 1.0f;
-        }
-      }
-      rs_l[r] = rs;
-      if constexpr (EPI == EPI_QUANT) {
-        sc_l[r] = sc;
-        inv_l[r] = 1.0f / sc;
-      }
-    }
-    __syncthreads();
+  i8_epilogue<BM, WM, WN, TM, TN, NW, NT, EPI>(p, acc, lds, row0, col0, wave, wm, wn, tid);
+}
+
+// ---- B fragments straight to registers ------------------------------------
+// 64 x 256 tile on 4 waves side by side (each 64 rows x 64 columns: 2 x 2
+// MFMA tiles). Only A goes through LDS (128-byte stage rows by
+// global_load_lds_dwordx4, NS-slot ring, one barrier per stage); each wave
+// loads its own B fragments from the fragment-ordered image (rh_weight::
+// d_frag) with one 16-byte global load per lane and fragment, D k-steps ahead
+// into a register ring. Per MFMA the CU's LDS then serves 0.5 KiB of A
+// fragment reads instead of 1 KiB of A and B, and no B byte is written to
+// LDS at all: the main loop of the LDS-staged kernel above is bound by LDS
+// bandwidth.
+//
+// Every stage issues the same loads in the same order (a compiler and
+// scheduler fence follows each A DMA, so no B load moves above it), so the
+// count of loads younger than a stage's A DMA is one constant: the ring is
+// primed as stages -(NS-1)..-1 would have issued it. Past the last stage the
+// k indices are clamped (an A reload into a freed slot, B reloads nobody
+// reads). Those B reloads may be dropped by the compiler as dead or merged
+// as duplicates, which would leave fewer younger loads than the constant
+// assumes, so the stages that follow one that issued them (the last NS-1)
+// wait for every outstanding load instead.
+// The B ring holds NS stages of k-steps, so with the stage loop unrolled by
+// NS every ring slot is a constant register set. NK > 0: the kernel is built
+// for exactly NK stages and the stage loop is unrolled completely; the
+// compiler then counts every B register's outstanding loads exactly (across
+// a loop back-edge it waits for all loads to drain, which empties the
+// prefetch ring once per NS stages). NK = 0: any K, a loop.
+// Compiler and scheduler fence: no memory access moves across it.
+__device__ __forceinline__ void load_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int NS, int EPI, int NK, int WGM = 1>
+__global__ __launch_bounds__(256 * WGM, 2 / WGM) void gemm_i8f_kernel(GemmI8Args p) {
+  constexpr int BM = 64 * WGM, BN = 256, NT = 256 * WGM, NW = 4 * WGM;
+  constexpr int BK = 128, CPR = BK / 16;  // A stage row bytes, 16-byte chunks per row
+  constexpr int WM = 64, WN = 64, TM = WM / 32, TN = WN / 32;
+  constexpr int KPS = BK / 32;               // k-steps per stage
+  constexpr int D = KPS * NS;                // B ring depth in k-steps
+  constexpr int kA = BM * BK;                // A bytes per stage
+  constexpr int LA = kA / (NT * 16);         // A DMA instructions per thread per stage
+  // loads younger than stage t's A DMA when stage t begins: the B loads of
+  // the NS-1 stages before it and the A DMAs of the NS-2 between
+  constexpr int kWaitA = (NS - 1) * KPS * TN + (NS - 2) * LA;
+  constexpr int kEpiBytes = NW * 32 * (WN + 4) * 4;
+  constexpr int kLds = NS * kA > kEpiBytes + 3 * BM * 4 ? NS * kA : kEpiBytes + 3 * BM * 4;
+  static_assert(LA >= 1 && kWaitA <= 63 && NS >= 2, "ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / 4, wn = wave % 4;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  int rb, cb;
+  tile_origin(tile, (p.M + BM - 1) / BM, tiles_n, p.tile_group, rb, cb);
+  const int row0 = rb * BM;
+  const int col0 = cb * BN;
+  const int nk = NK > 0 ? NK : (p.K + BK - 1) / BK;  // stages
+  const int nks = nk * KPS;  // k-steps (= kp / 32 of the weight)
+
+  // A DMA sources, as in gemm_i8_kernel (rows past M read row M-1).
+  const uint8_t* asrc[LA];
+  int achunk[LA];
+#pragma unroll
+  for (int j = 0; j < LA; j++) {
+    const int slot = (wave * LA + j) * 64 + lane;
+    const int r = slot / CPR;
+    achunk[j] = stage_slot_chunk<BK>(r, slot % CPR);
+    const int gr = row0 + r;
+    asrc[j] = p.A + (size_t)(gr < p.M ? gr : p.M - 1) * p.lda;
   }
-  constexpr int kLanesPerRow = WN / 4;
-  constexpr int kRowsPerPass = 64 / kLanesPerRow;
-  const int c4 = (lane % kLanesPerRow) * 4;
-  const int gcol = col0 + wn * WN + c4;
-  const bool col_ok = gcol < p.N;
-  v4f cs = {1.0f, 1.0f, 1.0f, 1.0f}, bs = {0.0f, 0.0f, 0.0f, 0.0f};
-  v4i corr = {0, 0, 0, 0};
-  if (col_ok) {
-    if (p.col_scales) cs = *reinterpret_cast<const v4f*>(p.col_scales + gcol);
-    if (p.bias) bs = *reinterpret_cast<const v4f*>(p.bias + gcol);
-    if (EPI == EPI_ACC && p.colsum) corr = *reinterpret_cast<const v4i*>(p.colsum + gcol) * 128;
-  }
+  auto issue_a = [&](int kt, int slot) {
+    kt = kt < nk ? kt : nk - 1;
+    uint8_t* s = lds + slot * kA;
+    const int k0 = kt * BK;
 #pragma unroll
-  for (int i = 0; i < TM; i++) {
-#pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++)
-        ep[((r >> 2) * 8 + fg * 4 + (r & 3)) * kEpiStride + j * 32 + fr] = acc[i][j][r];
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-    const int grow_base = row0 + wm * WM + i * 32;
-    if constexpr (EPI == EPI_F32) {
-      if (is_glu(p.act)) {
-        // Gated weight: tile columns 8t..8t+3 are gate rows, 8t+4..8t+7 the
-        // matching up rows. A lane reads both halves of one group of 8 and
-        // writes 4 outputs act(gate) * up at column (packed column) / 2.
-        constexpr int kL8 = WN / 8, kR8 = 64 / kL8;
-        const int c8 = (lane % kL8) * 8;
-        const int gpk = col0 + wn * WN + c8;
-        const bool pk_ok = gpk < p.N;
-        v4f csg = {1.0f, 1.0f, 1.0f, 1.0f}, csu = csg;
-        v4f bg = {0.0f, 0.0f, 0.0f, 0.0f}, bu = bg;
-        if (pk_ok) {
-          csg = *reinterpret_cast<const v4f*>(p.col_scales + gpk);
-          csu = *reinterpret_cast<const v4f*>(p.col_scales + gpk + 4);
-          if (p.bias) {
-            bg = *reinterpret_cast<const v4f*>(p.bias + gpk);
-            bu = *reinterpret_cast<const v4f*>(p.bias + gpk + 4);
-          }
-        }
-        for (int rr = lane / kL8; rr < 32; rr += kR8) {
-          const int grow = grow_base + rr;
-          const v4i ag = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8);
-          const v4i au = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c8 + 4);
-          if (grow < p.M && pk_ok) {
-            const float rs = rs_l[grow - row0];
-            v4f o;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              float g = (float)ag[e] * rs;
-              g = g * csg[e];
-              float u = (float)au[e] * rs;
-              u = u * csu[e];
-              if (p.bias) {
-                g = g + bg[e];
-                u = u + bu[e];
-              }
-              o[e] = glu_act(g, u, p.act);
-            }
-            *reinterpret_cast<v4f*>(static_cast<float*>(p.out) + (size_t)grow * p.ldo + gpk / 2) = o;
-          }
-        }
-        __builtin_amdgcn_wave_barrier();
-        continue;
-      }
+    for (int j = 0; j < LA; j++) {
+      int kb = k0 + achunk[j] * 16;
+      kb = kb < p.lda ? kb : 0;  // past the row: any in-bounds bytes (B is 0 there)
+      lds_dma16(asrc[j] + kb, s + (wave * LA + j) * 1024);
     }
-#pragma unroll 2
-    for (int rr = lane / kLanesPerRow; rr < 32; rr += kRowsPerPass) {
-      const int grow = grow_base + rr;
-      const bool ok = grow < p.M && col_ok;
-      const v4i a = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c4);
-      if constexpr (EPI == EPI_ACC) {
-        if (ok) {
-          v4i w;
+  };
+  // This lane's 16 bytes of each of the wave's column blocks; k-step ks is
+  // ks KiB further (np % 256 == 0 keeps every block of the tile in the image).
+  const int8_t* bsrc[TN];
 #pragma unroll
-          for (int e = 0; e < 4; e++) w[e] = (int)((uint32_t)a[e] + (uint32_t)corr[e]);
-          *reinterpret_cast<v4i*>(static_cast<int32_t*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
-        }
-      } else {
-        v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (ok) {
-          const float rs = rs_l[grow - row0];
+  for (int j = 0; j < TN; j++)
+    bsrc[j] = p.Bf + (size_t)((col0 + wn * WN + j * 32) >> 5) * nks * 1024 + lane * 16;
+  v4i bq[D][TN];
+  auto load_b = [&](int ks, v4i (&dst)[TN]) {
+    ks = ks < nks ? ks : nks - 1;
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            float x = (float)a[e] * rs;
-            x = x * cs[e];
-            if (p.bias) x = x + bs[e];
-            v[e] = apply_act(x, p.act);
-          }
-        }
-        if constexpr (EPI == EPI_F32) {
-          if (ok) *reinterpret_cast<v4f*>(static_cast<float*>(p.out) + (size_t)grow * p.ldo + gcol) = v;
-        } else if constexpr (EPI == EPI_BF16) {
-          if (ok) {
-            typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-            v4bf w = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
-            *reinterpret_cast<v4bf*>(static_cast<__bf16*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
-          }
-        } else if constexpr (EPI == EPI_ABSMAX) {
-          // |value| max over this row's columns of the tile; every lane takes
-          // part in the shuffles (invalid lanes contribute 0).
-          float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    for (int j = 0; j < TN; j++) dst[j] = *reinterpret_cast<const v4i*>(bsrc[j] + (size_t)ks * 1024);
+  };
+
+  v16i acc[TM][TN];
 #pragma unroll
-          for (int o = kLanesPerRow / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-          if (grow < p.M && (lane % kLanesPerRow) == 0)
-            atomicMax(reinterpret_cast<unsigned int*>(p.row_absmax) + grow, __float_as_uint(m));
-        } else {  // EPI_QUANT: QuantizeRowU8 with the row's |max| from pass 1
-          if (ok) {
-            const float scale = sc_l[grow - row0];
-            const float inv = inv_l[grow - row0];
-            const uint32_t w = quant_byte(v[0], inv) | (quant_byte(v[1], inv) << 8) |
-                               (quant_byte(v[2], inv) << 16) | (quant_byte(v[3], inv) << 24);
-            *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
-            if (gcol == 0) p.rs_out[grow] = scale;
-          }
-        }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = v16i{};
+  const int fr = lane & 31, fg = lane >> 5;
+
+  // Prime: stage 0's B k-steps, then for each virtual stage v = -(NS-1)..-1
+  // the A DMA of stage v + NS - 1 and the B loads of its k-steps + D.
+#pragma unroll
+  for (int s = 0; s < KPS; s++) load_b(s, bq[s]);
+#pragma unroll
+  for (int v = 0; v < NS - 1; v++) {
+    load_fence();
+    issue_a(v, v);
+    load_fence();
+#pragma unroll
+    for (int s = 0; s < KPS; s++) load_b((v + 1) * KPS + s, bq[(v + 1) * KPS + s]);
   }
+
+  constexpr int kUnroll = NK > 0 ? (NK + NS - 1) / NS : 1;
+#pragma unroll kUnroll
+  for (int t0 = 0; t0 < nk; t0 += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; u++) {
+      const int t = t0 + u;
+      if (t >= nk) break;
+      load_fence();
+      // this wave's A DMA of stage t has landed
+      if (t + NS - 1 >= nk) wait_vmcnt<0>();
+      else wait_vmcnt<kWaitA>();
+      stage_barrier();  // every wave's has; slot (t-1) % NS is free
+      issue_a(t + NS - 1, (u + NS - 1) % NS);
+      load_fence();
+      const uint8_t* sA = lds + u * kA;
+#pragma unroll
+      for (int s = 0; s < KPS; s++) {
+        const int rs = u * KPS + s;  // = (t * KPS + s) % D
+        v4i fa[TM];
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+          fa[i] = *reinterpret_cast<const v4i*>(
+                      sA + stage_frag_off<BK>(wm * WM + i * 32 + fr, 2 * s + fg)) ^
+                  (int)0x80808080;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], bq[rs][j], acc[i][j], 0, 0, 0);
+        load_b(t * KPS + s + D, bq[rs]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // The clamped refills past the last stage may still be landing in LDS.
+  wait_vmcnt<0>();
+  i8_epilogue<BM, WM, WN, TM, TN, NW, NT, EPI>(p, acc, lds, row0, col0, wave, wm, wn, tid);
+}
+
+template <int NS, int EPI, int WGM = 1>
+static hipError_t launch_frag(const GemmI8Args& a, hipStream_t s) {
+  const int tiles = ceil_div(a.M, 64 * WGM) * ceil_div(a.N, 256);
+  const dim3 g(tiles), b(256 * WGM);
+  // fully unrolled builds for the encoder widths (K = 768 and 3072)
+  switch (ceil_div(a.K, 128)) {
+    case 6: timed_launch((gemm_i8f_kernel<NS, EPI, 6, WGM>), g, b, 0, s, a); break;
+    case 24: timed_launch((gemm_i8f_kernel<NS, EPI, 24, WGM>), g, b, 0, s, a); break;
+    default: timed_launch((gemm_i8f_kernel<NS, EPI, 0, WGM>), g, b, 0, s, a);
+  }
+  return hipGetLastError();
 }
 
 template <int BM, int BN, int NS, int EPI, int WGN = 2, int BK = 64>
@@ -360,6 +544,10 @@ static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
     case 8: return launch_tile<256, 256, 2, EPI, 4, 128>(a, s);
     case 9: return launch_tile<128, 256, 2, EPI, 4, 128>(a, s);
     case 10: return launch_tile<128, 256, 3, EPI, 4, 128>(a, s);
+    case 11: return a.Bf ? launch_frag<3, EPI>(a, s) : hipErrorInvalidValue;
+    case 12: return a.Bf ? launch_frag<4, EPI>(a, s) : hipErrorInvalidValue;
+    case 13: return a.Bf ? launch_frag<2, EPI, 2>(a, s) : hipErrorInvalidValue;
+    case 14: return a.Bf ? launch_frag<3, EPI, 2>(a, s) : hipErrorInvalidValue;
     default: return launch_tile<128, 128, 4, EPI>(a, s);
   }
 }

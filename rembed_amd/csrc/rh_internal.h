@@ -129,6 +129,7 @@ struct GemmI8Args {
   int lda;           // bytes, multiple of 16
   const int8_t* B;   // s8 weights [Np][ldb], zero padded
   int ldb;           // bytes, multiple of kWeightKPad
+  const int8_t* Bf;  // the same weights in B-fragment order (rh_weight::d_frag)
   int M, N, K;
   const float* row_scales;  // [M]
   const float* col_scales;  // [N]
@@ -235,7 +236,7 @@ enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 
 // Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
 // tile: 0 = automatic, else one of the configurations RH_CTX_I8_TILE lists.
-constexpr int kI8TileConfigs = 10;
+constexpr int kI8TileConfigs = 14;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
 int pick_i8_tile(int M, int N, int K, int epi);
 // fills n floats with zero (graph-capture safe, unlike hipMemsetAsync)

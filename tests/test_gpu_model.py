@@ -169,7 +169,7 @@ def test_parts_on_streams_identical_planes(gpu_ctx, minilm, quant):
     assert np.array_equal(m.embed(ids, lens), one)
 
 
-@pytest.mark.parametrize("tile", [3, 7, 9, 10])
+@pytest.mark.parametrize("tile", [3, 7, 9, 10, 11, 12])
 def test_full_int8_forward_identical_on_every_tile(gpu_ctx, minilm_int8_big, tile):
     """The full-int8 forward (bf16 q|k|v rows, fp32 O / FFN rows, every
     epilogue the model uses) gives the same embeddings and hidden states, bit

@@ -110,7 +110,7 @@ def free_bytes():
     """hipMemGetInfo's free bytes on the current device (the library's
     contexts have set device 0)."""
     import ctypes
-    hip = ctypes.CDLL("libamdhip64.so")
+    hip = _lib.hip_runtime()
     free, total = ctypes.c_size_t(), ctypes.c_size_t()
     assert hip.hipDeviceSynchronize() == 0
     assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0

@@ -131,7 +131,7 @@ def test_i32_accumulators_bert_base_bit_exact(gpu_ctx, m, kn):
     assert np.array_equal(got[: m * n].reshape(m, n), want)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14])
 def test_every_int8_tile_config_bit_exact(gpu_ctx, tile):
     """Each int8 GEMM tile configuration (forced) gives the oracle's exact
     accumulators and dequantized outputs, including M/N/K tails."""
@@ -289,7 +289,7 @@ def test_linear_a8w8_bias_gelu_bit_exact(gpu_ctx):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14])
 def test_linear_u8_fused_quantization_bit_exact(gpu_ctx, tile):
     """FFN1 -> GELU -> QuantizeRowU8 in two GEMM passes (no fp32 rows) gives
     exactly QuantizeRowU8 of the reference's fp32 GELU rows."""
