@@ -388,17 +388,21 @@ static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
 // Tiles: 1 = 256x256, 2 = 256x128, 3 = 128x128 with 4 waves (2x2); 4 =
 // 256x256 and 5 = 256x128 with 8 waves (2x4, two per SIMD); for one
 // activation term and int8 weights also 6 = 256x256 and 7 = 256x128 on
-// 128-byte stages (two and three). Stages: as many as fit in 160 KiB of
-// LDS. fp32's four planes leave no room for 256x256 (1 and 4 fall back to 2
-// and 5). Automatic choice (measured on MI355X at M = 16384 over the
-// Qwen3/BERT linears; 8 waves 2-15% faster than 4 at the same tile): tile 6
-// for one-term W8, 4 for the other products when the 256x256 grid gives
-// every CU a workgroup, else 5, else 128x128.
+// 128-byte stages (two and three); 8 = 64x64 and 9 = 128x64 with 4 waves.
+// Stages: as many as fit in 160 KiB of LDS. fp32's four planes leave no room
+// for 256x256 (1 and 4 fall back to 2 and 5). Automatic choice (measured on
+// MI355X at M = 16384 over the Qwen3/BERT linears; 8 waves 2-15% faster than
+// 4 at the same tile): tile 6 for one-term W8, 4 for the other products
+// when the 256x256 grid gives every CU a workgroup, else 5, else 128x128
+// while its grid has at least 192 workgroups; below that (MiniLM's M ~ 2300,
+// or N = 384) 64x64, which keeps the CUs busy: at M = 2304 the weight-only
+// int8 linears take 9.8 / 5.6 / 11.6 µs (384x1152, 384x384, 1536x384)
+// against 10.6 / 9.5 / 20.0 with 128x128.
 int pick_planes_tile(int M, int N, int a_terms, int b_terms) {
   if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256)
     return a_terms == 1 && b_terms == 1 ? 6 : 4;
   if (ceil_div(M, 256) * ceil_div(N, 128) >= 256) return 5;
-  return 3;
+  return ceil_div(M, 128) * ceil_div(N, 128) >= 192 ? 3 : 8;
 }
 
 hipError_t launch_gemm_planes_qk(const GemmPlArgs& a, hipStream_t s) {
@@ -425,6 +429,8 @@ hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int
       case 5: return launch_pl<256, 128, 4, 1, 1, 4>(a, s);
       case 6: return launch_pl<256, 256, 2, 1, 1, 4, 64>(a, s);
       case 7: return launch_pl<256, 128, 3, 1, 1, 4, 64>(a, s);
+      case 8: return launch_pl<64, 64, 4, 1, 1>(a, s);
+      case 9: return launch_pl<128, 64, 4, 1, 1>(a, s);
       default: return launch_pl<128, 128, 4, 1, 1>(a, s);
     }
   }
@@ -434,6 +440,8 @@ hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int
       case 2: return launch_pl<256, 128, 4, 2, 1>(a, s);
       case 4: return launch_pl<256, 256, 3, 2, 1, 4>(a, s);
       case 5: return launch_pl<256, 128, 4, 2, 1, 4>(a, s);
+      case 8: return launch_pl<64, 64, 4, 2, 1>(a, s);
+      case 9: return launch_pl<128, 64, 4, 2, 1>(a, s);
       default: return launch_pl<128, 128, 3, 2, 1>(a, s);
     }
   }
@@ -443,6 +451,8 @@ hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int
       case 2: return launch_pl<256, 128, 3, 2, 2>(a, s);
       case 4:
       case 5: return launch_pl<256, 128, 3, 2, 2, 4>(a, s);
+      case 8: return launch_pl<64, 64, 4, 2, 2>(a, s);
+      case 9: return launch_pl<128, 64, 4, 2, 2>(a, s);
       default: return launch_pl<128, 128, 3, 2, 2>(a, s);
     }
   }
