@@ -234,6 +234,10 @@ def main():
                          "(two passes, no fp32 intermediate); split = fp32 rows + QuantizeRowU8")
     ap.add_argument("--no-u8-diff", action="store_true",
                     help="skip the per-layer u8 comparison with the oracle (full int8)")
+    ap.add_argument("--forwards-only", action="store_true",
+                    help="run only the default forward (warm-up, timed and profiled steps): "
+                         "no fp32-attention rate, host-buffer rate, oracle comparison or CPU "
+                         "baseline, so a profiler sees one kind of forward")
     ap.add_argument("--streams", type=int, choices=[1, 2, 3, 4], default=2,
                     help="run a batch as this many parts of whole texts on as many streams "
                          "(default 2); the roofline pass always runs one stream")
@@ -292,7 +296,7 @@ def main():
     # the reference's float32 attention arithmetic class, reported beside
     # `value` (the default for the quantized modes is bf16 operands).
     attn3_rate = None
-    if quant != 0:
+    if quant != 0 and not args.forwards_only:
         model.set_attention_precision(3)
         model.embed_device(ids_dev, lens, BATCH, SEQ, out_dev)
         ctx.sync()
@@ -339,17 +343,17 @@ def main():
     # The same forward through the host-buffer boundary (int64 ids up,
     # vectors back over PCIe each batch, one synchronous call per batch),
     # reported beside `value`, never as it.
-    host_steps = max(1, args.steps)
-    model.embed(ids, lens)
-    host_ms = []
-    for _ in range(host_steps):
-        t0 = time.perf_counter()
-        host_vec = model.embed(ids, lens)
-        host_ms.append((time.perf_counter() - t0) * 1e3)
-    host_rate = tokens * host_steps / (sum(host_ms) * 1e-3)
-
+    host_rate, host_ms = None, []
     vec = out_dev.download(np.float32, (BATCH, shape.hidden))
-    assert np.array_equal(vec, host_vec), "host-buffer and device-resident forwards differ"
+    if not args.forwards_only:
+        host_steps = max(1, args.steps)
+        model.embed(ids, lens)
+        for _ in range(host_steps):
+            t0 = time.perf_counter()
+            host_vec = model.embed(ids, lens)
+            host_ms.append((time.perf_counter() - t0) * 1e3)
+        host_rate = tokens * host_steps / (sum(host_ms) * 1e-3)
+        assert np.array_equal(vec, host_vec), "host-buffer and device-resident forwards differ"
     cfg_note = {"streams": args.streams}
     if quant == 2:
         cfg_note["ffn1"] = args.ffn1
@@ -370,7 +374,7 @@ def main():
         traffic = json.load(open(tpath)).get("bytes_per_launch")
 
     u8diff = None
-    if quant == 2 and not args.no_cpu_baseline and not args.no_u8_diff:
+    if quant == 2 and not (args.no_cpu_baseline or args.no_u8_diff or args.forwards_only):
         log("comparing u8 activations with the oracle, layer by layer")
         u8diff = u8_byte_diffs(ctx, shape, tensors, ids, lens)
         u8diff["oracle_vs_oracle_1ulp_embeddings"] = oracle_u8_sensitivity(
@@ -380,7 +384,7 @@ def main():
             f"embeddings {u8diff['oracle_vs_oracle_1ulp_embeddings']}")
 
     baseline = None
-    if not args.no_cpu_baseline:
+    if not (args.no_cpu_baseline or args.forwards_only):
         log("timing the CPU baseline")
         trunc = {"qwen3-0.6b-w8": 48, "gemma-300m-w8": 64}.get(args.workload)
         baseline = cpu_baseline(shape, tensors, ids, lens, quant, max_len=trunc)
@@ -429,10 +433,10 @@ def main():
                     "clock": "HIP events between steps on the library stream"},
         "median_tokens_per_s": round(tokens / (pct(step_ms, 50) * 1e-3), 1),
         "fp32_attention_tokens_per_s": None if attn3_rate is None else round(attn3_rate, 1),
-        "pcie_inclusive_tokens_per_s": round(host_rate, 1),
-        "pcie_inclusive_step_ms": {"median": round(pct(host_ms, 50), 4),
-                                   "p10": round(pct(host_ms, 10), 4),
-                                   "p90": round(pct(host_ms, 90), 4)},
+        "pcie_inclusive_tokens_per_s": None if host_rate is None else round(host_rate, 1),
+        "pcie_inclusive_step_ms": None if not host_ms else {
+            "median": round(pct(host_ms, 50), 4), "p10": round(pct(host_ms, 10), 4),
+            "p90": round(pct(host_ms, 90), 4)},
         "u8_vs_oracle": u8diff,
         "padded_slots_per_s": round(BATCH * SEQ * args.steps / elapsed, 1),
         "cpu_baseline": baseline,

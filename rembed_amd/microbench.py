@@ -8,6 +8,7 @@ stream. Usage:
     python -m rembed_amd.microbench --attention bert-base,qwen3-0.6b,gemma-global
 """
 import argparse
+import ctypes
 import json
 import sys
 
@@ -190,18 +191,27 @@ def bench_attention(ctx, name, iters, kernels):
 
 
 def copy_calibration(mib, iters):
-    """A device-to-device copy of `mib` MiB through torch's elementwise copy
-    kernel: each launch reads and writes exactly mib MiB, so a profiler's
-    per-dispatch byte counters can be scaled against it."""
-    import torch
-    n = mib * (1 << 20) // 4
-    src = torch.randn(n, device="cuda:0")
-    dst = torch.empty_like(src)
-    for _ in range(iters):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_mib": mib, "launches": iters,
-                      "bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4}))
+    """A device-to-device copy of `mib` MiB by the HIP runtime the library
+    uses (hipMemcpy, which runs as one blit kernel per call): each launch
+    reads and writes exactly mib MiB, so a profiler's per-dispatch byte
+    counters can be scaled against it."""
+    hip = _lib.hip_runtime()
+    ctx = T.Context(0)  # selects device 0 in the library's runtime
+    n = mib * (1 << 20)
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(src), ctypes.c_size_t(n)) == 0
+    assert hip.hipMalloc(ctypes.byref(dst), ctypes.c_size_t(n)) == 0
+    try:
+        assert hip.hipMemset(src, 1, ctypes.c_size_t(n)) == 0
+        for _ in range(iters):
+            assert hip.hipMemcpy(dst, src, ctypes.c_size_t(n), 3) == 0  # device to device
+        assert hip.hipDeviceSynchronize() == 0
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+        ctx.close()
+    print(json.dumps({"copy_mib": mib, "launches": iters, "kernel": "__amd_rocclr_copyBuffer",
+                      "bytes_read_per_launch": n, "bytes_written_per_launch": n}))
     return 0
 
 

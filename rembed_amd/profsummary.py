@@ -1,15 +1,19 @@
 """Summaries of rocprofv3 output for the committed profiles.
 
     python -m rembed_amd.profsummary stats  <kernel_stats.csv> <steps> <title> <command>
+    python -m rembed_amd.profsummary trace  <kernel_trace.csv> <first_kernel> <skip> <count>
+                                     <title> <command>
     python -m rembed_amd.profsummary traffic <fetch_dir_csv> <write_dir_csv>
                                      <copy_fetch_csv> <copy_write_csv> <copy_mib> <command>
     python -m rembed_amd.profsummary pmc <counter_collection.csv> <command>
 
 `stats` renders a --kernel-trace --stats table (per-kernel calls, average
 and per-step time). `traffic` turns two --pmc runs (FETCH_SIZE, then
-WRITE_SIZE, KiB per dispatch) into HBM bytes per launch, each counter scaled
-by what it reads for a plain device copy of known size, and prints the JSON
-that bench.py reads for the GEMM's `roofline.traffic`. `pmc` renders one
+WRITE_SIZE, KiB per dispatch) into bytes per launch past the L2, each counter
+scaled by what it reads for a plain device copy of known size, and prints the
+JSON that bench.py reads for the GEMM's `roofline.traffic`. FETCH_SIZE counts
+the L2's read misses (requests to the fabric, served by the MALL or HBM), not
+the bytes a kernel loads: reads that hit the L2 do not appear in it. `pmc` renders one
 --pmc pass of SQ instruction and busy counters per kernel: MFMA busy share,
 VALU and LDS instructions per MFMA, LDS bank-conflict share.
 """
@@ -44,6 +48,39 @@ def stats(path, steps, title, command):
     if gc:
         print(f"\nAll `{GEMM}` launches: {gc} calls, average {gt / gc / 1e3:.2f} µs, "
               f"{gt / 1e3 / steps:.1f} µs per step ({steps} steps incl. warm-up).")
+
+
+def trace(path, first, skip, count, title, command):
+    """Per-forward kernel times from a --kernel-trace CSV: the trace is cut
+    into forwards at each launch whose name contains `first` (the forward's
+    first kernel), the first `skip` forwards are dropped and the next `count`
+    are averaged, so warm-up and the other forwards a run makes (different
+    options, host-buffer calls) stay out of the table."""
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if first in r["Kernel_Name"]]
+    if len(starts) < skip + count + 1:
+        raise SystemExit(f"{len(starts)} forwards in the trace, need {skip + count + 1}")
+    sel = rows[starts[skip]:starts[skip + count]]
+    per = collections.defaultdict(list)
+    for r in sel:
+        per[r["Kernel_Name"]].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in per.values())
+    span = (int(sel[-1]["End_Timestamp"]) - int(sel[0]["Start_Timestamp"])) / 1e3 / count
+    print(f"# {title}\n\nCommand: `{command}`\n")
+    print(f"Forwards {skip + 1}-{skip + count} of the run (cut at each `{first}` launch), one "
+          f"stream: kernel time {total / count:.1f} µs per forward, {span:.1f} µs from the "
+          f"first kernel's start to the last one's end.\n")
+    print("| kernel | calls per forward | avg µs | µs per forward | share |")
+    print("|---|---:|---:|---:|---:|")
+    for name, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{name[:90]}` | {len(v) / count:g} | {sum(v) / len(v):.2f} | "
+              f"{sum(v) / count:.1f} | {100 * sum(v) / total:.1f}% |")
+    for fam in ("gemm_i8_kernel", "gemm_i8f_kernel", "gemm_planes_kernel", "gemm_bf16_kernel"):
+        g = [x for k, v in per.items() if fam + "<" in k for x in v]
+        if g:
+            print(f"\nAll `{fam}` launches: {len(g) / count:g} per forward, average "
+                  f"{sum(g) / len(g):.2f} µs, {sum(g) / count:.1f} µs per forward "
+                  f"({100 * sum(g) / total:.1f}% of the kernel time).")
 
 
 # MI355X: 8 XCDs of 32 CUs, 4 SIMDs per CU. GRBM_GUI_ACTIVE sums the XCDs'
@@ -89,12 +126,15 @@ def traffic(fetch, write, cfetch, cwrite, copy_mib, command):
     ck = max((k for k in cw if "copy" in k.lower()), key=lambda k: cw[k][1])
     f_scale = copy_kib / cf[ck][1]
     w_scale = copy_kib / cw[ck][1]
-    print("# HBM traffic per launch (rocprofv3 --pmc)\n")
+    print("# Traffic past the L2 per launch (rocprofv3 --pmc)\n")
     print(f"Command: `{command}`\n")
     print(f"Calibration: a {copy_mib} MiB device copy (`{ck}`) reads FETCH_SIZE "
           f"{cf[ck][1]:.0f} KiB and WRITE_SIZE {cw[ck][1]:.0f} KiB per launch, so the "
           f"counters are scaled by {f_scale:.3f} (fetch) and {w_scale:.3f} (write).\n")
-    print("| kernel | launches | fetch MB | write MB | total MB |")
+    print("Fetch = L2 read misses (FETCH_SIZE: requests that leave the L2 for the MALL or "
+          "HBM); reads served by the L2 are not in it. Write = bytes written back past the "
+          "L2 (WRITE_SIZE).\n")
+    print("| kernel | launches | L2-miss read MB | write MB | total MB |")
     print("|---|---:|---:|---:|---:|")
     g_n = g_b = 0.0
     for k in f:
@@ -118,6 +158,9 @@ def traffic(fetch, write, cfetch, cwrite, copy_mib, command):
 if __name__ == "__main__":
     if sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3])
+    elif sys.argv[1] == "trace":
+        trace(sys.argv[2], sys.argv[3], int(sys.argv[4]), int(sys.argv[5]), sys.argv[6],
+              sys.argv[7])
     elif sys.argv[1] == "stats":
         stats(sys.argv[2], int(sys.argv[3]), sys.argv[4], sys.argv[5])
     elif sys.argv[1] == "traffic":

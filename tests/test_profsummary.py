@@ -67,3 +67,28 @@ def test_stats_per_step_and_gemm_total(tmp_path, capsys):
     out = capsys.readouterr().out
     assert f"| `{GEMM}` | 4 | 100.00 | 200.0 | 95.2% |" in out
     assert "4 calls, average 100.00 µs, 200.0 µs per step" in out
+
+
+def test_trace_averages_the_selected_forwards(tmp_path, capsys):
+    """Forwards are cut at the first kernel's launches; the skipped ones and
+    everything after the window stay out of the means."""
+    rows, t = [], 0
+
+    def launch(name, us):
+        nonlocal t
+        rows.append([name, t, t + int(us * 1000)])
+        t += int(us * 1000) + 500
+
+    for f, gemm_us in enumerate([100.0, 10.0, 12.0, 999.0]):  # warm-up, 2 forwards, extra
+        launch("embed_ln_vec_kernel<3>", 5.0)
+        launch(GEMM, gemm_us)
+        launch(GEMM, gemm_us)
+    path = write_csv(tmp_path / "t.csv", ["Kernel_Name", "Start_Timestamp", "End_Timestamp"],
+                     rows)
+    P.trace(path, "embed_ln", 1, 2, "title", "cmd")
+    out = capsys.readouterr().out
+    assert f"| `{GEMM}` | 2 | 11.00 | 22.0 |" in out
+    assert "kernel time 27.0 µs per forward" in out
+    assert "All `gemm_i8_kernel` launches: 2 per forward, average 11.00 µs" in out
+    with pytest.raises(SystemExit):
+        P.trace(path, "embed_ln", 3, 2, "title", "cmd")
