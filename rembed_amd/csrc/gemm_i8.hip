@@ -18,10 +18,15 @@
 // bank conflicts. NS stages are in flight, one barrier per stage orders the
 // ring.
 //
-// Epilogue: per 32-row band a wave parks its accumulators in LDS and reads
-// rows back 4 columns per lane, so every output is a 4-wide vector store.
-// Variants (EPI): fp32 or bf16 values, the raw accumulators, or the two
-// passes of a fused row quantization (row |max| by atomics, then u8 bytes).
+// A second family (gemm_i8f_kernel, further down) stages only A in LDS and
+// loads B fragments straight into registers from a fragment-ordered copy of
+// the weight.
+//
+// Epilogue (shared by both): per 32-row band a wave parks its accumulators
+// in LDS and reads rows back 4 columns per lane, so every output is a
+// 4-wide vector store. Variants (EPI): fp32 or bf16 values, the raw
+// accumulators, or the two passes of a fused row quantization (row |max| by
+// atomics, then u8 bytes).
 #include "gemm_common.h"
 
 namespace rh {
