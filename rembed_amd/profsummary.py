@@ -2,7 +2,7 @@
 
     python -m rembed_amd.profsummary stats  <kernel_stats.csv> <steps> <title> <command>
     python -m rembed_amd.profsummary trace  <kernel_trace.csv> <first_kernel> <skip> <count>
-                                     <title> <command>
+                                     <title> <command> [<int8 GEMM rows M>]
     python -m rembed_amd.profsummary traffic <fetch_dir_csv> <write_dir_csv>
                                      <copy_fetch_csv> <copy_write_csv> <copy_mib> <command>
     python -m rembed_amd.profsummary pmc <counter_collection.csv> <command>
@@ -50,7 +50,45 @@ def stats(path, steps, title, command):
               f"{gt / 1e3 / steps:.1f} µs per step ({steps} steps incl. warm-up).")
 
 
-def trace(path, first, skip, count, title, command):
+# The int8 GEMMs of one BERT-base layer in launch order: name, K, N, bytes
+# per output element (QKV rows go to attention as bf16).
+BERT_BASE_I8_LAYER = [("QKV", 768, 2304, 2), ("O", 768, 768, 4), ("FFN1", 768, 3072, 4),
+                      ("FFN2", 3072, 768, 4)]
+INT8_PEAK_TOPS, HBM_PEAK_GBS = 5000.0, 8000.0
+
+
+def gemm_rooflines(times, m, layer=BERT_BASE_I8_LAYER, family="gemm_i8_kernel"):
+    """Per-shape roofline of the int8 GEMMs: times[i] are the durations (µs)
+    of the i-th such launch of each forward, in launch order; launch i runs
+    layer[i % len(layer)]. Algorithmic bytes: u8 A, s8 B, the output, row
+    scales and column scales / sums / bias."""
+    print(f"\nPer-shape roofline of the `{family}` launches (M = {m}; peaks 5.0 POP/s "
+          f"int8 MFMA, 8 TB/s HBM):\n")
+    print("| GEMM | K × N | avg µs | TOP/s | % int8 peak | algorithmic MB | GB/s | "
+          "% HBM peak | bound at peak |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---|")
+    tot_t = tot_min = 0.0
+    for i, (name, k, n, ob) in enumerate(layer):
+        ts = times[i::len(layer)]
+        if not ts:
+            continue
+        us = sum(ts) / len(ts)
+        ops = 2.0 * m * k * n
+        by = m * k + k * n + m * n * ob + 4 * m + 12 * n
+        tops = ops / (us * 1e-6) / 1e12
+        gbs = by / (us * 1e-6) / 1e9
+        t_mfma, t_hbm = ops / (INT8_PEAK_TOPS * 1e12) * 1e6, by / (HBM_PEAK_GBS * 1e9) * 1e6
+        tot_t += us
+        tot_min += max(t_mfma, t_hbm)
+        print(f"| {name} | {k} × {n} | {us:.2f} | {tops:.0f} | {100 * tops / INT8_PEAK_TOPS:.1f} % "
+              f"| {by / 1e6:.1f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} % | "
+              f"{'HBM' if t_hbm > t_mfma else 'MFMA'} ({max(t_mfma, t_hbm):.1f} µs) |")
+    if tot_t:
+        print(f"\nThe layer's int8 GEMMs take {tot_t:.1f} µs against {tot_min:.1f} µs at the "
+              f"binding peak of each: {100 * tot_min / tot_t:.1f} % of the combined roofline.")
+
+
+def trace(path, first, skip, count, title, command, gemm_m=0):
     """Per-forward kernel times from a --kernel-trace CSV: the trace is cut
     into forwards at each launch whose name contains `first` (the forward's
     first kernel), the first `skip` forwards are dropped and the next `count`
@@ -75,6 +113,19 @@ def trace(path, first, skip, count, title, command):
     for name, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
         print(f"| `{name[:90]}` | {len(v) / count:g} | {sum(v) / len(v):.2f} | "
               f"{sum(v) / count:.1f} | {100 * sum(v) / total:.1f}% |")
+    if gemm_m:
+        order = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in sel
+                 if "gemm_i8_kernel<" in r["Kernel_Name"]
+                 or "gemm_i8f_kernel<" in r["Kernel_Name"]]
+        per_fwd = len(order) // count
+        times = [[] for _ in range(per_fwd)]
+        for j, t in enumerate(order):
+            times[j % per_fwd].append(t)
+        # launch i of a forward is layer shape i % 4: flatten per shape
+        by_shape = [[] for _ in BERT_BASE_I8_LAYER]
+        for i, ts in enumerate(times):
+            by_shape[i % len(BERT_BASE_I8_LAYER)].extend(ts)
+        gemm_rooflines([sum(v) / len(v) for v in by_shape], gemm_m)
     for fam in ("gemm_i8_kernel", "gemm_i8f_kernel", "gemm_planes_kernel", "gemm_bf16_kernel"):
         g = [x for k, v in per.items() if fam + "<" in k for x in v]
         if g:
@@ -160,7 +211,7 @@ if __name__ == "__main__":
         pmc(sys.argv[2], sys.argv[3])
     elif sys.argv[1] == "trace":
         trace(sys.argv[2], sys.argv[3], int(sys.argv[4]), int(sys.argv[5]), sys.argv[6],
-              sys.argv[7])
+              sys.argv[7], int(sys.argv[8]) if len(sys.argv) > 8 else 0)
     elif sys.argv[1] == "stats":
         stats(sys.argv[2], int(sys.argv[3]), sys.argv[4], sys.argv[5])
     elif sys.argv[1] == "traffic":

@@ -139,3 +139,53 @@ def test_attention_argument_errors(gpu_ctx):
     with pytest.raises(RembedError):  # bf16 input at precision 3
         T.Attention(gpu_ctx, out, 64, buf, 1, 192, 0, 64, 128, cu, 1, 4, 1, 1, 64, 0.1,
                     precision=3)
+
+
+def test_modernbert_window_convention(gpu_ctx):
+    """ModernBERT's local layers keep keys within ±w of the query, inclusive
+    (masked iff j < i-w or j > i+w, filled with -1e30; modernbert.go:264-273,
+    w = LocalAttention/2). rh_attention's window counts |i-j| < window, so the
+    ModernBERT layer is window = w + 1. Checked against a float64 restatement
+    of ModernBERT's own mask and fill, with texts shorter and longer than
+    the window, at w = 64 (LocalAttention 128) and head dim 64."""
+    w, dh, heads = 64, 64, 12
+    lens = [1, 64, 65, 129, 130, 300]
+    say(f"modernbert window ±{w} lens={lens}")
+    rng = np.random.default_rng(77)
+    M = sum(lens)
+    ld = 3 * heads * dh
+    q_off, k_off, v_off = 0, heads * dh, 2 * heads * dh
+    x = (rng.standard_normal((M, ld)) * 1.5).astype(np.float32)
+    scale = 1.0 / np.sqrt(dh)
+    want = np.zeros((M, heads * dh), np.float64)
+    r0 = 0
+    for L in lens:
+        i = np.arange(L)[:, None]
+        j = np.arange(L)[None, :]
+        masked = (j < i - w) | (j > i + w)
+        for h in range(heads):
+            q = x[r0:r0 + L, q_off + h * dh:q_off + (h + 1) * dh].astype(np.float64)
+            k = x[r0:r0 + L, k_off + h * dh:k_off + (h + 1) * dh].astype(np.float64)
+            v = x[r0:r0 + L, v_off + h * dh:v_off + (h + 1) * dh].astype(np.float64)
+            s = q @ k.T * scale
+            s[masked] = -1e30
+            s -= s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(axis=1, keepdims=True)
+            want[r0:r0 + L, h * dh:(h + 1) * dh] = p @ v
+        r0 += L
+    cu_d = gpu_ctx.upload(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32))
+    out = gpu_ctx.upload(np.full((M, heads * dh), np.nan, np.float32))
+    T.Attention(gpu_ctx, out, heads * dh, gpu_ctx.upload(x), 0, ld, q_off, k_off, v_off, cu_d,
+                len(lens), max(lens), heads, heads, dh, scale, False, w + 1, 3)
+    gpu_ctx.sync()
+    got = out.download(np.float32, (M, heads * dh))
+    err = np.abs(got - want).max()
+    say(f"  max err {err:.3e}")
+    assert err <= 1e-4 * (1 + np.abs(want).max())
+    # the convention matters: one key fewer on each side is a different result
+    out2 = gpu_ctx.upload(np.full((M, heads * dh), np.nan, np.float32))
+    T.Attention(gpu_ctx, out2, heads * dh, gpu_ctx.upload(x), 0, ld, q_off, k_off, v_off, cu_d,
+                len(lens), max(lens), heads, heads, dh, scale, False, w, 3)
+    gpu_ctx.sync()
+    assert np.abs(out2.download(np.float32, (M, heads * dh)) - want).max() > 1e-3

@@ -92,3 +92,17 @@ def test_trace_averages_the_selected_forwards(tmp_path, capsys):
     assert "All `gemm_i8_kernel` launches: 2 per forward, average 11.00 µs" in out
     with pytest.raises(SystemExit):
         P.trace(path, "embed_ln", 3, 2, "title", "cmd")
+
+
+def test_gemm_rooflines_per_shape(capsys):
+    """Ops and algorithmic bytes per shape, the binding peak of each, and the
+    combined fraction: a launch at exactly its binding time scores 100 %."""
+    m = 1000
+    layer = [("A", 64, 64, 4), ("B", 4096, 4096, 4)]
+    t_a = (m * 64 + 64 * 64 + m * 64 * 4 + 4 * m + 12 * 64) / (P.HBM_PEAK_GBS * 1e9) * 1e6
+    t_b = 2.0 * m * 4096 * 4096 / (P.INT8_PEAK_TOPS * 1e12) * 1e6
+    P.gemm_rooflines([t_a, 2 * t_b], m, layer)
+    out = capsys.readouterr().out
+    assert "| A | 64 × 64 |" in out and "HBM (" in out
+    assert "| B | 4096 × 4096 |" in out and "MFMA (" in out and "50.0 % |" in out
+    assert f"{100 * (t_a + t_b) / (t_a + 2 * t_b):.1f} % of the combined roofline" in out
