@@ -255,6 +255,8 @@ int rh_layernorm(rh_context *ctx, float *x, const float *gamma,
 #define RH_ARCH_BERT 0   /* BERT / RoBERTa post-LN encoder (encoder.layer.N.* names) */
 #define RH_ARCH_QWEN3 1  /* Qwen3 causal decoder embedder (qwen3.go:395-548) */
 #define RH_ARCH_GEMMA3 2 /* EmbeddingGemma: Gemma 3 run bidirectionally (gemma3.go:206-384) */
+#define RH_ARCH_NOMIC 3  /* nomic-embed (nomic_bert): post-LN, RoPE, SwiGLU, bias-free (nomic.go:113-250) */
+#define RH_ARCH_MODERNBERT 4 /* ModernBERT: pre-LN, RoPE, global/local attention, GeGLU (modernbert.go:148-311) */
 #define RH_POOL_MEAN 0
 #define RH_POOL_CLS 1
 #define RH_POOL_LAST 2
@@ -277,13 +279,17 @@ typedef struct {
   float layer_norm_eps; /* 0 means 1e-12 (config.go:228-230) */
   int pooling;          /* RH_POOL_* */
   int normalize;        /* L2-normalize pooled vectors */
-  /* decoder family (config.go:56-77); ignored for RH_ARCH_BERT */
+  /* RoPE family (config.go:44-77); ignored for RH_ARCH_BERT. max_position
+   * is the longest text (RoPE table rows); nomic and ModernBERT have no
+   * kv head groups (kv_heads 0) and head_dim * heads == hidden. */
   int kv_heads;              /* NumKeyValueHeads (GQA); 0 = heads */
   int head_dim;              /* HeadDim; 0 = hidden / heads */
-  double rope_theta;         /* Qwen3 RopeTheta; Gemma GlobalRopeTheta */
-  double rope_local_theta;   /* Gemma LocalRopeTheta */
-  int sliding_window;        /* Gemma: local layers attend where |i-j| < window */
-  int sliding_pattern;       /* Gemma: layer l is global iff (l+1) % pattern == 0 */
+  double rope_theta;         /* Qwen3 / nomic RopeTheta; Gemma / ModernBERT GlobalRopeTheta */
+  double rope_local_theta;   /* Gemma / ModernBERT LocalRopeTheta */
+  int sliding_window;        /* Gemma: local layers attend where |i-j| < window;
+                                ModernBERT: LocalAttention, |i-j| <= window / 2 */
+  int sliding_pattern;       /* Gemma: layer l is global iff (l+1) % pattern == 0;
+                                ModernBERT: GlobalAttnEveryNLayers, global iff l % n == 0 */
   int query_pre_attn_scalar; /* Gemma: scores scaled by 1/sqrt(scalar) */
   int dense_hidden;          /* Gemma Dense head width (2_Dense/3_Dense); 0 = none */
   int reserved[8];           /* zero */
@@ -296,8 +302,9 @@ int rh_model_create(rh_context *ctx, const rh_model_config *cfg, int quant,
 /* Hand one HF tensor (by its safetensors name, with or without the
  * "bert."/"roberta." prefix; decoders: embed_tokens.weight,
  * norm.weight, layers.N.*, with or without "model.", and Gemma's Dense head
- * as "2_Dense.linear.weight" / "3_Dense.linear.weight") to the model; data
- * is copied. */
+ * as "2_Dense.linear.weight" / "3_Dense.linear.weight"; nomic:
+ * embeddings.*, emb_ln.*, encoder.layers.N.*; ModernBERT: embeddings.*,
+ * layers.N.*, final_norm.weight) to the model; data is copied. */
 int rh_model_set_tensor(rh_model *m, const char *name, const float *host,
                         const int64_t *shape, int ndim);
 /* Check every tensor is present, fuse Q|K|V (decoders: also gate|up into

@@ -24,6 +24,9 @@
  *   elementwise          KATs of tensor_test.go:154-268, float64 erf/tanh
  *   or_bert_*            composition pinned by source reading; invariants
  *                        (unit L2 norm, batch == single, mode agreement)
+ *   or_dec_* / or_renc_* independent float64 numpy compositions of the
+ *                        reference forwards, plus planted variants (operand
+ *                        order, mask bounds, layer schedule) that must fail
  */
 #ifndef REMBED_ORACLE_H
 #define REMBED_ORACLE_H
@@ -194,6 +197,45 @@ int or_dec_embed_batch_timed(const or_dec_model *m, const int32_t *ids,
                        const int32_t *lens, int batch, int stride, float *out,
                        int threads,
                         double *secs);
+
+/* ---- bias-free RoPE encoders (internal/model/nomic.go, modernbert.go) ---- */
+#define OR_ARCH_NOMIC 3
+#define OR_ARCH_MODERNBERT 4
+typedef struct {
+  int arch; /* OR_ARCH_NOMIC / OR_ARCH_MODERNBERT */
+  int vocab, hidden, layers, heads, inter;
+  float eps;
+  double rope_theta;       /* nomic RopeTheta; ModernBERT GlobalRopeTheta */
+  double rope_local_theta; /* ModernBERT LocalRopeTheta */
+  int local_attention;     /* ModernBERT: local layers keep |i-j| <= local_attention/2 */
+  int global_every;        /* ModernBERT: layer l is global iff l % global_every == 0 */
+  int pooling, normalize;
+  int max_seq;
+} or_renc_config;
+
+/* Per-layer tensors, HF layouts ([out][in] for projections):
+ * nomic (9):      attn.Wqkv attn.out_proj norm1.weight norm1.bias mlp.fc11
+ *                 mlp.fc12 mlp.fc2 norm2.weight norm2.bias
+ * ModernBERT (6): attn_norm (NULL for layer 0) attn.Wqkv attn.Wo mlp_norm
+ *                 mlp.Wi [2I][H] mlp.Wo
+ * Model tensors: embed (word / tok embeddings), nomic's token-type table
+ * (row 0 used) and emb_ln weight/bias, ModernBERT's embeddings.norm (emb_g)
+ * and final_norm; the others NULL. */
+#define OR_NOMIC_TENSORS_PER_LAYER 9
+#define OR_MODERNBERT_TENSORS_PER_LAYER 6
+
+typedef struct or_renc_model or_renc_model;
+or_renc_model *or_renc_create(const or_renc_config *cfg, int quant, const float *embed,
+                              const float *type_emb, const float *emb_g, const float *emb_b,
+                              const float *final_norm, const float *const *layer_tensors);
+void or_renc_free(or_renc_model *m);
+/* 0 fp32, 1 weight-only int8, 2 full int8: the mode layer 0's Wqkv took */
+int or_renc_quantized_kind(const or_renc_model *m);
+int or_renc_encode(const or_renc_model *m, const int32_t *ids, int seq, float *x);
+int or_renc_forward(const or_renc_model *m, const int32_t *ids, int seq, float *out);
+int or_renc_embed_batch_timed(const or_renc_model *m, const int32_t *ids,
+                              const int32_t *lens, int batch, int stride, float *out,
+                              int threads, double *secs);
 
 /* building blocks (exported for the unit tests) */
 void or_rope_table(float *cos_t, float *sin_t, int seq, int dh, double theta);

@@ -65,6 +65,12 @@ def _load():
         "or_dec_forward": (I, [P, P, I, P]),
         "or_dec_embed_batch": (I, [P, P, P, I, I, P, I]),
         "or_dec_embed_batch_timed": (I, [P, P, P, I, I, P, I, P]),
+        "or_renc_create": (P, [P, I, P, P, P, P, P, P]),
+        "or_renc_free": (None, [P]),
+        "or_renc_quantized_kind": (I, [P]),
+        "or_renc_encode": (I, [P, P, I, P]),
+        "or_renc_forward": (I, [P, P, I, P]),
+        "or_renc_embed_batch_timed": (I, [P, P, P, I, I, P, I, P]),
         "or_rope_table": (None, [P, P, I, I, ctypes.c_double]),
         "or_apply_rope": (None, [P, I, I, P, P]),
         "or_flash_causal_head": (None, [P, P, P, P, I, I, F]),
@@ -408,6 +414,103 @@ class DecoderOracle:
         st = lib.or_dec_embed_batch_timed(self.h, _p(ids), _p(lens), ids.shape[0],
                                           ids.shape[1], _p(out), threads,
                                           None if secs is None else _p(secs))
+        if st:
+            raise RuntimeError(f"oracle embed status {st}")
+        return out
+
+
+# ---- bias-free RoPE encoders (nomic-embed, ModernBERT) ------------------------------
+
+ARCH_NOMIC, ARCH_MODERNBERT = 3, 4
+
+
+class RencConfig(ctypes.Structure):
+    _fields_ = [("arch", ctypes.c_int), ("vocab", ctypes.c_int), ("hidden", ctypes.c_int),
+                ("layers", ctypes.c_int), ("heads", ctypes.c_int), ("inter", ctypes.c_int),
+                ("eps", ctypes.c_float), ("rope_theta", ctypes.c_double),
+                ("rope_local_theta", ctypes.c_double), ("local_attention", ctypes.c_int),
+                ("global_every", ctypes.c_int), ("pooling", ctypes.c_int),
+                ("normalize", ctypes.c_int), ("max_seq", ctypes.c_int)]
+
+
+NOMIC_LAYER_ORDER = [
+    "attn.Wqkv.weight", "attn.out_proj.weight", "norm1.weight", "norm1.bias",
+    "mlp.fc11.weight", "mlp.fc12.weight", "mlp.fc2.weight", "norm2.weight", "norm2.bias",
+]
+MODERNBERT_LAYER_ORDER = [
+    "attn_norm.weight", "attn.Wqkv.weight", "attn.Wo.weight", "mlp_norm.weight",
+    "mlp.Wi.weight", "mlp.Wo.weight",
+]
+
+
+class RopeEncoderOracle:
+    """The reference's per-text unpadded nomic-embed / ModernBERT forward on
+    the CPU (internal/model/nomic.go, modernbert.go). `shape` is a
+    rembed_amd.synthetic.RopeEncoderShape; tensors use HF names."""
+
+    def __init__(self, shape, tensors, quant):
+        self._keep = {k: f32(v) for k, v in tensors.items()}
+        t = self._keep
+        mb = shape.arch == ARCH_MODERNBERT
+        cfg = RencConfig(shape.arch, shape.vocab, shape.hidden, shape.layers, shape.heads,
+                         shape.intermediate, shape.eps, shape.rope_theta,
+                         shape.rope_local_theta, shape.local_attention, shape.global_every,
+                         shape.pooling, shape.normalize, shape.max_seq)
+        self.shape = shape
+        if mb:
+            ptrs = [t[f"layers.{l}.{n}"].ctypes.data if f"layers.{l}.{n}" in t else None
+                    for l in range(shape.layers) for n in MODERNBERT_LAYER_ORDER]
+            model = (t["embeddings.tok_embeddings.weight"], None, t["embeddings.norm.weight"],
+                     None, t["final_norm.weight"])
+        else:
+            ptrs = [t[f"encoder.layers.{l}.{n}"].ctypes.data
+                    for l in range(shape.layers) for n in NOMIC_LAYER_ORDER]
+            model = (t["embeddings.word_embeddings.weight"],
+                     t["embeddings.token_type_embeddings.weight"], t["emb_ln.weight"],
+                     t["emb_ln.bias"], None)
+        self._arr = (ctypes.c_void_p * len(ptrs))(*ptrs)
+        self.h = lib.or_renc_create(ctypes.byref(cfg), quant,
+                                    *[None if a is None else _p(a) for a in model],
+                                    ctypes.cast(self._arr, ctypes.c_void_p))
+        if not self.h:
+            raise RuntimeError("oracle: bad RoPE encoder config")
+
+    def close(self):
+        if self.h:
+            lib.or_renc_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def quantized_kind(self):
+        return lib.or_renc_quantized_kind(self.h)
+
+    def encode(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
+        st = lib.or_renc_encode(self.h, _p(ids), ids.shape[0], _p(out))
+        if st:
+            raise RuntimeError(f"oracle encode status {st}")
+        return out
+
+    def forward(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty(self.shape.hidden, np.float32)
+        st = lib.or_renc_forward(self.h, _p(ids), ids.shape[0], _p(out))
+        if st:
+            raise RuntimeError(f"oracle forward status {st}")
+        return out
+
+    def embed_batch(self, ids, lens, threads=1, secs=None):
+        """One forward per text across `threads`; `secs` (float64 [batch])
+        receives each text's forward time."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        lens = np.ascontiguousarray(lens, np.int32)
+        out = np.empty((ids.shape[0], self.shape.hidden), np.float32)
+        st = lib.or_renc_embed_batch_timed(self.h, _p(ids), _p(lens), ids.shape[0],
+                                           ids.shape[1], _p(out), threads,
+                                           None if secs is None else _p(secs))
         if st:
             raise RuntimeError(f"oracle embed status {st}")
         return out

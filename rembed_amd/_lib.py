@@ -27,7 +27,7 @@ RH_QUANT_NONE, RH_QUANT_WEIGHTS, RH_QUANT_FULL = 0, 1, 2
 RH_POOL_MEAN, RH_POOL_CLS, RH_POOL_LAST = 0, 1, 2
 RH_ACT_NONE, RH_ACT_GELU, RH_ACT_SWIGLU, RH_ACT_GEGLU = 0, 1, 2, 3
 RH_ACT_GEGLU_ERF = 4
-RH_ARCH_BERT, RH_ARCH_QWEN3, RH_ARCH_GEMMA3 = 0, 1, 2
+RH_ARCH_BERT, RH_ARCH_QWEN3, RH_ARCH_GEMMA3, RH_ARCH_NOMIC, RH_ARCH_MODERNBERT = 0, 1, 2, 3, 4
 RH_OPT_ATTN_PRECISION = 1
 RH_OPT_FUSED_FFN1 = 2
 RH_OPT_PRODUCER_PLANES = 3

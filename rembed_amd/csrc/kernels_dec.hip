@@ -34,11 +34,14 @@ __device__ __forceinline__ uint8_t qbyte(float v, float inv) {
 
 // ---- embeddings ---------------------------------------------------------------
 // embed_tokens rows (qwen3.go:460-467), scaled by float32(sqrt(H)) for Gemma
-// (gemma3.go:262-275), plus each row's position in its text for RoPE.
+// (gemma3.go:262-275), plus an optional row added to each (nomic's segment-0
+// row: w[j] + t[j], nomic.go:177-188), and each row's position in its text
+// for RoPE.
 __global__ __launch_bounds__(256) void embed_gather_kernel(
     const int32_t* __restrict__ ids, int stride, const int32_t* __restrict__ cu,
-    int batch, const float* __restrict__ word, int H, int vocab, float scale,
-    float* __restrict__ x, int32_t* __restrict__ pos, int* err_flag, int total) {
+    int batch, const float* __restrict__ word, const float* __restrict__ add_row, int H,
+    int vocab, float scale, float* __restrict__ x, int32_t* __restrict__ pos, int* err_flag,
+    int total) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRows + (threadIdx.x >> 6);
   if (row >= total) return;
@@ -60,29 +63,34 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(
   for (int j = lane * 4; j < H; j += 256) {
     v4f v = *reinterpret_cast<const v4f*>(src + j);
     if (scale != 1.0f) v = v * scale;
+    if (add_row) v = v + *reinterpret_cast<const v4f*>(add_row + j);
     *reinterpret_cast<v4f*>(dst + j) = v;
   }
 }
 
 hipError_t launch_embed_gather(const int32_t* ids, int stride, const int32_t* cu,
-                               int batch, const float* word, int H, int vocab,
-                               float scale, float* x, int32_t* pos, int* err_flag,
+                               int batch, const float* word, const float* add_row, int H,
+                               int vocab, float scale, float* x, int32_t* pos, int* err_flag,
                                int total_rows, hipStream_t s) {
   if (total_rows <= 0) return hipSuccess;
   if (H % 4) return hipErrorInvalidValue;
   hipLaunchKernelGGL(embed_gather_kernel, dim3(ceil_div(total_rows, kRows)), dim3(256), 0,
-                     s, ids, stride, cu, batch, word, H, vocab, scale, x, pos, err_flag,
-                     total_rows);
+                     s, ids, stride, cu, batch, word, add_row, H, vocab, scale, x, pos,
+                     err_flag, total_rows);
   return hipGetLastError();
 }
 
-// ---- residual + RMSNorm sandwich -------------------------------------------------
+// ---- residual + norm sandwich ----------------------------------------------------
 //   y' = post_g ? RMSNorm(y, post_g) : y   (Gemma post-norms, gemma3.go:357,376)
 //   x += y'                                 (Add, tensor.go:383-387)
 //   out = RMSNorm(x, pre_g)                 (the next sublayer's pre-norm)
-// out goes to fp32 rows and/or to the bf16 hi/lo planes of the next GEMM's
-// input, plus an optional QuantizeRowU8 of it for a full-int8 GEMM. V float4
-// per lane.
+// or, with layer_norm set, out = LayerNorm(x, pre_g, ln_b) (tensor.go:430-452:
+// biased variance, 1 / float32(sqrt(var + eps)), (v - mean) * inv * g + b;
+// a null ln_b adds zero, as ModernBERT's shared zero beta does). out goes to
+// fp32 rows and/or to the bf16 hi/lo planes of the next GEMM's input, plus
+// an optional QuantizeRowU8 of it for a full-int8 GEMM. When out is x itself
+// (a post-norm block, or the final norm) the sum is not stored first. V
+// float4 per lane.
 template <int V>
 __global__ __launch_bounds__(256) void rms_residual_kernel(RmsArgs p) {
   const int lane = threadIdx.x & 63;
@@ -118,20 +126,39 @@ __global__ __launch_bounds__(256) void rms_residual_kernel(RmsArgs p) {
         }
       }
     }
+    const bool store_sum = p.out != p.x;
 #pragma unroll
     for (int e = 0; e < V; e++) {
       const int j = (lane + 64 * e) * 4;
       if (j < H) {
         v[e] = v[e] + w[e];
-        *reinterpret_cast<v4f*>(xr + j) = v[e];
+        if (store_sum) *reinterpret_cast<v4f*>(xr + j) = v[e];
       }
     }
   }
-  float ss = 0.0f;
+  float inv, mean = 0.0f;
+  if (p.layer_norm) {
+    float s = 0.0f;  // lanes past H hold zeros
 #pragma unroll
-  for (int e = 0; e < V; e++)
-    ss += (v[e][0] * v[e][0] + v[e][1] * v[e][1]) + (v[e][2] * v[e][2] + v[e][3] * v[e][3]);
-  const float inv = rms_inv(wsum(ss), H, p.eps);
+    for (int e = 0; e < V; e++) s += (v[e][0] + v[e][1]) + (v[e][2] + v[e][3]);
+    mean = wsum(s) / (float)H;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int j = (lane + 64 * e) * 4;
+      if (j < H) {
+        const v4f d = v[e] - mean;
+        s2 += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+      }
+    }
+    inv = 1.0f / sqrtf(wsum(s2) / (float)H + p.eps);
+  } else {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < V; e++)
+      ss += (v[e][0] * v[e][0] + v[e][1] * v[e][1]) + (v[e][2] * v[e][2] + v[e][3] * v[e][3]);
+    inv = rms_inv(wsum(ss), H, p.eps);
+  }
   float mx = 0.0f;
 #pragma unroll
   for (int e = 0; e < V; e++) {
@@ -139,8 +166,15 @@ __global__ __launch_bounds__(256) void rms_residual_kernel(RmsArgs p) {
     if (j < H) {
       const v4f g = *reinterpret_cast<const v4f*>(p.pre_g + j);
       v4f o;
+      if (p.layer_norm) {
+        const v4f b = p.ln_b ? *reinterpret_cast<const v4f*>(p.ln_b + j)
+                             : v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int c = 0; c < 4; c++) o[c] = v[e][c] * inv * g[c];
+        for (int c = 0; c < 4; c++) o[c] = (v[e][c] - mean) * inv * g[c] + b[c];
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; c++) o[c] = v[e][c] * inv * g[c];
+      }
       v[e] = o;
       if (p.out) *reinterpret_cast<v4f*>(p.out + (size_t)row * H + j) = o;
       if (p.ph) store_planes4(p.ph, p.pl, (size_t)row * p.ldp + j, o);
@@ -168,7 +202,8 @@ __global__ __launch_bounds__(256) void rms_residual_kernel(RmsArgs p) {
 
 hipError_t launch_rms_residual(const RmsArgs& a, hipStream_t s) {
   if (a.m <= 0) return hipSuccess;
-  if (a.H % 4 || a.H > 4096 || (a.qa && a.ldq % 4) || (a.ph && (a.ldp % 64 || a.ldp < a.H)))
+  if (a.H % 4 || a.H > 4096 || (a.qa && a.ldq % 4) || (a.ph && (a.ldp % 64 || a.ldp < a.H)) ||
+      (a.layer_norm && a.post_g))
     return hipErrorInvalidValue;
   const dim3 grid(ceil_div(a.m, kRows)), block(256);
   const int v = ceil_div(a.H, 256);
@@ -183,9 +218,11 @@ hipError_t launch_rms_residual(const RmsArgs& a, hipStream_t s) {
 
 // ---- QK-norm + RoPE -----------------------------------------------------------------
 // Items are (row, head) over the q heads then the k heads of a fused q|k|v
-// row: RMSNorm of the head's dh values with its norm weight, then
-// rotate-half RoPE at the row's position (applyRoPE, modernbert.go:130-143:
-// each product rounded to float32 before the add). With `outh` the results
+// row: RMSNorm of the head's dh values with its norm weight (none when the
+// norm weights are null: nomic and ModernBERT rotate the raw projections,
+// nomic.go:210-211, modernbert.go:256-257), then rotate-half RoPE at the
+// row's position (applyRoPE, modernbert.go:130-143: each product rounded to
+// float32 before the add). With `outh` the results
 // go to bf16 rows of the same layout instead (round to nearest even), and
 // the v heads are converted too: the operands of a bf16 attention.
 // A wave takes kQkItems consecutive items, loading all of them before it
@@ -233,7 +270,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       }
       continue;
     }
-    const float* g = h < nq ? q_g : k_g;
+    const float* g = h < nq ? q_g : k_g;  // null: no QK-norm, RoPE only
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < 2; e++) ss += x1[it][e] * x1[it][e] + x2[it][e] * x2[it][e];
@@ -245,8 +282,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     for (int e = 0; e < 2; e++) {
       const int d = lane + 64 * e;
       if (d < half) {
-        const float a = x1[it][e] * inv * g[d];
-        const float b = x2[it][e] * inv * g[d + half];
+        const float a = g ? x1[it][e] * inv * g[d] : x1[it][e];
+        const float b = g ? x2[it][e] * inv * g[d + half] : x2[it][e];
         const float cc = c[d], ssn = sn[d];
         const float t0 = a * cc, t1 = b * ssn, t2 = b * cc, t3 = a * ssn;
         if (o) {
@@ -309,10 +346,15 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
         continue;
       }
       const float inv = rms_inv(ss, DH, eps);
-      const v4f g = *reinterpret_cast<const v4f*>((h < nq ? q_g : k_g) + d);
+      const float* gp = h < nq ? q_g : k_g;  // null: no QK-norm, RoPE only
       v4f xn, pn;
+      if (gp) {
+        const v4f g = *reinterpret_cast<const v4f*>(gp + d);
 #pragma unroll
-      for (int c = 0; c < 4; c++) xn[c] = x[it][c] * inv * g[c];
+        for (int c = 0; c < 4; c++) xn[c] = x[it][c] * inv * g[c];
+      } else {
+        xn = x[it];
+      }
 #pragma unroll
       for (int c = 0; c < 4; c++) pn[c] = __shfl_xor(xn[c], LPH / 2, 64);
       const bool first = l < LPH / 2;  // columns d < dh/2

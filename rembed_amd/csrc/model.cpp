@@ -38,9 +38,12 @@ struct Layer {
   float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
 };
 
-// One Qwen3 / Gemma3 layer on the device. q|k|v are fused into one weight
-// and gate|up into one gated weight; norm weights are uploaded as the
-// reference uses them (Gemma's with the unit offset folded in).
+// One layer of the RoPE family on the device: Qwen3, Gemma3, nomic-bert,
+// ModernBERT. q|k|v are fused into one weight and gate|up into one gated
+// weight; norm weights are uploaded as the reference uses them (Gemma's with
+// the unit offset folded in). nomic keeps norm1 in post_attn(_b) and norm2 in
+// post_ffn(_b); ModernBERT keeps attn_norm in in_norm (null for layer 0, an
+// identity in the reference) and mlp_norm in post_attn.
 struct DecLayer {
   rh_weight* qkv = nullptr;  // [qdim + 2 kvdim][H], or null when q, k, v are separate
   rh_weight* o = nullptr;    // [H][qdim]
@@ -53,6 +56,7 @@ struct DecLayer {
   rh_weight *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *up = nullptr;
   float *in_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr,
         *pre_ffn = nullptr, *post_ffn = nullptr;
+  float *post_attn_b = nullptr, *post_ffn_b = nullptr;  // nomic's LayerNorm betas
   bool global = true;
 };
 
@@ -98,7 +102,8 @@ struct WeightSet {
         destroy_weight(w);
         ctx_release(ctx);
       }
-      for (float* p : {L.in_norm, L.q_norm, L.k_norm, L.post_attn, L.pre_ffn, L.post_ffn})
+      for (float* p : {L.in_norm, L.q_norm, L.k_norm, L.post_attn, L.pre_ffn, L.post_ffn,
+                       L.post_attn_b, L.post_ffn_b})
         if (p) (void)hipFree(p);
     }
     for (float* p : bufs)
@@ -245,17 +250,23 @@ struct rh_model {
 
   int H() const { return cfg.hidden; }
   int I() const { return cfg.intermediate; }
-  bool decoder() const { return cfg.arch != RH_ARCH_BERT; }
+  // The RoPE family (Qwen3, Gemma3, nomic-bert, ModernBERT) runs
+  // forward_dec; BERT / RoBERTa run forward.
+  bool rope_family() const { return cfg.arch != RH_ARCH_BERT; }
   bool gemma() const { return cfg.arch == RH_ARCH_GEMMA3; }
+  bool nomic() const { return cfg.arch == RH_ARCH_NOMIC; }
+  bool modernbert() const { return cfg.arch == RH_ARCH_MODERNBERT; }
+  // nomic and ModernBERT normalize with LayerNorm, the decoders with RMSNorm
+  bool layer_norm() const { return nomic() || modernbert(); }
   int nq() const { return cfg.heads; }
-  int nkv() const { return decoder() && cfg.kv_heads > 0 ? cfg.kv_heads : cfg.heads; }
+  int nkv() const { return rope_family() && cfg.kv_heads > 0 ? cfg.kv_heads : cfg.heads; }
   int dh() const {
-    return decoder() && cfg.head_dim > 0 ? cfg.head_dim : cfg.hidden / cfg.heads;
+    return rope_family() && cfg.head_dim > 0 ? cfg.head_dim : cfg.hidden / cfg.heads;
   }
   int qdim() const { return nq() * dh(); }
   int kvdim() const { return nkv() * dh(); }
-  int qkv_width() const { return decoder() ? qdim() + 2 * kvdim() : 3 * cfg.hidden; }
-  int ctx_width() const { return decoder() ? qdim() : cfg.hidden; }
+  int qkv_width() const { return rope_family() ? qdim() + 2 * kvdim() : 3 * cfg.hidden; }
+  int ctx_width() const { return rope_family() ? qdim() : cfg.hidden; }
   int ldq_for(int k) const { return (int)round_up(k, 16); }
   // Does w take its input as producer-written planes? (w runs on planes and
   // K is a multiple of 64, so the producers' K columns fill the planes.)
@@ -298,7 +309,7 @@ struct rh_model {
       if (split_gu_any) RH_HIP(dalloc(&hid2, r * I));
       RH_HIP(dalloc(&qa, r * ldq_for(std::max(H, ctx_width()))));
       RH_HIP(dalloc(&qa2, r * ldq_for(I)));
-      if (decoder()) {
+      if (rope_family()) {
         RH_HIP(dalloc(&normed, r * H));
         RH_HIP(dalloc(&pos_d, r));
       }
@@ -474,7 +485,7 @@ int rh_model::join_parts(const std::vector<Part>& parts, hipStream_t s) {
 
 int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
                       int max_len, bool pool, float* out_dev) {
-  if (decoder()) return forward_dec(ids_dev, stride, cu, max_len, pool, out_dev);
+  if (rope_family()) return forward_dec(ids_dev, stride, cu, max_len, pool, out_dev);
   hipStream_t s = ctx->stream;
   const int batch = (int)cu.size() - 1;
   const int M = cu[batch];
@@ -689,8 +700,15 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
 }
 
 
-// encodeQwen3 (qwen3.go:395-548) / encodeGemma3 (gemma3.go:206-384) over the
-// packed batch, then ForwardWorkers' pooling (bert.go:657-689).
+// encodeQwen3 (qwen3.go:395-548) / encodeGemma3 (gemma3.go:206-384) /
+// encodeNomic (nomic.go:113-250) / encodeModernBERT (modernbert.go:148-311)
+// over the packed batch, then ForwardWorkers' pooling (bert.go:657-689).
+// The four share one layer loop: fused q|k|v, (QK-norm +) RoPE, attention,
+// output projection, a residual + norm, the gated MLP, a residual + norm.
+// What differs is the norm (RMSNorm / LayerNorm), where it sits (pre-norm:
+// the norm's output feeds the next GEMM and x keeps the sum; nomic's
+// post-norm: x itself is normalized and feeds the next GEMM), the attention
+// mask and scale, and the gate activation.
 int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
                           int max_len, bool pool, float* out_dev) {
   hipStream_t s = ctx->stream;
@@ -707,9 +725,11 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
   RH_HIP(hipEventRecord(cu_evt, s));
 
   const float emb_scale = gemma() ? (float)std::sqrt((double)H) : 1.0f;
-  RH_HIP(launch_embed_gather(ids_dev, stride, cu_d, batch, word, H, cfg.vocab, emb_scale, x,
-                             pos_d, err_d, M, s));
+  // nomic adds the segment-0 row (type0 is null for the others)
+  RH_HIP(launch_embed_gather(ids_dev, stride, cu_d, batch, word, type0, H, cfg.vocab,
+                             emb_scale, x, pos_d, err_d, M, s));
   const float e = eps();
+  const bool ln = layer_norm(), post = nomic();
   const int ldqH = ldq_for(std::max(H, qd)), ldqI = ldq_for(I);
   // this part's rows of a planes buffer
   auto at = [](Planes p, size_t r0) {
@@ -717,27 +737,31 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     if (p.lo) p.lo += r0 * p.ld;
     return p;
   };
-  // The pre-norms write what the next GEMM reads: fp32 rows, its bf16
-  // planes, or its u8 rows (RmsArgs), for rows [r0, r0 + m).
-  auto rms_to = [&](size_t r0, int m, hipStream_t ps, const float* yy, const float* post,
-                    const float* pre, const rh_weight* next, bool in_place_out) {
+  // The norms write what the next GEMM reads: its bf16 planes or its u8
+  // rows (RmsArgs), and fp32 rows: x itself when in_place (nomic's post-norm
+  // blocks, the embedding norm of nomic and ModernBERT, the final norm),
+  // else `normed` unless the planes replace them; rows [r0, r0 + m).
+  auto norm_to = [&](size_t r0, int m, hipStream_t ps, const float* yy, const float* post_g,
+                     const float* pre, const float* pre_b, const rh_weight* next,
+                     bool in_place) {
     RmsArgs ra{};
     ra.x = x + r0 * H;
     ra.y = yy ? yy + r0 * H : nullptr;
-    ra.post_g = post;
+    ra.post_g = post_g;
     ra.pre_g = pre;
+    ra.layer_norm = ln ? 1 : 0;
+    ra.ln_b = pre_b;
     ra.m = m;
     ra.H = H;
     ra.eps = e;
-    if (in_place_out) {
-      ra.out = ra.x;
-    } else if (planes_in(next)) {
+    const bool pl = planes_in(next);
+    if (in_place) ra.out = ra.x;
+    else if (!pl) ra.out = normed + r0 * H;
+    if (pl) {
       const Planes p = at(plane(0, next), r0);
       ra.ph = p.hi;
       ra.pl = p.lo;
       ra.ldp = p.ld;
-    } else {
-      ra.out = normed + r0 * H;
     }
     if (next && needs_q(next)) {
       ra.qa = qa + r0 * ldqH;
@@ -746,7 +770,12 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     }
     return launch_rms_residual(ra, ps);
   };
-  RH_HIP(rms_to(0, M, s, nullptr, nullptr, dlayers[0].in_norm, dlayers[0].qkv, false));
+  if (ln) {  // LayerNorm(x) in place: the embedding norm (nomic.go:176, modernbert.go:211)
+    RH_HIP(norm_to(0, M, s, nullptr, nullptr, emb_g, emb_b, dlayers[0].qkv, true));
+  } else {
+    RH_HIP(norm_to(0, M, s, nullptr, nullptr, dlayers[0].in_norm, nullptr, dlayers[0].qkv,
+                   false));
+  }
 
   // Parts (see plan_parts): allowed when no linear falls back to the
   // context's split workspace.
@@ -761,7 +790,7 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
   }
   std::vector<Part> parts;
   if ((st = plan_parts(cu, no_ws, s, parts))) return st;
-  const int glu = gemma() ? ACT_GEGLU : ACT_SWIGLU;
+  const int glu = gemma() ? ACT_GEGLU : modernbert() ? ACT_GEGLU_ERF : ACT_SWIGLU;
   auto layer = [&](size_t li, const Part& P) -> int {
     const DecLayer& L = dlayers[li];
     const hipStream_t ps = P.s;
@@ -775,22 +804,28 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     uint8_t* qa2p = qa2 + r0 * ldqI;
     float* rsp = rs + r0;
     float* rs2p = rs2 + r0;
+    float* xp = x + r0 * H;
+    // the fp32 rows the projections read: x itself after nomic's post-norms
+    // and for ModernBERT's layer 0 (its attention norm is an identity,
+    // modernbert.go:229-236), else the pre-norm's output
+    const float* attn_in = post || (modernbert() && li == 0) ? xp : normedp;
+    const float* mlp_in = post ? xp : normedp;
     int st;
     // attention block: fused q|k|v, QK-norm + RoPE, GQA attention, o_proj
     const Planes pq = at(plane(0, L.qkv), r0);
-    const bool local = gemma() && !L.global;
+    const bool local = (gemma() || modernbert()) && !L.global;
     // bf16 attention reads bf16 q|k|v rows: written by the q|k|v GEMM's
     // QK-norm + RoPE epilogue where that applies, else by the separate pass
     const bool hb = attn_precision == 1;
     bool fused_qk = false;
-    if (qk_epilogue && hb && L.qkv && planes_in(L.qkv)) {
+    if (qk_epilogue && hb && L.qkv && L.q_norm && planes_in(L.qkv)) {
       const QkEpilogue q{L.q_norm, L.k_norm, local ? cos_l : cos_g, local ? sin_l : sin_g,
                          pos_d + r0, nq(), nkv(), dh(), e};
       st = run_linear_qk(ctx, L.qkv, pq, Mp, q, qkvh + r0 * qkvw, qkvw, &fused_qk);
       if (st) return st;
     }
     if (!fused_qk && L.qkv) {
-      st = run_linear(ctx, L.qkv, normedp, H, Mp, qkvp, qkvw, ACT_NONE, nullptr, qap, ldqH,
+      st = run_linear(ctx, L.qkv, attn_in, H, Mp, qkvp, qkvw, ACT_NONE, nullptr, qap, ldqH,
                       rsp, false, planes_in(L.qkv) ? &pq : nullptr);
       if (st) return st;
     } else if (!fused_qk) {
@@ -799,7 +834,7 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
       const rh_weight* sep[3] = {L.q, L.k, L.v};
       const int col[3] = {0, qd, qd + kvd};
       for (int j = 0; j < 3; j++) {
-        st = run_linear(ctx, sep[j], normedp, H, Mp, qkvp + col[j], qkvw, ACT_NONE, nullptr,
+        st = run_linear(ctx, sep[j], attn_in, H, Mp, qkvp + col[j], qkvw, ACT_NONE, nullptr,
                         qap, ldqH, rsp, needs_q(sep[j]));
         if (st) return st;
       }
@@ -833,7 +868,10 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     aa.ctx_lo = po ? pov.lo : nullptr;
     aa.ldctx = po ? pov.ld : qd;
     aa.causal = cfg.arch == RH_ARCH_QWEN3 ? 1 : 0;
-    aa.window = local ? cfg.sliding_window : 0;
+    // the kernel keeps keys with |i - j| < window: Gemma's sliding_window as
+    // is (gemma3.go:331-351), ModernBERT's |i - j| <= local_attention / 2
+    // (modernbert.go:156,264-273) as local_attention / 2 + 1
+    aa.window = !local ? 0 : modernbert() ? cfg.sliding_window / 2 + 1 : cfg.sliding_window;
     double attn_ops = 0;
     for (int b = P.b0; b < P.b0 + P.nb; b++) {
       const double Lb = cu[b + 1] - cu[b];
@@ -847,15 +885,16 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     st = run_linear(ctx, L.o, ctxb + r0 * qd, qd, Mp, yp, H, ACT_NONE, nullptr, qap, ldqH, rsp,
                     needs_q(L.o) && !po, po ? &povp : nullptr);
     if (st) return st;
-    // x += [RMSNorm(attn, post_attn)]; normed = RMSNorm(x, pre-MLP norm)
-    RH_HIP(rms_to(r0, Mp, ps, y, gemma() ? L.post_attn : nullptr,
-                  gemma() ? L.pre_ffn : L.post_attn, L.gu, false));
+    // x += [RMSNorm(attn, post_attn)]; normed = norm(x, pre-MLP norm), or
+    // nomic's x = LayerNorm(x + attn, norm1) (nomic.go:226-227)
+    RH_HIP(norm_to(r0, Mp, ps, y, gemma() ? L.post_attn : nullptr,
+                   gemma() ? L.pre_ffn : L.post_attn, L.post_attn_b, L.gu, post));
     // gated MLP: one GEMM over gate|up writes act(gate) * up (as the down
     // projection's planes when it takes them), then down
     if (L.gu) {
       const Planes pg = at(plane(0, L.gu), r0), pd = at(plane(1, L.down), r0);
       const bool pdown = planes_in(L.down) && linear_on_planes(ctx, L.gu);
-      st = run_linear(ctx, L.gu, normedp, H, Mp, hidp, I, glu, nullptr, qap, ldqH, rsp, false,
+      st = run_linear(ctx, L.gu, mlp_in, H, Mp, hidp, I, glu, nullptr, qap, ldqH, rsp, false,
                       planes_in(L.gu) ? &pg : nullptr, pdown ? &pd : nullptr);
       if (st) return st;
       st = run_linear(ctx, L.down, hidp, I, Mp, yp, H, ACT_NONE, nullptr, qa2p, ldqI, rs2p,
@@ -864,10 +903,10 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
     } else {
       // gate and up in different modes: two GEMMs, the glue, then down
       float* hid2p = hid2 + r0 * I;
-      st = run_linear(ctx, L.gate, normedp, H, Mp, hidp, I, ACT_NONE, nullptr, qap, ldqH, rsp,
+      st = run_linear(ctx, L.gate, mlp_in, H, Mp, hidp, I, ACT_NONE, nullptr, qap, ldqH, rsp,
                       needs_q(L.gate));
       if (st) return st;
-      st = run_linear(ctx, L.up, normedp, H, Mp, hid2p, I, ACT_NONE, nullptr, qap, ldqH, rsp,
+      st = run_linear(ctx, L.up, mlp_in, H, Mp, hid2p, I, ACT_NONE, nullptr, qap, ldqH, rsp,
                       needs_q(L.up));
       if (st) return st;
       RH_HIP(launch_glu_rows(hidp, hid2p, hidp, (size_t)Mp * I, glu, ps));
@@ -876,11 +915,17 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
       if (st) return st;
     }
     // x += [RMSNorm(mlp, post_ffn)]; then the next layer's input norm, or the
-    // final RMSNorm in place (qwen3.go:543, gemma3.go:379)
+    // final norm in place (qwen3.go:543, gemma3.go:379, modernbert.go:307);
+    // nomic: x = LayerNorm(x + mlp, norm2), its last one the final norm
+    // (nomic.go:244-245)
     const bool last = li + 1 == dlayers.size();
-    RH_HIP(rms_to(r0, Mp, ps, y, gemma() ? L.post_ffn : nullptr,
-                  last ? final_norm : dlayers[li + 1].in_norm,
-                  last ? nullptr : dlayers[li + 1].qkv, last));
+    const rh_weight* next = last ? nullptr : dlayers[li + 1].qkv;
+    if (post) {
+      RH_HIP(norm_to(r0, Mp, ps, y, nullptr, L.post_ffn, L.post_ffn_b, next, true));
+    } else {
+      RH_HIP(norm_to(r0, Mp, ps, y, gemma() ? L.post_ffn : nullptr,
+                     last ? final_norm : dlayers[li + 1].in_norm, nullptr, next, last));
+    }
     return RH_OK;
   };
   // run_linear launches on ctx->stream: point it at each part's stream
@@ -1206,6 +1251,102 @@ static int finalize_decoder(rh_model* m) {
   return RH_OK;
 }
 
+// loadNomic (nomic.go:33-110) / loadModernBERT (modernbert.go:34-104): the
+// bias-free RoPE encoders, tensor names without a prefix. Each projection
+// goes through newDense on its own, as there: nomic's fc12 (silu-gated) and
+// fc11 form the gated pair (gate = fc12, up = fc11, nomic.go:232-242);
+// ModernBERT's Wi [2I][H] is one matrix whose halves are gate = Wi[:I] and
+// up = Wi[I:] (modernbert.go:292-301), so both halves take the one mode
+// newDense gives the whole matrix.
+static int finalize_renc(rh_model* m) {
+  const bool mb = m->modernbert();
+  const int H = m->cfg.hidden, I = m->cfg.intermediate, dh = m->dh();
+  const HostTensor *we, *tt = nullptr, *eg, *eb = nullptr, *fn = nullptr;
+  int st;
+  if (mb) {
+    if ((st = find_tensor(m, "", "embeddings.tok_embeddings.weight", {m->cfg.vocab, H}, &we)))
+      return st;
+    if ((st = find_tensor(m, "", "embeddings.norm.weight", {H}, &eg))) return st;
+    if ((st = find_tensor(m, "", "final_norm.weight", {H}, &fn))) return st;
+  } else {
+    if ((st = find_tensor(m, "", "embeddings.word_embeddings.weight", {m->cfg.vocab, H}, &we)))
+      return st;
+    if ((st = find_tensor(m, "", "embeddings.token_type_embeddings.weight", {2, H}, &tt)))
+      return st;
+    if ((st = find_tensor(m, "", "emb_ln.weight", {H}, &eg))) return st;
+    if ((st = find_tensor(m, "", "emb_ln.bias", {H}, &eb))) return st;
+  }
+  if ((st = upload(we->data.data(), we->data.size(), &m->word))) return st;
+  if ((st = upload(eg->data.data(), H, &m->emb_g))) return st;
+  if (eb && (st = upload(eb->data.data(), H, &m->emb_b))) return st;
+  if (tt && (st = upload(tt->data.data(), H, &m->type0))) return st;  // row 0
+  if (fn && (st = upload(fn->data.data(), H, &m->final_norm))) return st;
+  const int seq_cap = m->max_seq();
+  if ((st = upload_rope(seq_cap, dh, m->cfg.rope_theta, &m->cos_g, &m->sin_g))) return st;
+  if (mb && (st = upload_rope(seq_cap, dh, m->cfg.rope_local_theta, &m->cos_l, &m->sin_l)))
+    return st;
+  m->dlayers.resize(m->cfg.layers);
+  for (int l = 0; l < m->cfg.layers; l++) {
+    DecLayer& L = m->dlayers[l];
+    char buf[64];
+    if (mb) {
+      snprintf(buf, sizeof buf, "layers.%d.", l);
+      const std::string lp = buf;
+      const HostTensor *an = nullptr, *qkv, *wo, *mn, *wi, *wmo;
+      // layer 0's attention norm is an identity with no tensor (modernbert.go:74-81)
+      if (l != 0 && (st = find_tensor(m, "", lp + "attn_norm.weight", {H}, &an))) return st;
+      if ((st = find_tensor(m, "", lp + "attn.Wqkv.weight", {3 * H, H}, &qkv))) return st;
+      if ((st = find_tensor(m, "", lp + "attn.Wo.weight", {H, H}, &wo))) return st;
+      if ((st = find_tensor(m, "", lp + "mlp_norm.weight", {H}, &mn))) return st;
+      if ((st = find_tensor(m, "", lp + "mlp.Wi.weight", {2 * I, H}, &wi))) return st;
+      if ((st = find_tensor(m, "", lp + "mlp.Wo.weight", {H, I}, &wmo))) return st;
+      L.global = l % m->cfg.sliding_pattern == 0;  // modernbert.go:73
+      if ((st = new_dense(m, qkv->data.data(), nullptr, H, 3 * H, &L.qkv))) return st;
+      if ((st = new_dense(m, wo->data.data(), nullptr, H, H, &L.o))) return st;
+      const float* gate = wi->data.data();
+      const float* up = gate + (size_t)I * H;
+      const int mode = dense_mode(m, gate, H, 2 * I);
+      if (m->fuse_projections) {
+        if ((st = pack_weight_gated(m->ctx, mode, gate, up, H, I, &L.gu, true))) return st;
+      } else {
+        m->split_gu_any = true;
+        if ((st = pack_weight(m->ctx, mode, gate, nullptr, H, I, &L.gate, true))) return st;
+        if ((st = pack_weight(m->ctx, mode, up, nullptr, H, I, &L.up, true))) return st;
+      }
+      if ((st = new_dense(m, wmo->data.data(), nullptr, I, H, &L.down))) return st;
+      if (an && (st = upload(an->data.data(), H, &L.in_norm))) return st;
+      if ((st = upload(mn->data.data(), H, &L.post_attn))) return st;
+    } else {
+      snprintf(buf, sizeof buf, "encoder.layers.%d.", l);
+      const std::string lp = buf;
+      const HostTensor *qkv, *wo, *n1g, *n1b, *f11, *f12, *f2, *n2g, *n2b;
+      struct Need {
+        const char* name;
+        std::initializer_list<int64_t> shape;
+        const HostTensor** dst;
+      };
+      const Need needs[] = {
+          {"attn.Wqkv.weight", {3 * H, H}, &qkv}, {"attn.out_proj.weight", {H, H}, &wo},
+          {"norm1.weight", {H}, &n1g},           {"norm1.bias", {H}, &n1b},
+          {"mlp.fc11.weight", {I, H}, &f11},     {"mlp.fc12.weight", {I, H}, &f12},
+          {"mlp.fc2.weight", {H, I}, &f2},       {"norm2.weight", {H}, &n2g},
+          {"norm2.bias", {H}, &n2b},
+      };
+      for (const Need& n : needs)
+        if ((st = find_tensor(m, "", lp + n.name, n.shape, n.dst))) return st;
+      if ((st = new_dense(m, qkv->data.data(), nullptr, H, 3 * H, &L.qkv))) return st;
+      if ((st = new_dense(m, wo->data.data(), nullptr, H, H, &L.o))) return st;
+      if ((st = new_dense_gated(m, f12->data.data(), f11->data.data(), H, I, L))) return st;
+      if ((st = new_dense(m, f2->data.data(), nullptr, I, H, &L.down))) return st;
+      if ((st = upload(n1g->data.data(), H, &L.post_attn))) return st;
+      if ((st = upload(n1b->data.data(), H, &L.post_attn_b))) return st;
+      if ((st = upload(n2g->data.data(), H, &L.post_ffn))) return st;
+      if ((st = upload(n2b->data.data(), H, &L.post_ffn_b))) return st;
+    }
+  }
+  return RH_OK;
+}
+
 // ---- C ABI ------------------------------------------------------------------------
 
 #define MODEL_GUARD(m)                                                   \
@@ -1219,7 +1360,7 @@ extern "C" {
 int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_model** out) {
   return api_call([&]() -> int {
     if (!ctx || !cfg || !out) return fail(RH_ERR_INVALID, "null argument");
-    if (cfg->arch != RH_ARCH_BERT && cfg->arch != RH_ARCH_QWEN3 && cfg->arch != RH_ARCH_GEMMA3)
+    if (cfg->arch < RH_ARCH_BERT || cfg->arch > RH_ARCH_MODERNBERT)
       return fail(RH_ERR_INVALID, "unsupported arch");
     if (cfg->hidden <= 0 || cfg->heads <= 0) return fail(RH_ERR_INVALID, "bad hidden/heads");
     if (cfg->intermediate <= 0 || cfg->layers <= 0 || cfg->vocab <= 0 || cfg->max_position <= 0)
@@ -1235,6 +1376,24 @@ int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_m
       const int dh = cfg->hidden / cfg->heads;
       if (dh != 32 && dh != 64 && dh != 128)
         return fail(RH_ERR_INVALID, "head dim must be 32, 64 or 128");
+    } else if (cfg->arch == RH_ARCH_NOMIC || cfg->arch == RH_ARCH_MODERNBERT) {
+      // config.go:130-148,163-175
+      const int dh = cfg->head_dim > 0 ? cfg->head_dim : cfg->hidden / cfg->heads;
+      if (cfg->kv_heads != 0 && cfg->kv_heads != cfg->heads)
+        return fail(RH_ERR_INVALID, "nomic / ModernBERT attention has no kv head groups");
+      if (dh * cfg->heads != cfg->hidden)
+        return fail(RH_ERR_INVALID, "head_dim * heads must equal hidden");
+      if (dh != 32 && dh != 64 && dh != 128 && dh != 256)
+        return fail(RH_ERR_INVALID, "head dim must be 32, 64, 128 or 256");
+      if (cfg->intermediate % 16 != 0)
+        return fail(RH_ERR_INVALID, "intermediate must divide by 16");
+      if (cfg->rope_theta <= 0) return fail(RH_ERR_INVALID, "rope_theta must be positive");
+      if (cfg->arch == RH_ARCH_MODERNBERT &&
+          (cfg->rope_local_theta <= 0 || cfg->sliding_pattern < 1 || cfg->sliding_window < 2 ||
+           cfg->sliding_window % 2 != 0))
+        return fail(RH_ERR_INVALID,
+                    "ModernBERT needs local theta, global_attn_every_n_layers >= 1 and an even "
+                    "local_attention >= 2");
     } else {
       const int nkv = cfg->kv_heads > 0 ? cfg->kv_heads : cfg->heads;
       const int dh = cfg->head_dim > 0 ? cfg->head_dim : cfg->hidden / cfg->heads;
@@ -1330,7 +1489,9 @@ int rh_model_finalize(rh_model* m) {
     // object made so far, so the model is left empty rather than half built.
     int st;
     try {
-      st = m->decoder() ? finalize_decoder(m) : finalize_bert(m);
+      st = m->nomic() || m->modernbert() ? finalize_renc(m)
+           : m->rope_family()            ? finalize_decoder(m)
+                                         : finalize_bert(m);
     } catch (...) {
       m->release();
       throw;

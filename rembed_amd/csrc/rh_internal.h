@@ -318,17 +318,20 @@ struct AttnArgs {
 // precision: 1 = bf16 MFMA, 3 = three-term bf16 split (fp32-grade)
 hipError_t launch_attention(const AttnArgs& a, int precision, hipStream_t s);
 
-// ---- decoder-family row kernels (kernels_dec.hip) ---------------------------
+// ---- RoPE-family row kernels (kernels_dec.hip) ------------------------------
 // Token embeddings only (positions enter through RoPE): x[r] = word[id] * scale
-// (scale 1 for Qwen3, float32(sqrt(H)) for Gemma, gemma3.go:262-275); pos[r] =
-// the token's index in its text.
+// (+ add_row when given: nomic's segment-0 row, nomic.go:165-175) (scale 1 for
+// Qwen3, nomic and ModernBERT, float32(sqrt(H)) for Gemma, gemma3.go:262-275);
+// pos[r] = the token's index in its text.
 hipError_t launch_embed_gather(const int32_t* ids, int stride, const int32_t* cu,
-                               int batch, const float* word, int H, int vocab,
-                               float scale, float* x, int32_t* pos, int* err_flag,
+                               int batch, const float* word, const float* add_row, int H,
+                               int vocab, float scale, float* x, int32_t* pos, int* err_flag,
                                int total_rows, hipStream_t s);
-// Residual + RMSNorm sandwich per row (tensor.go:459-471):
+// Residual + norm sandwich per row (RMSNorm tensor.go:459-471, LayerNorm
+// tensor.go:430-452):
 //   y' = post_g ? RMSNorm(y, post_g) : y;  if (y) x += y';
-//   out = RMSNorm(x, pre_g) (out may alias x); optional u8 quantization of out.
+//   out = RMSNorm(x, pre_g), or LayerNorm(x, pre_g, ln_b) with layer_norm
+//   (out may alias x); optional u8 quantization of out.
 struct RmsArgs {
   float* x;              // [m][H] residual stream, updated in place when y
   const float* y;        // sublayer output to add, or null
@@ -343,10 +346,13 @@ struct RmsArgs {
   uint8_t* qa;           // QuantizeRowU8 of out [m][ldq], or null
   int ldq;
   float* row_scales;
+  int layer_norm;        // 0: RMSNorm (pre_g); 1: LayerNorm (pre_g, ln_b), post_g unused
+  const float* ln_b;     // LayerNorm beta, or null for a zero beta
 };
 hipError_t launch_rms_residual(const RmsArgs& a, hipStream_t s);
-// QK-norm (RMSNorm over each head's dh values) then rotate-half RoPE at the
-// row's position, in place on fused q|k rows (qwen3.go:484-516).
+// QK-norm (RMSNorm over each head's dh values; none when q_g and k_g are
+// null) then rotate-half RoPE at the row's position, in place on fused q|k
+// rows (qwen3.go:484-516; nomic.go:210-211, modernbert.go:256-257).
 hipError_t launch_qk_norm_rope(float* qkv, int ldqkv, int m, int nq, int nkv, int dh,
                                const float* q_g, const float* k_g, float eps,
                                const float* cos_t, const float* sin_t,

@@ -17,10 +17,12 @@ QUANT_NONE = _lib.RH_QUANT_NONE       # default fp32
 QUANT_WEIGHTS = _lib.RH_QUANT_WEIGHTS  # WithInt8 (rembed.go:67-69)
 QUANT_FULL = _lib.RH_QUANT_FULL        # WithInt8Activations (rembed.go:79-81)
 ARCH_BERT, ARCH_QWEN3, ARCH_GEMMA3 = _lib.RH_ARCH_BERT, _lib.RH_ARCH_QWEN3, _lib.RH_ARCH_GEMMA3
+ARCH_NOMIC, ARCH_MODERNBERT = _lib.RH_ARCH_NOMIC, _lib.RH_ARCH_MODERNBERT
 
 
 def make_config(shape):
-    """rh_model_config from a synthetic.BertShape or DecoderShape."""
+    """rh_model_config from a synthetic.BertShape, DecoderShape or
+    RopeEncoderShape."""
     c = _lib.ModelConfig()
     c.arch = getattr(shape, "arch", _lib.RH_ARCH_BERT)
     c.hidden = shape.hidden
@@ -35,6 +37,14 @@ def make_config(shape):
         c.max_position = shape.max_position
         c.position_offset = getattr(shape, "position_offset", 0)
         c.type_vocab = shape.type_vocab
+    elif c.arch in (_lib.RH_ARCH_NOMIC, _lib.RH_ARCH_MODERNBERT):  # config.go:44-53,163-175
+        c.max_position = shape.max_seq
+        c.head_dim = shape.head_dim
+        c.rope_theta = shape.rope_theta
+        c.rope_local_theta = shape.rope_local_theta
+        c.sliding_window = shape.local_attention
+        c.sliding_pattern = shape.global_every
+        c.type_vocab = 2 if c.arch == _lib.RH_ARCH_NOMIC else 0
     else:  # Qwen3 / Gemma3 (config.go:56-77)
         c.max_position = shape.max_seq
         c.kv_heads = shape.kv_heads

@@ -169,3 +169,98 @@ def decoder_tensors(shape: DecoderShape, seed: int = 0x5EED0001, bf16: bool = Fa
         t["2_Dense.linear.weight"] = normal(shape.dense_hidden, H)
         t["3_Dense.linear.weight"] = normal(H, shape.dense_hidden)
     return t
+
+
+# ---- bias-free RoPE encoders (nomic-embed, ModernBERT) ----------------------------
+
+ARCH_NOMIC, ARCH_MODERNBERT = 3, 4
+
+
+@dataclass(frozen=True)
+class RopeEncoderShape:
+    """Config of a nomic-embed / ModernBERT encoder (internal/model/config.go:44-53,
+    130-148,163-175); head_dim = hidden / heads."""
+    name: str
+    arch: int
+    layers: int
+    hidden: int
+    heads: int
+    intermediate: int
+    vocab: int
+    eps: float = 1e-12
+    rope_theta: float = 1000.0     # nomic RopeTheta / ModernBERT GlobalRopeTheta
+    rope_local_theta: float = 0.0  # ModernBERT LocalRopeTheta
+    local_attention: int = 0       # ModernBERT: local layers keep |i-j| <= local_attention/2
+    global_every: int = 1          # ModernBERT: layer l is global iff l % global_every == 0
+    pooling: int = 0               # 0 mean, 1 cls, 2 last token
+    normalize: int = 1
+    max_seq: int = 8192
+
+    @property
+    def head_dim(self):
+        return self.hidden // self.heads
+
+
+# nomic-embed-text-v1.5-shaped: 12 layers, hidden 768, 12 heads of 64, SwiGLU
+# 3072, RoPE base 1000, mean pooling.
+NOMIC_V15 = RopeEncoderShape("nomic-embed-text-v1.5", ARCH_NOMIC, 12, 768, 12, 3072, 30528,
+                             eps=1e-12, rope_theta=1000.0)
+# modernbert-embed-base-shaped: 22 layers, hidden 768, 12 heads of 64, GeGLU
+# 1152, every third layer global (theta 160000), the others local within ±64
+# tokens (theta 10000), mean pooling.
+MODERNBERT_BASE = RopeEncoderShape("modernbert-embed-base", ARCH_MODERNBERT, 22, 768, 12, 1152,
+                                   50368, eps=1e-5, rope_theta=160000.0,
+                                   rope_local_theta=10000.0, local_attention=128,
+                                   global_every=3)
+
+
+def rope_encoder_tensors(shape: RopeEncoderShape, seed: int = 0x5EED0001, std: float = 0.02):
+    """HF-named float32 tensors of a nomic-embed (internal/model/nomic.go:33-110)
+    or ModernBERT (internal/model/modernbert.go:34-104) encoder: projections
+    and embedding tables N(0, std), LayerNorm gammas 1 + N(0, std), nomic's
+    betas N(0, std); ModernBERT's layer 0 has no attention norm. (A larger
+    std on a small hidden size makes every sublayer move the output, for
+    tests that must see each one.)"""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    H, I = shape.hidden, shape.intermediate
+
+    def normal(*dims):
+        return rng.standard_normal(dims, dtype=np.float32) * np.float32(std)
+
+    def gamma(n):
+        return (np.float32(1.0) + normal(n)).astype(np.float32)
+
+    if shape.arch == ARCH_NOMIC:
+        t = {
+            "embeddings.word_embeddings.weight": normal(shape.vocab, H),
+            "embeddings.token_type_embeddings.weight": normal(2, H),
+            "emb_ln.weight": gamma(H),
+            "emb_ln.bias": normal(H),
+        }
+        for l in range(shape.layers):
+            p = f"encoder.layers.{l}."
+            t[p + "attn.Wqkv.weight"] = normal(3 * H, H)
+            t[p + "attn.out_proj.weight"] = normal(H, H)
+            t[p + "norm1.weight"] = gamma(H)
+            t[p + "norm1.bias"] = normal(H)
+            t[p + "mlp.fc11.weight"] = normal(I, H)
+            t[p + "mlp.fc12.weight"] = normal(I, H)
+            t[p + "mlp.fc2.weight"] = normal(H, I)
+            t[p + "norm2.weight"] = gamma(H)
+            t[p + "norm2.bias"] = normal(H)
+        return t
+    t = {
+        "embeddings.tok_embeddings.weight": normal(shape.vocab, H),
+        "embeddings.norm.weight": gamma(H),
+        "final_norm.weight": gamma(H),
+    }
+    for l in range(shape.layers):
+        p = f"layers.{l}."
+        if l:
+            t[p + "attn_norm.weight"] = gamma(H)
+        t[p + "attn.Wqkv.weight"] = normal(3 * H, H)
+        t[p + "attn.Wo.weight"] = normal(H, H)
+        t[p + "mlp_norm.weight"] = gamma(H)
+        t[p + "mlp.Wi.weight"] = normal(2 * I, H)
+        t[p + "mlp.Wo.weight"] = normal(H, I)
+    return t
