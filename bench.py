@@ -50,6 +50,13 @@ WORKLOADS = {
                       "256, GeGLU 1152, alternating window-512 / global), weight-only int8, "
                       "16 x 2048, mean pooling + Dense 768-3072-768", "weights", 16, 2048, 2048,
                       2048, 0),
+    "nomic-v1.5-int8": ("nomic-embed-text-v1.5-shaped post-LN encoder (12 layers, 768, 12 heads of "
+                        "64, RoPE, SwiGLU 3072), full int8, 64 texts, lengths U[64,256] padded to "
+                        "256, mean pooling + L2", "full", 64, 256, 64, 256, 1000),
+    "modernbert-base-w8": ("modernbert-embed-base-shaped pre-LN encoder (22 layers, 768, 12 heads "
+                           "of 64, GeGLU 1152, every third layer global, the rest within +-64 "
+                           "tokens), weight-only int8, 32 texts, lengths U[256,512] padded to 512, "
+                           "mean pooling + L2", "weights", 32, 512, 256, 512, 1000),
 }
 QUANTS = {"none": 0, "weights": 1, "full": 2}
 
@@ -94,6 +101,17 @@ def pct(x, q):
     return float(np.percentile(np.asarray(x, np.float64), q))
 
 
+def oracle_for(shape, tensors, quant):
+    """The oracle model of a synthetic shape's architecture."""
+    from oracle import oracle as O
+    from rembed_amd import synthetic as S
+    if isinstance(shape, S.RopeEncoderShape):
+        return O.RopeEncoderOracle(shape, tensors, quant)
+    if isinstance(shape, S.DecoderShape):
+        return O.DecoderOracle(shape, tensors, quant)
+    return O.BertOracle(shape, tensors, quant)
+
+
 def cpu_baseline(shape, tensors, ids, lens, quant, max_len=None):
     """The reference algorithm restated in C (the oracle) on the host cores,
     with the reference's batch policy (rembed.go:309-330): one serial
@@ -106,10 +124,9 @@ def cpu_baseline(shape, tensors, ids, lens, quant, max_len=None):
     28-layer 512-token text takes ~30 s on one core)."""
     from oracle import oracle as O
     cores = os.cpu_count() or 1
-    dec = hasattr(shape, "arch")
     if max_len:
         lens = np.minimum(lens, max_len)
-    orc = O.DecoderOracle(shape, tensors, quant) if dec else O.BertOracle(shape, tensors, quant)
+    orc = oracle_for(shape, tensors, quant)
     O.lib.or_set_gemm_impl(1 if quant == 2 else 0)
     try:
         orc.embed_batch(ids[:1], np.minimum(lens[:1], 32), threads=1)  # warm-up
@@ -215,6 +232,10 @@ def make_workload(name):
     if name.startswith("qwen3"):
         shape = S.QWEN3_0_6B
         return shape, S.decoder_tensors(shape, seed=0x5EED0001, bf16=True)
+    if name.startswith("nomic"):
+        return S.NOMIC_V15, S.rope_encoder_tensors(S.NOMIC_V15, seed=0x5EED0001)
+    if name.startswith("modernbert"):
+        return S.MODERNBERT_BASE, S.rope_encoder_tensors(S.MODERNBERT_BASE, seed=0x5EED0001)
     import dataclasses
     shape = dataclasses.replace(S.GEMMA3_300M, sliding_window=512, sliding_pattern=2,
                                 max_seq=2048)
@@ -370,11 +391,12 @@ def main():
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gemm_i8_traffic.json")
-    if quant == 2 and os.path.exists(tpath):
+    if args.workload == "bert-base-int8" and os.path.exists(tpath):  # measured on this workload
         traffic = json.load(open(tpath)).get("bytes_per_launch")
 
     u8diff = None
-    if quant == 2 and not (args.no_cpu_baseline or args.no_u8_diff or args.forwards_only):
+    bert = "embeddings.position_embeddings.weight" in tensors  # the BERT oracle's layer stops
+    if quant == 2 and bert and not (args.no_cpu_baseline or args.no_u8_diff or args.forwards_only):
         log("comparing u8 activations with the oracle, layer by layer")
         u8diff = u8_byte_diffs(ctx, shape, tensors, ids, lens)
         u8diff["oracle_vs_oracle_1ulp_embeddings"] = oracle_u8_sensitivity(
@@ -386,7 +408,8 @@ def main():
     baseline = None
     if not (args.no_cpu_baseline or args.forwards_only):
         log("timing the CPU baseline")
-        trunc = {"qwen3-0.6b-w8": 48, "gemma-300m-w8": 64}.get(args.workload)
+        trunc = {"qwen3-0.6b-w8": 48, "gemma-300m-w8": 64, "modernbert-base-w8": 160}.get(
+            args.workload)
         baseline = cpu_baseline(shape, tensors, ids, lens, quant, max_len=trunc)
         log(f"cpu baseline {baseline['value']:,.1f} tokens/s")
 
