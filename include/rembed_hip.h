@@ -378,6 +378,34 @@ int rh_model_embed_device(rh_model *m, const int32_t *ids_dev,
  * previous rh_model_embed_device calls. */
 int rh_model_check(rh_model *m);
 
+/* ---- tokenizer (host side: text -> the int64 ids rh_model_embed takes) ---- */
+typedef struct rh_tokenizer rh_tokenizer;
+/* tokenizer.New (tokenizer/tokenizer.go:39-72): a BERT WordPiece vocab, one
+ * token per line, id = line number (a later duplicate line wins).
+ * lower_case selects lowercasing + NFD accent stripping. cls_tok / sep_tok /
+ * unk_tok name the framing tokens; NULL or "" selects "[CLS]" / "[SEP]" /
+ * "[UNK]". RH_ERR_MISSING when one of them is not in the vocab,
+ * RH_ERR_INVALID when the file cannot be read. */
+int rh_tokenizer_wordpiece_load(const char *vocab_path, int lower_case, const char *cls_tok,
+                                const char *sep_tok, const char *unk_tok, rh_tokenizer **out);
+/* VocabSize (tokenizer.go:75): distinct vocab entries. */
+int64_t rh_tokenizer_vocab_size(const rh_tokenizer *t);
+/* Encode (tokenizer.go:198-216): the ids of one UTF-8 text (text_len bytes,
+ * invalid sequences dropped), [CLS] ... [SEP], at most max_len ids (max_len
+ * below 2 counts as 2). *n receives the count; RH_ERR_SHAPE when it exceeds
+ * capacity (nothing written). The attention mask of the reference is all
+ * ones over the n ids. */
+int rh_tokenizer_encode(const rh_tokenizer *t, const char *text, size_t text_len, int max_len,
+                        int64_t *ids, int capacity, int *n);
+/* Encode over a batch, in the layout rh_model_embed takes: ids is
+ * [batch][max(max_len, 2)], each row padded with pad_id after its lens[b]
+ * ids. No reference counterpart as one call (Embed encodes text by text,
+ * rembed.go:287-332). */
+int rh_tokenizer_encode_batch(const rh_tokenizer *t, const char *const *texts,
+                              const size_t *text_lens, int batch, int max_len, int64_t pad_id,
+                              int64_t *ids, int32_t *lens);
+void rh_tokenizer_destroy(rh_tokenizer *t);
+
 #ifdef __cplusplus
 }
 #endif

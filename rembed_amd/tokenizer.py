@@ -1,0 +1,63 @@
+"""Python mirror of rembed's BERT WordPiece tokenizer over the C ABI.
+
+WordPieceTokenizer follows tokenizer.New / Encode / VocabSize
+(tokenizer/tokenizer.go:39-216): the tokenization itself runs in the library
+(rh_tokenizer_*); this class only marshals text and ids.
+"""
+import ctypes
+
+import numpy as np
+
+from ._lib import check, lib
+
+MAX_SEQ_LEN = 512  # tokenizer.MaxSeqLen (tokenizer/tokenizer.go:19)
+
+
+class WordPieceTokenizer:
+    """A BERT WordPiece vocab (one token per line, id = line number)."""
+
+    def __init__(self, vocab_path, lower_case=True, cls_tok="", sep_tok="", unk_tok=""):
+        h = ctypes.c_void_p()
+        check(lib.rh_tokenizer_wordpiece_load(str(vocab_path).encode(), int(bool(lower_case)),
+                                              cls_tok.encode(), sep_tok.encode(),
+                                              unk_tok.encode(), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib.rh_tokenizer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def vocab_size(self):
+        return int(lib.rh_tokenizer_vocab_size(self.h))
+
+    def encode(self, text, max_len=MAX_SEQ_LEN):
+        """(ids, mask) of one text as int64 lists: [CLS] pieces [SEP], at most
+        max_len ids, mask all ones (Encode, tokenizer.go:198-216)."""
+        raw = text.encode("utf-8", "surrogatepass") if isinstance(text, str) else bytes(text)
+        cap = max(int(max_len), 2)
+        ids = np.empty(cap, np.int64)
+        n = ctypes.c_int()
+        check(lib.rh_tokenizer_encode(self.h, raw, len(raw), int(max_len), ids.ctypes.data, cap,
+                                      ctypes.byref(n)))
+        out = ids[:n.value].tolist()
+        return out, [1] * len(out)
+
+    def encode_batch(self, texts, max_len=MAX_SEQ_LEN, pad_id=0):
+        """Padded int64 ids [batch][max(max_len, 2)] and int32 lengths: the
+        inputs of Model.embed."""
+        raws = [t.encode("utf-8", "surrogatepass") if isinstance(t, str) else bytes(t)
+                for t in texts]
+        stride = max(int(max_len), 2)
+        ids = np.empty((len(raws), stride), np.int64)
+        lens = np.empty(len(raws), np.int32)
+        bufs = (ctypes.c_char_p * max(1, len(raws)))(*raws)
+        sizes = (ctypes.c_size_t * max(1, len(raws)))(*[len(r) for r in raws])
+        check(lib.rh_tokenizer_encode_batch(self.h, ctypes.cast(bufs, ctypes.c_void_p),
+                                            ctypes.cast(sizes, ctypes.c_void_p), len(raws),
+                                            int(max_len), int(pad_id), ids.ctypes.data,
+                                            lens.ctypes.data))
+        return ids, lens
