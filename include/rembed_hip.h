@@ -388,13 +388,30 @@ typedef struct rh_tokenizer rh_tokenizer;
  * RH_ERR_INVALID when the file cannot be read. */
 int rh_tokenizer_wordpiece_load(const char *vocab_path, int lower_case, const char *cls_tok,
                                 const char *sep_tok, const char *unk_tok, rh_tokenizer **out);
-/* VocabSize (tokenizer.go:75): distinct vocab entries. */
+/* Byte-level BPE, bpe.New (tokenizer/bpe/bpe.go:104-157): RoBERTa / GPT-2's
+ * vocab.json + merges.txt, GPT-2 pre-tokenizer, cls ... sep framing (the
+ * three tokens must be in the vocab). RH_ERR_INVALID for an unreadable or
+ * malformed file or a missing framing token. */
+int rh_tokenizer_bpe_load(const char *vocab_json, const char *merges_txt, const char *cls_tok,
+                          const char *sep_tok, const char *unk_tok, rh_tokenizer **out);
+/* Byte-level BPE from a HuggingFace tokenizer.json: with qwen = 0,
+ * NewFromTokenizerJSON (bpe.go:282-303, ModernBERT: NFC when declared, the
+ * added tokens matched leftmost-longest before BPE with their lstrip /
+ * rstrip whitespace rules, GPT-2 pre-tokenizer, cls ... sep); with
+ * qwen = 1, NewQwenFromTokenizerJSON (bpe.go:305-324, Qwen3: the Qwen
+ * pre-tokenizer and only a trailing eos, sep_tok; cls_tok and unk_tok may
+ * be NULL). */
+int rh_tokenizer_bpe_load_json(const char *tokenizer_json, int qwen, const char *cls_tok,
+                               const char *sep_tok, const char *unk_tok, rh_tokenizer **out);
+/* VocabSize (tokenizer.go:75, bpe.go:327): distinct vocab entries. */
 int64_t rh_tokenizer_vocab_size(const rh_tokenizer *t);
-/* Encode (tokenizer.go:198-216): the ids of one UTF-8 text (text_len bytes,
- * invalid sequences dropped), [CLS] ... [SEP], at most max_len ids (max_len
- * below 2 counts as 2). *n receives the count; RH_ERR_SHAPE when it exceeds
- * capacity (nothing written). The attention mask of the reference is all
- * ones over the n ids. */
+/* Encode (tokenizer.go:198-216, bpe.go:648-742): the ids of one UTF-8 text
+ * (text_len bytes), framed, at most max_len ids. WordPiece drops invalid
+ * UTF-8 and counts a max_len below 2 as 2; BPE reads invalid bytes as
+ * U+FFFD and keeps its framing (cls and sep, or Qwen's eos) whatever
+ * max_len. *n receives the count; RH_ERR_SHAPE when it exceeds capacity
+ * (nothing written). The attention mask of the reference is all ones over
+ * the n ids. */
 int rh_tokenizer_encode(const rh_tokenizer *t, const char *text, size_t text_len, int max_len,
                         int64_t *ids, int capacity, int *n);
 /* Encode over a batch, in the layout rh_model_embed takes: ids is

@@ -1,5 +1,6 @@
-// tokenizer.cpp — BERT WordPiece tokenization on the host, behind the C ABI
-// (rh_tokenizer_*): text in, the int64 ids rh_model_embed takes out.
+// tokenizer.cpp — BERT WordPiece tokenization on the host, and the C ABI of
+// every tokenizer kind (rh_tokenizer_*): text in, the int64 ids
+// rh_model_embed takes out. The byte-level BPE kind is in tokenizer_bpe.cpp.
 //
 // Mirrors tokenizer.New / Encode (tokenizer/tokenizer.go:39-216): a vocab of
 // one token per line (id = line number), HF BasicTokenizer cleaning and
@@ -19,72 +20,15 @@
 #include <vector>
 
 #include "rh_internal.h"
+#include "tokenizer_text.h"
 
 using namespace rh;
+using namespace rh::text;
 
 namespace {
 
-constexpr int kMaxWordChars = 100;      // max_input_chars_per_word (tokenizer.go:24)
+constexpr int kMaxWordChars = 100;         // max_input_chars_per_word (tokenizer.go:24)
 constexpr size_t kMaxLineBytes = 1 << 20;  // the vocab scanner's line limit (tokenizer.go:56)
-constexpr char32_t kReplacement = 0xFFFD;
-
-// One rune of a UTF-8 string the way Go's `for _, r := range s` decodes it:
-// an invalid or truncated sequence, an overlong form, a surrogate or a value
-// past U+10FFFF yields U+FFFD and consumes one byte.
-char32_t decode_rune(const unsigned char* s, size_t n, size_t* len) {
-  const unsigned char c = s[0];
-  *len = 1;
-  if (c < 0x80) return c;
-  int need;
-  char32_t r, lo;
-  if (c >= 0xC2 && c <= 0xDF) {
-    need = 1, r = c & 0x1F, lo = 0x80;
-  } else if (c >= 0xE0 && c <= 0xEF) {
-    need = 2, r = c & 0x0F, lo = 0x800;
-  } else if (c >= 0xF0 && c <= 0xF4) {
-    need = 3, r = c & 0x07, lo = 0x10000;
-  } else {
-    return kReplacement;
-  }
-  if ((size_t)need >= n) return kReplacement;
-  for (int i = 1; i <= need; i++) {
-    if ((s[i] & 0xC0) != 0x80) return kReplacement;
-    r = (r << 6) | (s[i] & 0x3F);
-  }
-  if (r < lo || r > 0x10FFFF || (r >= 0xD800 && r <= 0xDFFF)) return kReplacement;
-  *len = need + 1;
-  return r;
-}
-
-std::vector<char32_t> decode(const char* text, size_t n) {
-  std::vector<char32_t> out;
-  out.reserve(n);
-  const auto* s = reinterpret_cast<const unsigned char*>(text);
-  for (size_t i = 0; i < n;) {
-    size_t len;
-    out.push_back(decode_rune(s + i, n - i, &len));
-    i += len;
-  }
-  return out;
-}
-
-void append_utf8(std::string& out, char32_t r) {
-  if (r < 0x80) {
-    out.push_back((char)r);
-  } else if (r < 0x800) {
-    out.push_back((char)(0xC0 | (r >> 6)));
-    out.push_back((char)(0x80 | (r & 0x3F)));
-  } else if (r < 0x10000) {
-    out.push_back((char)(0xE0 | (r >> 12)));
-    out.push_back((char)(0x80 | ((r >> 6) & 0x3F)));
-    out.push_back((char)(0x80 | (r & 0x3F)));
-  } else {
-    out.push_back((char)(0xF0 | (r >> 18)));
-    out.push_back((char)(0x80 | ((r >> 12) & 0x3F)));
-    out.push_back((char)(0x80 | ((r >> 6) & 0x3F)));
-    out.push_back((char)(0x80 | (r & 0x3F)));
-  }
-}
 
 // isBertPunct (tokenizer.go:81-86): the four ASCII symbol ranges, else
 // Unicode category P.
@@ -103,15 +47,6 @@ bool is_cjk(char32_t r) {
          (r >= 0xF900 && r <= 0xFAFF) || (r >= 0x2F800 && r <= 0x2FA1F);
 }
 
-// Go's unicode.IsSpace: the Latin-1 set '\t' '\n' '\v' '\f' '\r' ' ' U+0085
-// U+00A0, else the White_Space property.
-bool is_space(char32_t r) {
-  if (r <= 0xFF)
-    return r == '\t' || r == '\n' || r == '\v' || r == '\f' || r == '\r' || r == ' ' ||
-           r == 0x85 || r == 0xA0;
-  return u_hasBinaryProperty((UChar32)r, UCHAR_WHITE_SPACE);
-}
-
 // Cc, Cf, Co, Cs: the category-C characters the cleaning step deletes (Cn,
 // unassigned, is kept; tokenizer.go:136-151).
 bool is_deleted_control(char32_t r) {
@@ -120,9 +55,7 @@ bool is_deleted_control(char32_t r) {
          t == U_SURROGATE;
 }
 
-}  // namespace
-
-struct rh_tokenizer {
+struct WordPiece final : rh_tokenizer {
   std::unordered_map<std::string, int64_t> vocab;
   bool lower = true;
   int64_t cls = 0, sep = 0, unk = 0;
@@ -213,8 +146,11 @@ struct rh_tokenizer {
     out.insert(out.end(), ids.begin(), ids.end());
   }
 
+  int64_t vocab_size() const override { return (int64_t)vocab.size(); }
+
   // Encode (tokenizer.go:198-216): [CLS] pieces [SEP], at most max_len ids.
-  void encode(const char* text, size_t n, int max_len, std::vector<int64_t>& ids) const {
+  void encode(const char* text, size_t n, int max_len,
+              std::vector<int64_t>& ids) const override {
     if (max_len < 2) max_len = 2;
     ids.clear();
     ids.push_back(cls);
@@ -236,6 +172,8 @@ struct rh_tokenizer {
   }
 };
 
+}  // namespace
+
 extern "C" {
 
 int rh_tokenizer_wordpiece_load(const char* vocab_path, int lower_case, const char* cls_tok,
@@ -255,7 +193,7 @@ int rh_tokenizer_wordpiece_load(const char* vocab_path, int lower_case, const ch
     const bool read_err = ferror(f) != 0;
     fclose(f);
     if (read_err) return fail(RH_ERR_INVALID, std::string("cannot read vocab ") + vocab_path);
-    std::unique_ptr<rh_tokenizer> t(new rh_tokenizer());
+    std::unique_ptr<WordPiece> t(new WordPiece());
     t->lower = lower_case != 0;
     // bufio.ScanLines: lines end at '\n', a trailing '\r' is dropped, a last
     // line without '\n' counts, an empty remainder after the last '\n' does
@@ -282,9 +220,7 @@ int rh_tokenizer_wordpiece_load(const char* vocab_path, int lower_case, const ch
   });
 }
 
-int64_t rh_tokenizer_vocab_size(const rh_tokenizer* t) {
-  return t ? (int64_t)t->vocab.size() : 0;
-}
+int64_t rh_tokenizer_vocab_size(const rh_tokenizer* t) { return t ? t->vocab_size() : 0; }
 
 int rh_tokenizer_encode(const rh_tokenizer* t, const char* text, size_t text_len, int max_len,
                         int64_t* ids, int capacity, int* n) {
@@ -310,7 +246,8 @@ int rh_tokenizer_encode_batch(const rh_tokenizer* t, const char* const* texts,
     std::vector<int64_t> v;
     for (int b = 0; b < batch; b++) {
       if (!texts[b] && text_lens[b]) return fail(RH_ERR_INVALID, "null text");
-      t->encode(texts[b] ? texts[b] : "", text_lens[b], stride, v);
+      t->encode(texts[b] ? texts[b] : "", text_lens[b], max_len, v);
+      if (v.size() > (size_t)stride) return fail(RH_ERR_INVALID, "encoded row exceeds max_len");
       int64_t* row = ids + (size_t)b * stride;
       memcpy(row, v.data(), v.size() * sizeof(int64_t));
       for (size_t i = v.size(); i < (size_t)stride; i++) row[i] = pad_id;
