@@ -403,13 +403,29 @@ int rh_tokenizer_bpe_load(const char *vocab_json, const char *merges_txt, const 
  * be NULL). */
 int rh_tokenizer_bpe_load_json(const char *tokenizer_json, int qwen, const char *cls_tok,
                                const char *sep_tok, const char *unk_tok, rh_tokenizer **out);
-/* VocabSize (tokenizer.go:75, bpe.go:327): distinct vocab entries. */
+/* SentencePiece Unigram, sentencepiece.New (tokenizer/sentencepiece/
+ * sentencepiece.go:47-103): an XLM-R-family sentencepiece.bpe.model (NMT-NFKC
+ * charsmap normalizer, Viterbi over the normal pieces), ids in HF's fairseq
+ * space (<s> 0, </s> 2, <unk> 3, pieces shifted by one). RH_ERR_INVALID for
+ * an unreadable or malformed model or one with USER_DEFINED / UNUSED / BYTE
+ * pieces. */
+int rh_tokenizer_sentencepiece_load(const char *model_path, rh_tokenizer **out);
+/* Normalize (sentencepiece.go:244), exposed for tests as the reference
+ * exposes it: the NMT-NFKC text (U+2581 for spaces) of a SentencePiece
+ * tokenizer, *n bytes into out; RH_ERR_SHAPE when capacity is short. */
+int rh_tokenizer_sentencepiece_normalize(const rh_tokenizer *t, const char *text,
+                                         size_t text_len, char *out, size_t capacity,
+                                         size_t *n);
+/* Gemma, gemma.New (tokenizer/gemma/gemma.go:58-111): a tokenizer.json with
+ * a byte-fallback BPE ("<0xNN>" pieces), space -> U+2581, <bos> ... <eos>. */
+int rh_tokenizer_gemma_load(const char *tokenizer_json, rh_tokenizer **out);
+/* VocabSize (tokenizer.go:75, bpe.go:327, sentencepiece.go:109, gemma.go:114). */
 int64_t rh_tokenizer_vocab_size(const rh_tokenizer *t);
-/* Encode (tokenizer.go:198-216, bpe.go:648-742): the ids of one UTF-8 text
- * (text_len bytes), framed, at most max_len ids. WordPiece drops invalid
- * UTF-8 and counts a max_len below 2 as 2; BPE reads invalid bytes as
- * U+FFFD and keeps its framing (cls and sep, or Qwen's eos) whatever
- * max_len. *n receives the count; RH_ERR_SHAPE when it exceeds capacity
+/* Encode (tokenizer.go:198-216, bpe.go:648-742, sentencepiece.go:205-241,
+ * gemma.go:235-254): the ids of one UTF-8 text (text_len bytes), framed, at
+ * most max_len ids. WordPiece drops invalid UTF-8 and counts a max_len below
+ * 2 as 2; the others read invalid bytes as U+FFFD and keep their framing
+ * (two ids, or Qwen's eos alone) whatever max_len. *n receives the count; RH_ERR_SHAPE when it exceeds capacity
  * (nothing written). The attention mask of the reference is all ones over
  * the n ids. */
 int rh_tokenizer_encode(const rh_tokenizer *t, const char *text, size_t text_len, int max_len,

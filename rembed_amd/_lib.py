@@ -54,6 +54,8 @@ EXPORTS = [
     "rh_model_quantized", "rh_model_quantized_activations", "rh_model_embed",
     "rh_model_embed_tokens", "rh_model_embed_device", "rh_model_check",
     "rh_tokenizer_wordpiece_load", "rh_tokenizer_bpe_load", "rh_tokenizer_bpe_load_json",
+    "rh_tokenizer_sentencepiece_load", "rh_tokenizer_sentencepiece_normalize",
+    "rh_tokenizer_gemma_load",
     "rh_tokenizer_vocab_size", "rh_tokenizer_encode",
     "rh_tokenizer_encode_batch", "rh_tokenizer_destroy",
 ]
@@ -150,6 +152,10 @@ def _load():
         "rh_tokenizer_bpe_load_json": (I, [ctypes.c_char_p, I, ctypes.c_char_p,
                                            ctypes.c_char_p, ctypes.c_char_p,
                                            ctypes.POINTER(P)]),
+        "rh_tokenizer_sentencepiece_load": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "rh_tokenizer_gemma_load": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "rh_tokenizer_sentencepiece_normalize": (I, [P, ctypes.c_char_p, S, P, S,
+                                                     ctypes.POINTER(S)]),
         "rh_tokenizer_vocab_size": (ctypes.c_int64, [P]),
         "rh_tokenizer_encode": (I, [P, ctypes.c_char_p, S, I, P, I, ctypes.POINTER(I)]),
         "rh_tokenizer_encode_batch": (I, [P, P, P, I, I, ctypes.c_int64, P, P]),

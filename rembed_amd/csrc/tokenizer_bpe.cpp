@@ -1,5 +1,6 @@
 // tokenizer_bpe.cpp — byte-level BPE tokenization on the host (RoBERTa /
-// GPT-2, ModernBERT, Qwen3), behind rh_tokenizer_bpe_load*.
+// GPT-2, ModernBERT, Qwen3), behind rh_tokenizer_bpe_load*, and Gemma's
+// byte-fallback BPE behind rh_tokenizer_gemma_load.
 //
 // Mirrors tokenizer/bpe/bpe.go: text (NFC-normalized when the
 // tokenizer.json declares it) is matched for added tokens leftmost-longest
@@ -660,6 +661,96 @@ std::unique_ptr<Bpe> parse_tokenizer_json(const char* path) {
   return t;
 }
 
+// ---- Gemma: SentencePiece-style BPE with byte fallback (tokenizer/gemma) -----------
+// The ASCII space becomes U+2581 and nothing else is normalized; BPE runs
+// over the whole normalized string; a rune absent from the vocab enters as
+// its UTF-8 bytes, each the "<0xNN>" piece; <bos> ... <eos> framing with
+// the pieces truncated to max_len - 2 (gemma.go:146-254).
+struct GemmaBpe final : rh_tokenizer {
+  std::unordered_map<std::string, int64_t> vocab;
+  std::unordered_map<std::string, int> ranks;  // first occurrence of a pair wins
+  int64_t bos = -1, eos = -1, unk = -1;
+
+  int64_t vocab_size() const override { return (int64_t)vocab.size(); }
+
+  void encode(const char* text, size_t n, int max_len,
+              std::vector<int64_t>& ids) const override {
+    // strings.ReplaceAll(text, " ", "\u2581") on the raw bytes, then the
+    // runes of the result (invalid bytes read as U+FFFD)
+    std::string norm;
+    norm.reserve(n + 16);
+    for (size_t i = 0; i < n; i++) {
+      if (text[i] == ' ') norm += "\xE2\x96\x81";
+      else norm.push_back(text[i]);
+    }
+    std::vector<std::string> syms;
+    const std::vector<char32_t> rs = decode(norm.data(), norm.size());
+    for (char32_t r : rs) {
+      std::string s;
+      append_utf8(s, r);
+      if (vocab.count(s)) {
+        syms.push_back(std::move(s));
+        continue;
+      }
+      for (unsigned char b : s) {
+        char piece[8];
+        snprintf(piece, sizeof piece, "<0x%02X>", b);
+        syms.push_back(piece);
+      }
+    }
+    std::vector<int64_t> pieces;
+    const int m = (int)syms.size();
+    if (m > 0) {
+      std::vector<int> next(m), prev(m);
+      std::vector<char> alive(m, 1);
+      for (int i = 0; i < m; i++) {
+        next[i] = i + 1;
+        prev[i] = i - 1;
+      }
+      next[m - 1] = -1;
+      struct Cand {
+        int rank, pos;
+        std::string left, right;
+        bool operator>(const Cand& o) const {
+          return rank != o.rank ? rank > o.rank : pos > o.pos;
+        }
+      };
+      std::priority_queue<Cand, std::vector<Cand>, std::greater<Cand>> heap;
+      auto push = [&](int left) {
+        if (left < 0) return;
+        const int right = next[left];
+        if (right < 0) return;
+        auto it = ranks.find(Bpe::pair_key(syms[left], syms[right]));
+        if (it != ranks.end()) heap.push(Cand{it->second, left, syms[left], syms[right]});
+      };
+      for (int i = 0; i < m; i++) push(i);
+      while (!heap.empty()) {
+        Cand c = heap.top();
+        heap.pop();
+        const int i = c.pos, j = next[i];
+        if (!alive[i] || j < 0 || syms[i] != c.left || syms[j] != c.right) continue;
+        syms[i] = c.left + c.right;
+        alive[j] = 0;
+        next[i] = next[j];
+        if (next[j] >= 0) prev[next[j]] = i;
+        push(prev[i]);
+        push(i);
+      }
+      for (int i = 0; i >= 0; i = next[i]) {
+        if (!alive[i]) continue;
+        auto it = vocab.find(syms[i]);
+        pieces.push_back(it == vocab.end() ? unk : it->second);
+      }
+    }
+    const size_t budget = (size_t)std::max(max_len - 2, 0);
+    if (pieces.size() > budget) pieces.resize(budget);
+    ids.clear();
+    ids.push_back(bos);
+    ids.insert(ids.end(), pieces.begin(), pieces.end());
+    ids.push_back(eos);
+  }
+};
+
 }  // namespace
 
 extern "C" {
@@ -732,6 +823,62 @@ int rh_tokenizer_bpe_load_json(const char* tokenizer_json, int qwen, const char*
         t->sep = t->lookup(sep_tok, "sep");
         t->unk = t->lookup(unk_tok, "unk");
       }
+      *out = t.release();
+      return RH_OK;
+    } catch (const std::invalid_argument& e) {
+      return fail(RH_ERR_INVALID, e.what());
+    }
+  });
+}
+
+// gemma.New (tokenizer/gemma/gemma.go:58-111): model.vocab, model.merges as
+// [[a, b]] pairs, byte_fallback required with every "<0xNN>" piece present,
+// and <bos> / <eos> / <unk> from added_tokens.
+int rh_tokenizer_gemma_load(const char* tokenizer_json, rh_tokenizer** out) {
+  return api_call([&]() -> int {
+    if (!tokenizer_json || !out) return fail(RH_ERR_INVALID, "null argument");
+    *out = nullptr;
+    try {
+      const Json j = parse_json_file(tokenizer_json);
+      const Json* model = j.get("model");
+      const Json* vocab = model ? model->get("vocab") : nullptr;
+      if (!vocab || vocab->kind != Json::Object || vocab->obj.empty())
+        return fail(RH_ERR_INVALID, "gemma: empty vocab");
+      const Json* bf = model->get("byte_fallback");
+      if (!bf || bf->kind != Json::Bool || !bf->b)
+        return fail(RH_ERR_INVALID, "gemma: byte_fallback is false (required)");
+      std::unique_ptr<GemmaBpe> t(new GemmaBpe());
+      for (const auto& kv : vocab->obj) t->vocab[kv.first] = json_int(kv.second, "a vocab id");
+      const Json* merges = model->get("merges");
+      if (merges && merges->kind == Json::Array) {
+        int rank = 0;
+        for (const Json& m : merges->arr) {
+          if (m.kind != Json::Array || m.arr.size() != 2 || m.arr[0].kind != Json::String ||
+              m.arr[1].kind != Json::String)
+            return fail(RH_ERR_INVALID, "gemma: a merge is not a pair");
+          t->ranks.emplace(Bpe::pair_key(m.arr[0].str, m.arr[1].str), rank++);
+        }
+      } else if (merges && merges->kind != Json::Null) {
+        return fail(RH_ERR_INVALID, "gemma: merges is not a list of pairs");
+      }
+      for (int b = 0; b < 256; b++) {
+        char piece[8];
+        snprintf(piece, sizeof piece, "<0x%02X>", b);
+        if (!t->vocab.count(piece))
+          return fail(RH_ERR_INVALID, std::string("gemma: byte fallback piece ") + piece +
+                                          " missing from the vocab");
+      }
+      if (const Json* at = j.get("added_tokens"))
+        for (const Json& a : at->arr) {
+          const Json* c = a.get("content");
+          const Json* id = a.get("id");
+          if (!c || c->kind != Json::String || !id) continue;
+          if (c->str == "<bos>") t->bos = json_int(*id, "an added token id");
+          else if (c->str == "<eos>") t->eos = json_int(*id, "an added token id");
+          else if (c->str == "<unk>") t->unk = json_int(*id, "an added token id");
+        }
+      if (t->bos < 0 || t->eos < 0 || t->unk < 0)
+        return fail(RH_ERR_INVALID, "gemma: missing <bos>/<eos>/<unk> in added_tokens");
       *out = t.release();
       return RH_OK;
     } catch (const std::invalid_argument& e) {

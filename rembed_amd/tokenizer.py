@@ -3,7 +3,9 @@
 WordPieceTokenizer follows tokenizer.New / Encode / VocabSize
 (tokenizer/tokenizer.go:39-216); BpeTokenizer follows bpe.New,
 NewFromTokenizerJSON and NewQwenFromTokenizerJSON
-(tokenizer/bpe/bpe.go:104-324). The tokenization itself runs in the library
+(tokenizer/bpe/bpe.go:104-324); SentencePieceTokenizer follows
+sentencepiece.New (tokenizer/sentencepiece/sentencepiece.go:47-241);
+GemmaTokenizer follows gemma.New (tokenizer/gemma/gemma.go:58-254). The tokenization itself runs in the library
 (rh_tokenizer_*); these classes only marshal text and ids.
 """
 import ctypes
@@ -102,3 +104,32 @@ class BpeTokenizer(_Tokenizer):
         check(lib.rh_tokenizer_bpe_load_json(str(path).encode(), 1, None, eos_tok.encode(),
                                              None, ctypes.byref(h)))
         return cls(h)
+
+
+class SentencePieceTokenizer(_Tokenizer):
+    """An XLM-R-family SentencePiece Unigram model (sentencepiece.bpe.model),
+    ids in HF's fairseq space."""
+
+    def __init__(self, model_path):
+        h = ctypes.c_void_p()
+        check(lib.rh_tokenizer_sentencepiece_load(str(model_path).encode(), ctypes.byref(h)))
+        super().__init__(h)
+
+    def normalize(self, text):
+        """The model's normalized text (Normalize, sentencepiece.go:244)."""
+        raw = _utf8(text)
+        cap = 4 * len(raw) + 64
+        buf = ctypes.create_string_buffer(cap)
+        n = ctypes.c_size_t()
+        check(lib.rh_tokenizer_sentencepiece_normalize(self.h, raw, len(raw), buf, cap,
+                                                       ctypes.byref(n)))
+        return buf.raw[:n.value].decode("utf-8")
+
+
+class GemmaTokenizer(_Tokenizer):
+    """Gemma's byte-fallback BPE from its tokenizer.json."""
+
+    def __init__(self, tokenizer_json):
+        h = ctypes.c_void_p()
+        check(lib.rh_tokenizer_gemma_load(str(tokenizer_json).encode(), ctypes.byref(h)))
+        super().__init__(h)
