@@ -344,13 +344,20 @@ void rh_model_destroy(rh_model *m);
  * leaves all of them in one mode (default), 0 = always as separate weights,
  * as the reference packs them (qwen3.go:479-481,528-529); a group whose
  * matrices fall back to different modes is always separate. Identical
- * results either way. */
+ * results either way.
+ * RH_OPT_FUSED_LN: 1 = a BERT-family full-int8 attention-output or FFN2
+ * projection whose output width is the hidden size (384, 768 or 1024)
+ * finishes whole rows in its epilogue: residual add, LayerNorm and the next
+ * int8 GEMM's u8 quantization in the same kernel, 0 = the linear writes
+ * fp32 rows and a separate residual + LayerNorm pass follows (default:
+ * measured faster); identical results. */
 #define RH_OPT_ATTN_PRECISION 1
 #define RH_OPT_FUSED_FFN1 2
 #define RH_OPT_PRODUCER_PLANES 3
 #define RH_OPT_STREAMS 4
 #define RH_OPT_QK_EPILOGUE 5
 #define RH_OPT_FUSE_PROJECTIONS 6
+#define RH_OPT_FUSED_LN 7
 int rh_model_set_option(rh_model *m, int option, int value);
 /* Model.Quantized / QuantizedActivations (bert.go:526-644). */
 int rh_model_quantized(const rh_model *m);

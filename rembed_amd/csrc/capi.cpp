@@ -408,6 +408,39 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
   return RH_OK;
 }
 
+// The full-int8 linear with the residual + LayerNorm finish (launch_gemm_i8_ln).
+int run_gemm_i8_ln(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
+                   const float* rs, int m, const I8LnArgs& f, double ops) {
+  if (m <= 0) return RH_OK;
+  if (w->mode != RH_MODE_A8W8 || !w->d_frag || w->glu)
+    return fail(RH_ERR_INVALID, "fused LayerNorm linear needs a full-int8 weight");
+  GemmI8Args g{};
+  g.A = qa;
+  g.lda = ldq;
+  g.B = static_cast<const int8_t*>(w->d_data);
+  g.ldb = w->kp;
+  g.Bf = static_cast<const int8_t*>(w->d_frag);
+  g.M = m;
+  g.N = w->n;
+  g.K = w->k;
+  g.row_scales = rs;
+  g.col_scales = w->d_scales;
+  g.colsum = w->d_colsum;
+  g.bias = w->d_bias;
+  g.act = ACT_NONE;
+  g.epi = EPI_F32;
+  g.tile_group = ctx->tile_group;
+  const double M = m, K = w->k, N = w->n;
+  // A, B, the residual read and written, the u8 rows, scales
+  const double bytes = M * K + K * N + 8 * M * N + (f.qa ? M * N + 4 * M : 0) + 4 * M + 16 * N;
+  int slot = -1;
+  hipError_t e = ctx->prof_begin(0, ops, bytes, &slot);
+  if (e == hipSuccess) e = launch_gemm_i8_ln(g, f, ctx->stream);
+  if (e == hipSuccess) e = ctx->prof_end(slot);
+  if (e != hipSuccess) return hip_fail(e, "int8 gemm + layernorm launch", __FILE__, __LINE__);
+  return RH_OK;
+}
+
 // Weight-only int8 / fp32 linear on bf16 planes: split the activations once
 // into the context workspace, then the planes GEMM. Rows go in chunks that
 // keep the kernel's 32-bit element offsets in range.

@@ -28,6 +28,7 @@
 // accumulators, or the two passes of a fused row quantization (row |max| by
 // atomics, then u8 bytes).
 #include "gemm_common.h"
+#include "rows_common.h"
 
 namespace rh {
 
@@ -388,11 +389,18 @@ __device__ __forceinline__ void load_fence() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NS, int EPI, int NK, int WGM = 1>
-__global__ __launch_bounds__(256 * WGM, 2 / WGM) void gemm_i8f_kernel(GemmI8Args p) {
-  constexpr int BM = 64 * WGM, BN = 256, NT = 256 * WGM, NW = 4 * WGM;
+// The main loop of the fragment-B kernels: A (BM rows of 128-byte stages)
+// by DMA into an NS-slot LDS ring, this wave's TN B fragments per k-step
+// straight to registers from the fragment-ordered weight, D = 4·NS k-steps
+// ahead; acc receives the wave's WM x (32·TN) int32 block at rows
+// row0 + wm·WM and columns colw. On return every load has landed and the
+// caller may reuse the LDS.
+template <int NS, int NK, int BM, int NT, int TM, int TN>
+__device__ __forceinline__ void i8f_main_loop(const GemmI8Args& p, uint8_t* lds,
+                                              v16i (&acc)[TM][TN], int row0, int colw,
+                                              int wave, int wm, int lane) {
   constexpr int BK = 128, CPR = BK / 16;  // A stage row bytes, 16-byte chunks per row
-  constexpr int WM = 64, WN = 64, TM = WM / 32, TN = WN / 32;
+  constexpr int WM = 32 * TM;
   constexpr int KPS = BK / 32;               // k-steps per stage
   constexpr int D = KPS * NS;                // B ring depth in k-steps
   constexpr int kA = BM * BK;                // A bytes per stage
@@ -400,24 +408,9 @@ __global__ __launch_bounds__(256 * WGM, 2 / WGM) void gemm_i8f_kernel(GemmI8Args
   // loads younger than stage t's A DMA when stage t begins: the B loads of
   // the NS-1 stages before it and the A DMAs of the NS-2 between
   constexpr int kWaitA = (NS - 1) * KPS * TN + (NS - 2) * LA;
-  constexpr int kEpiBytes = NW * 32 * (WN + 4) * 4;
-  constexpr int kLds = NS * kA > kEpiBytes + 3 * BM * 4 ? NS * kA : kEpiBytes + 3 * BM * 4;
   static_assert(LA >= 1 && kWaitA <= 63 && NS >= 2, "ring");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / 4, wn = wave % 4;
-  const int tiles_n = (p.N + BN - 1) / BN;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  int rb, cb;
-  tile_origin(tile, (p.M + BM - 1) / BM, tiles_n, p.tile_group, rb, cb);
-  const int row0 = rb * BM;
-  const int col0 = cb * BN;
   const int nk = NK > 0 ? NK : (p.K + BK - 1) / BK;  // stages
   const int nks = nk * KPS;  // k-steps (= kp / 32 of the weight)
-
   // A DMA sources, as in gemm_i8_kernel (rows past M read row M-1).
   const uint8_t* asrc[LA];
   int achunk[LA];
@@ -445,7 +438,7 @@ __global__ __launch_bounds__(256 * WGM, 2 / WGM) void gemm_i8f_kernel(GemmI8Args
   const int8_t* bsrc[TN];
 #pragma unroll
   for (int j = 0; j < TN; j++)
-    bsrc[j] = p.Bf + (size_t)((col0 + wn * WN + j * 32) >> 5) * nks * 1024 + lane * 16;
+    bsrc[j] = p.Bf + (size_t)((colw + j * 32) >> 5) * nks * 1024 + lane * 16;
   v4i bq[D][TN];
   auto load_b = [&](int ks, v4i (&dst)[TN]) {
     ks = ks < nks ? ks : nks - 1;
@@ -453,7 +446,6 @@ __global__ __launch_bounds__(256 * WGM, 2 / WGM) void gemm_i8f_kernel(GemmI8Args
     for (int j = 0; j < TN; j++) dst[j] = *reinterpret_cast<const v4i*>(bsrc[j] + (size_t)ks * 1024);
   };
 
-  v16i acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -509,7 +501,135 @@ __global__ __launch_bounds__(256 * WGM, 2 / WGM) void gemm_i8f_kernel(GemmI8Args
   }
   // The clamped refills past the last stage may still be landing in LDS.
   wait_vmcnt<0>();
+}
+
+template <int NS, int EPI, int NK, int WGM = 1>
+__global__ __launch_bounds__(256 * WGM, 2 / WGM) void gemm_i8f_kernel(GemmI8Args p) {
+  constexpr int BM = 64 * WGM, BN = 256, NT = 256 * WGM, NW = 4 * WGM;
+  constexpr int WM = 64, WN = 64, TM = WM / 32, TN = WN / 32;
+  constexpr int kA = BM * 128;  // A bytes per stage
+  constexpr int kEpiBytes = NW * 32 * (WN + 4) * 4;
+  constexpr int kLds = NS * kA > kEpiBytes + 3 * BM * 4 ? NS * kA : kEpiBytes + 3 * BM * 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / 4, wn = wave % 4;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  int rb, cb;
+  tile_origin(tile, (p.M + BM - 1) / BM, tiles_n, p.tile_group, rb, cb);
+  const int row0 = rb * BM;
+  const int col0 = cb * BN;
+  v16i acc[TM][TN];
+  i8f_main_loop<NS, NK, BM, NT, TM, TN>(p, lds, acc, row0, col0 + wn * WN, wave, wm, lane);
   i8_epilogue<BM, WM, WN, TM, TN, NW, NT, EPI>(p, acc, lds, row0, col0, wave, wm, wn, tid);
+}
+
+// ---- whole rows per workgroup, with the residual + LayerNorm epilogue ---------------
+// 64 rows x all N columns on NWN waves side by side (each 64 x 32·TN: 2 x TN
+// MFMA tiles), the main loop of the fragment-B kernels. The epilogue, per
+// 32-row band: every wave parks y = f32(acc)·rs·cs (+ bias) — the EPI_F32
+// epilogue's operations — in an LDS band [32][N + 8] (the two half-waves'
+// rows land 32 banks apart), then each wave takes whole rows: v = x + y and
+// ln_vec_finish, exactly add_ln_vec_kernel's steps. So the layer's two
+// passes (the linear's fp32 rows to HBM and back, then the residual add and
+// LayerNorm) become one kernel with identical results, and the fp32 y never
+// leaves the CU. With N the hidden width the grid has ceil(M / 64)
+// workgroups (158 at M = 10102): each streams the whole B image from L2.
+template <int NS, int NK, int NWN, int TN>
+__global__ __launch_bounds__(64 * NWN, 1) void gemm_i8_ln_kernel(GemmI8Args p, I8LnArgs f) {
+  constexpr int BM = 64, TM = 2, NT = 64 * NWN, WN = 32 * TN, N = NWN * WN;
+  constexpr int V = (N + 255) / 256;  // float4 groups per lane of a row
+  constexpr int kA = BM * 128;
+  constexpr int kStride = N + 8;      // floats per band row
+  constexpr int kBand = 32 * kStride * 4;
+  constexpr int kLds = NS * kA > kBand ? NS * kA : kBand;
+  static_assert(kLds <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row0 = blockIdx.x * BM;
+  v16i acc[TM][TN];
+  i8f_main_loop<NS, NK, BM, NT, TM, TN>(p, lds, acc, row0, wave * WN, wave, 0, lane);
+
+  const int fr = lane & 31, fg = lane >> 5;
+  float cs[TN], bs[TN];
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int col = wave * WN + j * 32 + fr;
+    cs[j] = p.col_scales[col];
+    bs[j] = p.bias ? p.bias[col] : 0.0f;
+  }
+  float* band = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    __syncthreads();  // the ring's last reads / the previous band's rows are done
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int lr = (r >> 2) * 8 + fg * 4 + (r & 3);  // the MFMA tile's row of element r
+      const int gr = row0 + i * 32 + lr;
+      const float rs = gr < p.M ? p.row_scales[gr] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        float y = (float)acc[i][j][r] * rs;
+        y = y * cs[j];
+        if (p.bias) y = y + bs[j];
+        band[lr * kStride + wave * WN + j * 32 + fr] = y;
+      }
+    }
+    __syncthreads();
+    for (int lr = wave; lr < 32; lr += NWN) {
+      const int grow = row0 + i * 32 + lr;
+      if (grow >= p.M) break;
+      float* xr = f.x + (size_t)grow * N;
+      v4f v[V];
+#pragma unroll
+      for (int e = 0; e < V; e++) {
+        const int j = (lane + 64 * e) * 4;
+        v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (j < N) {
+          t = *reinterpret_cast<const v4f*>(xr + j);
+          t = t + *reinterpret_cast<const v4f*>(band + lr * kStride + j);  // Add
+        }
+        v[e] = t;
+      }
+      ln_vec_finish<V>(v, lane, grow, N, f.gamma, f.beta, f.eps, xr, f.qa, f.ldq,
+                       f.row_scales, nullptr, nullptr, 0);
+    }
+  }
+}
+
+template <int NWN, int TN>
+static hipError_t launch_ln(const GemmI8Args& a, const I8LnArgs& f, hipStream_t s) {
+  const dim3 g(ceil_div(a.M, 64)), b(64 * NWN);
+  switch (ceil_div(a.K, 128)) {  // fully unrolled builds for the encoder widths
+    case 3: timed_launch((gemm_i8_ln_kernel<2, 3, NWN, TN>), g, b, 0, s, a, f); break;
+    case 6: timed_launch((gemm_i8_ln_kernel<2, 6, NWN, TN>), g, b, 0, s, a, f); break;
+    case 12: timed_launch((gemm_i8_ln_kernel<2, 12, NWN, TN>), g, b, 0, s, a, f); break;
+    case 24: timed_launch((gemm_i8_ln_kernel<2, 24, NWN, TN>), g, b, 0, s, a, f); break;
+    default: timed_launch((gemm_i8_ln_kernel<2, 0, NWN, TN>), g, b, 0, s, a, f);
+  }
+  return hipGetLastError();
+}
+
+bool gemm_i8_ln_supported(int n, int k) {
+  return (n == 384 || n == 768 || n == 1024) && k >= 1;
+}
+
+hipError_t launch_gemm_i8_ln(const GemmI8Args& a, const I8LnArgs& f, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (!a.Bf || a.epi != EPI_F32 || a.act != ACT_NONE || !f.x || !f.gamma || !f.beta ||
+      (f.qa && (!f.row_scales || f.ldq % 4)) || !gemm_i8_ln_supported(a.N, a.K))
+    return hipErrorInvalidValue;
+  switch (a.N) {
+    case 384: return launch_ln<4, 3>(a, f, s);
+    case 768: return launch_ln<8, 3>(a, f, s);
+    default: return launch_ln<8, 4>(a, f, s);  // 1024
+  }
 }
 
 template <int NS, int EPI, int WGM = 1>

@@ -134,6 +134,11 @@ struct rh_model {
   int32_t* pos_d = nullptr;
   int attn_precision = 3;
   bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
+  // RH_OPT_FUSED_LN: off by default; measured slower on BERT-base int8 at
+  // M = 10102 (2.947 vs 2.864 ms/step with two streams, 3.05 vs 2.97 with
+  // one): the whole-row tiles give 158 workgroups for 256 CUs, one per CU,
+  // and their main loop runs at ~80 % of the 128x256 tiles' rate per CU.
+  bool fused_ln = false;
   bool producer_planes = true;  // RH_OPT_PRODUCER_PLANES
   int streams = 2;              // RH_OPT_STREAMS
   // RH_OPT_QK_EPILOGUE: off by default; measured slower (Qwen3-0.6B W8
@@ -282,6 +287,26 @@ struct rh_model {
     return p;
   }
   float eps() const { return cfg.layer_norm_eps == 0.0f ? 1e-12f : cfg.layer_norm_eps; }
+  // Can w, a projection onto the hidden width followed by the residual +
+  // LayerNorm, finish those rows in its own epilogue? (A full-int8 weight
+  // with its fragment image, a supported width, and a next GEMM that takes
+  // u8 rows or nothing rather than bf16 planes.)
+  bool fuse_ln(const rh_weight* w, bool consumer_planes) const {
+    return fused_ln && w && w->mode == RH_MODE_A8W8 && w->d_frag && !w->glu &&
+           w->n == cfg.hidden && gemm_i8_ln_supported(w->n, w->k) && !consumer_planes;
+  }
+  I8LnArgs ln_args(float* xp, const float* g, const float* b, uint8_t* qa_out, int ldq,
+                   float* rs_out) const {
+    I8LnArgs f{};
+    f.x = xp;
+    f.gamma = g;
+    f.beta = b;
+    f.eps = eps();
+    f.qa = qa_out;
+    f.ldq = ldq;
+    f.row_scales = rs_out;
+    return f;
+  }
   int max_seq() const { return cfg.max_position - cfg.position_offset; }
 
   int ensure_ws(int rows, int batch, size_t ids_elems) {
@@ -614,15 +639,34 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     RH_HIP(launch_attention(aa, attn_precision, ps));
     RH_HIP(ctx->prof_end(slot));
     const Planes povp = at(pov);
-    st = run_linear(ctx, L.o, ctxp, H, Mp, yp, H, ACT_NONE, L.o->d_bias, qap, ldq_for(H),
-                    rsp, needs_q(L.o) && !po, po ? &povp : nullptr);
-    if (st) return st;
     const bool qf1 = needs_q(L.f1);
     const bool pf1 = planes_in(L.f1);
     const Planes pf1v = at(plane(0, L.f1));
-    RH_HIP(launch_add_layernorm(xp, yp, H, L.ln1_g, L.ln1_b, Mp, H, eps(),
-                                qf1 ? qap : nullptr, ldq_for(H), qf1 ? rsp : nullptr, ps,
-                                pf1 ? pf1v.hi : nullptr, pf1 ? pf1v.lo : nullptr, pf1v.ld));
+    if (fuse_ln(L.o, pf1) && !po) {
+      // x = LayerNorm(x + O(ctx)) (+ FFN1's u8 rows) in the projection's
+      // epilogue; the u8 rows may overwrite the projection's own input rows
+      RH_HIP(launch_quantize_rows_u8(ctxp, H, Mp, H, qap, ldq_for(H), rsp, ps));
+      st = run_gemm_i8_ln(ctx, L.o, qap, ldq_for(H), rsp, Mp,
+                          ln_args(xp, L.ln1_g, L.ln1_b, qf1 ? qap : nullptr, ldq_for(H),
+                                  qf1 ? rsp : nullptr),
+                          2.0 * MH * H * H);
+      if (st) return st;
+    } else {
+      st = run_linear(ctx, L.o, ctxp, H, Mp, yp, H, ACT_NONE, L.o->d_bias, qap, ldq_for(H),
+                      rsp, needs_q(L.o) && !po, po ? &povp : nullptr);
+      if (st) return st;
+      RH_HIP(launch_add_layernorm(xp, yp, H, L.ln1_g, L.ln1_b, Mp, H, eps(),
+                                  qf1 ? qap : nullptr, ldq_for(H), qf1 ? rsp : nullptr, ps,
+                                  pf1 ? pf1v.hi : nullptr, pf1 ? pf1v.lo : nullptr, pf1v.ld));
+    }
+    const bool last = li + 1 == layers.size();
+    const bool qn = !last && needs_q(layers[li + 1].qkv);
+    const bool xn_planes = !last && planes_in(layers[li + 1].qkv);
+    const Planes pnv = last ? Planes{} : at(plane(0, layers[li + 1].qkv));
+    // FFN2 finishes the layer (residual + LayerNorm + next QKV's u8 rows) in
+    // its epilogue on the split full-int8 path
+    const bool fused_ln2 = !(fused_ffn1 && qf1 && needs_q(L.f2)) && qf1 && needs_q(L.f2) &&
+                           fuse_ln(L.f2, xn_planes);
     if (fused_ffn1 && qf1 && needs_q(L.f2)) {
       // FFN1 + GELU + QuantizeRowU8 without the fp32 intermediate: pass 1
       // finds each row's |max| of the GELU output, pass 2 recomputes the
@@ -650,8 +694,15 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
                       rsp, false);
       if (st) return st;
       RH_HIP(launch_quantize_rows_u8(hidp, I, Mp, I, qa2p, ldq_for(I), rs2p, ps, ACT_GELU));
-      st = run_linear(ctx, L.f2, hidp, I, Mp, yp, H, ACT_NONE, L.f2->d_bias, qa2p,
-                      ldq_for(I), rs2p, false);
+      if (fused_ln2) {
+        st = run_gemm_i8_ln(ctx, L.f2, qa2p, ldq_for(I), rs2p, Mp,
+                            ln_args(xp, L.ln2_g, L.ln2_b, qn ? qap : nullptr, ldq_for(H),
+                                    qn ? rsp : nullptr),
+                            2.0 * MH * I * H);
+      } else {
+        st = run_linear(ctx, L.f2, hidp, I, Mp, yp, H, ACT_NONE, L.f2->d_bias, qa2p,
+                        ldq_for(I), rs2p, false);
+      }
       if (st) return st;
     } else {
       // FFN1's GELU output goes to FFN2's planes when FFN2 takes them
@@ -664,14 +715,12 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
                       ldq_for(I), rs2p, needs_q(L.f2) && !pf2, pf2 ? &pf2v : nullptr);
       if (st) return st;
     }
-    const bool last = li + 1 == layers.size();
-    const bool qn = !last && needs_q(layers[li + 1].qkv);
-    const bool xn_planes = !last && planes_in(layers[li + 1].qkv);
-    const Planes pnv = last ? Planes{} : at(plane(0, layers[li + 1].qkv));
-    RH_HIP(launch_add_layernorm(xp, yp, H, L.ln2_g, L.ln2_b, Mp, H, eps(),
-                                qn ? qap : nullptr, ldq_for(H), qn ? rsp : nullptr, ps,
-                                xn_planes ? pnv.hi : nullptr, xn_planes ? pnv.lo : nullptr,
-                                pnv.ld));
+    if (!fused_ln2) {
+      RH_HIP(launch_add_layernorm(xp, yp, H, L.ln2_g, L.ln2_b, Mp, H, eps(),
+                                  qn ? qap : nullptr, ldq_for(H), qn ? rsp : nullptr, ps,
+                                  xn_planes ? pnv.hi : nullptr, xn_planes ? pnv.lo : nullptr,
+                                  pnv.ld));
+    }
     return RH_OK;
   };
   // run_linear / run_gemm_i8 launch on ctx->stream: point it at each part's
@@ -1435,6 +1484,11 @@ int rh_model_set_option(rh_model* m, int option, int value) {
       m->fused_ffn1 = value != 0;
       return RH_OK;
     }
+    if (option == RH_OPT_FUSED_LN) {
+      if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fused LN must be 0 or 1");
+      m->fused_ln = value != 0;
+      return RH_OK;
+    }
     if (option == RH_OPT_PRODUCER_PLANES) {
       if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "producer planes must be 0 or 1");
       m->producer_planes = value != 0;
@@ -1536,6 +1590,7 @@ int rh_model_share(rh_model* src, rh_context* ctx, rh_model** out) {
     m->sin_l = src->sin_l;
     m->attn_precision = src->attn_precision;
     m->fused_ffn1 = src->fused_ffn1;
+    m->fused_ln = src->fused_ln;
     m->producer_planes = src->producer_planes;
     m->streams = src->streams;
     m->qk_epilogue = src->qk_epilogue;

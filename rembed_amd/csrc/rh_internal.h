@@ -238,6 +238,26 @@ enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 // tile: 0 = automatic, else one of the configurations RH_CTX_I8_TILE lists.
 constexpr int kI8TileConfigs = 14;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
+// The residual + LayerNorm finish of a full-int8 linear whose N is the
+// hidden width (the attention output and FFN2 projections of the BERT
+// family, bert.go:905-907,916-918): x = LayerNorm(x + dense(a)), and
+// optionally QuantizeRowU8 of the result for the next int8 GEMM.
+struct I8LnArgs {
+  float* x;             // [M][N] residual stream, replaced by the LayerNorm output
+  const float* gamma;   // [N]
+  const float* beta;    // [N]
+  float eps;
+  uint8_t* qa;          // [M][ldq] u8 of the result, or null (may alias the GEMM's A)
+  int ldq;
+  float* row_scales;    // [M] (may alias the GEMM's row scales)
+};
+// Whole output rows per workgroup (BM = 64, N in {384, 768, 1024}; needs
+// the fragment-ordered weight, epi EPI_F32 and no activation): the dequant
+// epilogue's values go through the same float operations, in the same
+// order, as the EPI_F32 GEMM followed by launch_add_layernorm, so both give
+// identical bits. hipErrorInvalidValue for a shape it does not cover.
+hipError_t launch_gemm_i8_ln(const GemmI8Args& a, const I8LnArgs& f, hipStream_t s);
+bool gemm_i8_ln_supported(int n, int k);
 int pick_i8_tile(int M, int N, int K, int epi);
 // fills n floats with zero (graph-capture safe, unlike hipMemsetAsync)
 hipError_t launch_fill_zero(float* x, int n, hipStream_t s);

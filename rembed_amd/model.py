@@ -123,6 +123,11 @@ class Model:
     def set_attention_precision(self, prec):
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_ATTN_PRECISION, prec))
 
+    def set_fused_ln(self, on=True):
+        """RH_OPT_FUSED_LN: full-int8 O / FFN2 projections finish the
+        residual add + LayerNorm in their epilogue (identical results)."""
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSED_LN, 1 if on else 0))
+
     def set_fused_ffn1(self, on):
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSED_FFN1, 1 if on else 0))
 

@@ -122,6 +122,33 @@ def test_fused_ffn1_identical(gpu_ctx, minilm):
     assert np.array_equal(plain, fused)
 
 
+@pytest.mark.parametrize("model", ["minilm", "bertbase"])
+@pytest.mark.parametrize("streams", [1, 2])
+def test_fused_ln_identical(gpu_ctx, request, model, streams):
+    """The full-int8 attention-output and FFN2 projections finishing the
+    residual add, LayerNorm and the next GEMM's u8 rows in their epilogue
+    (one kernel per block, whole rows per workgroup) give the same
+    embeddings and hidden states, bit for bit, as the projection's fp32
+    rows followed by the separate residual + LayerNorm pass
+    (bert.go:905-907,916-918): the same float operations in the same
+    order. MiniLM (hidden 384, K 384 and 1536) and BERT-base (768; 768 and
+    3072), ragged row tails included."""
+    from rembed_amd.model import Model
+    shape, t, ids, lens = request.getfixturevalue(model)
+    say(f"{shape.name}: {len(lens)} texts, {int(lens.sum())} rows, {streams} stream(s)")
+    m = Model(gpu_ctx, shape, t, 2)
+    m.set_streams(streams)
+    m.set_fused_ln(True)
+    fused = m.embed(ids, lens)
+    tok_fused = m.embed_tokens(ids, lens)
+    m.set_fused_ln(False)
+    plain = m.embed(ids, lens)
+    tok_plain = m.embed_tokens(ids, lens)
+    assert np.array_equal(fused, plain)
+    for a, b in zip(tok_fused, tok_plain):
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("quant", [0, 1], ids=["fp32", "w8"])
 def test_producer_planes_identical(gpu_ctx, minilm, quant):
     """Norms, attention and the FFN1 epilogue writing the next GEMM's bf16
