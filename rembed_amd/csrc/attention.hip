@@ -110,6 +110,46 @@ __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int
   return alpha;
 }
 
+// Output rows of one wave's 32 queries: O^T leaves the MFMAs with lane
+// (query fr, half fg) holding d = t*32 + i*8 + fg*4 + j, i.e. 32-byte pieces
+// of 32 different rows per store instruction. The wave parks its rows in its
+// own LDS region (row stride DH + 4 floats) and writes them back DH/4 lanes
+// per row, so every store instruction covers whole 128-byte lines of
+// consecutive rows. The caller has finished every LDS read of the key loop
+// on all waves (the region overlaps the K/V blocks).
+template <int DH>
+__device__ __forceinline__ void attn_store_rows(const AttnArgs& p, const v16f (&o)[DH / 32],
+                                                float inv, uint8_t* lds, int wave, int lane,
+                                                int r0, int qw0, int len, int h) {
+  constexpr int DT = DH / 32, kStride = DH + 4;
+  constexpr int LPR = DH / 4, RPI = 64 / LPR;  // lanes per row, rows per instruction
+  const int fr = lane & 31, fg = lane >> 5;
+  float* st = reinterpret_cast<float*>(lds) + wave * 32 * kStride;
+#pragma unroll
+  for (int t = 0; t < DT; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v4f w;
+#pragma unroll
+      for (int j = 0; j < 4; j++) w[j] = o[t][i * 4 + j] * inv;
+      *reinterpret_cast<v4f*>(st + fr * kStride + t * 32 + i * 8 + fg * 4) = w;
+    }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are in LDS
+  __builtin_amdgcn_wave_barrier();
+  const int c4 = (lane % LPR) * 4;
+#pragma unroll
+  for (int k = 0; k < 32 / RPI; k++) {
+    const int rr = lane / LPR + k * RPI;
+    const int q = qw0 + rr;
+    const v4f w = *reinterpret_cast<const v4f*>(st + rr * kStride + c4);
+    if (q < len) {
+      const size_t off = (size_t)(r0 + q) * p.ldctx + h * DH + c4;
+      if (p.ctx_hi) store_planes4(p.ctx_hi, p.ctx_lo, off, w);
+      else *reinterpret_cast<v4f*>(p.ctx + off) = w;
+    }
+  }
+}
+
 template <int DH, int PREC, typename TIn>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   const TIn* qkv = static_cast<const TIn*>(p.qkv);
@@ -121,7 +161,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   // XOR swizzle of 16-byte chunks inside a K row, kept inside the row
   // (a row holds DH/8 chunks: 4 for dh 32, 8 or more otherwise).
   constexpr int kSwz = DH / 8 >= 8 ? 7 : DH / 8 - 1;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[T * (kK + kV)];
+  constexpr int kOut = 4 * 32 * (DH + 4) * 4;  // output staging (attn_store_rows)
+  __shared__ __attribute__((aligned(16))) uint8_t lds[T * (kK + kV) > kOut ? T * (kK + kV) : kOut];
   uint8_t* sK = lds;
   uint8_t* sV = lds + T * kK;
 
@@ -292,20 +333,10 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   }
 
   const float ltot = lrun + __shfl_xor(lrun, 32, 64);
-  if (qi >= len) return;
-  const float inv = 1.0f / ltot;
-  const size_t orow = (size_t)(r0 + qi) * p.ldctx + h * DH;
-#pragma unroll
-  for (int t = 0; t < DT; t++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      v4f w;
-#pragma unroll
-      for (int j = 0; j < 4; j++) w[j] = o[t][i * 4 + j] * inv;
-      const size_t off = orow + t * 32 + i * 8 + fg * 4;
-      if (p.ctx_hi) store_planes4(p.ctx_hi, p.ctx_lo, off, w);
-      else *reinterpret_cast<v4f*>(p.ctx + off) = w;
-    }
+  // rows past the text divide by 1 (their values are never stored)
+  const float inv = 1.0f / (qi < len ? ltot : 1.0f);
+  __syncthreads();  // every wave's reads of the last key block are done
+  attn_store_rows<DH>(p, o, inv, lds, wave, lane, r0, q0 + wave * 32, len, h);
 }
 
 // ---- bf16 operands, pipelined --------------------------------------------------
@@ -336,7 +367,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   constexpr int kStage = 2 * kKB;             // K + V^T (same size)
   constexpr int kKLoads = kKB / (4 * 1024);   // DMA instructions per wave per block
   static_assert(kKLoads >= 1 && kKB % 4096 == 0, "K block must split into 4 waves x 1 KiB");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage];
+  constexpr int kOut = 4 * 32 * (DH + 4) * 4;  // output staging (attn_store_rows)
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage > kOut ? 2 * kStage : kOut];
 
   const int b = blockIdx.z, h = blockIdx.y;
   const int r0 = p.cu[b], len = p.cu[b + 1] - r0;
@@ -529,20 +561,9 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   }
 
   const float ltot = lrun + __shfl_xor(lrun, 32, 64);
-  if (qi >= len) return;
-  const float inv = 1.0f / ltot;
-  const size_t orow = (size_t)(r0 + qi) * p.ldctx + h * DH;
-#pragma unroll
-  for (int t = 0; t < DT; t++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      v4f w;
-#pragma unroll
-      for (int j = 0; j < 4; j++) w[j] = o[t][i * 4 + j] * inv;
-      const size_t off = orow + t * 32 + i * 8 + fg * 4;
-      if (p.ctx_hi) store_planes4(p.ctx_hi, p.ctx_lo, off, w);
-      else *reinterpret_cast<v4f*>(p.ctx + off) = w;
-    }
+  const float inv = 1.0f / (qi < len ? ltot : 1.0f);
+  // the loop's last barrier ordered every wave's reads of the key blocks
+  attn_store_rows<DH>(p, o, inv, lds, wave, lane, r0, q0 + wave * 32, len, h);
 }
 
 template <int DH>
