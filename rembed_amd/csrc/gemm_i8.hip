@@ -357,6 +357,156 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
   i8_epilogue<BM, WM, WN, TM, TN, NW, NT, EPI>(p, acc, lds, row0, col0, wave, wm, wn, tid);
 }
 
+// ---- 128x128 wave tiles for the long-K problems ---------------------------------
+// 256 x 256 tile on 4 waves (2 x 2), each wave 128 x 128 = 4 x 4 MFMA tiles with
+// its 256 accumulators in AGPRs: 0.5 KiB of LDS fragment reads per MFMA
+// against 1 KiB for the 64 x 64 waves above. K in 64-byte stages (i8_slot
+// rows), an NS-slot ring refilled right after each stage's barrier. The loop
+// body has no branch: stages past the last are clamped to it (a reload of
+// real bytes into a slot nobody reads again), so each stage is followed by
+// the same number of younger loads and every wait count is a constant — a
+// branch in the body made the compiler copy the 256 accumulators through
+// VGPRs at every back edge. The stage's DMA and the next k-step's fragment
+// reads are spread one per MFMA (sched_group_barrier), so their issue hides
+// behind the matrix core. Requires ceil(K / 64) % NS == 0 (launch_w4 checks).
+// The same products in the same k order as the other tiles: the same int32
+// accumulators.
+template <int NS, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_i8_w4_kernel(GemmI8Args p) {
+  constexpr int BM = 256, BN = 256, BK = 64, WGN = 2;
+  constexpr int NT = 256, NW = 4, CPR = BK / 16;
+  constexpr int WM = 128, WN = 128, TM = 4, TN = 4;
+  constexpr int kA = BM * BK, kB = BN * BK, kStage = kA + kB;
+  constexpr int LA = kA / (NT * 16), LB = kB / (NT * 16);  // 4 + 4
+  constexpr int kLoads = LA + LB;
+  constexpr int S = BK / 32;  // k-steps per stage
+  static_assert(NS >= 3 && NS * kStage <= 160 * 1024, "ring");
+  static_assert(NS * kStage >= NW * 32 * (WN + 4) * 4 + 3 * BM * 4, "epilogue LDS");
+  static_assert((NS - 2) * kLoads < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  int rb, cb;
+  tile_origin(tile, (p.M + BM - 1) / BM, tiles_n, p.tile_group, rb, cb);
+  const int row0 = rb * BM, col0 = cb * BN;
+  const int nk = (p.K + BK - 1) / BK;
+
+  // Per-lane sources (rows past M read row M-1; B rows are zero-padded to
+  // a multiple of 256, and B is zero past K).
+  const uint8_t* asrc[LA];
+  int achunk[LA];
+#pragma unroll
+  for (int j = 0; j < LA; j++) {
+    const int slot = (wave * LA + j) * 64 + lane;
+    const int r = slot / CPR;
+    achunk[j] = stage_slot_chunk<BK>(r, slot % CPR) * 16;
+    const int gr = row0 + r;
+    asrc[j] = p.A + (size_t)(gr < p.M ? gr : p.M - 1) * p.lda;
+  }
+  const int8_t* bsrc[LB];
+#pragma unroll
+  for (int j = 0; j < LB; j++) {
+    const int slot = (wave * LB + j) * 64 + lane;
+    const int r = slot / CPR;
+    bsrc[j] = p.B + (size_t)(col0 + r) * p.ldb + stage_slot_chunk<BK>(r, slot % CPR) * 16;
+  }
+  auto issue = [&](int kt, int slot) {
+    kt = kt < nk ? kt : nk - 1;
+    uint8_t* st = lds + slot * kStage;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int j = 0; j < LA; j++) {
+      int kb = k0 + achunk[j];
+      kb = kb < p.lda ? kb : 0;  // past the row: any in-bounds bytes (B is 0 there)
+      lds_dma16(asrc[j] + kb, st + (wave * LA + j) * 1024);
+    }
+#pragma unroll
+    for (int j = 0; j < LB; j++) lds_dma16(bsrc[j] + k0, st + kA + (wave * LB + j) * 1024);
+  };
+
+  v16i acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = v16i{};
+  // Fragment offsets: rows 32 apart sit 2 KiB apart (i8_slot's permutation
+  // depends on (r >> 2) & 3 only) and k-step s XORs the chunk index by 2s,
+  // so one base per operand serves every fragment.
+  const int fr = lane & 31, fg = lane >> 5;
+  const int abase = stage_frag_off<BK>(wm * WM + fr, fg);
+  const int bbase = kA + stage_frag_off<BK>(wn * WN + fr, fg);
+  v4i fa[2][TM], fb[2][TN];
+  auto load = [&](int slot, int s, v4i (&a)[TM], v4i (&b)[TN]) {
+    const uint8_t* st = lds + slot * kStage;
+    const int ab = abase ^ (32 * s), bb = bbase ^ (32 * s);
+#pragma unroll
+    for (int i = 0; i < TM; i++) a[i] = *reinterpret_cast<const v4i*>(st + ab + i * 32 * BK);
+#pragma unroll
+    for (int j = 0; j < TN; j++) b[j] = *reinterpret_cast<const v4i*>(st + bb + j * 32 * BK);
+  };
+  auto mma = [&](v4i (&a)[TM], const v4i (&b)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) a[i] ^= (int)0x80808080;  // u8 -> s8 (q = u8 - 128)
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+  };
+
+#pragma unroll
+  for (int st = 0; st < NS - 1; st++) issue(st, st);
+  wait_vmcnt<(NS - 2) * kLoads>();
+  stage_barrier();
+  issue(NS - 1, NS - 1);
+  load(0, 0, fa[0], fb[0]);
+  for (int kt0 = 0; kt0 < nk; kt0 += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; u++) {
+      const int kt = kt0 + u;
+#pragma unroll
+      for (int s = 0; s < S; s++) {
+        if (s + 1 < S) {
+          load(u, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+          mma(fa[s & 1], fb[s & 1]);
+#pragma unroll
+          for (int g = 0; g < TM + TN; g++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+        } else {
+          wait_lgkmcnt0();
+          // stage kt+1 has landed for this wave: NS-2 younger stages pending
+          wait_vmcnt<(NS - 2) * kLoads>();
+          stage_barrier();  // ... for every wave; slot u is free
+          issue(kt + NS, u);
+          load((u + 1) % NS, 0, fa[0], fb[0]);
+          mma(fa[s & 1], fb[s & 1]);
+#pragma unroll
+          for (int g = 0; g < kLoads; g++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (DMA)
+          }
+#pragma unroll
+          for (int g = 0; g < TM + TN; g++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  wait_vmcnt<0>();  // clamped refills may still be landing
+  i8_epilogue<BM, WM, WN, TM, TN, NW, NT, EPI>(p, acc, lds, row0, col0, wave, wm, wn, tid);
+}
+
 // ---- B fragments straight to registers ------------------------------------
 // 64 x 256 tile on 4 waves side by side (each 64 rows x 64 columns: 2 x 2
 // MFMA tiles). Only A goes through LDS (128-byte stage rows by
@@ -653,6 +803,18 @@ static hipError_t launch_tile(const GemmI8Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Tile 15: the 128x128-wave kernel with a four-slot ring where the stage
+// count allows it, else three, else tile 9.
+template <int EPI>
+static hipError_t launch_w4(const GemmI8Args& a, hipStream_t s) {
+  const int nk = ceil_div(a.K, 64);
+  const dim3 g(ceil_div(a.M, 256) * ceil_div(a.N, 256)), b(256);
+  if (nk % 4 == 0) timed_launch((gemm_i8_w4_kernel<4, EPI>), g, b, 0, s, a);
+  else if (nk % 3 == 0) timed_launch((gemm_i8_w4_kernel<3, EPI>), g, b, 0, s, a);
+  else return launch_tile<128, 256, 2, EPI, 4, 128>(a, s);
+  return hipGetLastError();
+}
+
 // 1 = 256x256, 2 = 256x128 and 3 = 128x128 with 4 stages; 4 = 256x128 and
 // 5 = 128x256 with 3 stages; 6 = 256x256 (4 stages) and 7 = 128x256 (3
 // stages) on 8 waves. Tiles 4, 5 and 7 take 72 KiB of LDS and <= 256
@@ -673,6 +835,7 @@ static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
     case 12: return a.Bf ? launch_frag<4, EPI>(a, s) : hipErrorInvalidValue;
     case 13: return a.Bf ? launch_frag<2, EPI, 2>(a, s) : hipErrorInvalidValue;
     case 14: return a.Bf ? launch_frag<3, EPI, 2>(a, s) : hipErrorInvalidValue;
+    case 15: return launch_w4<EPI>(a, s);
     default: return launch_tile<128, 128, 4, EPI>(a, s);
   }
 }
@@ -688,6 +851,11 @@ int pick_i8_tile(int M, int N, int K, int epi) {
   (void)epi;
   const int tiles = ceil_div(M, 128) * ceil_div(N, 256);
   if (tiles < 128) return 3;
+  // deep K on a grid of at least one 256x256 tile per CU: the 128x128-wave
+  // tile (4-12 % ahead of tiles 7 and 9 at M = 16384, K = 2048 and 3072)
+  const int nk = ceil_div(K, 64);
+  if (K >= 2048 && ceil_div(M, 256) * ceil_div(N, 256) >= 256 && (nk % 4 == 0 || nk % 3 == 0))
+    return 15;
   return (K >= 2048 || tiles <= 256) ? 9 : 7;
 }
 

@@ -236,7 +236,7 @@ enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 
 // Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
 // tile: 0 = automatic, else one of the configurations RH_CTX_I8_TILE lists.
-constexpr int kI8TileConfigs = 14;
+constexpr int kI8TileConfigs = 15;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
 // The residual + LayerNorm finish of a full-int8 linear whose N is the
 // hidden width (the attention output and FFN2 projections of the BERT

@@ -131,7 +131,7 @@ def test_i32_accumulators_bert_base_bit_exact(gpu_ctx, m, kn):
     assert np.array_equal(got[: m * n].reshape(m, n), want)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15])
 def test_every_int8_tile_config_bit_exact(gpu_ctx, tile):
     """Each int8 GEMM tile configuration (forced) gives the oracle's exact
     accumulators and dequantized outputs, including M/N/K tails."""
@@ -289,7 +289,39 @@ def test_linear_a8w8_bias_gelu_bit_exact(gpu_ctx):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14])
+@pytest.mark.parametrize("mkn", [(4096, 2048, 4096), (4352, 3072, 4096)], ids=["ring4", "ring3"])
+def test_int8_big_grid_tile_matches(gpu_ctx, mkn):
+    """Where the automatic choice takes tile 15 (K >= 2048 and at least 256
+    tiles of 256x256; a four-slot ring at K = 2048, three at 3072 with
+    partial row tiles) its int32 accumulators and dequantized rows equal
+    tile 9's bit for bit (tile 15 itself is pinned to the oracle on the
+    smaller shapes of test_every_int8_tile_config_bit_exact)."""
+    from rembed_amd._lib import RH_CTX_I8_TILE
+    t = T()
+    m, k, n = mkn
+    say(f"int8 auto (tile 15) vs tile 9 m={m} k={k} n={n}")
+    rng = np.random.default_rng(m + k)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.05).astype(np.float32)
+    pb = t.PackB8VNNI(gpu_ctx, bT, k, n)
+    outs = []
+    for tile in (0, 9):
+        gpu_ctx.set_option(RH_CTX_I8_TILE, tile)
+        try:
+            dst, qa, rs = run_vnni(gpu_ctx, a, pb, m)
+            ldq = t.ldq_for(k)
+            dq = gpu_ctx.upload(np.ascontiguousarray(qa))
+            acc = gpu_ctx.alloc(m * n * 4)
+            t.GemmU8S8I32(gpu_ctx, acc, dq, ldq, pb, m)
+            gpu_ctx.sync()
+            outs.append((dst, acc.download(np.int32, (m, n))))
+        finally:
+            gpu_ctx.set_option(RH_CTX_I8_TILE, 0)
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert np.array_equal(outs[0][0], outs[1][0])
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15])
 def test_linear_u8_fused_quantization_bit_exact(gpu_ctx, tile):
     """FFN1 -> GELU -> QuantizeRowU8 in two GEMM passes (no fp32 rows) gives
     exactly QuantizeRowU8 of the reference's fp32 GELU rows."""
