@@ -67,7 +67,10 @@ void *rh_context_stream(rh_context *ctx);
  *                    (three stages, two workgroups per CU), 6 = 256x256,
  *                    7 = 128x256 (eight waves), 8 = 256x256, 9 = 128x256
  *                    (eight waves, two 128-byte k stages), 10 = 128x256
- *                    (eight waves, three 128-byte k stages)
+ *                    (eight waves, three 128-byte k stages), 11-14 = 64x256
+ *                    and 128x256 with B fragments loaded to registers (A8W8
+ *                    weights), 15 = 256x256 on four 128x128 waves (a four-
+ *                    or three-stage ring by ceil(K/64), else 9)
  *   RH_CTX_BF_ALGO   weight-only int8 / fp32 GEMMs: 0 = activations split
  *                    once into bf16 hi/lo planes and weights stored as bf16
  *                    planes (default), 1 = split inside the GEMM's main loop
