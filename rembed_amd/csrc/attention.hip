@@ -492,6 +492,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     kb_lo = max(0, q0 - p.window + 1) / kAttnKV;
     kb_hi = min(kb_hi, (qlast + p.window - 1) / kAttnKV + 1);
   }
+  // every query sees every key of its text: the only mask is the text's end
+  const bool text_mask = !p.causal && p.window <= 0;
 
   issue_k(kb_lo, 0);
   load_v(kb_lo);
@@ -526,15 +528,32 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
             sK + kr * kRowB + (((2 * s + fg) ^ attn_kswz<DH>(kr)) << 4));
         sc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sc[t2], 0, 0, 0);
       }
+    // Bidirectional attention masks only the keys past the text, the same
+    // keys for every query: one more MFMA per tile adds -inf to their
+    // scores (k-element 0 of a mask fragment times q-element 0 = 1; every
+    // other product is 0 * 0) and +0 to the rest, which leaves those sums
+    // as they were, in place of a compare and select per score.
+    const bool key_tail = key0 + kAttnKV > len;
+    if (text_mask && key_tail) {
+      const v8bf q1 = {(__bf16)(fg == 0 ? 1.0f : 0.0f), (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f,
+                       (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f};
+#pragma unroll
+      for (int t2 = 0; t2 < 2; t2++) {
+        const bool past = key0 + t2 * 32 + fr >= len;
+        const v8bf km = {(__bf16)(fg == 0 && past ? -INFINITY : 0.0f), (__bf16)0.0f, (__bf16)0.0f,
+                         (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f};
+        sc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, q1, sc[t2], 0, 0, 0);
+      }
+    }
 
     // Scale, mask (only blocks that cross some query's visible range), online
     // softmax; the output is rescaled only when some query's reference max
-    // moved.
-    const bool masked = __any(key0 < klo || key0 + kAttnKV - 1 > khi);
+    // moved, and never on the first block (the output is still zero).
+    const bool masked = !text_mask && __any(key0 < klo || key0 + kAttnKV - 1 > khi);
     bool rescale;
     const float alpha =
         attn_softmax_block(sc, key0, fg, klo, khi, masked, cs, mrun, lrun, rescale);
-    if (rescale) {
+    if (rescale && kb != kb_lo) {
 #pragma unroll
       for (int t = 0; t < DT; t++)
 #pragma unroll
