@@ -110,6 +110,27 @@ __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int
   return alpha;
 }
 
+// Workgroup -> (text b, head h, query block). Workgroups are dealt to the 8
+// XCDs round-robin (workgroup w runs on XCD w % 8), and the query blocks
+// of one text read the same K and V rows, as do the q heads of one kv head
+// (GQA): ids are laid out so that all workgroups of one (text, kv head)
+// unit share an XCD and its L2, units spread over the XCDs. Returns false
+// past the last unit.
+__device__ __forceinline__ bool attn_block(const AttnArgs& p, int& b, int& h, int& qb) {
+  const int nqb = (p.max_len + kAttnQ - 1) / kAttnQ;
+  const int G = p.heads / p.kv_heads;
+  const int nv = G * nqb;  // workgroups per unit
+  const int w = blockIdx.x;
+  const int t = w >> 3;
+  const int v = t % nv;
+  const int u = (t / nv) * 8 + (w & 7);
+  if (u >= p.batch * p.kv_heads) return false;
+  qb = v % nqb;
+  b = u / p.kv_heads;
+  h = (u % p.kv_heads) * G + v / nqb;
+  return true;
+}
+
 // Output rows of one wave's 32 queries: O^T leaves the MFMAs with lane
 // (query fr, half fg) holding d = t*32 + i*8 + fg*4 + j, i.e. 32-byte pieces
 // of 32 different rows per store instruction. The wave parks its rows in its
@@ -166,9 +187,10 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   uint8_t* sK = lds;
   uint8_t* sV = lds + T * kK;
 
-  const int b = blockIdx.z, h = blockIdx.y;
+  int b, h, qb;
+  if (!attn_block(p, b, h, qb)) return;
   const int r0 = p.cu[b], len = p.cu[b + 1] - r0;
-  const int q0 = blockIdx.x * kAttnQ;
+  const int q0 = qb * kAttnQ;
   if (q0 >= len) return;
   const int kvh = h / (p.heads / p.kv_heads);
 
@@ -370,9 +392,10 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   constexpr int kOut = 4 * 32 * (DH + 4) * 4;  // output staging (attn_store_rows)
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage > kOut ? 2 * kStage : kOut];
 
-  const int b = blockIdx.z, h = blockIdx.y;
+  int b, h, qb;
+  if (!attn_block(p, b, h, qb)) return;
   const int r0 = p.cu[b], len = p.cu[b + 1] - r0;
-  const int q0 = blockIdx.x * kAttnQ;
+  const int q0 = qb * kAttnQ;
   if (q0 >= len) return;
   const int kvh = h / (p.heads / p.kv_heads);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -587,7 +610,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
 
 template <int DH>
 static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s) {
-  dim3 grid(ceil_div(a.max_len, kAttnQ), a.heads, a.batch);
+  const int units = a.batch * a.kv_heads;
+  const dim3 grid(8 * ceil_div(a.max_len, kAttnQ) * (a.heads / a.kv_heads) * ceil_div(units, 8));
   if (a.in_bf16)  // bf16 input carries no low half: one-term products
     timed_launch((attention_bf16_kernel<DH>), grid, dim3(256), 0, s, a);
   else if (precision == 3)
@@ -599,6 +623,7 @@ static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s
 
 hipError_t launch_attention(const AttnArgs& a, int precision, hipStream_t s) {
   if (a.batch <= 0 || a.max_len <= 0) return hipSuccess;
+  if (a.kv_heads <= 0 || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
   switch (a.dh) {
     case 32: return launch_attn_dh<32>(a, precision, s);
     case 64: return launch_attn_dh<64>(a, precision, s);
