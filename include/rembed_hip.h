@@ -340,8 +340,8 @@ void rh_model_destroy(rh_model *m);
  * 1 = one stream. Every setting gives identical results.
  * RH_OPT_QK_EPILOGUE: 1 = a decoder's weight-only int8 q|k|v projection
  * applies QK-norm + RoPE in its GEMM epilogue and writes the bf16 rows
- * attention reads (where the shape allows), 0 = fp32 rows and a separate
- * pass (default: measured faster); both give identical results.
+ * attention reads (where the shape allows; default: measured faster),
+ * 0 = fp32 rows and a separate pass; both give identical results.
  * RH_OPT_FUSE_PROJECTIONS (set before rh_model_finalize): 1 = a decoder
  * layer's q, k, v (and gate, up) are packed as one weight where newDense
  * leaves all of them in one mode (default), 0 = always as separate weights,

@@ -217,8 +217,21 @@ __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
       const float* src0 = reinterpret_cast<const float*>(lds) +
                           (wm * WGN + c / WN) * 32 * kEpiStride + c % WN;
       typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-#pragma unroll 4
-      for (int rr = wn; rr < 32; rr += WGN) {
+      // This wave's rows of the band: their cos/sin pieces are loaded before
+      // the first row's store, so no table load queues behind a store
+      // (vmcnt counts both in order).
+      constexpr int RPW = 32 / WGN;
+      v4f ccs[RPW], sns[RPW];
+#pragma unroll
+      for (int k = 0; k < RPW; k++) {
+        const int wr = i * 32 + wn + k * WGN;  // row within the wave row (uniform)
+        const int pos = __builtin_amdgcn_readlane(wr < 64 ? qk_pos0 : qk_pos1, wr & 63);
+        ccs[k] = *reinterpret_cast<const v4f*>(p.qk_cos + (size_t)pos * half + dp);
+        sns[k] = *reinterpret_cast<const v4f*>(p.qk_sin + (size_t)pos * half + dp);
+      }
+#pragma unroll
+      for (int k = 0; k < RPW; k++) {
+        const int rr = wn + k * WGN;
         v4f x = *reinterpret_cast<const v4f*>(src0 + rr * kEpiStride);
         const int grow = grow_base + rr;
         const bool ok = grow < p.M;
@@ -230,10 +243,7 @@ __global__ __launch_bounds__(128 * WGN) void gemm_planes_kernel(GemmPlArgs p) {
         float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
         for (int o = lph >> 1; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
         v4bf* out = reinterpret_cast<v4bf*>(p.qk_out + (size_t)grow * p.ldc + gcol);
-        const int wr = i * 32 + rr;  // row within the wave row (uniform)
-        const int pos = __builtin_amdgcn_readlane(wr < 64 ? qk_pos0 : qk_pos1, wr & 63);
-        const v4f cc = *reinterpret_cast<const v4f*>(p.qk_cos + (size_t)pos * half + dp);
-        const v4f sn = *reinterpret_cast<const v4f*>(p.qk_sin + (size_t)pos * half + dp);
+        const v4f cc = ccs[k], sn = sns[k];
         const float inv = rms_inv(ss, dh, p.qk_eps);
         v4f xn, pn;
 #pragma unroll

@@ -141,11 +141,12 @@ struct rh_model {
   bool fused_ln = false;
   bool producer_planes = true;  // RH_OPT_PRODUCER_PLANES
   int streams = 2;              // RH_OPT_STREAMS
-  // RH_OPT_QK_EPILOGUE: off by default; measured slower (Qwen3-0.6B W8
-  // 686K vs 689K tokens/s, EmbeddingGemma 1.59M vs 1.68M): each epilogue
-  // row's cos/sin loads wait behind the previous row's stores (vmcnt counts
-  // both), which costs more than the separate pass's traffic.
-  bool qk_epilogue = false;
+  // RH_OPT_QK_EPILOGUE: on by default since the epilogue loads each band's
+  // cos/sin pieces before its first store (Qwen3-0.6B W8 22.4 against
+  // 23.1-23.4 ms/step, EmbeddingGemma 18.6 against 18.8); with a load per
+  // row behind the previous row's store (vmcnt counts both) it had been
+  // slower than the separate pass.
+  bool qk_epilogue = true;
   // RH_OPT_FUSE_PROJECTIONS: decoder q|k|v and gate|up packed as one weight
   // each where newDense leaves the group in one mode (default), or always
   // as separate weights like the reference; set before finalize.
