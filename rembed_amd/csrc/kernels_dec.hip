@@ -419,14 +419,32 @@ __global__ __launch_bounds__(256) void dense_matvec_kernel(const float* __restri
   const int o = blockIdx.x * 256 + threadIdx.x;
   if (o >= outn) return;
   const float* w = wT + o;
+  // The sum runs i = 0, 1, ... as in the reference; only the loads run
+  // ahead: two register blocks of U weights, the next block's loads in
+  // flight while the current one is summed (each thread's chain waited on
+  // every block's memory latency before).
+  constexpr int U = 32;
   float acc = 0.0f;
   int i = 0;
-  for (; i + 8 <= in; i += 8) {
-    float t[8];
+  float ta[U], tb[U];
+  auto fill = [&](float (&t)[U], int i0) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) t[e] = w[(size_t)(i + e) * outn];
+    for (int e = 0; e < U; e++) t[e] = w[(size_t)(i0 + e) * outn];
+  };
+  auto sum = [&](const float (&t)[U], int i0) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) acc = acc + t[e] * xs[i + e];
+    for (int e = 0; e < U; e++) acc = acc + t[e] * xs[i0 + e];
+  };
+  if (in >= U) fill(ta, 0);
+  for (; i + 2 * U <= in; i += 2 * U) {
+    fill(tb, i + U);
+    sum(ta, i);
+    if (i + 3 * U <= in) fill(ta, i + 2 * U);
+    sum(tb, i + U);
+  }
+  if (i + U <= in) {  // one loaded block left
+    sum(ta, i);
+    i += U;
   }
   for (; i < in; i++) acc = acc + w[(size_t)i * outn] * xs[i];
   y[(size_t)b * outn + o] = acc;

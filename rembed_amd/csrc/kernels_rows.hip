@@ -355,7 +355,7 @@ hipError_t launch_layernorm(float* x, const float* gamma, const float* beta,
 // Pooling (bert.go:657-703): one thread per (text, column). CLS / last token
 // copy a row; mean sums the column over the text's rows in ascending order
 // in float32 (poolMean's order), then multiplies by float32(1/len). The
-// column loop is unrolled so the independent row loads overlap.
+// row loads run a register block ahead of the sum.
 __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x, int H,
                                                    const int32_t* __restrict__ cu,
                                                    int pooling, float* __restrict__ out) {
@@ -370,14 +370,29 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x, 
     v = x[(size_t)(r0 + len - 1) * H + j];
   } else {
     const float* col = x + (size_t)r0 * H + j;
+    // ascending rows; the loads run a block of U rows ahead of the sum
+    constexpr int U = 32;
     float s = 0.0f;
     int i = 0;
-    for (; i + 8 <= len; i += 8) {
-      float t[8];
+    float ta[U], tb[U];
+    auto fill = [&](float (&t)[U], int i0) {
 #pragma unroll
-      for (int e = 0; e < 8; e++) t[e] = col[(size_t)(i + e) * H];
+      for (int e = 0; e < U; e++) t[e] = col[(size_t)(i0 + e) * H];
+    };
+    auto sum = [&](const float (&t)[U]) {
 #pragma unroll
-      for (int e = 0; e < 8; e++) s += t[e];
+      for (int e = 0; e < U; e++) s += t[e];
+    };
+    if (len >= U) fill(ta, 0);
+    for (; i + 2 * U <= len; i += 2 * U) {
+      fill(tb, i + U);
+      sum(ta);
+      if (i + 3 * U <= len) fill(ta, i + 2 * U);
+      sum(tb);
+    }
+    if (i + U <= len) {  // one loaded block left
+      sum(ta);
+      i += U;
     }
     for (; i < len; i++) s += col[(size_t)i * H];
     v = s * (1.0f / (float)len);
