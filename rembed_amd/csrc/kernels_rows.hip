@@ -230,7 +230,9 @@ __global__ __launch_bounds__(256) void add_ln_kernel(
 // 4(l + 64e) .. +3. With ph the normalized row also goes to the bf16 hi/lo
 // planes [m][ldp] of the next weight-only int8 / fp32 GEMM's input (pl may
 // be null).
-template <int V>
+// R rows per wave: every row's loads are issued before the first row's
+// reductions.
+template <int V, int R = 1>
 __global__ __launch_bounds__(256) void add_ln_vec_kernel(
     float* __restrict__ x, const float* __restrict__ y, int ldy,
     const float* __restrict__ gamma, const float* __restrict__ beta, int m,
@@ -238,22 +240,32 @@ __global__ __launch_bounds__(256) void add_ln_vec_kernel(
     float* __restrict__ row_scales, __bf16* __restrict__ ph, __bf16* __restrict__ pl,
     int ldp) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= m) return;
-  float* xr = x + (size_t)row * H;
-  const float* yr = y ? y + (size_t)row * ldy : nullptr;
-  v4f v[V];
+  const int row0 = (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * R;
+  if (row0 >= m) return;
+  v4f v[R][V];
 #pragma unroll
-  for (int e = 0; e < V; e++) {
-    const int j = (lane + 64 * e) * 4;
-    v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (j < H) {
-      t = *reinterpret_cast<const v4f*>(xr + j);
-      if (yr) t = t + *reinterpret_cast<const v4f*>(yr + j);  // Add, tensor.go:383-387
+  for (int r = 0; r < R; r++) {
+    const int row = row0 + r < m ? row0 + r : row0;
+    const float* xr = x + (size_t)row * H;
+    const float* yr = y ? y + (size_t)row * ldy : nullptr;
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int j = (lane + 64 * e) * 4;
+      v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (j < H) {
+        t = *reinterpret_cast<const v4f*>(xr + j);
+        if (yr) t = t + *reinterpret_cast<const v4f*>(yr + j);  // Add, tensor.go:383-387
+      }
+      v[r][e] = t;
     }
-    v[e] = t;
   }
-  ln_vec_finish<V>(v, lane, row, H, gamma, beta, eps, xr, qa, ldq, row_scales, ph, pl, ldp);
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = row0 + r;
+    if (row < m)
+      ln_vec_finish<V>(v[r], lane, row, H, gamma, beta, eps, x + (size_t)row * H, qa, ldq,
+                       row_scales, ph, pl, ldp);
+  }
 }
 
 // Embeddings + LayerNorm, float4 rows (H % 4 == 0, 16-byte aligned tables).
@@ -316,8 +328,10 @@ template <int V>
 static void launch_alnv(float* x, const float* y, int ldy, const float* gamma,
                         const float* beta, int m, int H, float eps, uint8_t* qa, int ldq,
                         float* rs, __bf16* ph, __bf16* pl, int ldp, hipStream_t s) {
-  hipLaunchKernelGGL((add_ln_vec_kernel<V>), dim3(ceil_div(m, kRowsPerBlock)), dim3(256),
-                     0, s, x, y, ldy, gamma, beta, m, H, eps, qa, ldq, rs, ph, pl, ldp);
+  constexpr int R = 2;
+  hipLaunchKernelGGL((add_ln_vec_kernel<V, R>), dim3(ceil_div(m, kRowsPerBlock * R)),
+                     dim3(256), 0, s, x, y, ldy, gamma, beta, m, H, eps, qa, ldq, rs, ph, pl,
+                     ldp);
 }
 
 hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
