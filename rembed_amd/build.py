@@ -59,23 +59,7 @@ def build(verbose=True):
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
-    build_devprobe()
     return LIB
-
-
-PROBE_SRC = os.path.join(HERE, "devprobe", "devprobe.hip")
-PROBE = os.path.join(HERE, "devprobe", "devprobe")
-
-
-def build_devprobe():
-    """The device-probe microbenchmark (a standalone executable; not linked
-    into the library)."""
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", PROBE_SRC, "-o", PROBE]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {PROBE_SRC}:\n{r.stderr}")
-    return PROBE
 
 
 if __name__ == "__main__":
