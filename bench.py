@@ -190,13 +190,14 @@ def oracle_u8_sensitivity(shape, tensors, ids, lens, texts=4):
     return rows
 
 
-def u8_byte_diffs(ctx, shape, tensors, ids, lens, texts=4, precisions=(1, 3)):
+def u8_byte_diffs(ctx, shape, tensors, ids, lens, texts=4, precisions=(1, 3, "exact")):
     """Per layer, the u8 bytes of the next layer's activation rows
     (QuantizeRowU8 of the hidden states after layer L, pack_vnni.go:85-117)
     that differ between the device's full-int8 forward and the oracle's, over
-    the first `texts` texts, for each attention precision: device models of
-    1..L layers, the oracle stopped after L layers, both sides quantized by
-    the oracle's quantizer."""
+    the first `texts` texts, for each attention precision and for the
+    byte-exact forward (RH_OPT_EXACT): device models of 1..L layers, the
+    oracle stopped after L layers, both sides quantized by the oracle's
+    quantizer."""
     import dataclasses
 
     from oracle import oracle as O
@@ -209,14 +210,19 @@ def u8_byte_diffs(ctx, shape, tensors, ids, lens, texts=4, precisions=(1, 3)):
         want = [_u8_rows(orc.encode(ids[t, :lens[t]], L)) for t in range(texts)]
         total = sum(w.size for w in want)
         for p in precisions:
-            m.set_attention_precision(p)
+            if p == "exact":
+                m.set_exact(True)
+            else:
+                m.set_exact(False)
+                m.set_attention_precision(p)
             toks = m.embed_tokens(ids[:texts], lens[:texts])
             rows[p].append(sum(int(np.count_nonzero(_u8_rows(toks[t]) != want[t]))
                                for t in range(texts)))
         m.close()
     orc.close()
-    return {"per_layer_bytes_differing": {f"attention_precision_{p}": rows[p]
-                                          for p in precisions},
+    return {"per_layer_bytes_differing": {
+                (f"attention_precision_{p}" if p != "exact" else "exact_forward"): rows[p]
+                for p in precisions},
             "bytes_per_layer": total, "texts": texts,
             "what": "QuantizeRowU8 of the hidden states after each layer (the next "
                     "layer's u8 q|k|v input), device full-int8 forward vs the oracle's"}
@@ -284,6 +290,11 @@ def main():
     ctx = T.Context(0)
     model = Model(ctx, shape, tensors, quant)
     model.set_streams(args.streams)
+    bert = "embeddings.position_embeddings.weight" in tensors  # the BERT family
+    # `value` runs attention in float32-grade arithmetic (the three-term bf16
+    # split), the reference's float32 attention class; bf16 operands and the
+    # reference-order (byte-exact) forward are timed beside it.
+    model.set_attention_precision(3)
     if quant == 2:
         assert model.quantized_activations(), "full-int8 path did not take"
         model.set_fused_ffn1(args.ffn1 == "fused")
@@ -313,21 +324,29 @@ def main():
     step_ms = ev.step_ms()
     model.check()
 
-    # The same K steps with fp32-grade attention (three-term bf16 split),
-    # the reference's float32 attention arithmetic class, reported beside
-    # `value` (the default for the quantized modes is bf16 operands).
-    attn3_rate = None
-    if quant != 0 and not args.forwards_only:
-        model.set_attention_precision(3)
+    def rate_with(setup, undo):
+        """tokens/s of K more steps with the model reconfigured by setup()."""
+        setup()
         model.embed_device(ids_dev, lens, BATCH, SEQ, out_dev)
         ctx.sync()
         t2 = time.perf_counter()
         for _ in range(args.steps):
             model.embed_device(ids_dev, lens, BATCH, SEQ, out_dev)
         ctx.sync()
-        attn3_rate = tokens * args.steps / (time.perf_counter() - t2)
-        model.set_attention_precision(1)
+        r = tokens * args.steps / (time.perf_counter() - t2)
+        undo()
         model.check()
+        return r
+
+    # Beside `value`: bf16 attention operands (fp32 softmax and accumulation),
+    # and for the BERT family the byte-exact forward (RH_OPT_EXACT: LayerNorm
+    # sums and attention in the reference's own float32 order).
+    attn1_rate = exact_rate = None
+    if quant != 0 and not args.forwards_only:
+        attn1_rate = rate_with(lambda: model.set_attention_precision(1),
+                               lambda: model.set_attention_precision(3))
+    if bert and not args.forwards_only:
+        exact_rate = rate_with(lambda: model.set_exact(True), lambda: model.set_exact(False))
 
     # The roofline: the same K steps again with a HIP event pair attached to
     # every GEMM / attention / split dispatch (the library's profiler, on
@@ -378,14 +397,9 @@ def main():
     cfg_note = {"streams": args.streams}
     if quant == 2:
         cfg_note["ffn1"] = args.ffn1
-    if quant != 0:
-        # what the quantized forward computes besides its int8 GEMMs
-        cfg_note["attention"] = ("bf16 MFMA operands, fp32 softmax and accumulation "
-                                 "(RH_OPT_ATTN_PRECISION 1)")
-        if quant == 2:
-            cfg_note["qkv_rows"] = "bf16 (the q|k|v GEMM's epilogue rounds to the attention operands)"
-    else:
-        cfg_note["attention"] = "three-term bf16 split, fp32-grade (RH_OPT_ATTN_PRECISION 3)"
+        cfg_note["qkv_rows"] = "fp32"
+    cfg_note["attention"] = ("fp32-grade: q|k|v and P split into bf16 hi/lo, three MFMA "
+                             "products, fp32 softmax and accumulation (RH_OPT_ATTN_PRECISION 3)")
     norms = np.linalg.norm(vec.astype(np.float64), axis=1)
     assert np.all(np.abs(norms - 1) < 1e-4), "embeddings are not unit vectors"
 
@@ -395,7 +409,6 @@ def main():
         traffic = json.load(open(tpath)).get("bytes_per_launch")
 
     u8diff = None
-    bert = "embeddings.position_embeddings.weight" in tensors  # the BERT oracle's layer stops
     if quant == 2 and bert and not (args.no_cpu_baseline or args.no_u8_diff or args.forwards_only):
         log("comparing u8 activations with the oracle, layer by layer")
         u8diff = u8_byte_diffs(ctx, shape, tensors, ids, lens)
@@ -455,7 +468,8 @@ def main():
                     "p90": round(pct(step_ms, 90), 4), "steps": int(step_ms.size),
                     "clock": "HIP events between steps on the library stream"},
         "median_tokens_per_s": round(tokens / (pct(step_ms, 50) * 1e-3), 1),
-        "fp32_attention_tokens_per_s": None if attn3_rate is None else round(attn3_rate, 1),
+        "bf16_attention_tokens_per_s": None if attn1_rate is None else round(attn1_rate, 1),
+        "exact_tokens_per_s": None if exact_rate is None else round(exact_rate, 1),
         "pcie_inclusive_tokens_per_s": None if host_rate is None else round(host_rate, 1),
         "pcie_inclusive_step_ms": None if not host_ms else {
             "median": round(pct(host_ms, 50), 4), "p10": round(pct(host_ms, 10), 4),

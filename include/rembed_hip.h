@@ -119,7 +119,11 @@ int rh_profile_read(rh_context *ctx, int kind, rh_profile_stat *out);
  * q_off + h*dh, its kv head h / (heads/kv_heads) at k_off / v_off.
  * causal: key j visible to query i only if j <= i; window > 0: only if
  * |i - j| < window. precision 1: bf16 MFMA operands; 3: hi/lo bf16 split,
- * fp32-grade (f32 input only). out is f32 [M][ldout], head h at h*dh.
+ * fp32-grade (f32 input only); 4: the reference's own float32 order
+ * (MatMulSerial's dot4 and remainder columns, Softmax with expNonPos;
+ * tensor.go:284-330,389-428, dot_amd64.s:13-94), bit-identical to it (f32
+ * input, no mask, heads == kv_heads, dh 32/64/128). out is f32 [M][ldout],
+ * head h at h*dh.
  * dh in {32, 64, 128, 256}; ldqkv and the offsets multiples of 8, ldout of 4.
  * Enqueued on the context's stream. */
 int rh_attention(rh_context *ctx, const void *qkv, int in_bf16, int ldqkv, int q_off,
@@ -248,8 +252,11 @@ int rh_linear_noalloc(rh_context *ctx, float *dst, const float *a, const rh_weig
 
 /* Elementwise entry points used by parity tests (dev pointers). */
 int rh_gelu(rh_context *ctx, float *x, size_t n);          /* tensor.go:508-538 */
+/* LayerNorm (tensor.go:433-452). Bit-identical to the reference (float32
+ * sums in column order) for n % 4 == 0, n <= 1024 and 16-byte aligned
+ * pointers; other shapes reduce across a wave (within float32 rounding). */
 int rh_layernorm(rh_context *ctx, float *x, const float *gamma,
-                 const float *beta, int m, int n, float eps); /* tensor.go:433-452 */
+                 const float *beta, int m, int n, float eps);
 
 /* ---- encoder model ------------------------------------------------------------
  * Replaces model.Load + Model.Forward/ForwardTokens + the Embed batch loop
@@ -353,7 +360,14 @@ void rh_model_destroy(rh_model *m);
  * finishes whole rows in its epilogue: residual add, LayerNorm and the next
  * int8 GEMM's u8 quantization in the same kernel, 0 = the linear writes
  * fp32 rows and a separate residual + LayerNorm pass follows (default:
- * measured faster); identical results. */
+ * measured faster); identical results.
+ * RH_OPT_EXACT (BERT family): 1 = LayerNorm's mean and variance are float32
+ * sums in column order (tensor.go:433-452) and attention runs in the
+ * reference's float32 order on fp32 q|k|v rows (MatMulSerial/dot4,
+ * Softmax; bert.go:853-902), so a full-int8 forward's activations, GEMM
+ * inputs and vectors are byte-identical to the reference's; 0 = the
+ * wave-parallel LayerNorm and the RH_OPT_ATTN_PRECISION attention (default).
+ * The fused-LN epilogue is not used while it is set. */
 #define RH_OPT_ATTN_PRECISION 1
 #define RH_OPT_FUSED_FFN1 2
 #define RH_OPT_PRODUCER_PLANES 3
@@ -361,6 +375,7 @@ void rh_model_destroy(rh_model *m);
 #define RH_OPT_QK_EPILOGUE 5
 #define RH_OPT_FUSE_PROJECTIONS 6
 #define RH_OPT_FUSED_LN 7
+#define RH_OPT_EXACT 8
 int rh_model_set_option(rh_model *m, int option, int value);
 /* Model.Quantized / QuantizedActivations (bert.go:526-644). */
 int rh_model_quantized(const rh_model *m);

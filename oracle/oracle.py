@@ -237,6 +237,43 @@ def layernorm(x, g, b, eps):
     return x
 
 
+def matmul_serial(a, bT):
+    """MatMulSerial (tensor.go:284-330): dot4 over column quads, in-order
+    scalar sums for the n % 4 remainder columns."""
+    a, bT = f32(a), f32(bT)
+    m, k = a.shape
+    n = bT.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib.or_matmul_serial(_p(out), _p(a), _p(bT), m, k, n)
+    return out
+
+
+def softmax(x):
+    """Softmax (tensor.go:389-428) over the rows of x."""
+    x = f32(x).copy()
+    m, n = x.shape
+    lib.or_softmax(_p(x), m, n)
+    return x
+
+
+def attention_ref(qkv, lens, heads, dh, scale, q_off, k_off, v_off):
+    """bert.go:853-902 per text and head: scores = MatMulSerial(Qh, Kh),
+    scores *= scale (float32), Softmax, ctx = MatMulSerial(P, Vhᵀ)."""
+    qkv = f32(qkv)
+    out = np.zeros((qkv.shape[0], heads * dh), np.float32)
+    r0 = 0
+    for L in lens:
+        rows = slice(r0, r0 + L)
+        for h in range(heads):
+            q = qkv[rows, q_off + h * dh:q_off + (h + 1) * dh]
+            k = qkv[rows, k_off + h * dh:k_off + (h + 1) * dh]
+            v = qkv[rows, v_off + h * dh:v_off + (h + 1) * dh]
+            sc = matmul_serial(q, k) * np.float32(scale)
+            out[rows, h * dh:(h + 1) * dh] = matmul_serial(softmax(sc), np.ascontiguousarray(v.T))
+        r0 += L
+    return out
+
+
 # ---- BERT model ------------------------------------------------------------------
 
 class BertConfig(ctypes.Structure):

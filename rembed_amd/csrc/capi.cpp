@@ -837,8 +837,12 @@ int rh_attention(rh_context* ctx, const void* qkv, int in_bf16, int ldqkv, int q
       return fail(RH_ERR_SHAPE, "attention head dim must be 32, 64, 128 or 256");
     if (heads < 1 || kv_heads < 1 || heads % kv_heads)
       return fail(RH_ERR_SHAPE, "heads must be a positive multiple of kv_heads");
-    if (precision != 1 && precision != 3) return fail(RH_ERR_INVALID, "precision must be 1 or 3");
+    if (precision != 1 && precision != 3 && precision != 4)
+      return fail(RH_ERR_INVALID, "precision must be 1, 3 or 4");
     if (in_bf16 && precision != 1) return fail(RH_ERR_INVALID, "bf16 input takes precision 1");
+    if (precision == 4 && (causal || window || heads != kv_heads || dh == 256))
+      return fail(RH_ERR_INVALID,
+                  "reference-order attention: no mask, heads == kv_heads, dh 32, 64 or 128");
     if (batch < 0 || max_len < 0 || window < 0) return fail(RH_ERR_INVALID, "negative size");
     if (ldqkv % 8 || q_off % 8 || k_off % 8 || v_off % 8 || ldout % 4 || q_off < 0 ||
         k_off < 0 || v_off < 0 || ((uintptr_t)qkv & 15) || ((uintptr_t)out & 15))
@@ -864,7 +868,8 @@ int rh_attention(rh_context* ctx, const void* qkv, int in_bf16, int ldqkv, int q
     a.window = window;
     int slot = -1;
     RH_HIP(ctx->prof_begin(3, 0.0, 0.0, &slot));
-    RH_HIP(launch_attention(a, precision, ctx->stream));
+    if (precision == 4) RH_HIP(launch_attention_exact(a, ctx->stream));
+    else RH_HIP(launch_attention(a, precision, ctx->stream));
     RH_HIP(ctx->prof_end(slot));
     return RH_OK;
   });
@@ -1225,7 +1230,12 @@ int rh_layernorm(rh_context* ctx, float* x, const float* gamma, const float* bet
     if (m < 0 || n < 1 || n > 2048) return fail(RH_ERR_INVALID, "bad shape (n <= 2048)");
     if (m > 0 && (!x || !gamma || !beta)) return fail(RH_ERR_INVALID, "null argument");
     CTX_GUARD(ctx);
-    RH_HIP(launch_layernorm(x, gamma, beta, m, n, eps, ctx->stream));
+    // the reference's column-order sums where the row layout allows
+    // (every model width); wave-parallel sums otherwise
+    const bool exact = n % 4 == 0 && n <= 1024 &&
+                       (((uintptr_t)x | (uintptr_t)gamma | (uintptr_t)beta) & 15) == 0;
+    RH_HIP(launch_add_layernorm(x, nullptr, 0, gamma, beta, m, n, eps, nullptr, 0, nullptr,
+                                ctx->stream, nullptr, nullptr, 0, exact));
     return RH_OK;
   });
 }

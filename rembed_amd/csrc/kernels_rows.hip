@@ -305,6 +305,151 @@ __global__ __launch_bounds__(256) void embed_ln_vec_kernel(EmbedArgs p, int tota
                    p.qa, p.ldq, p.row_scales, p.ph, p.pl, p.ldp);
 }
 
+// ---- LayerNorm in the reference's own order ---------------------------------
+// tensor.go:433-452 sums each row left to right in float32: once for the mean,
+// once for the variance (d*d rounded, then added). R rows per one-wave
+// workgroup: the rows arrive coalesced in registers (lane l holds columns
+// 4(l + 64e) .. +3) and are parked in LDS; lane r < R walks row r's two sums
+// serially (the only serial part); the normalization itself runs coalesced
+// again (ln_vec_apply). inv = 1/float32(sqrt(float64(var+eps))).
+template <int V, int R>
+__device__ __forceinline__ void ln_exact_rows(v4f (&v)[R][V], int row0, int nrows, int H,
+                                              float eps, const float* __restrict__ gamma,
+                                              const float* __restrict__ beta, float* x,
+                                              uint8_t* qa, int ldq, float* rs, __bf16* ph,
+                                              __bf16* pl, int ldp) {
+  // row pitch: 16 bytes past a multiple of 1 KiB, so the R lanes' float4
+  // reads of one column group fall in distinct banks
+  constexpr int S = V * 256 + 4;
+  __shared__ __attribute__((aligned(16))) float rowbuf[R * S];
+  __shared__ float stat[2 * R];
+  const int lane = threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int j = (lane + 64 * e) * 4;
+      if (j < H) *reinterpret_cast<v4f*>(rowbuf + r * S + j) = v[r][e];
+    }
+  __syncthreads();
+  if (lane < R) {  // mean: sum in column order, then / n
+    const float* rp = rowbuf + lane * S;
+    float s = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < H; j += 4) {
+      const v4f a = *reinterpret_cast<const v4f*>(rp + j);
+      s = s + a[0];
+      s = s + a[1];
+      s = s + a[2];
+      s = s + a[3];
+    }
+    stat[lane] = s / (float)H;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const float mean = stat[r];
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int j = (lane + 64 * e) * 4;
+      if (j < H) {
+        const v4f d = v[r][e] - mean;
+        *reinterpret_cast<v4f*>(rowbuf + r * S + j) = d * d;
+      }
+    }
+  }
+  __syncthreads();
+  if (lane < R) {  // variance: the rounded squares summed in column order
+    const float* rp = rowbuf + lane * S;
+    float s = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < H; j += 4) {
+      const v4f a = *reinterpret_cast<const v4f*>(rp + j);
+      s = s + a[0];
+      s = s + a[1];
+      s = s + a[2];
+      s = s + a[3];
+    }
+    const float var = s / (float)H;
+    stat[R + lane] = 1.0f / (float)sqrt((double)(var + eps));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    if (r < nrows) {
+      const int row = row0 + r;
+      ln_vec_apply<V>(v[r], lane, row, H, stat[r], stat[R + r], gamma, beta,
+                      x + (size_t)row * H, qa, ldq, rs, ph, pl, ldp);
+    }
+  }
+}
+
+template <int V, int R>
+__global__ __launch_bounds__(64) void add_ln_exact_kernel(
+    float* __restrict__ x, const float* __restrict__ y, int ldy,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int m, int H, float eps,
+    uint8_t* __restrict__ qa, int ldq, float* __restrict__ row_scales,
+    __bf16* __restrict__ ph, __bf16* __restrict__ pl, int ldp) {
+  const int lane = threadIdx.x;
+  const int row0 = blockIdx.x * R;
+  v4f v[R][V];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = row0 + r;
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int j = (lane + 64 * e) * 4;
+      v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (row < m && j < H) {
+        t = *reinterpret_cast<const v4f*>(x + (size_t)row * H + j);
+        if (y) t = t + *reinterpret_cast<const v4f*>(y + (size_t)row * ldy + j);  // Add
+      }
+      v[r][e] = t;
+    }
+  }
+  ln_exact_rows<V, R>(v, row0, min(R, m - row0), H, eps, gamma, beta, x, qa, ldq, row_scales,
+                      ph, pl, ldp);
+}
+
+template <int V, int R>
+__global__ __launch_bounds__(64) void embed_ln_exact_kernel(EmbedArgs p, int total) {
+  const int lane = threadIdx.x;
+  const int row0 = blockIdx.x * R;
+  v4f v[R][V];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = min(row0 + r, total - 1);
+    int b = 0;
+    for (int base = 1; base < p.batch; base += 64) {
+      const int i = base + lane;
+      b += __popcll(__ballot(i < p.batch && p.cu[i] <= row));
+    }
+    const int t = row - p.cu[b];
+    int id = p.ids[(size_t)b * p.stride + t];
+    if (id < 0 || id >= p.vocab) {
+      if (lane == 0) *p.err_flag = 1;
+      id = id < 0 ? 0 : p.vocab - 1;  // stay in bounds; the call reports failure
+    }
+    const float* w = p.word + (size_t)id * p.H;
+    const float* ps = p.pos + (size_t)(t + p.pos_off) * p.H;
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int j = (lane + 64 * e) * 4;
+      v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (j < p.H) {
+        // bert.go:801-812: row = w + p (+ t)
+        a = *reinterpret_cast<const v4f*>(w + j) + *reinterpret_cast<const v4f*>(ps + j);
+        if (p.type0) a = a + *reinterpret_cast<const v4f*>(p.type0 + j);
+      }
+      v[r][e] = a;
+    }
+  }
+  ln_exact_rows<V, R>(v, row0, min(R, total - row0), p.H, p.eps, p.gamma, p.beta, p.x, p.qa,
+                      p.ldq, p.row_scales, p.ph, p.pl, p.ldp);
+}
+
+constexpr int kExactRows = 8;  // rows per one-wave workgroup of the exact LayerNorm
+
 hipError_t launch_embed_layernorm(const EmbedArgs& a, int total, hipStream_t s) {
   if (total <= 0) return hipSuccess;
   if (a.H > 64 * kMaxPerLane) return hipErrorInvalidValue;
@@ -314,8 +459,18 @@ hipError_t launch_embed_layernorm(const EmbedArgs& a, int total, hipStream_t s) 
                      reinterpret_cast<uintptr_t>(a.beta) | reinterpret_cast<uintptr_t>(a.x)) &
                     15) == 0;
   if (a.ph && (!vec || a.ldp % 64 || a.ldp < a.H)) return hipErrorInvalidValue;
-  const dim3 grid(ceil_div(total, kRowsPerBlock)), block(256);
   const int v = ceil_div(a.H, 256);
+  if (a.exact) {
+    if (!vec || v > 4) return hipErrorInvalidValue;
+    constexpr int R = kExactRows;
+    const dim3 g(ceil_div(total, R)), b(64);
+    if (v <= 1) hipLaunchKernelGGL((embed_ln_exact_kernel<1, R>), g, b, 0, s, a, total);
+    else if (v <= 2) hipLaunchKernelGGL((embed_ln_exact_kernel<2, R>), g, b, 0, s, a, total);
+    else if (v <= 3) hipLaunchKernelGGL((embed_ln_exact_kernel<3, R>), g, b, 0, s, a, total);
+    else hipLaunchKernelGGL((embed_ln_exact_kernel<4, R>), g, b, 0, s, a, total);
+    return hipGetLastError();
+  }
+  const dim3 grid(ceil_div(total, kRowsPerBlock)), block(256);
   if (vec && v <= 1) hipLaunchKernelGGL((embed_ln_vec_kernel<1>), grid, block, 0, s, a, total);
   else if (vec && v <= 2) hipLaunchKernelGGL((embed_ln_vec_kernel<2>), grid, block, 0, s, a, total);
   else if (vec && v <= 3) hipLaunchKernelGGL((embed_ln_vec_kernel<3>), grid, block, 0, s, a, total);
@@ -338,7 +493,7 @@ hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
                                 const float* gamma, const float* beta, int m,
                                 int H, float eps, uint8_t* qa, int ldq,
                                 float* row_scales, hipStream_t s, __bf16* ph, __bf16* pl,
-                                int ldp) {
+                                int ldp, bool exact) {
   if (m <= 0) return hipSuccess;
   if (H > 64 * kMaxPerLane) return hipErrorInvalidValue;
   const bool vec = H % 4 == 0 && (!y || ldy % 4 == 0) && (!qa || ldq % 4 == 0) &&
@@ -346,6 +501,21 @@ hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
                      reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) &
                     15) == 0;
   if (ph && (!vec || ldp % 64 || ldp < H)) return hipErrorInvalidValue;
+  if (exact) {
+    const int v = ceil_div(H, 256);
+    if (!vec || v > 4) return hipErrorInvalidValue;
+    constexpr int R = kExactRows;
+    const dim3 g(ceil_div(m, R)), b(64);
+#define RH_ALNX(V)                                                                         \
+  hipLaunchKernelGGL((add_ln_exact_kernel<V, R>), g, b, 0, s, x, y, ldy, gamma, beta, m, H, \
+                     eps, qa, ldq, row_scales, ph, pl, ldp)
+    if (v <= 1) RH_ALNX(1);
+    else if (v <= 2) RH_ALNX(2);
+    else if (v <= 3) RH_ALNX(3);
+    else RH_ALNX(4);
+#undef RH_ALNX
+    return hipGetLastError();
+  }
   if (vec) {
     const int v = ceil_div(H, 256);
     if (v <= 1) launch_alnv<1>(x, y, ldy, gamma, beta, m, H, eps, qa, ldq, row_scales, ph, pl, ldp, s);
@@ -415,21 +585,30 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x, 
 }
 
 // L2Normalize (tensor.go:540-554) of each [H] row in place: float64 sum of
-// squares, scale by float32(1/sqrt(sum)); an all-zero row is left as is.
+// squares in column order (the squares of float32 values are exact in
+// float64; one lane adds them as the reference's loop does), scale by
+// float32(1/sqrt(sum)); an all-zero row is left as is.
 __global__ __launch_bounds__(256) void l2_rows_kernel(float* __restrict__ y, int H) {
-  __shared__ double red[256];
+  __shared__ double sq[2048];
+  __shared__ float inv_s;
+  __shared__ int zero_s;
   float* o = y + (size_t)blockIdx.x * H;
-  double ss = 0.0;
-  for (int j = threadIdx.x; j < H; j += 256) ss += (double)o[j] * (double)o[j];
-  red[threadIdx.x] = ss;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+  double sum = 0.0;
+  for (int j0 = 0; j0 < H; j0 += 2048) {  // 2048 columns at a time through LDS
+    const int n = min(2048, H - j0);
+    for (int j = threadIdx.x; j < n; j += 256) sq[j] = (double)o[j0 + j] * (double)o[j0 + j];
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int j = 0; j < n; j++) sum = sum + sq[j];
     __syncthreads();
   }
-  const double sum = red[0];
-  if (sum == 0.0) return;
-  const float inv = (float)(1.0 / sqrt(sum));
+  if (threadIdx.x == 0) {
+    zero_s = sum == 0.0;
+    inv_s = (float)(1.0 / sqrt(sum));
+  }
+  __syncthreads();
+  if (zero_s) return;
+  const float inv = inv_s;
   for (int j = threadIdx.x; j < H; j += 256) o[j] = o[j] * inv;
 }
 

@@ -134,6 +134,10 @@ struct rh_model {
   int32_t* pos_d = nullptr;
   int attn_precision = 3;
   bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
+  // RH_OPT_EXACT (BERT family): LayerNorm's sums and attention in the
+  // reference's own float32 order (fp32 q|k|v rows), so a full-int8 forward
+  // is byte-identical to the reference's
+  bool exact = false;
   // RH_OPT_FUSED_LN: off by default; measured slower on BERT-base int8 at
   // M = 10102 (2.947 vs 2.864 ms/step with two streams, 3.05 vs 2.97 with
   // one): the whole-row tiles give 158 workgroups for 256 CUs, one per CU,
@@ -293,7 +297,7 @@ struct rh_model {
   // with its fragment image, a supported width, and a next GEMM that takes
   // u8 rows or nothing rather than bf16 planes.)
   bool fuse_ln(const rh_weight* w, bool consumer_planes) const {
-    return fused_ln && w && w->mode == RH_MODE_A8W8 && w->d_frag && !w->glu &&
+    return fused_ln && !exact && w && w->mode == RH_MODE_A8W8 && w->d_frag && !w->glu &&
            w->n == cfg.hidden && gemm_i8_ln_supported(w->n, w->k) && !consumer_planes;
   }
   I8LnArgs ln_args(float* xp, const float* g, const float* b, uint8_t* qa_out, int ldq,
@@ -547,6 +551,7 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
   ea.ldq = ldq_for(H);
   ea.row_scales = q0 ? rs : nullptr;
   ea.err_flag = err_d;
+  ea.exact = exact;
   // the first QKV's planes, when it takes them
   const bool p0 = !layers.empty() && planes_in(layers[0].qkv);
   if (p0) {
@@ -603,7 +608,7 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     // weight is full-int8. When attention runs on bf16 operands, a full-int8
     // QKV writes bf16 directly (attention would round the fp32 values to the
     // same bf16 on load), halving the write.
-    const bool qkv_bf16 = needs_q(L.qkv) && attn_precision == 1;
+    const bool qkv_bf16 = needs_q(L.qkv) && attn_precision == 1 && !exact;
     if (qkv_bf16) {
       st = run_gemm_i8(ctx, L.qkv, qap, ldq_for(H), rsp, Mp, EPI_BF16, qkvh + r0 * 3 * H,
                        3 * H, ACT_NONE, L.qkv->d_bias, nullptr, nullptr, 2.0 * MH * H * 3 * H);
@@ -637,7 +642,8 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     aa.ldctx = po ? pov.ld : H;
     int slot = -1;
     RH_HIP(ctx->prof_begin(3, part_attn_ops(P), 0.0, &slot));
-    RH_HIP(launch_attention(aa, attn_precision, ps));
+    if (exact) RH_HIP(launch_attention_exact(aa, ps));
+    else RH_HIP(launch_attention(aa, attn_precision, ps));
     RH_HIP(ctx->prof_end(slot));
     const Planes povp = at(pov);
     const bool qf1 = needs_q(L.f1);
@@ -658,7 +664,8 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
       if (st) return st;
       RH_HIP(launch_add_layernorm(xp, yp, H, L.ln1_g, L.ln1_b, Mp, H, eps(),
                                   qf1 ? qap : nullptr, ldq_for(H), qf1 ? rsp : nullptr, ps,
-                                  pf1 ? pf1v.hi : nullptr, pf1 ? pf1v.lo : nullptr, pf1v.ld));
+                                  pf1 ? pf1v.hi : nullptr, pf1 ? pf1v.lo : nullptr, pf1v.ld,
+                                  exact));
     }
     const bool last = li + 1 == layers.size();
     const bool qn = !last && needs_q(layers[li + 1].qkv);
@@ -720,7 +727,7 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
       RH_HIP(launch_add_layernorm(xp, yp, H, L.ln2_g, L.ln2_b, Mp, H, eps(),
                                   qn ? qap : nullptr, ldq_for(H), qn ? rsp : nullptr, ps,
                                   xn_planes ? pnv.hi : nullptr, xn_planes ? pnv.lo : nullptr,
-                                  pnv.ld));
+                                  pnv.ld, exact));
     }
     return RH_OK;
   };
@@ -1485,6 +1492,13 @@ int rh_model_set_option(rh_model* m, int option, int value) {
       m->fused_ffn1 = value != 0;
       return RH_OK;
     }
+    if (option == RH_OPT_EXACT) {
+      if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "exact must be 0 or 1");
+      if (value && m->rope_family())
+        return fail(RH_ERR_INVALID, "the exact forward is for the BERT family");
+      m->exact = value != 0;
+      return RH_OK;
+    }
     if (option == RH_OPT_FUSED_LN) {
       if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fused LN must be 0 or 1");
       m->fused_ln = value != 0;
@@ -1591,6 +1605,7 @@ int rh_model_share(rh_model* src, rh_context* ctx, rh_model** out) {
     m->sin_l = src->sin_l;
     m->attn_precision = src->attn_precision;
     m->fused_ffn1 = src->fused_ffn1;
+    m->exact = src->exact;
     m->fused_ln = src->fused_ln;
     m->producer_planes = src->producer_planes;
     m->streams = src->streams;

@@ -296,6 +296,7 @@ struct EmbedArgs {
   __bf16* ph = nullptr;    // optional bf16 hi/lo planes [M][ldp] of the first
   __bf16* pl = nullptr;    // weight-only int8 / fp32 GEMM's input (pl may be
   int ldp = 0;             // null)
+  bool exact = false;      // LayerNorm's sums in the reference's column order
 };
 hipError_t launch_embed_layernorm(const EmbedArgs& a, int total_rows,
                                   hipStream_t s);
@@ -303,11 +304,14 @@ hipError_t launch_embed_layernorm(const EmbedArgs& a, int total_rows,
 // x = LayerNorm(x + y) (bert.go:906-907,917-918); optional u8 quantization
 // of the result for the next full-int8 GEMM, or its bf16 hi/lo planes
 // [m][ldp] (ldp % 64 == 0, >= H) for the next weight-only int8 / fp32 GEMM.
+// exact: the mean and variance are float32 sums in column order, as
+// tensor.go:433-452 takes them (H % 4 == 0, 16-byte aligned rows), so the
+// result is bit-identical to the reference's; otherwise wave-parallel sums.
 hipError_t launch_add_layernorm(float* x, const float* y, int ldy,
                                 const float* gamma, const float* beta, int m,
                                 int H, float eps, uint8_t* qa, int ldq,
                                 float* row_scales, hipStream_t s, __bf16* ph = nullptr,
-                                __bf16* pl = nullptr, int ldp = 0);
+                                __bf16* pl = nullptr, int ldp = 0, bool exact = false);
 // standalone LayerNorm (tests)
 hipError_t launch_layernorm(float* x, const float* gamma, const float* beta,
                             int m, int H, float eps, hipStream_t s);
@@ -337,6 +341,10 @@ struct AttnArgs {
 };
 // precision: 1 = bf16 MFMA, 3 = three-term bf16 split (fp32-grade)
 hipError_t launch_attention(const AttnArgs& a, int precision, hipStream_t s);
+// The same attention in the reference's float32 operation order
+// (MatMulSerial/dot4, Softmax; attention_exact.hip): bit-identical context
+// rows. fp32 q|k|v, no causal or window mask, heads == kv_heads, dh 32/64/128.
+hipError_t launch_attention_exact(const AttnArgs& a, hipStream_t s);
 
 // ---- RoPE-family row kernels (kernels_dec.hip) ------------------------------
 // Token embeddings only (positions enter through RoPE): x[r] = word[id] * scale
@@ -387,7 +395,8 @@ hipError_t launch_dense_head(const float* pooled, int batch, int H, int D, const
 // gated-MLP glue for gate and up packed as separate weights.
 hipError_t launch_glu_rows(const float* gate, const float* up, float* out, size_t n, int act,
                            hipStream_t s);
-// L2Normalize (tensor.go:540-554) of `rows` rows of [H] in place.
+// L2Normalize (tensor.go:540-554) of `rows` rows of [H] in place: the
+// float64 sum of squares in column order, as the reference takes it.
 hipError_t launch_l2_rows(float* y, int rows, int H, hipStream_t s);
 
 }  // namespace rh

@@ -30,35 +30,20 @@ __device__ __forceinline__ uint8_t quant_u8(float v, float inv) {
   return (uint8_t)q;
 }
 
-// LayerNorm of the row held as float4 in v[] (lane l holds columns
-// 4(l + 64e) .. +3; zeros past H), written to xr, optionally to the bf16
-// hi/lo planes [..][ldp] of the next weight-only int8 / fp32 GEMM (pl may be
-// null) and quantized into qa/row_scales (tensor.go:433-452: biased
-// variance, inv = 1/float32(sqrt(var+eps)), out = (v-mean)*inv*g + b; the
-// sums run per lane over its float4 groups, then across the wave).
+// The elementwise half of LayerNorm (tensor.go:448-451) for the row held as
+// float4 in v[] (lane l holds columns 4(l + 64e) .. +3; zeros past H), given
+// its mean and inv = 1/float32(sqrt(var+eps)): out = (v-mean)*inv*g + b,
+// written to xr, optionally to the bf16 hi/lo planes [..][ldp] of the next
+// weight-only int8 / fp32 GEMM (pl may be null) and quantized into
+// qa/row_scales (QuantizeRowU8).
 template <int V>
-__device__ __forceinline__ void ln_vec_finish(v4f (&v)[V], int lane, int row, int H,
-                                              const float* __restrict__ gamma,
-                                              const float* __restrict__ beta, float eps,
-                                              float* __restrict__ xr, uint8_t* __restrict__ qa,
-                                              int ldq, float* __restrict__ row_scales,
-                                              __bf16* __restrict__ ph, __bf16* __restrict__ pl,
-                                              int ldp) {
-  float s = 0.0f;
-#pragma unroll
-  for (int e = 0; e < V; e++) s += (v[e][0] + v[e][1]) + (v[e][2] + v[e][3]);
-  const float mean = wave_sum(s) / (float)H;
-  float s2 = 0.0f;
-#pragma unroll
-  for (int e = 0; e < V; e++) {
-    const int j = (lane + 64 * e) * 4;
-    if (j < H) {
-      const v4f d = v[e] - mean;
-      s2 += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
-    }
-  }
-  const float var = wave_sum(s2) / (float)H;
-  const float inv = 1.0f / sqrtf(var + eps);
+__device__ __forceinline__ void ln_vec_apply(v4f (&v)[V], int lane, int row, int H, float mean,
+                                             float inv, const float* __restrict__ gamma,
+                                             const float* __restrict__ beta,
+                                             float* __restrict__ xr, uint8_t* __restrict__ qa,
+                                             int ldq, float* __restrict__ row_scales,
+                                             __bf16* __restrict__ ph, __bf16* __restrict__ pl,
+                                             int ldp) {
   float mx = 0.0f;
 #pragma unroll
   for (int e = 0; e < V; e++) {
@@ -92,6 +77,37 @@ __device__ __forceinline__ void ln_vec_finish(v4f (&v)[V], int lane, int row, in
     for (int j = H + lane * 4; j < ldq; j += 256) *reinterpret_cast<uint32_t*>(q + j) = 0u;
     if (lane == 0) row_scales[row] = scale;
   }
+}
+
+// LayerNorm of the row held as float4 in v[] (layout as ln_vec_apply), with
+// the mean and variance reduced across the wave (per lane over its float4
+// groups, then a butterfly): biased variance, inv = 1/float32(sqrt(var+eps))
+// (tensor.go:433-452). The sums' order differs from the reference's
+// column-order loop; ln_exact_* keep that order.
+template <int V>
+__device__ __forceinline__ void ln_vec_finish(v4f (&v)[V], int lane, int row, int H,
+                                              const float* __restrict__ gamma,
+                                              const float* __restrict__ beta, float eps,
+                                              float* __restrict__ xr, uint8_t* __restrict__ qa,
+                                              int ldq, float* __restrict__ row_scales,
+                                              __bf16* __restrict__ ph, __bf16* __restrict__ pl,
+                                              int ldp) {
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < V; e++) s += (v[e][0] + v[e][1]) + (v[e][2] + v[e][3]);
+  const float mean = wave_sum(s) / (float)H;
+  float s2 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int j = (lane + 64 * e) * 4;
+    if (j < H) {
+      const v4f d = v[e] - mean;
+      s2 += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+    }
+  }
+  const float var = wave_sum(s2) / (float)H;
+  const float inv = 1.0f / sqrtf(var + eps);
+  ln_vec_apply<V>(v, lane, row, H, mean, inv, gamma, beta, xr, qa, ldq, row_scales, ph, pl, ldp);
 }
 
 }  // namespace rh

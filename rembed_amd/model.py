@@ -123,6 +123,12 @@ class Model:
     def set_attention_precision(self, prec):
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_ATTN_PRECISION, prec))
 
+    def set_exact(self, on=True):
+        """RH_OPT_EXACT (BERT family): LayerNorm's sums and attention in the
+        reference's own float32 order, so a full-int8 forward is
+        byte-identical to the reference's (False: the default kernels)."""
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_EXACT, 1 if on else 0))
+
     def set_fused_ln(self, on=True):
         """RH_OPT_FUSED_LN: full-int8 O / FFN2 projections finish the
         residual add + LayerNorm in their epilogue (identical results)."""
