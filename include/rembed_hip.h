@@ -131,6 +131,18 @@ int rh_attention(rh_context *ctx, const void *qkv, int in_bf16, int ldqkv, int q
                  int kv_heads, int dh, float scale, int causal, int window, int precision,
                  float *out, int ldout);
 
+/* rh_attention at fp32-grade precision with the q|k|v rows given as their
+ * bf16 split: qkv_hi = bf16(x), qkv_lo = bf16(x - hi), both [M][ldqkv] bf16
+ * (what the full-int8 q|k|v projection writes for this attention). Three
+ * bf16 MFMA products per step (hi·hi + hi·lo + lo·hi), fp32 softmax and
+ * accumulation; same masks and layout as rh_attention, dh 32/64/128.
+ * Replaces: the per-text head loops of bert.go:853-902, qwen3.go:319-390,
+ * gemma3.go:318-356, like rh_attention. */
+int rh_attention_planes(rh_context *ctx, const void *qkv_hi, const void *qkv_lo, int ldqkv,
+                        int q_off, int k_off, int v_off, const int32_t *cu, int batch,
+                        int max_len, int heads, int kv_heads, int dh, float scale, int causal,
+                        int window, float *out, int ldout);
+
 /* ---- weights (tensor level) --------------------------------------------------
  * Quantize/pack on the host exactly as the reference does, then upload once
  * to HBM; the handle owns the device copy until rh_weight_destroy.
@@ -333,7 +345,8 @@ int rh_model_finalize(rh_model *m);
 int rh_model_share(rh_model *src, rh_context *ctx, rh_model **out);
 void rh_model_destroy(rh_model *m);
 /* Per-model switches. RH_OPT_ATTN_PRECISION: 1 = bf16 attention operands,
- * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE).
+ * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE and,
+ * in every mode, for RH_ARCH_BERT).
  * RH_OPT_FUSED_FFN1: 1 = full-int8 FFN1 writes u8 rows directly (two GEMM
  * passes, no fp32 intermediate), 0 = fp32 GELU rows then QuantizeRowU8
  * (default); both give identical bytes. RH_OPT_PRODUCER_PLANES: 1 = the

@@ -46,7 +46,7 @@ EXPORTS = [
     "rh_context_destroy", "rh_context_sync", "rh_context_stream",
     "rh_context_set_option", "rh_malloc", "rh_free", "rh_memcpy_h2d",
     "rh_memcpy_d2h", "rh_profile_enable", "rh_profile_read", "rh_pack_weight",
-    "rh_pack_weight_gated", "rh_attention",
+    "rh_pack_weight_gated", "rh_attention", "rh_attention_planes",
     "rh_weight_destroy", "rh_weight_info", "rh_weight_export",
     "rh_quantize_rows_u8", "rh_gelu_quantize_rows_u8", "rh_matmul", "rh_matmul_packed", "rh_matmul_packed8",
     "rh_matmul_packed_vnni", "rh_gemm_u8s8_i32", "rh_linear", "rh_linear_u8",
@@ -117,6 +117,8 @@ def _load():
         "rh_profile_read": (I, [P, I, ctypes.POINTER(ProfileStat)]),
         "rh_pack_weight": (I, [P, I, P, P, I, I, ctypes.POINTER(P)]),
         "rh_pack_weight_gated": (I, [P, I, P, P, I, I, ctypes.POINTER(P)]),
+        "rh_attention_planes": (I, [P, P, P, I, I, I, I, P, I, I, I, I, I, ctypes.c_float, I, I,
+                                    P, I]),
         "rh_attention": (I, [P, P, I, I, I, I, I, P, I, I, I, I, I, ctypes.c_float, I, I, I, P,
                              I]),
         "rh_weight_destroy": (None, [P]),

@@ -380,13 +380,14 @@ __device__ __forceinline__ int attn_kswz(int r) {
   return (r / W) & ((C < 16 ? C : 16) - 1);
 }
 
-template <int DH>
+template <int DH, int T>
 __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   const __bf16* qkv = static_cast<const __bf16*>(p.qkv);
+  const __bf16* qkv_lo = static_cast<const __bf16*>(p.qkv_lo);  // T == 2
   constexpr int KS = DH / 16, DT = DH / 32;
   constexpr int kRowB = DH * 2;               // bytes of one K row
   constexpr int kKB = kAttnKV * kRowB;        // K block bytes
-  constexpr int kStage = 2 * kKB;             // K + V^T (same size)
+  constexpr int kStage = 2 * kKB * T;         // K + V^T (same size), per plane
   constexpr int kKLoads = kKB / (4 * 1024);   // DMA instructions per wave per block
   static_assert(kKLoads >= 1 && kKB % 4096 == 0, "K block must split into 4 waves x 1 KiB");
   constexpr int kOut = 4 * 32 * (DH + 4) * 4;  // output staging (attn_store_rows)
@@ -404,12 +405,14 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   const int qi = q0 + wave * 32 + fr;
 
   // Q fragments (B operand of S^T), straight from the bf16 rows.
-  v8bf qf[KS];
+  v8bf qf[KS], ql[KS];
   {
-    const __bf16* qrow =
-        qkv + (size_t)(r0 + (qi < len ? qi : len - 1)) * p.ldqkv + p.q_off + h * DH;
+    const size_t qo = (size_t)(r0 + (qi < len ? qi : len - 1)) * p.ldqkv + p.q_off + h * DH;
 #pragma unroll
-    for (int s = 0; s < KS; s++) qf[s] = *reinterpret_cast<const v8bf*>(qrow + s * 16 + fg * 8);
+    for (int s = 0; s < KS; s++) {
+      qf[s] = *reinterpret_cast<const v8bf*>(qkv + qo + s * 16 + fg * 8);
+      if constexpr (T == 2) ql[s] = *reinterpret_cast<const v8bf*>(qkv_lo + qo + s * 16 + fg * 8);
+    }
   }
 
   // K DMA: this lane's slot in each of its 1 KiB blocks -> (row, chunk).
@@ -420,15 +423,20 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     k_row[j] = off / kRowB;
     k_chunk[j] = ((off % kRowB) >> 4) ^ attn_kswz<DH>(k_row[j]);
   }
-  const __bf16* kbase = qkv + p.k_off + kvh * DH;
-  const __bf16* vbase = qkv + p.v_off + kvh * DH;
+  // plane t of a stage: K at t * 2 * kKB, V^T right after it
+  const size_t kvo = (size_t)p.k_off + kvh * DH, vvo = (size_t)p.v_off + kvh * DH;
   auto issue_k = [&](int kb, int buf) {
-    uint8_t* sK = lds + buf * kStage;
 #pragma unroll
-    for (int j = 0; j < kKLoads; j++) {
-      const int kg = kb * kAttnKV + k_row[j];
-      const __bf16* src = kbase + (size_t)(r0 + (kg < len ? kg : len - 1)) * p.ldqkv + k_chunk[j] * 8;
-      lds_dma16(src, sK + (wave * kKLoads + j) * 1024);
+    for (int t = 0; t < T; t++) {
+      uint8_t* sK = lds + buf * kStage + t * 2 * kKB;
+      const __bf16* kbase = (t ? qkv_lo : qkv) + kvo;
+#pragma unroll
+      for (int j = 0; j < kKLoads; j++) {
+        const int kg = kb * kAttnKV + k_row[j];
+        const __bf16* src =
+            kbase + (size_t)(r0 + (kg < len ? kg : len - 1)) * p.ldqkv + k_chunk[j] * 8;
+        lds_dma16(src, sK + (wave * kKLoads + j) * 1024);
+      }
     }
   };
   // V, two ways to the V^T block (same bytes):
@@ -446,24 +454,30 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   constexpr int kVItems = kPairs ? 32 * (DH / 8) : 256;
   constexpr int kVPer = (kVItems + 255) / 256;
   constexpr int kVRegs = kPairs ? 2 : 8;
-  v4i vx[kVPer][kVRegs];
+  v4i vx[T][kVPer][kVRegs];
   auto load_v = [&](int kb) {
 #pragma unroll
-    for (int u = 0; u < kVPer; u++) {
-      const int w = tid + u * 256;
-      if (kVItems % 256 != 0 && w >= kVItems) break;
-      const int kg = w / (DH / 8), db = w % (DH / 8);
+    for (int t = 0; t < T; t++) {
+      const __bf16* vbase = (t ? qkv_lo : qkv) + vvo;
 #pragma unroll
-      for (int x = 0; x < kVRegs; x++) {
-        const int key = kb * kAttnKV +
-                        (kPairs ? 2 * kg + x : (kg >> 1) * 16 + (x >> 2) * 8 + (kg & 1) * 4 + (x & 3));
-        vx[u][x] = *reinterpret_cast<const v4i*>(
-            vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 8);
+      for (int u = 0; u < kVPer; u++) {
+        const int w = tid + u * 256;
+        if (kVItems % 256 != 0 && w >= kVItems) break;
+        const int kg = w / (DH / 8), db = w % (DH / 8);
+#pragma unroll
+        for (int x = 0; x < kVRegs; x++) {
+          const int key = kb * kAttnKV + (kPairs ? 2 * kg + x
+                                                 : (kg >> 1) * 16 + (x >> 2) * 8 + (kg & 1) * 4 + (x & 3));
+          vx[t][u][x] = *reinterpret_cast<const v4i*>(
+              vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 8);
+        }
       }
     }
   };
   auto write_vt = [&](int buf) {
-    uint8_t* sV = lds + buf * kStage + kKB;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+    uint8_t* sV = lds + buf * kStage + t * 2 * kKB + kKB;
 #pragma unroll
     for (int u = 0; u < kVPer; u++) {
       const int w = tid + u * 256;
@@ -475,7 +489,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
         const int word = ((k >> 3) & 1) * 2 + ((k & 3) >> 1);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-          const uint32_t a = (uint32_t)vx[u][0][e >> 1], c = (uint32_t)vx[u][1][e >> 1];
+          const uint32_t a = (uint32_t)vx[t][u][0][e >> 1], c = (uint32_t)vx[t][u][1][e >> 1];
           const uint32_t pair =
               (e & 1) ? ((a >> 16) | (c & 0xffff0000u)) : ((a & 0xffffu) | (c << 16));
           *reinterpret_cast<uint32_t*>(sV + lds_off(db * 8 + e, chunk) + word * 4) = pair;
@@ -486,7 +500,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
           v4i lo, hi;
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const uint32_t a = (uint32_t)vx[u][2 * i][j], c = (uint32_t)vx[u][2 * i + 1][j];
+            const uint32_t a = (uint32_t)vx[t][u][2 * i][j], c = (uint32_t)vx[t][u][2 * i + 1][j];
             lo[i] = (int)((a & 0xffffu) | (c << 16));
             hi[i] = (int)((a >> 16) | (c & 0xffff0000u));
           }
@@ -495,6 +509,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
           *reinterpret_cast<v4i*>(sV + lds_off(d + 1, kg)) = hi;
         }
       }
+    }
     }
   };
 
@@ -532,6 +547,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     }
     const uint8_t* sK = lds + buf * kStage;
     const uint8_t* sV = sK + kKB;
+    const uint8_t* sKl = sK + 2 * kKB;  // T == 2: the lo planes
+    const uint8_t* sVl = sKl + kKB;
     const int key0 = kb * kAttnKV;
 
     // A wave whose queries all lie past the text only helps stage blocks.
@@ -547,9 +564,14 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
 #pragma unroll
       for (int t2 = 0; t2 < 2; t2++) {
         const int kr = t2 * 32 + fr;
-        const v8bf kf = *reinterpret_cast<const v8bf*>(
-            sK + kr * kRowB + (((2 * s + fg) ^ attn_kswz<DH>(kr)) << 4));
+        const int ko = kr * kRowB + (((2 * s + fg) ^ attn_kswz<DH>(kr)) << 4);
+        const v8bf kf = *reinterpret_cast<const v8bf*>(sK + ko);
         sc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sc[t2], 0, 0, 0);
+        if constexpr (T == 2) {  // hi·lo + lo·hi: the fp32-grade split
+          const v8bf kl = *reinterpret_cast<const v8bf*>(sKl + ko);
+          sc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, ql[s], sc[t2], 0, 0, 0);
+          sc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qf[s], sc[t2], 0, 0, 0);
+        }
       }
     // Bidirectional attention masks only the keys past the text, the same
     // keys for every query: one more MFMA per tile adds -inf to their
@@ -587,13 +609,24 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     // chunk kc is register sc[kc/2][(kc%2)*8 + e], V^T chunk 2kc + g.
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) {
-      v8bf ph;
+      v8bf ph, pl;
 #pragma unroll
-      for (int e = 0; e < 8; e++) ph[e] = (__bf16)sc[kc >> 1][(kc & 1) * 8 + e];
+      for (int e = 0; e < 8; e++) {
+        const float x = sc[kc >> 1][(kc & 1) * 8 + e];
+        const __bf16 hi = (__bf16)x;
+        ph[e] = hi;
+        if constexpr (T == 2) pl[e] = (__bf16)(x - (float)hi);
+      }
 #pragma unroll
       for (int t = 0; t < DT; t++) {
-        const v8bf vf = *reinterpret_cast<const v8bf*>(sV + lds_off(t * 32 + fr, 2 * kc + fg));
+        const int vo = lds_off(t * 32 + fr, 2 * kc + fg);
+        const v8bf vf = *reinterpret_cast<const v8bf*>(sV + vo);
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[t], 0, 0, 0);
+        if constexpr (T == 2) {
+          const v8bf vl = *reinterpret_cast<const v8bf*>(sVl + vo);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, o[t], 0, 0, 0);
+        }
       }
     }
     }
@@ -612,8 +645,15 @@ template <int DH>
 static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s) {
   const int units = a.batch * a.kv_heads;
   const dim3 grid(8 * ceil_div(a.max_len, kAttnQ) * (a.heads / a.kv_heads) * ceil_div(units, 8));
-  if (a.in_bf16)  // bf16 input carries no low half: one-term products
-    timed_launch((attention_bf16_kernel<DH>), grid, dim3(256), 0, s, a);
+  if (a.in_bf16 == 2) {  // hi/lo planes: the three-term products, pipelined
+    if constexpr (DH <= 128) {
+      if (precision != 3 || !a.qkv_lo) return hipErrorInvalidValue;
+      timed_launch((attention_bf16_kernel<DH, 2>), grid, dim3(256), 0, s, a);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (a.in_bf16)  // bf16 input carries no low half: one-term products
+    timed_launch((attention_bf16_kernel<DH, 1>), grid, dim3(256), 0, s, a);
   else if (precision == 3)
     timed_launch((attention_kernel<DH, 3, float>), grid, dim3(256), 0, s, a);
   else

@@ -374,8 +374,10 @@ int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up
 
 int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                 const float* rs, int m, int epi, void* out, int ldo, int act,
-                const float* bias, float* row_absmax, float* rs_out, double ops) {
+                const float* bias, float* row_absmax, float* rs_out, double ops,
+                void* out_lo) {
   if (m <= 0) return RH_OK;
+  if (epi == EPI_PLANES && !out_lo) return fail(RH_ERR_INVALID, "planes epilogue needs a lo plane");
   GemmI8Args g{};
   g.A = qa;
   g.lda = ldq;
@@ -390,6 +392,7 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
   g.colsum = w->d_colsum;
   g.bias = bias;
   g.out = out;
+  g.out_lo = out_lo;
   g.ldo = ldo;
   g.act = act;
   g.epi = epi;
@@ -397,7 +400,7 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
   g.rs_out = rs_out;
   g.tile_group = ctx->tile_group;
   const double M = m, K = w->k, N = w->n;
-  static const double out_bytes[] = {4, 2, 0, 1, 4};  // per output element
+  static const double out_bytes[] = {4, 2, 0, 1, 4, 4};  // per output element
   const double bytes = M * K + K * N + M * N * out_bytes[epi] + 4 * M + 8 * N +
                        (bias ? 4 * N : 0) + (epi == EPI_QUANT ? 4 * M : 0);
   int slot = -1;
@@ -823,6 +826,49 @@ int rh_profile_read(rh_context* ctx, int kind, rh_profile_stat* out) {
       st.total_bytes += r.bytes;
     }
     *out = st;
+    return RH_OK;
+  });
+}
+
+int rh_attention_planes(rh_context* ctx, const void* qkv_hi, const void* qkv_lo, int ldqkv,
+                        int q_off, int k_off, int v_off, const int32_t* cu, int batch,
+                        int max_len, int heads, int kv_heads, int dh, float scale, int causal,
+                        int window, float* out, int ldout) {
+  return api_call([&]() -> int {
+    if (!qkv_hi || !qkv_lo || !cu || !out) return fail(RH_ERR_INVALID, "null argument");
+    if (dh != 32 && dh != 64 && dh != 128)
+      return fail(RH_ERR_SHAPE, "planes attention head dim must be 32, 64 or 128");
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads)
+      return fail(RH_ERR_SHAPE, "heads must be a positive multiple of kv_heads");
+    if (batch < 0 || max_len < 0 || window < 0) return fail(RH_ERR_INVALID, "negative size");
+    if (ldqkv % 8 || q_off % 8 || k_off % 8 || v_off % 8 || ldout % 4 || q_off < 0 ||
+        k_off < 0 || v_off < 0 || ((uintptr_t)qkv_hi & 15) || ((uintptr_t)qkv_lo & 15) ||
+        ((uintptr_t)out & 15))
+      return fail(RH_ERR_SHAPE, "attention rows and offsets must be 16-byte aligned");
+    CTX_GUARD(ctx);
+    AttnArgs a{};
+    a.qkv = qkv_hi;
+    a.qkv_lo = qkv_lo;
+    a.in_bf16 = 2;
+    a.ldqkv = ldqkv;
+    a.q_off = q_off;
+    a.k_off = k_off;
+    a.v_off = v_off;
+    a.cu = cu;
+    a.batch = batch;
+    a.max_len = max_len;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.dh = dh;
+    a.scale = scale;
+    a.ctx = out;
+    a.ldctx = ldout;
+    a.causal = causal ? 1 : 0;
+    a.window = window;
+    int slot = -1;
+    RH_HIP(ctx->prof_begin(3, 0.0, 0.0, &slot));
+    RH_HIP(launch_attention(a, 3, ctx->stream));
+    RH_HIP(ctx->prof_end(slot));
     return RH_OK;
   });
 }

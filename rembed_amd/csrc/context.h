@@ -126,7 +126,8 @@ int run_linear_qk(Context* ctx, const rh_weight* w, const Planes& pin, int m,
                   const QkEpilogue& q, __bf16* out, int ldo, bool* applied);
 int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                 const float* rs, int m, int epi, void* out, int ldo, int act,
-                const float* bias, float* row_absmax, float* rs_out, double ops);
+                const float* bias, float* row_absmax, float* rs_out, double ops,
+                void* out_lo = nullptr);
 // run_gemm_i8 with the residual + LayerNorm finish (launch_gemm_i8_ln).
 int run_gemm_i8_ln(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                    const float* rs, int m, const I8LnArgs& f, double ops);

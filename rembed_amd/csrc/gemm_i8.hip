@@ -181,6 +181,10 @@ __device__ __forceinline__ void i8_epilogue(const GemmI8Args& p, v16i (&acc)[TM]
             v4bf w = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
             *reinterpret_cast<v4bf*>(static_cast<__bf16*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
           }
+        } else if constexpr (EPI == EPI_PLANES) {
+          if (ok)
+            store_planes4(static_cast<__bf16*>(p.out), static_cast<__bf16*>(p.out_lo),
+                          (size_t)grow * p.ldo + gcol, v);
         } else if constexpr (EPI == EPI_ABSMAX) {
           // |value| max over this row's columns of the tile; every lane takes
           // part in the shuffles (invalid lanes contribute 0).
@@ -868,6 +872,7 @@ hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s) {
     case EPI_ABSMAX: return launch_epi<EPI_ABSMAX>(a, tile, s);
     case EPI_QUANT: return launch_epi<EPI_QUANT>(a, tile, s);
     case EPI_ACC: return launch_epi<EPI_ACC>(a, tile, s);
+    case EPI_PLANES: return launch_epi<EPI_PLANES>(a, tile, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -608,10 +608,27 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     // weight is full-int8. When attention runs on bf16 operands, a full-int8
     // QKV writes bf16 directly (attention would round the fp32 values to the
     // same bf16 on load), halving the write.
+    // With fp32-grade attention it writes the rows' bf16 hi/lo split as two
+    // planes (the same bytes as fp32 rows), which attention stages without a
+    // conversion: hi in qkvh, lo in the fp32 q|k|v buffer's first half.
+    // A weight-only int8 / fp32 q|k|v linear on bf16 planes writes the same
+    // split through its planes epilogue.
     const bool qkv_bf16 = needs_q(L.qkv) && attn_precision == 1 && !exact;
+    const bool qkv_planes = attn_precision == 3 && !exact && dh <= 128 &&
+                            (needs_q(L.qkv) || linear_on_planes(ctx, L.qkv));
+    __bf16* qkv_lo = reinterpret_cast<__bf16*>(qkv);
     if (qkv_bf16) {
       st = run_gemm_i8(ctx, L.qkv, qap, ldq_for(H), rsp, Mp, EPI_BF16, qkvh + r0 * 3 * H,
                        3 * H, ACT_NONE, L.qkv->d_bias, nullptr, nullptr, 2.0 * MH * H * 3 * H);
+    } else if (qkv_planes && needs_q(L.qkv)) {
+      st = run_gemm_i8(ctx, L.qkv, qap, ldq_for(H), rsp, Mp, EPI_PLANES, qkvh + r0 * 3 * H,
+                       3 * H, ACT_NONE, L.qkv->d_bias, nullptr, nullptr, 2.0 * MH * H * 3 * H,
+                       qkv_lo + r0 * 3 * H);
+    } else if (qkv_planes) {
+      const Planes pq = at(plane(0, L.qkv));
+      const Planes pout{qkvh + r0 * 3 * H, qkv_lo + r0 * 3 * H, 3 * H};
+      st = run_linear(ctx, L.qkv, xp, H, Mp, nullptr, 3 * H, ACT_NONE, L.qkv->d_bias, qap,
+                      ldq_for(H), rsp, false, x_planes ? &pq : nullptr, &pout);
     } else {
       const Planes pq = at(plane(0, L.qkv));
       st = run_linear(ctx, L.qkv, xp, H, Mp, qkv + r0 * 3 * H, 3 * H, ACT_NONE, L.qkv->d_bias,
@@ -619,8 +636,9 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     }
     if (st) return st;
     AttnArgs aa{};
-    aa.qkv = qkv_bf16 ? (const void*)qkvh : (const void*)qkv;  // rows are absolute (cu)
-    aa.in_bf16 = qkv_bf16 ? 1 : 0;
+    aa.qkv = qkv_bf16 || qkv_planes ? (const void*)qkvh : (const void*)qkv;  // absolute rows
+    aa.qkv_lo = qkv_planes ? qkv_lo : nullptr;
+    aa.in_bf16 = qkv_bf16 ? 1 : (qkv_planes ? 2 : 0);
     aa.ldqkv = 3 * H;
     aa.q_off = 0;
     aa.k_off = H;
@@ -1472,7 +1490,10 @@ int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_m
     ctx_retain(ctx);
     m->cfg = *cfg;
     m->quant = quant;
-    m->attn_precision = quant == RH_QUANT_NONE ? 3 : 1;
+    // fp32-grade attention (the reference's attention is float32) for the
+    // BERT family in every mode; the RoPE family's quantized modes keep bf16
+    // operands (their dh-256 fp32-grade kernel is the unpipelined one)
+    m->attn_precision = quant == RH_QUANT_NONE || cfg->arch == RH_ARCH_BERT ? 3 : 1;
     *out = m;
     return RH_OK;
   });

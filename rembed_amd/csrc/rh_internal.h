@@ -121,7 +121,9 @@ enum I8Epi : int {
                    // (atomic max on the float bits; zero it beforehand)
   EPI_QUANT = 3,   // out u8 [M][ldo] = QuantizeRowU8(value row) using
                    // row_absmax from a preceding EPI_ABSMAX pass; rs_out[M]
-  EPI_ACC = 4      // out int32 [M][ldo] = reference-form accumulators
+  EPI_ACC = 4,     // out int32 [M][ldo] = reference-form accumulators
+  EPI_PLANES = 5   // out / out_lo bf16 [M][ldo]: hi = bf16(value), lo =
+                   // bf16(value - hi), both rounded to nearest even
 };
 
 struct GemmI8Args {
@@ -136,6 +138,7 @@ struct GemmI8Args {
   const int32_t* colsum;    // [N]
   const float* bias;        // [N] or null
   void* out;                // per epi; rows 16-byte aligned
+  void* out_lo;             // EPI_PLANES: the lo plane (same layout as out)
   int ldo;                  // elements, multiple of 4
   int act;
   int epi;
@@ -323,7 +326,8 @@ hipError_t launch_pool(const float* x, int H, const int32_t* cu, int batch,
 // Multi-head attention over a packed varlen batch (bert.go:853-902 per
 // text): q/k/v read from the fused QKV rows, ctx written [M][H].
 struct AttnArgs {
-  const void* qkv;   // [M][ldqkv] fp32, or bf16 when in_bf16
+  const void* qkv;   // [M][ldqkv] fp32 (in_bf16 0), bf16 (1), or the bf16 hi plane (2)
+  const void* qkv_lo;  // in_bf16 2: the bf16 lo plane, hi + lo = the fp32 rows' split
   int in_bf16;
   int ldqkv;
   int q_off, k_off, v_off;  // column offsets of head 0
@@ -339,7 +343,9 @@ struct AttnArgs {
   int causal;  // key j visible to query i only if j <= i (qwen3.go:307-390)
   int window;  // > 0: key j visible only if |i - j| < window (gemma3.go:339-347)
 };
-// precision: 1 = bf16 MFMA, 3 = three-term bf16 split (fp32-grade)
+// precision: 1 = bf16 MFMA, 3 = three-term bf16 split (fp32-grade; with
+// in_bf16 2 the split arrives as hi/lo planes and runs on the pipelined
+// kernel, dh <= 128)
 hipError_t launch_attention(const AttnArgs& a, int precision, hipStream_t s);
 // The same attention in the reference's float32 operation order
 // (MatMulSerial/dot4, Softmax; attention_exact.hip): bit-identical context

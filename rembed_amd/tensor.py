@@ -226,6 +226,14 @@ def Attention(ctx, out, ldout, qkv, in_bf16, ldqkv, q_off, k_off, v_off, cu, bat
                            window, precision, out.ptr, ldout))
 
 
+def AttentionPlanes(ctx, out, ldout, hi, lo, ldqkv, q_off, k_off, v_off, cu, batch, max_len,
+                    heads, kv_heads, dh, scale, causal=False, window=0):
+    """fp32-grade attention on the q|k|v rows' bf16 hi/lo split (rh_attention_planes)."""
+    check(lib.rh_attention_planes(ctx.h, hi.ptr, lo.ptr, ldqkv, q_off, k_off, v_off, cu.ptr,
+                                  batch, max_len, heads, kv_heads, dh, float(scale),
+                                  int(causal), window, out.ptr, ldout))
+
+
 def Linear(ctx, dst, a, pb, m, act=_lib.RH_ACT_NONE, qa=None, ldq=0, row_scales=None):
     """applyDense with fused bias/activation (bert.go:282-301)."""
     check(lib.rh_linear(ctx.h, dst.ptr, a.ptr, pb.h, m, act,

@@ -11,7 +11,8 @@ window |i-j| < w, grouped kv heads).
   block pipeline and the masks against an independently staged kernel.
 * Both are within the bf16-P bound of the float64 reference (P is rounded
   to bf16 before P·V: relative 2^-9 per weight), and precision 3 (hi/lo
-  split) within 1e-4 of the output scale.
+  split) within 1e-4 of the output scale; so is the pipelined three-term
+  kernel fed the rows' bf16 hi/lo planes (rh_attention_planes, dh <= 128).
 * Texts of length 1, block edges (63/64/65, 127/128/129), windows shorter
   and longer than the text, GQA groups of 1, 2 and 3, and EmbeddingGemma's
   window of 512 at lengths 511, 512, 513 and 2048.
@@ -125,6 +126,20 @@ def test_attention_kernels(gpu_ctx, case):
     err_f = np.abs(got_f3 - want_f).max()
     say(f"  split max err {err_f:.3e}")
     assert err_f <= 1e-4 * (1 + np.abs(want_f).max())
+    if dh <= 128:
+        # the same split handed over as bf16 hi/lo planes (what the full-int8
+        # q|k|v projection writes), on the pipelined three-term kernel
+        hi = to_bf16_bits(x)
+        lo = to_bf16_bits(x - bf16_value(hi))
+        out = gpu_ctx.upload(np.full((M, heads * dh), np.nan, np.float32))
+        hd, ld_ = gpu_ctx.upload(hi), gpu_ctx.upload(lo)
+        T.AttentionPlanes(gpu_ctx, out, heads * dh, hd, ld_, ld, q_off, k_off, v_off, cu_d,
+                          len(lens), max_len, heads, kv_heads, dh, scale, causal, window)
+        gpu_ctx.sync()
+        got_p = out.download(np.float32, (M, heads * dh))
+        err_p = np.abs(got_p - want_f).max()
+        say(f"  planes max err {err_p:.3e}")
+        assert err_p <= 1e-4 * (1 + np.abs(want_f).max())
 
 
 def test_attention_argument_errors(gpu_ctx):
