@@ -279,6 +279,9 @@ int rh_layernorm(rh_context *ctx, float *x, const float *gamma,
 #define RH_ARCH_GEMMA3 2 /* EmbeddingGemma: Gemma 3 run bidirectionally (gemma3.go:206-384) */
 #define RH_ARCH_NOMIC 3  /* nomic-embed (nomic_bert): post-LN, RoPE, SwiGLU, bias-free (nomic.go:113-250) */
 #define RH_ARCH_MODERNBERT 4 /* ModernBERT: pre-LN, RoPE, global/local attention, GeGLU (modernbert.go:148-311) */
+#define RH_ARCH_DISTILBERT 5 /* DistilBERT: the BERT flow on transformer.layer.N.* names, no token-type table (bert.go:399-470,491-493) */
+#define RH_ARCH_MPNET 6      /* MPNet: the BERT flow on attention.attn.* names, no token-type table, a bucketed
+                                relative-position bias added to the scaled scores (bert.go:123-150,439-452,495-503,816-830,876-890) */
 #define RH_POOL_MEAN 0
 #define RH_POOL_CLS 1
 #define RH_POOL_LAST 2
@@ -314,7 +317,8 @@ typedef struct {
                                 ModernBERT: GlobalAttnEveryNLayers, global iff l % n == 0 */
   int query_pre_attn_scalar; /* Gemma: scores scaled by 1/sqrt(scalar) */
   int dense_hidden;          /* Gemma Dense head width (2_Dense/3_Dense); 0 = none */
-  int reserved[8];           /* zero */
+  int rel_buckets;           /* MPNet: relative_attention_num_buckets (32, config.go:219-221) */
+  int reserved[7];           /* zero */
 } rh_model_config;
 
 typedef struct rh_model rh_model;

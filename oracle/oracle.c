@@ -716,8 +716,30 @@ struct or_bert_model {
   or_bert_config cfg;
   int quant;
   const float *word_emb, *pos_emb, *type_emb, *emb_ln_g, *emb_ln_b;
+  const float *rel_bias; /* MPNet [rel_buckets][heads], or NULL */
   or_layer *layers;
 };
+
+/* relPosBucket, bert.go:123-150: n = -rel; the sign picks the table half;
+ * |n| < maxExact keeps its own bucket, larger distances share buckets
+ * spaced by log(|n| / maxExact) / log(128 / maxExact) (float64), clamped
+ * to the half's last bucket. */
+int or_rel_pos_bucket(int rel, int num_buckets) {
+  int n = -rel;
+  int half = num_buckets / 2;
+  int ret = 0;
+  if (n < 0) {
+    ret = half;
+    n = -n;
+  }
+  int max_exact = half / 2;
+  if (n < max_exact) return ret + n;
+  int v = max_exact + (int)(log((double)n / (double)max_exact) /
+                            log(128.0 / (double)max_exact) * (double)(half - max_exact));
+  return ret + (v < half - 1 ? v : half - 1);
+}
+
+void or_bert_set_rel_bias(or_bert_model *m, const float *table) { m->rel_bias = table; }
 
 void or__dense_init(or_dense *d, const float *raw, int owned_raw,
                        const float *bias, int owned_bias, int in, int out,
@@ -880,7 +902,7 @@ int or_bert_encode_layers(const or_bert_model *m, const int32_t *ids, int seq,
   if (layers < 0 || layers > c->layers) return OR_ERR_SEQ;
   int H = c->hidden, I = c->inter, heads = c->heads, dh = H / heads;
   if (seq <= 0) return OR_ERR_SEQ;
-  if (seq > c->max_pos) return OR_ERR_SEQ;
+  if (seq > c->max_pos - c->pos_off) return OR_ERR_SEQ;
   for (int i = 0; i < seq; i++)
     if (ids[i] < 0 || ids[i] >= c->vocab) return OR_ERR_VOCAB;
 
@@ -898,7 +920,7 @@ int or_bert_encode_layers(const or_bert_model *m, const int32_t *ids, int seq,
    * (bert.go:796-814). */
   for (int i = 0; i < seq; i++) {
     const float *w = m->word_emb + (size_t)ids[i] * H;
-    const float *p = m->pos_emb + (size_t)i * H;
+    const float *p = m->pos_emb + (size_t)(i + c->pos_off) * H;
     float *row = x + (size_t)i * H;
     if (m->type_emb) {
       for (int j = 0; j < H; j++) row[j] = w[j] + p[j] + m->type_emb[j];
@@ -922,7 +944,18 @@ int or_bert_encode_layers(const or_bert_model *m, const int32_t *ids, int seq,
         for (int d = 0; d < dh; d++) vt[(size_t)d * seq + i] = row[2 * H + off + d];
       }
       or_matmul_serial(sc, qh, kh, seq, dh, seq);
-      for (size_t i = 0; i < (size_t)seq * seq; i++) sc[i] *= scale;
+      if (m->rel_bias) {
+        /* MPNet (bert.go:876-890): scores*scale rounded, then + the bias of
+         * bucket(j - i) */
+        for (int i = 0; i < seq; i++)
+          for (int j = 0; j < seq; j++) {
+            const float s = sc[(size_t)i * seq + j] * scale;
+            sc[(size_t)i * seq + j] =
+                s + m->rel_bias[(size_t)or_rel_pos_bucket(j - i, c->rel_buckets) * heads + h];
+          }
+      } else {
+        for (size_t i = 0; i < (size_t)seq * seq; i++) sc[i] *= scale;
+      }
       or_softmax(sc, seq, seq);
       or_matmul_serial(ch, sc, vt, seq, seq, dh);
       for (int i = 0; i < seq; i++)

@@ -111,6 +111,9 @@ typedef struct {
   float eps;
   int pooling;   /* OR_POOL_* */
   int normalize; /* L2-normalize the pooled vector */
+  int pos_off;   /* Config.PositionOffset (config.go:84-89): position row of
+                    token i is i + pos_off; texts up to max_pos - pos_off */
+  int rel_buckets; /* MPNet: buckets of the relative-position bias (0: none) */
 } or_bert_config;
 
 /* Per-layer tensor order inside `layer_tensors` (16 per layer, HF layouts):
@@ -129,6 +132,12 @@ or_bert_model *or_bert_create(const or_bert_config *cfg, int quant,
                               const float *emb_ln_b,
                               const float *const *layer_tensors);
 void or_bert_free(or_bert_model *m);
+/* MPNet's shared relative-position bias table [rel_buckets][heads]
+ * (encoder.relative_attention_bias.weight, bert.go:511-519), borrowed. */
+void or_bert_set_rel_bias(or_bert_model *m, const float *table);
+/* relPosBucket (bert.go:123-150): the bias bucket of relative position
+ * rel = j - i (HF's relative_position_bucket, max distance 128). */
+int or_rel_pos_bucket(int rel, int num_buckets);
 
 /* encodeWorkers (bert.go:740-923): one unpadded forward over seq ids,
  * writing the final hidden states [seq][H]. */

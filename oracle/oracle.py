@@ -47,6 +47,8 @@ def _load():
         "or_dot4": (None, [P, P, P, P, P, P, I]),
         "or_matmul_serial": (None, [P, P, P, I, I, I]),
         "or_bert_create": (P, [P, I, P, P, P, P, P, P]),
+        "or_bert_set_rel_bias": (None, [P, P]),
+        "or_rel_pos_bucket": (I, [I, I]),
         "or_bert_free": (None, [P]),
         "or_bert_encode": (I, [P, P, I, P]),
         "or_bert_encode_layers": (I, [P, P, I, P, I]),
@@ -281,7 +283,13 @@ class BertConfig(ctypes.Structure):
                 ("layers", ctypes.c_int), ("heads", ctypes.c_int),
                 ("inter", ctypes.c_int), ("max_pos", ctypes.c_int),
                 ("type_vocab", ctypes.c_int), ("eps", ctypes.c_float),
-                ("pooling", ctypes.c_int), ("normalize", ctypes.c_int)]
+                ("pooling", ctypes.c_int), ("normalize", ctypes.c_int),
+                ("pos_off", ctypes.c_int), ("rel_buckets", ctypes.c_int)]
+
+
+def rel_pos_bucket(rel, num_buckets=32):
+    """relPosBucket (bert.go:123-150), the oracle's restatement."""
+    return lib.or_rel_pos_bucket(rel, num_buckets)
 
 
 LAYER_ORDER = [
@@ -300,24 +308,34 @@ class BertOracle:
     """The reference's per-text unpadded BERT forward on the CPU."""
 
     def __init__(self, shape, tensors, quant):
+        """BERT/RoBERTa, DistilBERT (transformer.layer.N names, no token-type
+        table) or MPNet (attention.attn names, relative-position bias), by
+        shape.arch (bert.go:378-522)."""
+        from rembed_amd.synthetic import layer_names
         self._keep = {k: f32(v) for k, v in tensors.items()}
         t = self._keep
+        arch = getattr(shape, "arch", 0)
+        rel = getattr(shape, "rel_buckets", 0)
         cfg = BertConfig(shape.vocab, shape.hidden, shape.layers, shape.heads,
                          shape.intermediate, shape.max_position, shape.type_vocab,
-                         shape.eps, shape.pooling, shape.normalize)
+                         shape.eps, shape.pooling, shape.normalize,
+                         getattr(shape, "position_offset", 0), rel)
         self.shape = shape
-        layer_ptrs = [t[f"encoder.layer.{l}.{n}"].ctypes.data
-                      for l in range(shape.layers) for n in LAYER_ORDER]
+        layer_ptrs = [t[n].ctypes.data for l in range(shape.layers)
+                      for n in layer_names(arch, l)]
         self._arr = (ctypes.c_void_p * len(layer_ptrs))(*layer_ptrs)
+        tt = t.get("embeddings.token_type_embeddings.weight")
         self.h = lib.or_bert_create(
             ctypes.byref(cfg), quant,
             _p(t["embeddings.word_embeddings.weight"]),
             _p(t["embeddings.position_embeddings.weight"]),
-            _p(t["embeddings.token_type_embeddings.weight"]),
+            None if tt is None else _p(tt),
             _p(t["embeddings.LayerNorm.weight"]), _p(t["embeddings.LayerNorm.bias"]),
             ctypes.cast(self._arr, ctypes.c_void_p))
         if not self.h:
             raise RuntimeError("oracle: bad BERT config")
+        if rel:
+            lib.or_bert_set_rel_bias(self.h, _p(t["encoder.relative_attention_bias.weight"]))
 
     def close(self):
         if self.h:

@@ -28,6 +28,7 @@ RH_POOL_MEAN, RH_POOL_CLS, RH_POOL_LAST = 0, 1, 2
 RH_ACT_NONE, RH_ACT_GELU, RH_ACT_SWIGLU, RH_ACT_GEGLU = 0, 1, 2, 3
 RH_ACT_GEGLU_ERF = 4
 RH_ARCH_BERT, RH_ARCH_QWEN3, RH_ARCH_GEMMA3, RH_ARCH_NOMIC, RH_ARCH_MODERNBERT = 0, 1, 2, 3, 4
+RH_ARCH_DISTILBERT, RH_ARCH_MPNET = 5, 6
 RH_OPT_ATTN_PRECISION = 1
 RH_OPT_FUSED_FFN1 = 2
 RH_OPT_PRODUCER_PLANES = 3
@@ -81,7 +82,7 @@ class ModelConfig(ctypes.Structure):
         ("rope_theta", ctypes.c_double), ("rope_local_theta", ctypes.c_double),
         ("sliding_window", ctypes.c_int), ("sliding_pattern", ctypes.c_int),
         ("query_pre_attn_scalar", ctypes.c_int), ("dense_hidden", ctypes.c_int),
-        ("reserved", ctypes.c_int * 8),
+        ("rel_buckets", ctypes.c_int), ("reserved", ctypes.c_int * 7),
     ]
 
 

@@ -110,6 +110,26 @@ __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int
   return alpha;
 }
 
+// MPNet (bert.go:876-890): scores become score·scale + bias(j - i), the
+// bias of the head's relative-position bucket; the softmax then takes them
+// with cs = log2 e. Lane layout as attn_softmax_block (query qi; keys key0 +
+// t2*32 + i*8 + fg*4 + j). Relative positions outside the table belong to
+// masked keys or unstored queries and are clamped into it.
+__device__ __forceinline__ void attn_rel_bias(const AttnArgs& p, v16f (&sc)[2], int h, int qi,
+                                              int key0, int fg) {
+  const int c = p.rel_center;
+  const float* rb = p.rel_bias + (size_t)h * (2 * c + 1) + c;
+#pragma unroll
+  for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int d = min(max(key0 + t2 * 32 + i * 8 + fg * 4 + j - qi, -c), c);
+        sc[t2][i * 4 + j] = sc[t2][i * 4 + j] * p.scale + rb[d];
+      }
+}
+
 // Workgroup -> (text b, head h, query block). Workgroups are dealt to the 8
 // XCDs round-robin (workgroup w runs on XCD w % 8), and the query blocks
 // of one text read the same K and V rows, as do the q heads of one kv head
@@ -303,8 +323,10 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     // query's reference max moved.
     const bool masked = __any(key0 < klo || key0 + kAttnKV - 1 > khi);
     bool rescale;
-    const float alpha =
-        attn_softmax_block(sc, key0, fg, klo, khi, masked, cs, mrun, lrun, rescale);
+    if (p.rel_bias) attn_rel_bias(p, sc, h, qi, key0, fg);
+    const float alpha = attn_softmax_block(sc, key0, fg, klo, khi, masked,
+                                           p.rel_bias ? 1.44269504088896341f : cs, mrun,
+                                           lrun, rescale);
     if (rescale) {
 #pragma unroll
       for (int t = 0; t < DT; t++)
@@ -596,8 +618,10 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     // moved, and never on the first block (the output is still zero).
     const bool masked = !text_mask && __any(key0 < klo || key0 + kAttnKV - 1 > khi);
     bool rescale;
-    const float alpha =
-        attn_softmax_block(sc, key0, fg, klo, khi, masked, cs, mrun, lrun, rescale);
+    if (p.rel_bias) attn_rel_bias(p, sc, h, qi, key0, fg);
+    const float alpha = attn_softmax_block(sc, key0, fg, klo, khi, masked,
+                                           p.rel_bias ? 1.44269504088896341f : cs, mrun,
+                                           lrun, rescale);
     if (rescale && kb != kb_lo) {
 #pragma unroll
       for (int t = 0; t < DT; t++)

@@ -185,6 +185,11 @@ __global__ __launch_bounds__(256) void attention_exact_kernel(AttnArgs p) {
         }
         sa = sa * p.scale;  // scores *= scale (bert.go:884-886)
         sb = sb * p.scale;
+        if (p.rel_bias) {  // MPNet: + the bias of bucket(j - i), after the scale
+          const float* rb = p.rel_bias + (size_t)h * (2 * p.rel_center + 1) + p.rel_center + j;
+          sa = sa + rb[-(q0 + min(i, nq - 1))];
+          sb = sb + rb[-(q0 + min(i + H2, nq - 1))];
+        }
         P[i * lp + j] = sa;
         P[(i + H2) * lp + j] = sb;
         mxa = fmaxf(mxa, sa);

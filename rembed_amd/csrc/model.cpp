@@ -124,6 +124,9 @@ struct rh_model {
 
   float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_g = nullptr,
         *emb_b = nullptr;
+  // MPNet: the relative-position bias per head and relative position,
+  // [heads][2 * max_seq - 1], entry (h, j - i + max_seq - 1)
+  float* rel_bias = nullptr;
   std::vector<Layer> layers;
   // decoder family
   std::vector<DecLayer> dlayers;
@@ -199,7 +202,7 @@ struct rh_model {
     return std::make_shared<WeightSet>(
         ctx, layers, dlayers,
         std::vector<float*>{word, pos, type0, emb_g, emb_b, final_norm, dense1, dense2, cos_g,
-                            sin_g, cos_l, sin_l});
+                            sin_g, cos_l, sin_l, rel_bias});
   }
 
   void release_ws() {
@@ -245,7 +248,7 @@ struct rh_model {
     weights.reset();
     layers.clear();
     dlayers.clear();
-    word = pos = type0 = emb_g = emb_b = nullptr;
+    word = pos = type0 = emb_g = emb_b = rel_bias = nullptr;
     final_norm = dense1 = dense2 = cos_g = sin_g = cos_l = sin_l = nullptr;
     if (err_d) (void)hipFree(err_d);
     err_d = nullptr;
@@ -262,7 +265,11 @@ struct rh_model {
   int I() const { return cfg.intermediate; }
   // The RoPE family (Qwen3, Gemma3, nomic-bert, ModernBERT) runs
   // forward_dec; BERT / RoBERTa run forward.
-  bool rope_family() const { return cfg.arch != RH_ARCH_BERT; }
+  // BERT, DistilBERT and MPNet share the post-LN flow (encodeWorkers,
+  // bert.go:740-923); the rest are the RoPE family
+  bool rope_family() const {
+    return cfg.arch != RH_ARCH_BERT && cfg.arch != RH_ARCH_DISTILBERT && cfg.arch != RH_ARCH_MPNET;
+  }
   bool gemma() const { return cfg.arch == RH_ARCH_GEMMA3; }
   bool nomic() const { return cfg.arch == RH_ARCH_NOMIC; }
   bool modernbert() const { return cfg.arch == RH_ARCH_MODERNBERT; }
@@ -650,6 +657,8 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
     aa.kv_heads = heads;
     aa.dh = dh;
     aa.scale = (float)(1.0 / std::sqrt((double)dh));
+    aa.rel_bias = rel_bias;
+    aa.rel_center = max_seq() - 1;
     // the attention output goes straight to the output projection's planes
     // when it takes them (absolute rows, like the q|k|v rows)
     const bool po = planes_in(L.o);
@@ -1033,7 +1042,7 @@ int rh_model::forward_dec(const int32_t* ids_dev, int stride, const std::vector<
 
 // ---- tensor bookkeeping ----------------------------------------------------------
 
-static const char* kPrefixes[] = {"", "bert.", "roberta.", "distilbert."};
+static const char* kPrefixes[] = {"", "bert.", "roberta.", "mpnet.", "distilbert."};
 
 static int find_tensor(rh_model* m, const std::string& prefix, const std::string& name,
                        std::initializer_list<int64_t> shape, const HostTensor** out) {
@@ -1097,33 +1106,103 @@ static int dense_mode(const rh_model* m, const float* raw, int in, int out) {
   return RH_MODE_F32;
 }
 
+// relPosBucket (bert.go:123-150), HF's relative_position_bucket with
+// max_distance 128: n = -(j - i); the sign picks the table half; |n| below
+// half/2 keeps its own bucket, larger distances share log-spaced buckets
+// (float64 log), clamped to the half's last.
+static int rel_pos_bucket(int rel, int buckets) {
+  int n = -rel, ret = 0;
+  const int half = buckets / 2, exact = half / 2;
+  if (n < 0) {
+    ret = half;
+    n = -n;
+  }
+  if (n < exact) return ret + n;
+  const int v = exact + (int)(std::log((double)n / exact) / std::log(128.0 / exact) *
+                              (double)(half - exact));
+  return ret + std::min(v, half - 1);
+}
+
+// Load (bert.go:307-524) for BERT / RoBERTa, DistilBERT and MPNet: the same
+// post-LN layers under each one's tensor names (bert.go:399-470); only BERT
+// and RoBERTa have a token-type table (row 0 used); MPNet adds one shared
+// [buckets][heads] relative-position bias table (bert.go:511-519), expanded
+// here once into the per-head table over every relative position a text can
+// have (the reference rebuilds its [heads][2 seq - 1] slice per forward,
+// bert.go:816-830).
 static int finalize_bert(rh_model* m) {
   const int H = m->cfg.hidden, I = m->cfg.intermediate;
+  const bool distil = m->cfg.arch == RH_ARCH_DISTILBERT, mpnet = m->cfg.arch == RH_ARCH_MPNET;
   std::string prefix;
   for (const char* p : kPrefixes)
     if (m->pending.count(std::string(p) + "embeddings.word_embeddings.weight")) prefix = p;
-  const HostTensor *we, *pe, *tt, *eg, *eb;
+  const HostTensor *we, *pe, *tt = nullptr, *eg, *eb;
   int st;
   if ((st = find_tensor(m, prefix, "embeddings.word_embeddings.weight", {m->cfg.vocab, H}, &we)))
     return st;
   if ((st = find_tensor(m, prefix, "embeddings.position_embeddings.weight",
                         {m->cfg.max_position, H}, &pe)))
     return st;
-  if ((st = find_tensor(m, prefix, "embeddings.token_type_embeddings.weight", {-1, H}, &tt)))
-    return st;
-  if (tt->shape[0] < 1) return fail(RH_ERR_MISSING, "token_type_embeddings has no rows");
+  if (!distil && !mpnet) {
+    if ((st = find_tensor(m, prefix, "embeddings.token_type_embeddings.weight", {-1, H}, &tt)))
+      return st;
+    if (tt->shape[0] < 1) return fail(RH_ERR_MISSING, "token_type_embeddings has no rows");
+  }
   if ((st = find_tensor(m, prefix, "embeddings.LayerNorm.weight", {H}, &eg))) return st;
   if ((st = find_tensor(m, prefix, "embeddings.LayerNorm.bias", {H}, &eb))) return st;
   if ((st = upload(we->data.data(), we->data.size(), &m->word))) return st;
   if ((st = upload(pe->data.data(), pe->data.size(), &m->pos))) return st;
-  if ((st = upload(tt->data.data(), H, &m->type0))) return st;
+  if (tt && (st = upload(tt->data.data(), H, &m->type0))) return st;
   if ((st = upload(eg->data.data(), H, &m->emb_g))) return st;
   if ((st = upload(eb->data.data(), H, &m->emb_b))) return st;
+  if (mpnet) {
+    const int nb = m->cfg.rel_buckets, heads = m->cfg.heads, L = m->max_seq();
+    const HostTensor* rb;
+    if ((st = find_tensor(m, prefix, "encoder.relative_attention_bias.weight", {nb, heads}, &rb)))
+      return st;
+    const int nd = 2 * L - 1;
+    std::vector<float> tab((size_t)heads * nd);
+    for (int d = -(L - 1); d <= L - 1; d++) {
+      const int b = rel_pos_bucket(d, nb);
+      for (int h = 0; h < heads; h++) tab[(size_t)h * nd + d + L - 1] = rb->data[(size_t)b * heads + h];
+    }
+    if ((st = upload(tab.data(), tab.size(), &m->rel_bias))) return st;
+  }
+
+  // tensor names per layer: BERT / RoBERTa, DistilBERT, MPNet
+  struct Names {
+    const char *q, *qb, *k, *kb, *v, *vb, *o, *ob, *g1, *b1, *f1, *f1b, *f2, *f2b, *g2, *b2;
+  };
+  static const Names kBert = {"attention.self.query.weight", "attention.self.query.bias",
+                              "attention.self.key.weight", "attention.self.key.bias",
+                              "attention.self.value.weight", "attention.self.value.bias",
+                              "attention.output.dense.weight", "attention.output.dense.bias",
+                              "attention.output.LayerNorm.weight", "attention.output.LayerNorm.bias",
+                              "intermediate.dense.weight", "intermediate.dense.bias",
+                              "output.dense.weight", "output.dense.bias",
+                              "output.LayerNorm.weight", "output.LayerNorm.bias"};
+  static const Names kDistil = {"attention.q_lin.weight", "attention.q_lin.bias",
+                                "attention.k_lin.weight", "attention.k_lin.bias",
+                                "attention.v_lin.weight", "attention.v_lin.bias",
+                                "attention.out_lin.weight", "attention.out_lin.bias",
+                                "sa_layer_norm.weight", "sa_layer_norm.bias",
+                                "ffn.lin1.weight", "ffn.lin1.bias", "ffn.lin2.weight",
+                                "ffn.lin2.bias", "output_layer_norm.weight",
+                                "output_layer_norm.bias"};
+  static const Names kMpnet = {"attention.attn.q.weight", "attention.attn.q.bias",
+                               "attention.attn.k.weight", "attention.attn.k.bias",
+                               "attention.attn.v.weight", "attention.attn.v.bias",
+                               "attention.attn.o.weight", "attention.attn.o.bias",
+                               "attention.LayerNorm.weight", "attention.LayerNorm.bias",
+                               "intermediate.dense.weight", "intermediate.dense.bias",
+                               "output.dense.weight", "output.dense.bias",
+                               "output.LayerNorm.weight", "output.LayerNorm.bias"};
+  const Names& nm = distil ? kDistil : (mpnet ? kMpnet : kBert);
 
   m->layers.resize(m->cfg.layers);
   for (int l = 0; l < m->cfg.layers; l++) {
     char p[64];
-    snprintf(p, sizeof p, "encoder.layer.%d.", l);
+    snprintf(p, sizeof p, distil ? "transformer.layer.%d." : "encoder.layer.%d.", l);
     const std::string lp = p;
     const HostTensor *qw, *qb, *kw, *kb, *vw, *vb, *ow, *ob, *g1, *b1, *f1w, *f1b, *f2w,
         *f2b, *g2, *b2;
@@ -1133,22 +1212,10 @@ static int finalize_bert(rh_model* m) {
       const HostTensor** dst;
     };
     const Need needs[] = {
-        {"attention.self.query.weight", {H, H}, &qw},
-        {"attention.self.query.bias", {H}, &qb},
-        {"attention.self.key.weight", {H, H}, &kw},
-        {"attention.self.key.bias", {H}, &kb},
-        {"attention.self.value.weight", {H, H}, &vw},
-        {"attention.self.value.bias", {H}, &vb},
-        {"attention.output.dense.weight", {H, H}, &ow},
-        {"attention.output.dense.bias", {H}, &ob},
-        {"attention.output.LayerNorm.weight", {H}, &g1},
-        {"attention.output.LayerNorm.bias", {H}, &b1},
-        {"intermediate.dense.weight", {I, H}, &f1w},
-        {"intermediate.dense.bias", {I}, &f1b},
-        {"output.dense.weight", {H, I}, &f2w},
-        {"output.dense.bias", {H}, &f2b},
-        {"output.LayerNorm.weight", {H}, &g2},
-        {"output.LayerNorm.bias", {H}, &b2},
+        {nm.q, {H, H}, &qw},   {nm.qb, {H}, &qb},   {nm.k, {H, H}, &kw},   {nm.kb, {H}, &kb},
+        {nm.v, {H, H}, &vw},   {nm.vb, {H}, &vb},   {nm.o, {H, H}, &ow},   {nm.ob, {H}, &ob},
+        {nm.g1, {H}, &g1},     {nm.b1, {H}, &b1},   {nm.f1, {I, H}, &f1w}, {nm.f1b, {I}, &f1b},
+        {nm.f2, {H, I}, &f2w}, {nm.f2b, {H}, &f2b}, {nm.g2, {H}, &g2},     {nm.b2, {H}, &b2},
     };
     for (const Need& n : needs)
       if ((st = find_tensor(m, prefix, lp + n.name, n.shape, n.dst))) return st;
@@ -1435,15 +1502,24 @@ extern "C" {
 int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_model** out) {
   return api_call([&]() -> int {
     if (!ctx || !cfg || !out) return fail(RH_ERR_INVALID, "null argument");
-    if (cfg->arch < RH_ARCH_BERT || cfg->arch > RH_ARCH_MODERNBERT)
+    if (cfg->arch < RH_ARCH_BERT || cfg->arch > RH_ARCH_MPNET)
       return fail(RH_ERR_INVALID, "unsupported arch");
+    const bool bert_family = cfg->arch == RH_ARCH_BERT || cfg->arch == RH_ARCH_DISTILBERT ||
+                             cfg->arch == RH_ARCH_MPNET;
     if (cfg->hidden <= 0 || cfg->heads <= 0) return fail(RH_ERR_INVALID, "bad hidden/heads");
     if (cfg->intermediate <= 0 || cfg->layers <= 0 || cfg->vocab <= 0 || cfg->max_position <= 0)
       return fail(RH_ERR_INVALID, "bad config sizes");
     if (cfg->hidden % 64 != 0 || cfg->hidden > 4096)
       return fail(RH_ERR_INVALID, "hidden must be a multiple of 64 and <= 4096");
     if (quant < RH_QUANT_NONE || quant > RH_QUANT_FULL) return fail(RH_ERR_INVALID, "bad quant");
-    if (cfg->arch == RH_ARCH_BERT) {
+    if (bert_family) {
+      // MPNet's bucketing is HF's at 32 buckets (config.go:219-221); the
+      // others have no relative-position bias
+      if ((cfg->arch == RH_ARCH_MPNET) != (cfg->rel_buckets != 0) ||
+          (cfg->rel_buckets != 0 && cfg->rel_buckets != 32))
+        return fail(RH_ERR_INVALID, "relative-position buckets: 32 for MPNet, 0 otherwise");
+      if (cfg->position_offset < 0 || cfg->position_offset >= cfg->max_position)
+        return fail(RH_ERR_INVALID, "bad position offset");
       if (cfg->intermediate % 4 != 0)
         return fail(RH_ERR_INVALID, "intermediate must divide by 4");
       if (cfg->hidden % cfg->heads != 0 || cfg->hidden > 2048)
@@ -1493,7 +1569,7 @@ int rh_model_create(rh_context* ctx, const rh_model_config* cfg, int quant, rh_m
     // fp32-grade attention (the reference's attention is float32) for the
     // BERT family in every mode; the RoPE family's quantized modes keep bf16
     // operands (their dh-256 fp32-grade kernel is the unpipelined one)
-    m->attn_precision = quant == RH_QUANT_NONE || cfg->arch == RH_ARCH_BERT ? 3 : 1;
+    m->attn_precision = quant == RH_QUANT_NONE || bert_family ? 3 : 1;
     *out = m;
     return RH_OK;
   });

@@ -342,6 +342,10 @@ struct AttnArgs {
   int ldctx;
   int causal;  // key j visible to query i only if j <= i (qwen3.go:307-390)
   int window;  // > 0: key j visible only if |i - j| < window (gemma3.go:339-347)
+  // MPNet: score(i, j) = score*scale + rel_bias[h * (2 * rel_center + 1) +
+  // (j - i) + rel_center] (bert.go:876-890), or null
+  const float* rel_bias;
+  int rel_center;
 };
 // precision: 1 = bf16 MFMA, 3 = three-term bf16 split (fp32-grade; with
 // in_bf16 2 the split arrives as hi/lo planes and runs on the pipelined

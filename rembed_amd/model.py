@@ -18,6 +18,7 @@ QUANT_WEIGHTS = _lib.RH_QUANT_WEIGHTS  # WithInt8 (rembed.go:67-69)
 QUANT_FULL = _lib.RH_QUANT_FULL        # WithInt8Activations (rembed.go:79-81)
 ARCH_BERT, ARCH_QWEN3, ARCH_GEMMA3 = _lib.RH_ARCH_BERT, _lib.RH_ARCH_QWEN3, _lib.RH_ARCH_GEMMA3
 ARCH_NOMIC, ARCH_MODERNBERT = _lib.RH_ARCH_NOMIC, _lib.RH_ARCH_MODERNBERT
+ARCH_DISTILBERT, ARCH_MPNET = _lib.RH_ARCH_DISTILBERT, _lib.RH_ARCH_MPNET
 
 
 def make_config(shape):
@@ -33,10 +34,11 @@ def make_config(shape):
     c.layer_norm_eps = shape.eps
     c.pooling = shape.pooling
     c.normalize = shape.normalize
-    if c.arch == _lib.RH_ARCH_BERT:
+    if c.arch in (_lib.RH_ARCH_BERT, _lib.RH_ARCH_DISTILBERT, _lib.RH_ARCH_MPNET):
         c.max_position = shape.max_position
         c.position_offset = getattr(shape, "position_offset", 0)
         c.type_vocab = shape.type_vocab
+        c.rel_buckets = getattr(shape, "rel_buckets", 0)
     elif c.arch in (_lib.RH_ARCH_NOMIC, _lib.RH_ARCH_MODERNBERT):  # config.go:44-53,163-175
         c.max_position = shape.max_seq
         c.head_dim = shape.head_dim

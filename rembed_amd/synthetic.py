@@ -17,6 +17,9 @@ from dataclasses import dataclass
 import numpy as np
 
 
+ARCH_BERT, ARCH_DISTILBERT, ARCH_MPNET = 0, 5, 6  # RH_ARCH_* of the BERT family
+
+
 @dataclass(frozen=True)
 class BertShape:
     name: str
@@ -30,10 +33,46 @@ class BertShape:
     eps: float = 1e-12
     pooling: int = 0      # 0 mean, 1 cls, 2 last
     normalize: int = 1
+    arch: int = ARCH_BERT  # BERT / RoBERTa, DistilBERT or MPNet names and attention
+    position_offset: int = 0  # Config.PositionOffset (config.go:84-89)
+    rel_buckets: int = 0  # MPNet's relative-position bias buckets
 
 
 MINILM_L6 = BertShape("minilm-l6", 6, 384, 12, 1536, pooling=0)
 BERT_BASE = BertShape("bert-base", 12, 768, 12, 3072, pooling=1)
+# multi-qa-distilbert-cos-v1 / all-mpnet-base-v2 shapes (the reference's
+# testdata goldens for the two architectures); DistilBERT has no token-type
+# table, MPNet neither, and MPNet's position rows start past pad_token_id = 1
+# (config.go:84-89) with 32 relative-position buckets (config.go:219-224).
+DISTILBERT_BASE = BertShape("distilbert-base", 6, 768, 12, 3072, type_vocab=0, pooling=1,
+                            arch=ARCH_DISTILBERT)
+MPNET_BASE = BertShape("mpnet-base", 12, 768, 12, 3072, vocab=30527, max_position=514,
+                       type_vocab=0, eps=1e-5, pooling=0, arch=ARCH_MPNET, position_offset=2,
+                       rel_buckets=32)
+
+
+def layer_names(arch, l):
+    """The 16 per-layer tensor names, in the order q_w q_b k_w k_b v_w v_b
+    o_w o_b ln1_g ln1_b f1_w f1_b f2_w f2_b ln2_g ln2_b (bert.go:399-470)."""
+    if arch == ARCH_DISTILBERT:
+        p = f"transformer.layer.{l}."
+        attn = [p + f"attention.{n}_lin.{w}" for n in ("q", "k", "v", "out") for w in ("weight", "bias")]
+        return attn + [p + "sa_layer_norm.weight", p + "sa_layer_norm.bias",
+                       p + "ffn.lin1.weight", p + "ffn.lin1.bias",
+                       p + "ffn.lin2.weight", p + "ffn.lin2.bias",
+                       p + "output_layer_norm.weight", p + "output_layer_norm.bias"]
+    p = f"encoder.layer.{l}."
+    if arch == ARCH_MPNET:
+        attn = [p + f"attention.attn.{n}.{w}" for n in ("q", "k", "v", "o") for w in ("weight", "bias")]
+        ln1 = [p + "attention.LayerNorm.weight", p + "attention.LayerNorm.bias"]
+    else:
+        attn = [p + f"attention.self.{n}.{w}" for n in ("query", "key", "value")
+                for w in ("weight", "bias")]
+        attn += [p + "attention.output.dense.weight", p + "attention.output.dense.bias"]
+        ln1 = [p + "attention.output.LayerNorm.weight", p + "attention.output.LayerNorm.bias"]
+    return attn + ln1 + [p + "intermediate.dense.weight", p + "intermediate.dense.bias",
+                         p + "output.dense.weight", p + "output.dense.bias",
+                         p + "output.LayerNorm.weight", p + "output.LayerNorm.bias"]
 
 
 def bert_tensors(shape: BertShape, seed: int = 0x5EED0001):
@@ -50,25 +89,21 @@ def bert_tensors(shape: BertShape, seed: int = 0x5EED0001):
     t = {
         "embeddings.word_embeddings.weight": normal(shape.vocab, H),
         "embeddings.position_embeddings.weight": normal(shape.max_position, H),
-        "embeddings.token_type_embeddings.weight": normal(shape.type_vocab, H),
-        "embeddings.LayerNorm.weight": gamma(H),
-        "embeddings.LayerNorm.bias": normal(H),
     }
+    if shape.type_vocab:
+        t["embeddings.token_type_embeddings.weight"] = normal(shape.type_vocab, H)
+    t["embeddings.LayerNorm.weight"] = gamma(H)
+    t["embeddings.LayerNorm.bias"] = normal(H)
     for l in range(shape.layers):
-        p = f"encoder.layer.{l}."
-        for nm in ("query", "key", "value"):
-            t[p + f"attention.self.{nm}.weight"] = normal(H, H)
-            t[p + f"attention.self.{nm}.bias"] = normal(H)
-        t[p + "attention.output.dense.weight"] = normal(H, H)
-        t[p + "attention.output.dense.bias"] = normal(H)
-        t[p + "attention.output.LayerNorm.weight"] = gamma(H)
-        t[p + "attention.output.LayerNorm.bias"] = normal(H)
-        t[p + "intermediate.dense.weight"] = normal(I, H)
-        t[p + "intermediate.dense.bias"] = normal(I)
-        t[p + "output.dense.weight"] = normal(H, I)
-        t[p + "output.dense.bias"] = normal(H)
-        t[p + "output.LayerNorm.weight"] = gamma(H)
-        t[p + "output.LayerNorm.bias"] = normal(H)
+        names = layer_names(shape.arch, l)
+        dims = [(H, H), (H,)] * 4 + [None, None, (I, H), (I,), (H, I), (H,), None, None]
+        for nm, d in zip(names, dims):
+            t[nm] = gamma(H) if d is None and nm.endswith("weight") else (
+                normal(H) if d is None else normal(*d))
+    if shape.rel_buckets:
+        # MPNet's bias table, scaled like a trained one (O(1) logits) so it
+        # moves the softmax
+        t["encoder.relative_attention_bias.weight"] = normal(shape.rel_buckets, shape.heads) * 25
     return t
 
 
