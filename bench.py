@@ -265,6 +265,9 @@ def main():
                     help="run only the default forward (warm-up, timed and profiled steps): "
                          "no fp32-attention rate, host-buffer rate, oracle comparison or CPU "
                          "baseline, so a profiler sees one kind of forward")
+    ap.add_argument("--graph", choices=["on", "off"], default="off",
+                    help="BERT family: replay each batch shape's forward as a recorded HIP "
+                         "graph (RH_OPT_GRAPH)")
     ap.add_argument("--streams", type=int, choices=[1, 2, 3, 4], default=2,
                     help="run a batch as this many parts of whole texts on as many streams "
                          "(default 2); the roofline pass always runs one stream")
@@ -295,6 +298,8 @@ def main():
     # split), the reference's float32 attention class; bf16 operands and the
     # reference-order (byte-exact) forward are timed beside it.
     model.set_attention_precision(3)
+    if bert:
+        model.set_graph(args.graph == "on")
     if quant == 2:
         assert model.quantized_activations(), "full-int8 path did not take"
         model.set_fused_ffn1(args.ffn1 == "fused")
@@ -395,6 +400,8 @@ def main():
         host_rate = tokens * host_steps / (sum(host_ms) * 1e-3)
         assert np.array_equal(vec, host_vec), "host-buffer and device-resident forwards differ"
     cfg_note = {"streams": args.streams}
+    if bert:
+        cfg_note["graph"] = args.graph
     if quant == 2:
         cfg_note["ffn1"] = args.ffn1
         cfg_note["qkv_rows"] = "fp32"

@@ -384,7 +384,13 @@ void rh_model_destroy(rh_model *m);
  * Softmax; bert.go:853-902), so a full-int8 forward's activations, GEMM
  * inputs and vectors are byte-identical to the reference's; 0 = the
  * wave-parallel LayerNorm and the RH_OPT_ATTN_PRECISION attention (default).
- * The fused-LN epilogue is not used while it is set. */
+ * The fused-LN epilogue is not used while it is set.
+ * RH_OPT_GRAPH (BERT family): 1 = a forward's launches are recorded once
+ * per batch shape (row offsets, ids and output buffers, model and context
+ * settings) as a HIP graph and replayed on the next call with the same
+ * shape; 0 = launched one by one. The graph holds kernels and stream
+ * fork/join edges only (no memset or allocation); identical results. Used
+ * where the forward needs no context split workspace and profiling is off. */
 #define RH_OPT_ATTN_PRECISION 1
 #define RH_OPT_FUSED_FFN1 2
 #define RH_OPT_PRODUCER_PLANES 3
@@ -393,6 +399,7 @@ void rh_model_destroy(rh_model *m);
 #define RH_OPT_FUSE_PROJECTIONS 6
 #define RH_OPT_FUSED_LN 7
 #define RH_OPT_EXACT 8
+#define RH_OPT_GRAPH 9
 int rh_model_set_option(rh_model *m, int option, int value);
 /* Model.Quantized / QuantizedActivations (bert.go:526-644). */
 int rh_model_quantized(const rh_model *m);

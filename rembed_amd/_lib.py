@@ -37,6 +37,7 @@ RH_OPT_QK_EPILOGUE = 5
 RH_OPT_FUSE_PROJECTIONS = 6
 RH_OPT_FUSED_LN = 7
 RH_OPT_EXACT = 8
+RH_OPT_GRAPH = 9
 RH_CTX_F32_ALGO, RH_CTX_W8_TERMS, RH_CTX_I8_TILE, RH_CTX_BF_ALGO, RH_CTX_BF_TILE = 1, 2, 3, 4, 5
 RH_CTX_TILE_GROUP = 6
 RH_NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024

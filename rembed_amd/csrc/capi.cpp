@@ -733,6 +733,7 @@ int rh_context_set_option(rh_context* ctx, int option, int value) {
   return api_call([&]() -> int {
     if (!ctx) return fail(RH_ERR_INVALID, "null context");
     std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->generation++;
     switch (option) {
       case RH_CTX_F32_ALGO:
         if (value != F32_SPLIT3 && value != F32_NATIVE) return fail(RH_ERR_INVALID, "unknown fp32 algo");

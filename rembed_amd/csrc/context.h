@@ -24,6 +24,9 @@ struct rh_context {
   int bf_algo = 0;   // W8/F32 GEMM: 0 = bf16 planes (pre-split), 1 = in-kernel split
   int bf_tile = 0;   // 0 = automatic bf16-planes GEMM tile choice
   int tile_group = 4;  // GEMM tile order: row blocks per group (1 = row-major)
+  // bumped by every rh_context_set_option: forwards recorded as HIP graphs
+  // under older settings are re-recorded
+  int generation = 0;
   // grow-only device workspace (bf16 planes of the activations); the context
   // serializes its calls, so one buffer serves every GEMM on its stream
   void* ws = nullptr;

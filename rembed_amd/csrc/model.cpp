@@ -238,6 +238,7 @@ struct rh_model {
         (void)hipEventDestroy(e);
         e = nullptr;
       }
+    drop_graph();
     release_ws();
     // Drop this handle's reference to the weights; a model that never
     // finalized (or failed to) owns what it built so far and frees it here.
@@ -323,8 +324,10 @@ struct rh_model {
 
   int ensure_ws(int rows, int batch, size_t ids_elems) {
     const int H = this->H(), I = this->I();
-    if (rows > cap || batch > cap_batch || ids_elems > cap_ids)
+    if (rows > cap || batch > cap_batch || ids_elems > cap_ids) {
       RH_HIP(hipStreamSynchronize(ctx->stream));  // buffers may be in flight
+      drop_graph();  // a recorded forward holds the old buffers' addresses
+    }
     if (rows > cap) {
       int newcap = (int)round_up(rows, 256);
       for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
@@ -462,6 +465,26 @@ struct rh_model {
   int join_parts(const std::vector<Part>& parts, hipStream_t s);
 
   // The forward over rows already planned; ids_dev is [batch][stride].
+  // RH_OPT_GRAPH: the BERT family's forward recorded once per batch shape
+  // (row offsets, ids and output buffers, settings) as a HIP graph and
+  // replayed; any change of shape, option or workspace records it again.
+  bool use_graph = false;
+  struct Graph {
+    std::vector<int32_t> cu;
+    const int32_t* ids = nullptr;
+    int stride = 0, max_len = 0, generation = -1;
+    bool pool = false;
+    float* out = nullptr;
+    hipGraphExec_t exec = nullptr;
+  } graph;
+  void drop_graph() {
+    if (graph.exec) (void)hipGraphExecDestroy(graph.exec);
+    graph = Graph{};
+  }
+  int ensure_streams();
+  bool bert_no_ws() const;
+  int forward_bert(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
+                   int max_len, bool pool, float* out_dev);
   int forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
               int max_len, bool pool, float* out_dev);
   int forward_dec(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
@@ -520,14 +543,36 @@ int rh_model::join_parts(const std::vector<Part>& parts, hipStream_t s) {
   return RH_OK;
 }
 
+// Streams and events the parts use, created before a recording (so nothing
+// is created while the stream is captured).
+int rh_model::ensure_streams() {
+  if (!ev_fork) RH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+  for (int k = 1; k < streams; k++) {
+    if (!sx[k]) RH_HIP(hipStreamCreate(&sx[k]));
+    if (!ev_join[k]) RH_HIP(hipEventCreateWithFlags(&ev_join[k], hipEventDisableTiming));
+  }
+  return RH_OK;
+}
+
+// No linear of the BERT-family forward falls back to the context's split
+// workspace (full int8, or every input arrives as producer-written planes):
+// the condition for parts on streams and for recording the forward.
+bool rh_model::bert_no_ws() const {
+  bool no_ws = true;
+  for (const Layer& L : layers) {
+    no_ws = no_ws && !uses_split_ws(L.qkv, planes_in(L.qkv)) &&
+            !uses_split_ws(L.o, planes_in(L.o)) && !uses_split_ws(L.f1, planes_in(L.f1)) &&
+            !uses_split_ws(L.f2, planes_in(L.f2) && linear_on_planes(ctx, L.f1));
+  }
+  return no_ws;
+}
+
 int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
                       int max_len, bool pool, float* out_dev) {
   if (rope_family()) return forward_dec(ids_dev, stride, cu, max_len, pool, out_dev);
   hipStream_t s = ctx->stream;
   const int batch = (int)cu.size() - 1;
   const int M = cu[batch];
-  const int H = this->H(), I = this->I();
-  const int heads = cfg.heads, dh = H / heads;
   int st = ensure_ws(M, batch, 0);
   if (st) return st;
   // Row offsets: reuse the pinned buffer once its previous copy finished.
@@ -536,6 +581,52 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
   RH_HIP(hipMemcpyAsync(cu_d, cu_pinned, (batch + 1) * sizeof(int32_t),
                         hipMemcpyHostToDevice, s));
   RH_HIP(hipEventRecord(cu_evt, s));
+  if (!use_graph || ctx->profiling || !bert_no_ws())
+    return forward_bert(ids_dev, stride, cu, max_len, pool, out_dev);
+  if (graph.exec && graph.cu == cu && graph.ids == ids_dev && graph.stride == stride &&
+      graph.max_len == max_len && graph.pool == pool && graph.out == out_dev &&
+      graph.generation == ctx->generation) {
+    RH_HIP(hipGraphLaunch(graph.exec, s));
+    return RH_OK;
+  }
+  drop_graph();
+  if ((st = ensure_streams())) return st;
+  // Record the forward's launches (every part's stream joins the capture
+  // through the fork/join events), then replay the graph. The forward has
+  // no memset, allocation or host synchronization once the workspace is
+  // sized, so the recording holds only kernels and event edges.
+  RH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  st = forward_bert(ids_dev, stride, cu, max_len, pool, out_dev);
+  hipGraph_t g = nullptr;
+  const hipError_t ec = hipStreamEndCapture(s, &g);
+  if (st || ec != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    return st ? st : hip_fail(ec, "forward capture", __FILE__, __LINE__);
+  }
+  hipGraphExec_t exec = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (ei != hipSuccess) return hip_fail(ei, "graph instantiate", __FILE__, __LINE__);
+  graph.cu = cu;
+  graph.ids = ids_dev;
+  graph.stride = stride;
+  graph.max_len = max_len;
+  graph.pool = pool;
+  graph.out = out_dev;
+  graph.generation = ctx->generation;
+  graph.exec = exec;
+  RH_HIP(hipGraphLaunch(exec, s));
+  return RH_OK;
+}
+
+int rh_model::forward_bert(const int32_t* ids_dev, int stride, const std::vector<int32_t>& cu,
+                           int max_len, bool pool, float* out_dev) {
+  hipStream_t s = ctx->stream;
+  const int batch = (int)cu.size() - 1;
+  const int M = cu[batch];
+  const int H = this->H(), I = this->I();
+  const int heads = cfg.heads, dh = H / heads;
+  int st;
 
   // Embeddings + LayerNorm (+ u8 quantization when the first QKV is int8).
   const bool q0 = !layers.empty() && needs_q(layers[0].qkv);
@@ -571,14 +662,8 @@ int rh_model::forward(const int32_t* ids_dev, int stride, const std::vector<int3
 
   // Parts (see plan_parts): allowed when no linear falls back to the
   // context's split workspace.
-  bool no_ws = true;
-  for (const Layer& L : layers) {
-    no_ws = no_ws && !uses_split_ws(L.qkv, planes_in(L.qkv)) &&
-            !uses_split_ws(L.o, planes_in(L.o)) && !uses_split_ws(L.f1, planes_in(L.f1)) &&
-            !uses_split_ws(L.f2, planes_in(L.f2) && linear_on_planes(ctx, L.f1));
-  }
   std::vector<Part> parts;
-  if ((st = plan_parts(cu, no_ws, s, parts))) return st;
+  if ((st = plan_parts(cu, bert_no_ws(), s, parts))) return st;
   auto part_attn_ops = [&](const Part& P) {
     double ops = 0;
     for (int b = P.b0; b < P.b0 + P.nb; b++) {
@@ -1579,6 +1664,12 @@ int rh_model_set_option(rh_model* m, int option, int value) {
   return api_call([&]() -> int {
     if (!m) return fail(RH_ERR_INVALID, "null model");
     std::lock_guard<std::mutex> lk(m->mu);
+    m->drop_graph();  // a recorded forward follows the settings it was recorded under
+    if (option == RH_OPT_GRAPH) {
+      if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "graph must be 0 or 1");
+      m->use_graph = value != 0;
+      return RH_OK;
+    }
     if (option == RH_OPT_ATTN_PRECISION) {
       if (value != 1 && value != 3) return fail(RH_ERR_INVALID, "attn precision must be 1 or 3");
       m->attn_precision = value;
@@ -1703,6 +1794,7 @@ int rh_model_share(rh_model* src, rh_context* ctx, rh_model** out) {
     m->attn_precision = src->attn_precision;
     m->fused_ffn1 = src->fused_ffn1;
     m->exact = src->exact;
+    m->use_graph = src->use_graph;
     m->fused_ln = src->fused_ln;
     m->producer_planes = src->producer_planes;
     m->streams = src->streams;

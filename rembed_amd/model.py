@@ -131,6 +131,11 @@ class Model:
         byte-identical to the reference's (False: the default kernels)."""
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_EXACT, 1 if on else 0))
 
+    def set_graph(self, on=True):
+        """RH_OPT_GRAPH (BERT family): record a forward once per batch shape
+        as a HIP graph and replay it (identical results)."""
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_GRAPH, 1 if on else 0))
+
     def set_fused_ln(self, on=True):
         """RH_OPT_FUSED_LN: full-int8 O / FFN2 projections finish the
         residual add + LayerNorm in their epilogue (identical results)."""
