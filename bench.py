@@ -294,10 +294,14 @@ def main():
     model = Model(ctx, shape, tensors, quant)
     model.set_streams(args.streams)
     bert = "embeddings.position_embeddings.weight" in tensors  # the BERT family
-    # `value` runs attention in float32-grade arithmetic (the three-term bf16
-    # split), the reference's float32 attention class; bf16 operands and the
-    # reference-order (byte-exact) forward are timed beside it.
-    model.set_attention_precision(3)
+    # `value` runs the library's default attention: for the BERT family
+    # float32-grade arithmetic (the three-term bf16 split on the q|k|v
+    # rows' hi/lo planes), the reference's float32 attention class; for the
+    # RoPE family's quantized modes bf16 operands. The other precision and,
+    # for the BERT family, the reference-order (byte-exact) forward are
+    # timed beside it.
+    prec = 3 if (bert or quant == 0) else 1
+    model.set_attention_precision(prec)
     if bert:
         model.set_graph(args.graph == "on")
     if quant == 2:
@@ -343,13 +347,15 @@ def main():
         model.check()
         return r
 
-    # Beside `value`: bf16 attention operands (fp32 softmax and accumulation),
-    # and for the BERT family the byte-exact forward (RH_OPT_EXACT: LayerNorm
-    # sums and attention in the reference's own float32 order).
-    attn1_rate = exact_rate = None
+    # Beside `value`: the other attention precision (bf16 operands with fp32
+    # softmax and accumulation, or the fp32-grade split), and for the BERT
+    # family the byte-exact forward (RH_OPT_EXACT: LayerNorm sums and
+    # attention in the reference's own float32 order).
+    other_rate = exact_rate = None
+    other = 1 if prec == 3 else 3
     if quant != 0 and not args.forwards_only:
-        attn1_rate = rate_with(lambda: model.set_attention_precision(1),
-                               lambda: model.set_attention_precision(3))
+        other_rate = rate_with(lambda: model.set_attention_precision(other),
+                               lambda: model.set_attention_precision(prec))
     if bert and not args.forwards_only:
         exact_rate = rate_with(lambda: model.set_exact(True), lambda: model.set_exact(False))
 
@@ -404,9 +410,12 @@ def main():
         cfg_note["graph"] = args.graph
     if quant == 2:
         cfg_note["ffn1"] = args.ffn1
-        cfg_note["qkv_rows"] = "fp32"
-    cfg_note["attention"] = ("fp32-grade: q|k|v and P split into bf16 hi/lo, three MFMA "
-                             "products, fp32 softmax and accumulation (RH_OPT_ATTN_PRECISION 3)")
+        cfg_note["qkv_rows"] = ("bf16 hi/lo planes of the fp32 rows (the q|k|v GEMM's epilogue "
+                                "writes the split)" if prec == 3 and bert else "fp32")
+    cfg_note["attention"] = (
+        "fp32-grade: q|k|v and P split into bf16 hi/lo, three MFMA products, fp32 softmax "
+        "and accumulation (RH_OPT_ATTN_PRECISION 3)" if prec == 3 else
+        "bf16 MFMA operands, fp32 softmax and accumulation (RH_OPT_ATTN_PRECISION 1)")
     norms = np.linalg.norm(vec.astype(np.float64), axis=1)
     assert np.all(np.abs(norms - 1) < 1e-4), "embeddings are not unit vectors"
 
@@ -475,7 +484,8 @@ def main():
                     "p90": round(pct(step_ms, 90), 4), "steps": int(step_ms.size),
                     "clock": "HIP events between steps on the library stream"},
         "median_tokens_per_s": round(tokens / (pct(step_ms, 50) * 1e-3), 1),
-        "bf16_attention_tokens_per_s": None if attn1_rate is None else round(attn1_rate, 1),
+        ("bf16_attention_tokens_per_s" if other == 1 else "fp32_attention_tokens_per_s"):
+            None if other_rate is None else round(other_rate, 1),
         "exact_tokens_per_s": None if exact_rate is None else round(exact_rate, 1),
         "pcie_inclusive_tokens_per_s": None if host_rate is None else round(host_rate, 1),
         "pcie_inclusive_step_ms": None if not host_ms else {
