@@ -1,0 +1,137 @@
+// blaslt_ref.cpp — the vendor-library comparison line of the int8 GEMM
+// microbenchmark: hipBLASLt's int8 x int8 -> int32 GEMM at the encoder's
+// shapes, C[M][N] = A[M][K] · B[N][K]^T (row-major, the reference's bT
+// layout), every heuristic candidate (up to 16) timed with HIP events, the
+// fastest reported. Built and run by `python -m rembed_amd.microbench
+// --hipblaslt`; not part of the library.
+//
+// Output: one JSON object per shape on stdout.
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <random>
+#include <vector>
+
+#define HCHK(x)                                                              \
+  do {                                                                       \
+    hipError_t e_ = (x);                                                     \
+    if (e_ != hipSuccess) {                                                  \
+      fprintf(stderr, "HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); \
+      return 1;                                                              \
+    }                                                                        \
+  } while (0)
+#define BCHK(x)                                                              \
+  do {                                                                       \
+    hipblasStatus_t s_ = (x);                                                \
+    if (s_ != HIPBLAS_STATUS_SUCCESS) {                                      \
+      fprintf(stderr, "hipBLASLt status %d at %s:%d\n", (int)s_, __FILE__, __LINE__); \
+      return 1;                                                              \
+    }                                                                        \
+  } while (0)
+
+static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters) {
+  std::vector<int8_t> a((size_t)M * K), b((size_t)N * K);
+  std::mt19937 g(7);
+  for (auto& v : a) v = (int8_t)(g() & 255);
+  for (auto& v : b) v = (int8_t)(g() & 255);
+  int8_t *dA, *dB;
+  int32_t* dC;
+  void* ws;
+  const size_t ws_bytes = 64u << 20;
+  HCHK(hipMalloc(&dA, a.size()));
+  HCHK(hipMalloc(&dB, b.size()));
+  HCHK(hipMalloc(&dC, (size_t)M * N * 4));
+  HCHK(hipMalloc(&ws, ws_bytes));
+  HCHK(hipMemcpy(dA, a.data(), a.size(), hipMemcpyHostToDevice));
+  HCHK(hipMemcpy(dB, b.data(), b.size(), hipMemcpyHostToDevice));
+
+  // Column-major view: C^T (N x M, ld N) = op(B^T as K x N, ld K)^T · (A^T as K x M, ld K).
+  hipblasLtMatmulDesc_t op;
+  BCHK(hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32I, HIP_R_32I));
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  BCHK(hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)));
+  BCHK(hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)));
+  hipblasLtMatrixLayout_t la, lb, lc;
+  BCHK(hipblasLtMatrixLayoutCreate(&la, HIP_R_8I, K, N, K));
+  BCHK(hipblasLtMatrixLayoutCreate(&lb, HIP_R_8I, K, M, K));
+  BCHK(hipblasLtMatrixLayoutCreate(&lc, HIP_R_32I, N, M, N));
+  hipblasLtMatmulPreference_t pref;
+  BCHK(hipblasLtMatmulPreferenceCreate(&pref));
+  BCHK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                             &ws_bytes, sizeof(ws_bytes)));
+  hipblasLtMatmulHeuristicResult_t res[16];
+  int n = 0;
+  BCHK(hipblasLtMatmulAlgoGetHeuristic(h, op, la, lb, lc, lc, pref, 16, res, &n));
+  const int32_t alpha = 1, beta = 0;
+  hipEvent_t e0, e1;
+  HCHK(hipEventCreate(&e0));
+  HCHK(hipEventCreate(&e1));
+  float best = 1e30f;
+  int best_i = -1, tried = 0;
+  for (int i = 0; i < n; i++) {
+    if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > ws_bytes) continue;
+    auto run = [&]() {
+      return hipblasLtMatmul(h, op, &alpha, dB, la, dA, lb, &beta, dC, lc, dC, lc, &res[i].algo,
+                             ws, ws_bytes, 0);
+    };
+    if (run() != HIPBLAS_STATUS_SUCCESS) continue;
+    HCHK(hipDeviceSynchronize());
+    HCHK(hipEventRecord(e0, 0));
+    for (int r = 0; r < iters; r++) BCHK(run());
+    HCHK(hipEventRecord(e1, 0));
+    HCHK(hipEventSynchronize(e1));
+    float ms = 0;
+    HCHK(hipEventElapsedTime(&ms, e0, e1));
+    const float us = ms * 1000.0f / iters;
+    tried++;
+    if (us < best) {
+      best = us;
+      best_i = i;
+    }
+  }
+  // spot check of the best candidate's int32 accumulators
+  int bad = -1;
+  if (best_i >= 0) {
+    BCHK(hipblasLtMatmul(h, op, &alpha, dB, la, dA, lb, &beta, dC, lc, dC, lc, &res[best_i].algo,
+                         ws, ws_bytes, 0));
+    std::vector<int32_t> c((size_t)M * N);
+    HCHK(hipMemcpy(c.data(), dC, c.size() * 4, hipMemcpyDeviceToHost));
+    bad = 0;
+    for (int s = 0; s < 64; s++) {
+      const int r = (s * 7919) % M, col = (s * 104729) % N;
+      long acc = 0;
+      for (int k = 0; k < K; k++) acc += (long)a[(size_t)r * K + k] * b[(size_t)col * K + k];
+      if ((int32_t)acc != c[(size_t)r * N + col]) bad++;
+    }
+  }
+  const double ops = 2.0 * M * K * N;
+  printf("{\"m\": %d, \"k\": %d, \"n\": %d, \"candidates\": %d, \"timed\": %d, \"best_us\": %.2f, "
+         "\"tops\": %.0f, \"check_bad\": %d}\n",
+         M, K, N, n, tried, best, ops / (best * 1e-6) / 1e12, bad);
+  fflush(stdout);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  hipblasLtMatrixLayoutDestroy(la);
+  hipblasLtMatrixLayoutDestroy(lb);
+  hipblasLtMatrixLayoutDestroy(lc);
+  hipblasLtMatmulDescDestroy(op);
+  (void)hipFree(dA);
+  (void)hipFree(dB);
+  (void)hipFree(dC);
+  (void)hipFree(ws);
+  return 0;
+}
+
+int main(int argc, char** argv) {
+  const int M = argc > 1 ? atoi(argv[1]) : 10102;
+  const int iters = argc > 2 ? atoi(argv[2]) : 20;
+  hipblasLtHandle_t h;
+  BCHK(hipblasLtCreate(&h));
+  const int shapes[][2] = {{768, 2304}, {768, 768}, {768, 3072}, {3072, 768}};
+  for (auto& s : shapes)
+    if (time_shape(h, M, s[0], s[1], iters)) return 1;
+  hipblasLtDestroy(h);
+  return 0;
+}

@@ -59,7 +59,24 @@ def build(verbose=True):
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_blaslt_ref()
     return LIB
+
+
+BLASLT_SRC = os.path.join(HERE, "blaslt_ref.cpp")
+BLASLT_BIN = os.path.join(HERE, "blaslt_ref")
+
+
+def build_blaslt_ref():
+    """The hipBLASLt comparison program of the int8 GEMM microbenchmark
+    (`python -m rembed_amd.microbench --hipblaslt`); not linked into the
+    library."""
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", BLASLT_SRC, "-lhipblaslt",
+           "-o", BLASLT_BIN]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {BLASLT_SRC}:\n{r.stderr}")
+    return BLASLT_BIN
 
 
 if __name__ == "__main__":

@@ -110,19 +110,32 @@ __device__ __forceinline__ float dot_serial_ref(const float (&a)[DH], const floa
   return s;
 }
 
-// Rows c0 .. c0+63 of the (text-local) key or value head into
-// chunk[64][exact_cpitch(DH)] (zeros past the text's last row).
+// Rows c0 .. c0+63 of the (text-local) key or value head, staged through
+// registers: fetch() issues this thread's 16-byte loads (zeros past the
+// text's last row) so they fly while the previous chunk is consumed,
+// commit() writes them to chunk[64][exact_cpitch(DH)].
 template <int DH>
-__device__ __forceinline__ void exact_stage(const float* __restrict__ src, int ld, int c0,
-                                            int len, float* __restrict__ chunk) {
-  constexpr int kVec = kXK * DH / 4, CP = exact_cpitch(DH);
-  for (int v = threadIdx.x; v < kVec; v += 256) {
-    const int r = v / (DH / 4), c = v % (DH / 4);
-    v4f x = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (c0 + r < len) x = *reinterpret_cast<const v4f*>(src + (size_t)(c0 + r) * ld + c * 4);
-    *reinterpret_cast<v4f*>(chunk + r * CP + c * 4) = x;
+struct ExactChunk {
+  static constexpr int kPer = kXK * DH / 4 / 256;  // float4 per thread
+  v4f x[kPer];
+  __device__ __forceinline__ void fetch(const float* __restrict__ src, int ld, int c0, int len) {
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+      const int v = threadIdx.x + u * 256;
+      const int r = v / (DH / 4), c = v % (DH / 4);
+      x[u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      if (c0 + r < len) x[u] = *reinterpret_cast<const v4f*>(src + (size_t)(c0 + r) * ld + c * 4);
+    }
   }
-}
+  __device__ __forceinline__ void commit(float* __restrict__ chunk) const {
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+      const int v = threadIdx.x + u * 256;
+      const int r = v / (DH / 4), c = v % (DH / 4);
+      *reinterpret_cast<v4f*>(chunk + r * exact_cpitch(DH) + c * 4) = x[u];
+    }
+  }
+};
 
 template <int DH>
 __device__ __forceinline__ void load_row(const float* __restrict__ src, float (&q)[DH]) {
@@ -159,6 +172,9 @@ __global__ __launch_bounds__(256) void attention_exact_kernel(AttnArgs p) {
   const float* kbase = base + p.k_off + h * DH;
   const float* vbase = base + p.v_off + h * DH;
 
+  ExactChunk<DH> stage;
+  stage.fetch(kbase, p.ldqkv, 0, len);
+
   // ---- scores: thread (queries i and i + 16, key group g of 16) -------------
   {
     const int i = t % H2, g = t / H2;
@@ -170,7 +186,11 @@ __global__ __launch_bounds__(256) void attention_exact_kernel(AttnArgs p) {
     float mxa = -INFINITY, mxb = -INFINITY;
     for (int c0 = 0; c0 < len; c0 += kXK) {
       __syncthreads();  // the previous chunk's reads are done
-      exact_stage<DH>(kbase, p.ldqkv, c0, len, chunk);
+      stage.commit(chunk);
+      // the next chunk's loads fly while this one is consumed: the next key
+      // chunk, or after the last one the first value chunk
+      if (c0 + kXK < len) stage.fetch(kbase, p.ldqkv, c0 + kXK, len);
+      else stage.fetch(vbase, p.ldqkv, 0, len);
       __syncthreads();
       for (int kk = g; kk < kXK; kk += 16) {
         const int j = c0 + kk;
@@ -238,7 +258,8 @@ __global__ __launch_bounds__(256) void attention_exact_kernel(AttnArgs p) {
   const float* pb = P + (i + H2) * lp;
   for (int c0 = 0; c0 < len; c0 += kXK) {
     __syncthreads();  // previous chunk's reads (and, first time, the row sums) done
-    exact_stage<DH>(vbase, p.ldqkv, c0, len, chunk);
+    stage.commit(chunk);
+    if (c0 + kXK < len) stage.fetch(vbase, p.ldqkv, c0 + kXK, len);
     __syncthreads();
     const float ia = rinv[i], ib = rinv[i + H2];
     const int kend = min(kXK, nb8 - c0);

@@ -6,6 +6,7 @@ Each case is timed with the library's per-launch HIP events on its own
 stream. Usage:
     python -m rembed_amd.microbench [--m 10102] [--iters 20] [--modes i8,w8,f32]
     python -m rembed_amd.microbench --attention bert-base,qwen3-0.6b,gemma-global
+    python -m rembed_amd.microbench --hipblaslt   (the vendor library at the same shapes)
 """
 import argparse
 import ctypes
@@ -234,10 +235,18 @@ def main():
     ap.add_argument("--f32-choice", action="store_true",
                     help="only compare the fp32 linear's algorithms (time and error) "
                          "at the shapes")
+    ap.add_argument("--hipblaslt", action="store_true",
+                    help="only time hipBLASLt's int8 GEMM (every heuristic candidate, the "
+                         "fastest reported) at the BERT-base shapes and --m, int32 out")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
     args = ap.parse_args()
+    if args.hipblaslt:
+        import os
+        import subprocess
+        exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "blaslt_ref")
+        return subprocess.run([exe, str(args.m), str(args.iters)]).returncode
     if args.copy_mib:
         return copy_calibration(args.copy_mib, args.iters)
     if args.attention:

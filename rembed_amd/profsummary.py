@@ -51,8 +51,9 @@ def stats(path, steps, title, command):
 
 
 # The int8 GEMMs of one BERT-base layer in launch order: name, K, N, bytes
-# per output element (QKV rows go to attention as bf16).
-BERT_BASE_I8_LAYER = [("QKV", 768, 2304, 2), ("O", 768, 768, 4), ("FFN1", 768, 3072, 4),
+# per output element (QKV rows go to fp32-grade attention as bf16 hi/lo
+# planes, 2 + 2 bytes).
+BERT_BASE_I8_LAYER = [("QKV", 768, 2304, 4), ("O", 768, 768, 4), ("FFN1", 768, 3072, 4),
                       ("FFN2", 3072, 768, 4)]
 INT8_PEAK_TOPS, HBM_PEAK_GBS = 5000.0, 8000.0
 
