@@ -53,6 +53,12 @@ WORKLOADS = {
     "nomic-v1.5-int8": ("nomic-embed-text-v1.5-shaped post-LN encoder (12 layers, 768, 12 heads of "
                         "64, RoPE, SwiGLU 3072), full int8, 64 texts, lengths U[64,256] padded to "
                         "256, mean pooling + L2", "full", 64, 256, 64, 256, 1000),
+    "mpnet-base-int8": ("all-mpnet-base-v2-shaped encoder (12 layers, 768, 12 heads of 64, "
+                        "relative-position bias), full int8, 64 texts, lengths U[64,256] padded "
+                        "to 256, mean pooling + L2", "full", 64, 256, 64, 256, 1000),
+    "distilbert-base-int8": ("multi-qa-distilbert-cos-v1-shaped encoder (6 layers, 768, 12 heads "
+                             "of 64), full int8, 64 texts, lengths U[64,256] padded to 256, CLS "
+                             "pooling + L2", "full", 64, 256, 64, 256, 1000),
     "modernbert-base-w8": ("modernbert-embed-base-shaped pre-LN encoder (22 layers, 768, 12 heads "
                            "of 64, GeGLU 1152, every third layer global, the rest within +-64 "
                            "tokens), weight-only int8, 32 texts, lengths U[256,512] padded to 512, "
@@ -233,6 +239,10 @@ def make_workload(name):
     from rembed_amd import synthetic as S
     if name.startswith("bert-base"):
         return S.BERT_BASE, S.bert_tensors(S.BERT_BASE, seed=0x5EED0001)
+    if name.startswith("mpnet"):
+        return S.MPNET_BASE, S.bert_tensors(S.MPNET_BASE, seed=0x5EED0001)
+    if name.startswith("distilbert"):
+        return S.DISTILBERT_BASE, S.bert_tensors(S.DISTILBERT_BASE, seed=0x5EED0001)
     if name.startswith("minilm"):
         return S.MINILM_L6, S.bert_tensors(S.MINILM_L6, seed=0x5EED0001)
     if name.startswith("qwen3"):
@@ -466,7 +476,8 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": ("gemm_i8_kernel" if quant == 2 else "gemm_planes_kernel") +
+            "kernel": ("gemm_i8_kernel / gemm_i8f_kernel" if quant == 2 else
+                       "gemm_planes_kernel") +
                       f" (all {gemm['launches'] // args.steps} GEMM launches per step)",
             "achieved": round(achieved, 2),
             "peak": peak,

@@ -350,7 +350,8 @@ int rh_model_share(rh_model *src, rh_context *ctx, rh_model **out);
 void rh_model_destroy(rh_model *m);
 /* Per-model switches. RH_OPT_ATTN_PRECISION: 1 = bf16 attention operands,
  * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE and,
- * in every mode, for RH_ARCH_BERT).
+ * in every mode, for the BERT family: RH_ARCH_BERT, RH_ARCH_DISTILBERT,
+ * RH_ARCH_MPNET).
  * RH_OPT_FUSED_FFN1: 1 = full-int8 FFN1 writes u8 rows directly (two GEMM
  * passes, no fp32 intermediate), 0 = fp32 GELU rows then QuantizeRowU8
  * (default); both give identical bytes. RH_OPT_PRODUCER_PLANES: 1 = the

@@ -22,7 +22,8 @@ import csv
 import json
 import sys
 
-GEMM = "gemm_i8_kernel"
+# the full-int8 GEMM family: the LDS-staged tiles and the fragment-ordered-B tiles
+GEMM = ("gemm_i8_kernel<", "gemm_i8f_kernel<")
 
 
 def _kernel_means(path):
@@ -42,11 +43,11 @@ def stats(path, steps, title, command):
         t = float(r["TotalDurationNs"])
         print(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
               f"{t / 1e3 / steps:.1f} | {100 * t / total:.1f}% |")
-    gemm = [r for r in rows if GEMM in r["Name"]]
+    gemm = [r for r in rows if any(g in r["Name"] for g in GEMM)]
     gt = sum(float(r["TotalDurationNs"]) for r in gemm)
     gc = sum(int(r["Calls"]) for r in gemm)
     if gc:
-        print(f"\nAll `{GEMM}` launches: {gc} calls, average {gt / gc / 1e3:.2f} µs, "
+        print(f"\nAll int8 GEMM launches: {gc} calls, average {gt / gc / 1e3:.2f} µs, "
               f"{gt / 1e3 / steps:.1f} µs per step ({steps} steps incl. warm-up).")
 
 
@@ -196,13 +197,13 @@ def traffic(fetch, write, cfetch, cwrite, copy_mib, command):
         fb = f[k][1] * 1024 * f_scale
         wb = w[k][1] * 1024 * w_scale
         print(f"| `{k[:90]}` | {n} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | {(fb + wb) / 1e6:.1f} |")
-        if GEMM in k:
+        if any(g in k for g in GEMM):
             g_n += n
             g_b += n * (fb + wb)
     out = {"bytes_per_launch": g_b / g_n if g_n else None, "launches": int(g_n),
            "fetch_scale": f_scale, "write_scale": w_scale}
-    print(f"\nAverage over all `{GEMM}` launches: {out['bytes_per_launch'] / 1e6:.1f} MB "
-          "per launch.\n")
+    print(f"\nAverage over all int8 GEMM launches (`gemm_i8_kernel`, `gemm_i8f_kernel`): "
+          f"{out['bytes_per_launch'] / 1e6:.1f} MB per launch.\n")
     print("```json\n" + json.dumps(out) + "\n```")
     return out
 
