@@ -110,6 +110,27 @@ __device__ __forceinline__ float attn_softmax_block(v16f (&sc)[2], int key0, int
   return alpha;
 }
 
+// P's bf16 split for the fp32-grade products: hi = bf16(x), lo = bf16(x -
+// hi), both rounded to nearest even, two scores per conversion; hi as a float
+// is its half of the packed pair moved to the upper 16 bits (exact).
+__device__ __forceinline__ void attn_split8(const v16f& s, int base, v8bf& ph, v8bf& pl) {
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  typedef float v2f __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const float x0 = s[base + e], x1 = s[base + e + 1];
+    const v2bf h = __builtin_convertvector((v2f){x0, x1}, v2bf);
+    const uint32_t u = __builtin_bit_cast(uint32_t, h);
+    const float h0 = __uint_as_float(u << 16), h1 = __uint_as_float(u & 0xffff0000u);
+    const float l0 = x0 - h0, l1 = x1 - h1;
+    const v2bf l = __builtin_convertvector((v2f){l0, l1}, v2bf);
+    ph[e] = h[0];
+    ph[e + 1] = h[1];
+    pl[e] = l[0];
+    pl[e + 1] = l[1];
+  }
+}
+
 // MPNet (bert.go:876-890): scores become score·scale + bias(j - i), the
 // bias of the head's relative-position bucket; the softmax then takes them
 // with cs = log2 e. Lane layout as attn_softmax_block (query qi; keys key0 +
@@ -340,12 +361,11 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) {
       v8bf ph, pl;
+      if constexpr (PREC == 3) {
+        attn_split8(sc[kc >> 1], (kc & 1) * 8, ph, pl);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const float x = sc[kc >> 1][(kc & 1) * 8 + e];
-        const __bf16 hi = (__bf16)x;
-        ph[e] = hi;
-        if constexpr (PREC == 3) pl[e] = (__bf16)(x - (float)hi);
+        for (int e = 0; e < 8; e++) ph[e] = (__bf16)sc[kc >> 1][(kc & 1) * 8 + e];
       }
 #pragma unroll
       for (int t = 0; t < DT; t++) {
@@ -634,12 +654,11 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) {
       v8bf ph, pl;
+      if constexpr (T == 2) {
+        attn_split8(sc[kc >> 1], (kc & 1) * 8, ph, pl);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const float x = sc[kc >> 1][(kc & 1) * 8 + e];
-        const __bf16 hi = (__bf16)x;
-        ph[e] = hi;
-        if constexpr (T == 2) pl[e] = (__bf16)(x - (float)hi);
+        for (int e = 0; e < 8; e++) ph[e] = (__bf16)sc[kc >> 1][(kc & 1) * 8 + e];
       }
 #pragma unroll
       for (int t = 0; t < DT; t++) {
