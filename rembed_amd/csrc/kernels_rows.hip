@@ -312,6 +312,47 @@ __global__ __launch_bounds__(256) void embed_ln_vec_kernel(EmbedArgs p, int tota
 // 4(l + 64e) .. +3) and are parked in LDS; lane r < R walks row r's two sums
 // serially (the only serial part); the normalization itself runs coalesced
 // again (ln_vec_apply). inv = 1/float32(sqrt(float64(var+eps))).
+// s += the 32 values of a, one at a time in index order.
+__device__ __forceinline__ void add_in_order(float& s, const v4f (&a)[8]) {
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    s = s + a[u][0];
+    s = s + a[u][1];
+    s = s + a[u][2];
+    s = s + a[u][3];
+  }
+}
+
+__device__ __forceinline__ void load32(v4f (&a)[8], const float* p) {
+#pragma unroll
+  for (int u = 0; u < 8; u++) a[u] = *reinterpret_cast<const v4f*>(p + 4 * u);
+}
+
+// Float32 sum of rp[0..n) in column order, one dependent add per element
+// (n % 4 == 0, rp 16-byte aligned, in LDS). The next 32 values are read
+// while the current 32 are added, so the LDS latency stays off the chain.
+__device__ __forceinline__ float serial_sum(const float* rp, int n) {
+  float s = 0.0f;
+  v4f a[8], b[8];  // two blocks of 32 values in turn
+  const int n32 = n & ~31;
+  if (n32) load32(a, rp);
+  for (int j = 0; j < n32; j += 64) {
+    if (j + 32 < n32) load32(b, rp + j + 32);
+    add_in_order(s, a);
+    if (j + 32 >= n32) break;
+    if (j + 64 < n32) load32(a, rp + j + 64);
+    add_in_order(s, b);
+  }
+  for (int j = n32; j < n; j += 4) {
+    const v4f v = *reinterpret_cast<const v4f*>(rp + j);
+    s = s + v[0];
+    s = s + v[1];
+    s = s + v[2];
+    s = s + v[3];
+  }
+  return s;
+}
+
 template <int V, int R>
 __device__ __forceinline__ void ln_exact_rows(v4f (&v)[R][V], int row0, int nrows, int H,
                                               float eps, const float* __restrict__ gamma,
@@ -332,19 +373,7 @@ __device__ __forceinline__ void ln_exact_rows(v4f (&v)[R][V], int row0, int nrow
       if (j < H) *reinterpret_cast<v4f*>(rowbuf + r * S + j) = v[r][e];
     }
   __syncthreads();
-  if (lane < R) {  // mean: sum in column order, then / n
-    const float* rp = rowbuf + lane * S;
-    float s = 0.0f;
-#pragma unroll 8
-    for (int j = 0; j < H; j += 4) {
-      const v4f a = *reinterpret_cast<const v4f*>(rp + j);
-      s = s + a[0];
-      s = s + a[1];
-      s = s + a[2];
-      s = s + a[3];
-    }
-    stat[lane] = s / (float)H;
-  }
+  if (lane < R) stat[lane] = serial_sum(rowbuf + lane * S, H) / (float)H;  // mean
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -360,17 +389,7 @@ __device__ __forceinline__ void ln_exact_rows(v4f (&v)[R][V], int row0, int nrow
   }
   __syncthreads();
   if (lane < R) {  // variance: the rounded squares summed in column order
-    const float* rp = rowbuf + lane * S;
-    float s = 0.0f;
-#pragma unroll 8
-    for (int j = 0; j < H; j += 4) {
-      const v4f a = *reinterpret_cast<const v4f*>(rp + j);
-      s = s + a[0];
-      s = s + a[1];
-      s = s + a[2];
-      s = s + a[3];
-    }
-    const float var = s / (float)H;
+    const float var = serial_sum(rowbuf + lane * S, H) / (float)H;
     stat[R + lane] = 1.0f / (float)sqrt((double)(var + eps));
   }
   __syncthreads();
@@ -392,21 +411,36 @@ __global__ __launch_bounds__(64) void add_ln_exact_kernel(
     __bf16* __restrict__ ph, __bf16* __restrict__ pl, int ldp) {
   const int lane = threadIdx.x;
   const int row0 = blockIdx.x * R;
+  // Every load of the workgroup's rows is issued before any is used (clamped
+  // in-bounds addresses, out-of-range slots zeroed afterwards): a load
+  // guarded together with its use would wait for each row in turn.
   v4f v[R][V];
 #pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int row = row0 + r;
+  for (int r = 0; r < R; r++)
 #pragma unroll
     for (int e = 0; e < V; e++) {
-      const int j = (lane + 64 * e) * 4;
-      v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (row < m && j < H) {
-        t = *reinterpret_cast<const v4f*>(x + (size_t)row * H + j);
-        if (y) t = t + *reinterpret_cast<const v4f*>(y + (size_t)row * ldy + j);  // Add
-      }
-      v[r][e] = t;
+      const int j = min((lane + 64 * e) * 4, H - 4);
+      v[r][e] = *reinterpret_cast<const v4f*>(x + (size_t)min(row0 + r, m - 1) * H + j);
     }
+  if (y) {  // Add
+    v4f w[R][V];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int e = 0; e < V; e++) {
+        const int j = min((lane + 64 * e) * 4, H - 4);
+        w[r][e] = *reinterpret_cast<const v4f*>(y + (size_t)min(row0 + r, m - 1) * ldy + j);
+      }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int e = 0; e < V; e++) v[r][e] = v[r][e] + w[r][e];
   }
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int e = 0; e < V; e++)
+      if (row0 + r >= m || (lane + 64 * e) * 4 >= H) v[r][e] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   ln_exact_rows<V, R>(v, row0, min(R, m - row0), H, eps, gamma, beta, x, qa, ldq, row_scales,
                       ph, pl, ldp);
 }
