@@ -684,6 +684,239 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   attn_store_rows<DH>(p, o, inv, lds, wave, lane, r0, q0 + wave * 32, len, h);
 }
 
+// Head dim 256 on bf16 rows (EmbeddingGemma): eight waves of 16 queries on
+// v_mfma_f32_16x16x32_bf16, two waves per SIMD. With 32 queries per wave
+// (the kernel above) o, the Q fragments and the S tiles fill a wave's 256
+// registers and one wave per SIMD waits on every LDS read; here o is 64
+// registers, Q 32, S 16.
+// 16x16x32 operand layouts (checked on the GPU): A lane l holds row l % 16,
+// k = 8 (l / 16) .. +7; B lane l holds column l % 16, the same k; C lane l
+// holds column l % 16, rows 4 (l / 16) .. +3.
+// * S^T = K·Q^T per 16-key tile t: lane (query fr = l % 16, group fg = l /
+//   16) holds keys 16t + 4fg + i. A query's 64 scores of a block sit in
+//   the four lanes fr, fr+16, fr+32, fr+48 (two shuffles per statistic).
+// * O^T += V^T·P^T per 32-key step kc: lane (fr, fg) feeds B element j with
+//   its own scores, key 32kc + 4fg + j (j < 4) or 32kc + 16 + 4fg + j - 4;
+//   V^T rows hold the keys in that order (chunk 4kc + fg of a 128-byte row
+//   is lane group fg's eight keys), so a V^T fragment is one 16-byte read.
+constexpr int kH256Waves = 8;
+
+__global__ __launch_bounds__(64 * kH256Waves) void attention_h256_kernel(AttnArgs p) {
+  constexpr int DH = 256, KS = DH / 32, NDT = DH / 16;
+  constexpr int kRowB = DH * 2;               // bytes of one K row (512)
+  constexpr int kKB = kAttnKV * kRowB;        // K block bytes (32 KiB) = V^T block bytes
+  constexpr int kStage = 2 * kKB;             // K + V^T
+  constexpr int kKLoads = kKB / (kH256Waves * 1024);  // DMA instructions per wave (4)
+  constexpr int kStride = DH + 4;             // output staging row (floats)
+  constexpr int kOut = kH256Waves * 16 * kStride * 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage > kOut ? 2 * kStage : kOut];
+  const __bf16* qkv = static_cast<const __bf16*>(p.qkv);
+
+  int b, h, qb;
+  if (!attn_block(p, b, h, qb)) return;
+  const int r0 = p.cu[b], len = p.cu[b + 1] - r0;
+  const int q0 = qb * kAttnQ;
+  if (q0 >= len) return;
+  const int kvh = h / (p.heads / p.kv_heads);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, fg = lane >> 4;
+  const int qw0 = q0 + wave * 16;
+  const int qi = qw0 + fr;
+
+  // Q fragments (B operand of S^T): k-step s, elements s*32 + 8fg .. +7
+  v8bf qf[KS];
+  {
+    const size_t qo = (size_t)(r0 + (qi < len ? qi : len - 1)) * p.ldqkv + p.q_off + h * DH;
+#pragma unroll
+    for (int s = 0; s < KS; s++) qf[s] = *reinterpret_cast<const v8bf*>(qkv + qo + s * 32 + fg * 8);
+  }
+
+  // K DMA: 1 KiB blocks of the 64 x 512-byte block, chunk swizzled by row
+  int k_row[kKLoads], k_chunk[kKLoads];
+#pragma unroll
+  for (int j = 0; j < kKLoads; j++) {
+    const int off = (wave * kKLoads + j) * 1024 + lane * 16;
+    k_row[j] = off / kRowB;
+    k_chunk[j] = ((off % kRowB) >> 4) ^ attn_kswz<DH>(k_row[j]);
+  }
+  const __bf16* kbase = qkv + p.k_off + kvh * DH;
+  const __bf16* vbase = qkv + p.v_off + kvh * DH;
+  auto issue_k = [&](int kb, int buf) {
+    uint8_t* sK = lds + buf * kStage;
+#pragma unroll
+    for (int j = 0; j < kKLoads; j++) {
+      const int kg = kb * kAttnKV + k_row[j];
+      lds_dma16(kbase + (size_t)(r0 + (kg < len ? kg : len - 1)) * p.ldqkv + k_chunk[j] * 8,
+                sK + (wave * kKLoads + j) * 1024);
+    }
+  };
+  // V: thread (key group kgp = tid / 64: kc = kgp / 4, fg' = kgp % 4; d block
+  // db = tid % 64 of 4 dims) loads its 8 keys' 4 dims (8 bytes each) and
+  // writes 4 V^T rows, 16 bytes each, at chunk kgp.
+  const int kgp = tid >> 6, db = tid & 63;
+  int vkey[8];
+#pragma unroll
+  for (int x = 0; x < 8; x++)
+    vkey[x] = (kgp >> 2) * 32 + (x < 4 ? 4 * (kgp & 3) + x : 16 + 4 * (kgp & 3) + x - 4);
+  uint2 vx[8];
+  auto load_v = [&](int kb) {
+#pragma unroll
+    for (int x = 0; x < 8; x++) {
+      const int key = kb * kAttnKV + vkey[x];
+      vx[x] = *reinterpret_cast<const uint2*>(
+          vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 4);
+    }
+  };
+  auto write_vt = [&](int buf) {
+    uint8_t* sV = lds + buf * kStage + kKB;
+#pragma unroll
+    for (int dd = 0; dd < 4; dd++) {
+      // byte selectors of v_perm_b32 for the low / high 16 bits of each source
+      v4i w;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t a = dd < 2 ? vx[2 * q].x : vx[2 * q].y;
+        const uint32_t c = dd < 2 ? vx[2 * q + 1].x : vx[2 * q + 1].y;
+        w[q] = (int)((dd & 1) ? ((a >> 16) | (c & 0xffff0000u)) : ((a & 0xffffu) | (c << 16)));
+      }
+      *reinterpret_cast<v4i*>(sV + lds_off(db * 4 + dd, kgp)) = w;
+    }
+  };
+
+  v4f o[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; t++) o[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  float mref = -INFINITY, lrun = 0.0f;
+  const float cs = p.scale * 1.44269504088896341f;  // scores in log2 units
+  int klo, khi;
+  attn_key_range(p, qi, len, klo, khi);
+  int kb_lo = 0, kb_hi = (len + kAttnKV - 1) / kAttnKV;
+  const int qlast = min(q0 + kAttnQ, len) - 1;
+  if (p.causal) kb_hi = min(kb_hi, qlast / kAttnKV + 1);
+  if (p.window > 0) {
+    kb_lo = max(0, q0 - p.window + 1) / kAttnKV;
+    kb_hi = min(kb_hi, (qlast + p.window - 1) / kAttnKV + 1);
+  }
+
+  issue_k(kb_lo, 0);
+  load_v(kb_lo);
+  write_vt(0);
+  __syncthreads();
+
+  for (int kb = kb_lo; kb < kb_hi; kb++) {
+    const int buf = (kb - kb_lo) & 1;
+    const bool next = kb + 1 < kb_hi;
+    if (next) {
+      issue_k(kb + 1, buf ^ 1);
+      load_v(kb + 1);
+    }
+    const uint8_t* sK = lds + buf * kStage;
+    const uint8_t* sV = sK + kKB;
+    const int key0 = kb * kAttnKV;
+
+    if (qw0 < len) {  // a wave whose queries all lie past the text only stages
+      v4f sc[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) sc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int kr = t * 16 + fr;
+          const v8bf kf = *reinterpret_cast<const v8bf*>(
+              sK + kr * kRowB + (((4 * s + fg) ^ attn_kswz<DH>(kr)) << 4));
+          sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], sc[t], 0, 0, 0);
+        }
+      // keys outside this lane's query range (text end, causal, window): one
+      // uniform branch around the range tests
+      const bool masked = __any(key0 < klo || key0 + kAttnKV - 1 > khi);
+      if (masked) {
+        const unsigned span = (unsigned)(khi - klo);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const unsigned off = (unsigned)(key0 + t * 16 + 4 * fg + i - klo);
+            sc[t][i] = off > span ? -INFINITY : sc[t][i];
+          }
+      }
+      // online softmax (the scheme of attn_softmax_block): reference max in
+      // log2 units, moved only when a block's max exceeds it by more than 8
+      float smax = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) smax = fmaxf(smax, sc[t][i]);
+      smax = fmaxf(smax, __shfl_xor(smax, 16, 64));
+      smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+      const float mloc = smax * cs;
+      const bool up = mloc > mref + 8.0f;
+      const bool rescale = __any(up);
+      float alpha = 1.0f;
+      if (up) {
+        alpha = __builtin_amdgcn_exp2f(mref - mloc);
+        mref = mloc;
+      }
+      const float m = mref == -INFINITY ? 0.0f : mref;
+      float psum = 0.0f;
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][i], cs, -m));
+          sc[t][i] = pv;
+          psum += pv;
+        }
+      lrun = lrun * alpha + psum;
+      if (rescale && kb != kb_lo) {
+#pragma unroll
+        for (int t = 0; t < NDT; t++) o[t] *= alpha;
+      }
+      // O^T += V^T · P^T, two 32-key steps
+#pragma unroll
+      for (int kc = 0; kc < 2; kc++) {
+        v8bf ph;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          ph[j] = (__bf16)sc[2 * kc][j];
+          ph[4 + j] = (__bf16)sc[2 * kc + 1][j];
+        }
+#pragma unroll
+        for (int t = 0; t < NDT; t++) {
+          const v8bf vf = *reinterpret_cast<const v8bf*>(sV + lds_off(t * 16 + fr, 4 * kc + fg));
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, ph, o[t], 0, 0, 0);
+        }
+      }
+    }
+
+    if (next) write_vt(buf ^ 1);
+    __syncthreads();  // next block landed (vmcnt) and this block's reads are done
+  }
+
+  // the row sum over the four lane groups of a query, then the rows leave
+  // through LDS (the loop's last barrier ordered every read of the blocks)
+  float ltot = lrun + __shfl_xor(lrun, 16, 64);
+  ltot = ltot + __shfl_xor(ltot, 32, 64);
+  const float inv = 1.0f / (qi < len ? ltot : 1.0f);
+  float* st = reinterpret_cast<float*>(lds) + wave * 16 * kStride;
+#pragma unroll
+  for (int t = 0; t < NDT; t++)
+    *reinterpret_cast<v4f*>(st + fr * kStride + t * 16 + 4 * fg) = o[t] * inv;
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are in LDS
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int rr = 0; rr < 16; rr++) {
+    const int q = qw0 + rr;
+    if (q < len) {
+      const v4f w = *reinterpret_cast<const v4f*>(st + rr * kStride + lane * 4);
+      const size_t off = (size_t)(r0 + q) * p.ldctx + h * DH + lane * 4;
+      if (p.ctx_hi) store_planes4(p.ctx_hi, p.ctx_lo, off, w);
+      else *reinterpret_cast<v4f*>(p.ctx + off) = w;
+    }
+  }
+}
+
 template <int DH>
 static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s) {
   const int units = a.batch * a.kv_heads;
@@ -695,8 +928,15 @@ static hipError_t launch_attn_dh(const AttnArgs& a, int precision, hipStream_t s
     } else {
       return hipErrorInvalidValue;
     }
-  } else if (a.in_bf16)  // bf16 input carries no low half: one-term products
-    timed_launch((attention_bf16_kernel<DH, 1>), grid, dim3(256), 0, s, a);
+  } else if (a.in_bf16) {  // bf16 input carries no low half: one-term products
+    // head dim 256: the 16x16x32 kernel (two waves per SIMD; 324 against 372
+    // µs at EmbeddingGemma's global layer, 186 against 219 at its window-512
+    // layers), the 32x32 one where a relative-position bias is added
+    if (DH == 256 && !a.rel_bias)
+      timed_launch(attention_h256_kernel, grid, dim3(64 * kH256Waves), 0, s, a);
+    else
+      timed_launch((attention_bf16_kernel<DH, 1>), grid, dim3(256), 0, s, a);
+  }
   else if (precision == 3)
     timed_launch((attention_kernel<DH, 3, float>), grid, dim3(256), 0, s, a);
   else

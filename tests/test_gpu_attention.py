@@ -9,6 +9,9 @@ window |i-j| < w, grouped kv heads).
   issues the same MFMAs in the same order) agree bit for bit: this pins the
   bf16 kernel's K/V staging, its V^T transposition and key order, the
   block pipeline and the masks against an independently staged kernel.
+  Head dim 256 on bf16 rows runs its own 16x16x32 kernel (two waves per
+  SIMD), whose products sum in another order: a wrong key order, staging
+  or mask there moves the output by O(|v|), far past the bound below.
 * Both are within the bf16-P bound of the float64 reference (P is rounded
   to bf16 before P·V: relative 2^-9 per weight), and precision 3 (hi/lo
   split) within 1e-4 of the output scale; so is the pipelined three-term
@@ -114,14 +117,21 @@ def test_attention_kernels(gpu_ctx, case):
     got_f1 = run(gpu_ctx.upload(xb), 0, 1)
     got_f3 = run(gpu_ctx.upload(x), 0, 3)
     assert np.all(np.isfinite(got_bf))
-    diff = np.argwhere(got_bf != got_f1)
-    assert diff.size == 0, f"bf16 kernel differs from the fp32-input kernel at {diff[:3].tolist()}"
+    if dh < 256:
+        # the pipelined bf16 kernel and the fp32-input kernel run the same
+        # 32x32 products in the same order
+        diff = np.argwhere(got_bf != got_f1)
+        assert diff.size == 0, f"bf16 kernel differs from the fp32-input kernel at {diff[:3].tolist()}"
+    # head dim 256 on bf16 rows runs the 16x16x32 kernel (its products sum in
+    # another order); it and the fp32-input kernel are held to the bound below
 
     want_b = reference(xb, lens, heads, kv_heads, dh, scale, causal, window, q_off, k_off, v_off)
     vmax = np.abs(xb[:, v_off:]).max()
     err_b = np.abs(got_bf - want_b).max()
-    say(f"  bf16 max err {err_b:.3e} (vmax {vmax:.2f})")
+    err_b1 = np.abs(got_f1 - want_b).max()
+    say(f"  bf16 max err {err_b:.3e}, fp32-input kernel {err_b1:.3e} (vmax {vmax:.2f})")
     assert err_b <= 2.0 ** -8 * vmax + 1e-5
+    assert err_b1 <= 2.0 ** -8 * vmax + 1e-5
     want_f = reference(x, lens, heads, kv_heads, dh, scale, causal, window, q_off, k_off, v_off)
     err_f = np.abs(got_f3 - want_f).max()
     say(f"  split max err {err_f:.3e}")
