@@ -1,15 +1,19 @@
-// blaslt_ref.cpp — the vendor-library comparison line of the int8 GEMM
-// microbenchmark: hipBLASLt's int8 x int8 -> int32 GEMM at the encoder's
-// shapes, C[M][N] = A[M][K] · B[N][K]^T (row-major, the reference's bT
-// layout), every heuristic candidate (up to 16) timed with HIP events, the
-// fastest reported. Built and run by `python -m rembed_amd.microbench
-// --hipblaslt`; not part of the library.
+// blaslt_ref.cpp — the vendor-library comparison lines of the GEMM
+// microbenchmarks: hipBLASLt's int8 x int8 -> int32 GEMM (mode i8) or bf16 x
+// bf16 -> fp32 GEMM with fp32 accumulation (mode bf16) at the given shapes,
+// C[M][N] = A[M][K] · B[N][K]^T (row-major, the reference's bT layout),
+// every heuristic candidate (up to 16) timed with HIP events, the fastest
+// reported. Built and run by `python -m rembed_amd.microbench --hipblaslt`;
+// not part of the library.
 //
+// Usage: blaslt_ref [M] [iters] [i8|bf16] ["k,n;k,n;..."]
 // Output: one JSON object per shape on stdout.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
+#include <cstring>
+#include <utility>
 #include <cstdio>
 #include <cstdlib>
 #include <random>
@@ -32,32 +36,51 @@
     }                                                                        \
   } while (0)
 
-static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters) {
-  std::vector<int8_t> a((size_t)M * K), b((size_t)N * K);
+// bf16 bits of small integers (exact in bf16, so the spot check is exact)
+static uint16_t bf16_of(int v) {
+  const float f = (float)v;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (uint16_t)(u >> 16);
+}
+
+static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters, bool bf16) {
+  const size_t es = bf16 ? 2 : 1;  // input element bytes; outputs are 4 bytes
+  std::vector<int> a((size_t)M * K), b((size_t)N * K);
   std::mt19937 g(7);
-  for (auto& v : a) v = (int8_t)(g() & 255);
-  for (auto& v : b) v = (int8_t)(g() & 255);
-  int8_t *dA, *dB;
-  int32_t* dC;
+  for (auto& v : a) v = bf16 ? (int)(g() % 9) - 4 : (int8_t)(g() & 255);
+  for (auto& v : b) v = bf16 ? (int)(g() % 9) - 4 : (int8_t)(g() & 255);
+  std::vector<uint8_t> ha(a.size() * es), hb(b.size() * es);
+  for (size_t i = 0; i < a.size(); i++) {
+    if (bf16) reinterpret_cast<uint16_t*>(ha.data())[i] = bf16_of(a[i]);
+    else ha[i] = (uint8_t)(int8_t)a[i];
+  }
+  for (size_t i = 0; i < b.size(); i++) {
+    if (bf16) reinterpret_cast<uint16_t*>(hb.data())[i] = bf16_of(b[i]);
+    else hb[i] = (uint8_t)(int8_t)b[i];
+  }
+  void *dA, *dB, *dC;
   void* ws;
   const size_t ws_bytes = 64u << 20;
-  HCHK(hipMalloc(&dA, a.size()));
-  HCHK(hipMalloc(&dB, b.size()));
+  HCHK(hipMalloc(&dA, ha.size()));
+  HCHK(hipMalloc(&dB, hb.size()));
   HCHK(hipMalloc(&dC, (size_t)M * N * 4));
   HCHK(hipMalloc(&ws, ws_bytes));
-  HCHK(hipMemcpy(dA, a.data(), a.size(), hipMemcpyHostToDevice));
-  HCHK(hipMemcpy(dB, b.data(), b.size(), hipMemcpyHostToDevice));
+  HCHK(hipMemcpy(dA, ha.data(), ha.size(), hipMemcpyHostToDevice));
+  HCHK(hipMemcpy(dB, hb.data(), hb.size(), hipMemcpyHostToDevice));
+  const hipDataType tin = bf16 ? HIP_R_16BF : HIP_R_8I, tout = bf16 ? HIP_R_32F : HIP_R_32I;
 
   // Column-major view: C^T (N x M, ld N) = op(B^T as K x N, ld K)^T · (A^T as K x M, ld K).
   hipblasLtMatmulDesc_t op;
-  BCHK(hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32I, HIP_R_32I));
+  BCHK(hipblasLtMatmulDescCreate(&op, bf16 ? HIPBLAS_COMPUTE_32F : HIPBLAS_COMPUTE_32I,
+                                 bf16 ? HIP_R_32F : HIP_R_32I));
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   BCHK(hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)));
   BCHK(hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)));
   hipblasLtMatrixLayout_t la, lb, lc;
-  BCHK(hipblasLtMatrixLayoutCreate(&la, HIP_R_8I, K, N, K));
-  BCHK(hipblasLtMatrixLayoutCreate(&lb, HIP_R_8I, K, M, K));
-  BCHK(hipblasLtMatrixLayoutCreate(&lc, HIP_R_32I, N, M, N));
+  BCHK(hipblasLtMatrixLayoutCreate(&la, tin, K, N, K));
+  BCHK(hipblasLtMatrixLayoutCreate(&lb, tin, K, M, K));
+  BCHK(hipblasLtMatrixLayoutCreate(&lc, tout, N, M, N));
   hipblasLtMatmulPreference_t pref;
   BCHK(hipblasLtMatmulPreferenceCreate(&pref));
   BCHK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
@@ -65,7 +88,10 @@ static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters) {
   hipblasLtMatmulHeuristicResult_t res[16];
   int n = 0;
   BCHK(hipblasLtMatmulAlgoGetHeuristic(h, op, la, lb, lc, lc, pref, 16, res, &n));
-  const int32_t alpha = 1, beta = 0;
+  const int32_t alpha_i = 1, beta_i = 0;
+  const float alpha_f = 1.0f, beta_f = 0.0f;
+  const void* alpha = bf16 ? (const void*)&alpha_f : (const void*)&alpha_i;
+  const void* beta = bf16 ? (const void*)&beta_f : (const void*)&beta_i;
   hipEvent_t e0, e1;
   HCHK(hipEventCreate(&e0));
   HCHK(hipEventCreate(&e1));
@@ -74,7 +100,7 @@ static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters) {
   for (int i = 0; i < n; i++) {
     if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > ws_bytes) continue;
     auto run = [&]() {
-      return hipblasLtMatmul(h, op, &alpha, dB, la, dA, lb, &beta, dC, lc, dC, lc, &res[i].algo,
+      return hipblasLtMatmul(h, op, alpha, dB, la, dA, lb, beta, dC, lc, dC, lc, &res[i].algo,
                              ws, ws_bytes, 0);
     };
     if (run() != HIPBLAS_STATUS_SUCCESS) continue;
@@ -92,10 +118,10 @@ static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters) {
       best_i = i;
     }
   }
-  // spot check of the best candidate's int32 accumulators
+  // spot check of the best candidate's outputs (exact: small integers)
   int bad = -1;
   if (best_i >= 0) {
-    BCHK(hipblasLtMatmul(h, op, &alpha, dB, la, dA, lb, &beta, dC, lc, dC, lc, &res[best_i].algo,
+    BCHK(hipblasLtMatmul(h, op, alpha, dB, la, dA, lb, beta, dC, lc, dC, lc, &res[best_i].algo,
                          ws, ws_bytes, 0));
     std::vector<int32_t> c((size_t)M * N);
     HCHK(hipMemcpy(c.data(), dC, c.size() * 4, hipMemcpyDeviceToHost));
@@ -104,13 +130,16 @@ static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters) {
       const int r = (s * 7919) % M, col = (s * 104729) % N;
       long acc = 0;
       for (int k = 0; k < K; k++) acc += (long)a[(size_t)r * K + k] * b[(size_t)col * K + k];
-      if ((int32_t)acc != c[(size_t)r * N + col]) bad++;
+      const int32_t got = c[(size_t)r * N + col];
+      float gf;
+      memcpy(&gf, &got, 4);
+      if (bf16 ? (gf != (float)acc) : ((int32_t)acc != got)) bad++;
     }
   }
   const double ops = 2.0 * M * K * N;
-  printf("{\"m\": %d, \"k\": %d, \"n\": %d, \"candidates\": %d, \"timed\": %d, \"best_us\": %.2f, "
-         "\"tops\": %.0f, \"check_bad\": %d}\n",
-         M, K, N, n, tried, best, ops / (best * 1e-6) / 1e12, bad);
+  printf("{\"mode\": \"%s\", \"m\": %d, \"k\": %d, \"n\": %d, \"candidates\": %d, "
+         "\"timed\": %d, \"best_us\": %.2f, \"tops\": %.0f, \"check_bad\": %d}\n",
+         bf16 ? "bf16" : "i8", M, K, N, n, tried, best, ops / (best * 1e-6) / 1e12, bad);
   fflush(stdout);
   hipblasLtMatmulPreferenceDestroy(pref);
   hipblasLtMatrixLayoutDestroy(la);
@@ -127,11 +156,22 @@ static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters) {
 int main(int argc, char** argv) {
   const int M = argc > 1 ? atoi(argv[1]) : 10102;
   const int iters = argc > 2 ? atoi(argv[2]) : 20;
+  const bool bf16 = argc > 3 && strcmp(argv[3], "bf16") == 0;
+  std::vector<std::pair<int, int>> shapes = {{768, 2304}, {768, 768}, {768, 3072}, {3072, 768}};
+  if (argc > 4) {  // "k,n;k,n;..."
+    shapes.clear();
+    for (const char* q = argv[4]; *q;) {
+      int k = 0, n = 0, used = 0;
+      if (sscanf(q, "%d,%d%n", &k, &n, &used) != 2) return 2;
+      shapes.push_back({k, n});
+      q += used;
+      if (*q == ';') q++;
+    }
+  }
   hipblasLtHandle_t h;
   BCHK(hipblasLtCreate(&h));
-  const int shapes[][2] = {{768, 2304}, {768, 768}, {768, 3072}, {3072, 768}};
   for (auto& s : shapes)
-    if (time_shape(h, M, s[0], s[1], iters)) return 1;
+    if (time_shape(h, M, s.first, s.second, iters, bf16)) return 1;
   hipblasLtDestroy(h);
   return 0;
 }

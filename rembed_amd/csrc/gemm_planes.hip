@@ -402,15 +402,19 @@ static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
 // Stages: as many as fit in 160 KiB of LDS. fp32's four planes leave no room
 // for 256x256 (1 and 4 fall back to 2 and 5). Automatic choice (measured on
 // MI355X at M = 16384 over the Qwen3/BERT linears; 8 waves 2-15% faster than
-// 4 at the same tile): tile 6 for one-term W8, 4 for the other products
-// when the 256x256 grid gives every CU a workgroup, else 5, else 128x128
+// 4 at the same tile): tile 6 for one-term W8 when the 256x256 grid gives
+// at least every other CU a workgroup, 4 for the other products when it
+// gives every CU one, else 5, else 128x128
 // while its grid has at least 192 workgroups; below that (MiniLM's M ~ 2300,
 // or N = 384) 64x64, which keeps the CUs busy: at M = 2304 the weight-only
 // int8 linears take 9.8 / 5.6 / 11.6 µs (384x1152, 384x384, 1536x384)
 // against 10.6 / 9.5 / 20.0 with 128x128.
 int pick_planes_tile(int M, int N, int a_terms, int b_terms) {
-  if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256)
-    return a_terms == 1 && b_terms == 1 ? 6 : 4;
+  // one term: at M = 16384, K = 3072, N = 768 the 192 tiles of tile 6 take
+  // 91 µs against 120 for the 384 tiles of 256x128 (tile 6 fastest at every
+  // Qwen3 and Gemma shape, M = 16384 and 32768)
+  if (a_terms == 1 && b_terms == 1 && ceil_div(M, 256) * ceil_div(N, 256) >= 128) return 6;
+  if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256) return 4;
   if (ceil_div(M, 256) * ceil_div(N, 128) >= 256) return 5;
   return ceil_div(M, 128) * ceil_div(N, 128) >= 192 ? 3 : 8;
 }

@@ -236,8 +236,9 @@ def main():
                     help="only compare the fp32 linear's algorithms (time and error) "
                          "at the shapes")
     ap.add_argument("--hipblaslt", action="store_true",
-                    help="only time hipBLASLt's int8 GEMM (every heuristic candidate, the "
-                         "fastest reported) at the BERT-base shapes and --m, int32 out")
+                    help="only time hipBLASLt's GEMM (every heuristic candidate, the fastest "
+                         "reported) at --m and --shapes (default: BERT-base): int8 with "
+                         "int32 out, or with --modes bf16 bf16 with fp32 out")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -246,7 +247,10 @@ def main():
         import os
         import subprocess
         exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "blaslt_ref")
-        return subprocess.run([exe, str(args.m), str(args.iters)]).returncode
+        cmd = [exe, str(args.m), str(args.iters), "bf16" if args.modes == "bf16" else "i8"]
+        if args.shapes:
+            cmd.append(args.shapes)
+        return subprocess.run(cmd).returncode
     if args.copy_mib:
         return copy_calibration(args.copy_mib, args.iters)
     if args.attention:
