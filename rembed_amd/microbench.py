@@ -140,8 +140,10 @@ ATTN_CASES = {
 
 def bench_attention(ctx, name, iters, kernels):
     """rh_attention at a workload's shape on random bf16-representable
-    q|k|v rows; `kernels`: "bf16" (bf16 rows, the pipelined kernel) and/or
-    "f32" (the same values as fp32 rows at precision 1)."""
+    q|k|v rows; `kernels`: "bf16" (bf16 rows, the pipelined kernel), "f32"
+    (the same values as fp32 rows at precision 1) and/or "planes" (fp32 rows'
+    bf16 hi/lo planes, rh_attention_planes: the fp32-grade three-term kernel,
+    head dim <= 128; FLOPs counted once)."""
     dh, heads, kv, causal, window, texts, length = ATTN_CASES[name]
     rng = np.random.default_rng(2)
     lens = (rng.integers(64, 257, texts) if length is None else np.full(texts, length))
@@ -152,6 +154,11 @@ def bench_attention(ctx, name, iters, kernels):
     bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
     bufs = {"bf16": (ctx.upload(bits), 1),
             "f32": (ctx.upload((bits.astype(np.uint32) << 16).view(np.float32)), 0)}
+    if "planes" in kernels:  # hi = the rounded bits, lo = bf16 of the remainder
+        hi_f = (bits.astype(np.uint32) << 16).view(np.float32)
+        r = (x - hi_f).view(np.uint32).astype(np.uint64)
+        lo = ((r + 0x7FFF + ((r >> 16) & 1)) >> 16).astype(np.uint16)
+        bufs["planes"] = ((ctx.upload(bits), ctx.upload(lo)), 2)
     cu = ctx.upload(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32))
     out = ctx.alloc(M * heads * dh * 4)
     pairs = 0.0
@@ -171,9 +178,14 @@ def bench_attention(ctx, name, iters, kernels):
         buf, in_bf16 = bufs[kern]
 
         def run():
-            T.Attention(ctx, out, heads * dh, buf, in_bf16, ld, 0, heads * dh, (heads + kv) * dh,
-                        cu, texts, int(lens.max()), heads, kv, dh, 1.0 / np.sqrt(dh), causal,
-                        window, 1)
+            if in_bf16 == 2:
+                T.AttentionPlanes(ctx, out, heads * dh, buf[0], buf[1], ld, 0, heads * dh,
+                                  (heads + kv) * dh, cu, texts, int(lens.max()), heads, kv, dh,
+                                  1.0 / np.sqrt(dh), causal, window)
+            else:
+                T.Attention(ctx, out, heads * dh, buf, in_bf16, ld, 0, heads * dh,
+                            (heads + kv) * dh, cu, texts, int(lens.max()), heads, kv, dh,
+                            1.0 / np.sqrt(dh), causal, window, 1)
         for _ in range(3):
             run()
         ctx.sync()
@@ -231,7 +243,8 @@ def main():
     ap.add_argument("--attention", default="",
                     help="only time rh_attention at these shapes (comma list of "
                          + ",".join(ATTN_CASES) + ")")
-    ap.add_argument("--attn-kernels", default="bf16", help="bf16 and/or f32 (comma list)")
+    ap.add_argument("--attn-kernels", default="bf16",
+                    help="bf16, f32 and/or planes (comma list)")
     ap.add_argument("--f32-choice", action="store_true",
                     help="only compare the fp32 linear's algorithms (time and error) "
                          "at the shapes")
