@@ -6,6 +6,7 @@
     python -m rembed_amd.profsummary traffic <fetch_dir_csv> <write_dir_csv>
                                      <copy_fetch_csv> <copy_write_csv> <copy_mib> <command>
     python -m rembed_amd.profsummary pmc <counter_collection.csv> <command>
+    python -m rembed_amd.profsummary waits <counter_collection.csv> <command>
 
 `stats` renders a --kernel-trace --stats table (per-kernel calls, average
 and per-step time). `traffic` turns two --pmc runs (FETCH_SIZE, then
@@ -15,7 +16,9 @@ JSON that bench.py reads for the GEMM's `roofline.traffic`. FETCH_SIZE counts
 the L2's read misses (requests to the fabric, served by the MALL or HBM), not
 the bytes a kernel loads: reads that hit the L2 do not appear in it. `pmc` renders one
 --pmc pass of SQ instruction and busy counters per kernel: MFMA busy share,
-VALU and LDS instructions per MFMA, LDS bank-conflict share.
+VALU and LDS instructions per MFMA, LDS bank-conflict share. `waits` renders
+a pass of SQ_WAVE_CYCLES, SQ_WAIT_ANY, SQ_WAIT_INST_ANY, SQ_ACTIVE_INST_VALU
+and SQ_ACTIVE_INST_LDS as shares of the waves' summed lifetime.
 """
 import collections
 import csv
@@ -208,12 +211,39 @@ def traffic(fetch, write, cfetch, cwrite, copy_mib, command):
     return out
 
 
+def waits(path, command):
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    for r in csv.DictReader(open(path)):
+        per[r["Kernel_Name"]][r["Counter_Name"]].append(float(r["Counter_Value"]))
+
+    def mean(k, c):
+        v = per[k].get(c)
+        return sum(v) / len(v) if v else 0.0
+    print("## Where the waves' cycles go\n")
+    print(f"Command: `{command}`\n")
+    print("Shares of SQ_WAVE_CYCLES (the summed lifetime of the kernel's waves): waiting on "
+          "any dependency (s_waitcnt on loads or LDS, barriers: SQ_WAIT_ANY), waiting to "
+          "issue (SQ_WAIT_INST_ANY), and issuing VALU / LDS instructions.\n")
+    print("| kernel | wait (any) | wait to issue | VALU issue | LDS issue |")
+    print("|---|---:|---:|---:|---:|")
+    rows = sorted(per, key=lambda k: -mean(k, "SQ_WAVE_CYCLES") * len(per[k]["SQ_WAVE_CYCLES"]))
+    for k in rows:
+        wc = mean(k, "SQ_WAVE_CYCLES")
+        if wc <= 0 or "rocclr" in k:
+            continue
+        sh = [mean(k, c) / wc for c in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_VALU",
+                                        "SQ_ACTIVE_INST_LDS")]
+        print(f"| `{k[:80]}` | " + " | ".join(f"{100 * x:.0f}%" for x in sh) + " |")
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3])
     elif sys.argv[1] == "trace":
         trace(sys.argv[2], sys.argv[3], int(sys.argv[4]), int(sys.argv[5]), sys.argv[6],
               sys.argv[7], int(sys.argv[8]) if len(sys.argv) > 8 else 0)
+    elif sys.argv[1] == "waits":
+        waits(sys.argv[2], sys.argv[3])
     elif sys.argv[1] == "stats":
         stats(sys.argv[2], int(sys.argv[3]), sys.argv[4], sys.argv[5])
     elif sys.argv[1] == "traffic":
