@@ -398,7 +398,9 @@ static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
 // Tiles: 1 = 256x256, 2 = 256x128, 3 = 128x128 with 4 waves (2x2); 4 =
 // 256x256 and 5 = 256x128 with 8 waves (2x4, two per SIMD); for one
 // activation term and int8 weights also 6 = 256x256 and 7 = 256x128 on
-// 128-byte stages (two and three); 8 = 64x64 and 9 = 128x64 with 4 waves.
+// 128-byte stages (two and three); 8 = 64x64 and 9 = 128x64 with 4 waves;
+// 10 = 128x256 with 8 waves on three 64-byte stages (72 KiB: two workgroups
+// per CU), for one term.
 // Stages: as many as fit in 160 KiB of LDS. fp32's four planes leave no room
 // for 256x256 (1 and 4 fall back to 2 and 5). Automatic choice (measured on
 // MI355X at M = 16384 over the Qwen3/BERT linears; 8 waves 2-15% faster than
@@ -409,11 +411,19 @@ static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
 // or N = 384) 64x64, which keeps the CUs busy: at M = 2304 the weight-only
 // int8 linears take 9.8 / 5.6 / 11.6 µs (384x1152, 384x384, 1536x384)
 // against 10.6 / 9.5 / 20.0 with 128x128.
-int pick_planes_tile(int M, int N, int a_terms, int b_terms) {
+int pick_planes_tile(int M, int N, int K, int a_terms, int b_terms) {
   // one term: at M = 16384, K = 3072, N = 768 the 192 tiles of tile 6 take
-  // 91 µs against 120 for the 384 tiles of 256x128 (tile 6 fastest at every
-  // Qwen3 and Gemma shape, M = 16384 and 32768)
-  if (a_terms == 1 && b_terms == 1 && ceil_div(M, 256) * ceil_div(N, 256) >= 128) return 6;
+  // 91 µs against 120 for the 384 tiles of 256x128
+  if (a_terms == 1 && b_terms == 1 && ceil_div(M, 256) * ceil_div(N, 256) >= 128) {
+    // Past one round, with the last round at most half full and a short K,
+    // tile 6's tail is one 256x256 workgroup per busy CU; the 128x256 tile
+    // with two workgroups per CU halves it. K = 768: M = 24576, N = 768
+    // (1.125 rounds) 47.9 against 56.1 µs; M = 16384, N = 1280 (1.25) 48.5
+    // against 57.4; N = 2304 (2.25) 84.4 against 89.1. At 1.875 rounds, whole
+    // rounds, below one round and K = 2048 tile 6 stays ahead.
+    const int t6 = ceil_div(M, 256) * ceil_div(N, 256), tail = t6 % 256;
+    return t6 > 256 && tail != 0 && tail <= 128 && K <= 1536 ? 10 : 6;
+  }
   if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256) return 4;
   // 256x128 down to half a round of tiles (fp32 at M = 10102, N = 768: 240
   // tiles, 43.5 / 154 µs at K = 768 / 3072 against 53.6 / 190 on 128x128)
@@ -436,7 +446,8 @@ hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int
                               hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (a.lda % 64 != 0 || a.ldb % 64 != 0) return hipErrorInvalidValue;
-  if (tile <= 0 || tile > kPlanesTileConfigs) tile = pick_planes_tile(a.M, a.N, a_terms, b_terms);
+  if (tile <= 0 || tile > kPlanesTileConfigs)
+    tile = pick_planes_tile(a.M, a.N, a.K, a_terms, b_terms);
   if (a_terms == 1 && b_terms == 1) {
     switch (tile) {
       case 1: return launch_pl<256, 256, 4, 1, 1>(a, s);
@@ -447,6 +458,7 @@ hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int
       case 7: return launch_pl<256, 128, 3, 1, 1, 4, 64>(a, s);
       case 8: return launch_pl<64, 64, 4, 1, 1>(a, s);
       case 9: return launch_pl<128, 64, 4, 1, 1>(a, s);
+      case 10: return launch_pl<128, 256, 3, 1, 1, 4>(a, s);
       default: return launch_pl<128, 128, 4, 1, 1>(a, s);
     }
   }

@@ -225,7 +225,7 @@ __device__ __forceinline__ void store_planes4(__bf16* hi, __bf16* lo, size_t off
 // past K): hi = bf16(x), lo = bf16(x - float(hi)), both rounded to nearest even
 hipError_t launch_split_bf16(const float* a, int lda_f, int M, int K, __bf16* hi, __bf16* lo,
                              int ldk, hipStream_t s);
-constexpr int kPlanesTileConfigs = 9;
+constexpr int kPlanesTileConfigs = 10;
 hipError_t launch_gemm_planes(const GemmPlArgs& a, int a_terms, int b_terms, int tile,
                               hipStream_t s);
 // The q|k|v projection with the QK-norm + RoPE epilogue (a.qk_out set): one

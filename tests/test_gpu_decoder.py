@@ -52,17 +52,21 @@ def oracle_dense(mode, bT, a):
 
 # bf: the weight-only int8 / fp32 GEMM on pre-split bf16 planes (0) or with
 # the split in its main loop (1); full int8 has one path
-@pytest.mark.parametrize("mode,bf", [(_lib.RH_MODE_F32, 0), (_lib.RH_MODE_F32, 1),
-                                     (_lib.RH_MODE_W8, 0), (_lib.RH_MODE_W8, 1),
-                                     (_lib.RH_MODE_A8W8, 0)],
-                         ids=["f32", "f32-inloop", "w8", "w8-inloop", "a8w8"])
+@pytest.mark.parametrize("mode,bf,tile", [(_lib.RH_MODE_F32, 0, 0), (_lib.RH_MODE_F32, 1, 0),
+                                          (_lib.RH_MODE_W8, 0, 0), (_lib.RH_MODE_W8, 1, 0),
+                                          (_lib.RH_MODE_W8, 0, 6), (_lib.RH_MODE_W8, 0, 10),
+                                          (_lib.RH_MODE_A8W8, 0, 0)],
+                         ids=["f32", "f32-inloop", "w8", "w8-inloop", "w8-tile6", "w8-tile10",
+                              "a8w8"])
 @pytest.mark.parametrize("act", [_lib.RH_ACT_SWIGLU, _lib.RH_ACT_GEGLU, _lib.RH_ACT_GEGLU_ERF],
                          ids=["swiglu", "geglu-tanh", "geglu-erf"])
-def test_gated_linear_matches_oracle(gpu_ctx, mode, bf, act):
+def test_gated_linear_matches_oracle(gpu_ctx, mode, bf, tile, act):
+    """Gated linear against the oracle; tile forces a planes tile (6 and 10
+    are the two the automatic choice gives large one-term GLU linears)."""
     ctx = gpu_ctx
     rng = np.random.default_rng(10 * mode + act)
     m, k, i = 301, 384, 528
-    say(f"gated linear mode={mode} bf_algo={bf} act={act} m={m} k={k} i={i}")
+    say(f"gated linear mode={mode} bf_algo={bf} tile={tile} act={act} m={m} k={k} i={i}")
     a = rng.standard_normal((m, k)).astype(np.float32)
     gate = (rng.standard_normal((i, k)) * 0.05).astype(np.float32)
     up = (rng.standard_normal((i, k)) * 0.05).astype(np.float32)
@@ -72,11 +76,13 @@ def test_gated_linear_matches_oracle(gpu_ctx, mode, bf, act):
     ldq = T.ldq_for(k)
     qa, rs = ctx.alloc(m * ldq), ctx.alloc(m * 4)
     ctx.set_bf_algo(bf)
+    ctx.set_option(_lib.RH_CTX_BF_TILE, tile)
     try:
         T.Linear(ctx, out, a_d, pw, m, act, qa, ldq, rs)
         ctx.sync()
     finally:
         ctx.set_bf_algo(0)
+        ctx.set_option(_lib.RH_CTX_BF_TILE, 0)
     got = out.download(np.float32, (m, i))
     g = oracle_dense(mode, gate, a)
     u = oracle_dense(mode, up, a)

@@ -111,7 +111,7 @@ def test_w8_signed_permutation_exact(gpu_ctx, shape, bf, terms):
     assert bad.size == 0, f"first mismatch {bad[:3].tolist()}"
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 @pytest.mark.parametrize("mode,terms", [(_lib.RH_MODE_F32, 2), (_lib.RH_MODE_W8, 1),
                                         (_lib.RH_MODE_W8, 2)], ids=["f32", "w8", "w8-2terms"])
 def test_every_planes_tile_exact(gpu_ctx, tile, mode, terms):
