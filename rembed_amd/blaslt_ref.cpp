@@ -6,7 +6,11 @@
 // reported. Built and run by `python -m rembed_amd.microbench --hipblaslt`;
 // not part of the library.
 //
-// Usage: blaslt_ref [M] [iters] [i8|bf16] ["k,n;k,n;..."]
+// Usage: blaslt_ref [M] [iters] [i8|i8q|bf16] ["k,n;k,n;..."]
+// i8 takes uniformly random bytes; i8q takes the bytes of normally
+// distributed rows quantized per row to ±127 (A as its activations' signed
+// bytes, B per output channel), the operands the encoder's int8 GEMMs see
+// and the library's own microbenchmark times.
 // Output: one JSON object per shape on stdout.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
@@ -50,16 +54,43 @@ static float bf16_value(uint16_t b) {
   return f;
 }
 
-static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters, bool bf16) {
-  // Uniformly random operands (the matrix cores' clock depends on how many
-  // bits toggle, so low-entropy inputs would time faster than real ones):
-  // int8 bytes, or bf16 values uniform in [-2, 2).
+// rows x k signed bytes: each row's normal draws scaled by 127 / max|row|
+// and rounded to nearest even (the reference's per-row quantization)
+static void quantized_normal_rows(std::mt19937& g, int rows, int k, std::vector<uint8_t>& h,
+                                  std::vector<double>& v) {
+  std::normal_distribution<float> nd(0.0f, 1.0f);
+  std::vector<float> row(k);
+  for (int r = 0; r < rows; r++) {
+    float mx = 0.0f;
+    for (int i = 0; i < k; i++) {
+      row[i] = nd(g);
+      mx = std::max(mx, std::fabs(row[i]));
+    }
+    const float inv = mx > 0.0f ? 127.0f / mx : 1.0f;
+    for (int i = 0; i < k; i++) {
+      const int q = std::max(-127, std::min(127, (int)std::nearbyint(row[i] * inv)));
+      h[(size_t)r * k + i] = (uint8_t)(int8_t)q;
+      v[(size_t)r * k + i] = q;
+    }
+  }
+}
+
+static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters, bool bf16,
+                      bool quantized) {
+  // Uniformly random operands by default (the matrix cores' clock depends on
+  // how many bits toggle, so low-entropy inputs time faster than high-entropy
+  // ones): int8 bytes, or bf16 values uniform in [-2, 2). quantized: the
+  // per-row quantized normal bytes of the encoder's operands.
   const size_t es = bf16 ? 2 : 1;  // input element bytes; outputs are 4 bytes
   std::vector<double> a((size_t)M * K), b((size_t)N * K);
   std::vector<uint8_t> ha(a.size() * es), hb(b.size() * es);
   std::mt19937 g(7);
   std::uniform_real_distribution<float> u(-2.0f, 2.0f);
-  for (size_t i = 0; i < a.size(); i++) {
+  if (quantized) {
+    quantized_normal_rows(g, M, K, ha, a);
+    quantized_normal_rows(g, N, K, hb, b);
+  }
+  for (size_t i = 0; i < a.size() && !quantized; i++) {
     if (bf16) {
       const uint16_t h = bf16_bits(u(g));
       reinterpret_cast<uint16_t*>(ha.data())[i] = h;
@@ -69,7 +100,7 @@ static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters, bool 
       a[i] = (int8_t)ha[i];
     }
   }
-  for (size_t i = 0; i < b.size(); i++) {
+  for (size_t i = 0; i < b.size() && !quantized; i++) {
     if (bf16) {
       const uint16_t h = bf16_bits(u(g));
       reinterpret_cast<uint16_t*>(hb.data())[i] = h;
@@ -164,7 +195,8 @@ static int time_shape(hipblasLtHandle_t h, int M, int K, int N, int iters, bool 
   const double ops = 2.0 * M * K * N;
   printf("{\"mode\": \"%s\", \"m\": %d, \"k\": %d, \"n\": %d, \"candidates\": %d, "
          "\"timed\": %d, \"best_us\": %.2f, \"tops\": %.0f, \"check_bad\": %d}\n",
-         bf16 ? "bf16" : "i8", M, K, N, n, tried, best, ops / (best * 1e-6) / 1e12, bad);
+         bf16 ? "bf16" : quantized ? "i8q" : "i8", M, K, N, n, tried, best,
+         ops / (best * 1e-6) / 1e12, bad);
   fflush(stdout);
   hipblasLtMatmulPreferenceDestroy(pref);
   hipblasLtMatrixLayoutDestroy(la);
@@ -182,6 +214,7 @@ int main(int argc, char** argv) {
   const int M = argc > 1 ? atoi(argv[1]) : 10102;
   const int iters = argc > 2 ? atoi(argv[2]) : 20;
   const bool bf16 = argc > 3 && strcmp(argv[3], "bf16") == 0;
+  const bool quantized = argc > 3 && strcmp(argv[3], "i8q") == 0;
   std::vector<std::pair<int, int>> shapes = {{768, 2304}, {768, 768}, {768, 3072}, {3072, 768}};
   if (argc > 4) {  // "k,n;k,n;..."
     shapes.clear();
@@ -196,7 +229,7 @@ int main(int argc, char** argv) {
   hipblasLtHandle_t h;
   BCHK(hipblasLtCreate(&h));
   for (auto& s : shapes)
-    if (time_shape(h, M, s.first, s.second, iters, bf16)) return 1;
+    if (time_shape(h, M, s.first, s.second, iters, bf16, quantized)) return 1;
   hipblasLtDestroy(h);
   return 0;
 }

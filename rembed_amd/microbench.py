@@ -23,13 +23,18 @@ PEAK = {"i8": 5000.0, "w8": 2500.0, "f32": 2500.0}  # TOP/s of the MFMA used
 
 
 def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u8=False, bf=0,
-               group=4):
+               group=4, uniform=False):
+    """Normal weights and activations (an encoder's distribution); uniform:
+    values uniform in [-1, 1), whose int8 images are near-uniform bytes
+    (the matrix cores clock lower on high-entropy operands)."""
     rng = np.random.default_rng(k * 7 + n)
-    bT = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
+    draw = ((lambda shape: rng.uniform(-1.0, 1.0, shape).astype(np.float32)) if uniform
+            else (lambda shape: rng.standard_normal(shape, dtype=np.float32)))
+    bT = (draw((n, k)) * 0.02).astype(np.float32)
     bias = rng.standard_normal(n, dtype=np.float32) * 0.02
     pack = {"i8": T.PackB8VNNI, "w8": T.PackB8, "f32": T.PackB}[mode]
     pb = pack(ctx, bT, k, n, bias=bias)
-    a = ctx.upload(rng.standard_normal((m, k), dtype=np.float32))
+    a = ctx.upload(draw((m, k)))
     dst = ctx.alloc(m * n * 4)
     ldq = T.ldq_for(k)
     qa = ctx.alloc(m * ldq)
@@ -76,7 +81,7 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
     ctx.set_option(_lib.RH_CTX_TILE_GROUP, 4)
     split_us = sp["total_ms"] * 1e3 / sp["launches"] if sp["launches"] else 0.0
     return {"mode": mode, "m": m, "k": k, "n": n, "act": act, "tile": tile, "bf": bf,
-            "group": group,
+            "group": group, "operands": "uniform" if uniform else "normal",
             "acc_only": acc_only, "fused_u8": fused_u8, "us": round(us, 2),
             "split_us": round(split_us, 2), "tops": round(tops, 1),
             "frac": round(tops / PEAK[mode], 4),
@@ -252,6 +257,13 @@ def main():
                     help="only time hipBLASLt's GEMM (every heuristic candidate, the fastest "
                          "reported) at --m and --shapes (default: BERT-base): int8 with "
                          "int32 out, or with --modes bf16 bf16 with fp32 out")
+    ap.add_argument("--uniform-operands", action="store_true",
+                    help="time the library's GEMMs on uniform operands (near-uniform int8 "
+                         "bytes) instead of normal ones")
+    ap.add_argument("--quantized-operands", action="store_true",
+                    help="with --hipblaslt (int8): per-row quantized normal operand bytes, "
+                         "as this benchmark feeds the library's GEMMs, instead of uniformly "
+                         "random bytes")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -260,7 +272,8 @@ def main():
         import os
         import subprocess
         exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "blaslt_ref")
-        cmd = [exe, str(args.m), str(args.iters), "bf16" if args.modes == "bf16" else "i8"]
+        cmd = [exe, str(args.m), str(args.iters),
+               "bf16" if args.modes == "bf16" else "i8q" if args.quantized_operands else "i8"]
         if args.shapes:
             cmd.append(args.shapes)
         return subprocess.run(cmd).returncode
@@ -299,7 +312,8 @@ def main():
                     for bf in bfs:
                         for grp in [int(g) for g in args.groups.split(",")]:
                             r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile,
-                                           bf=bf, group=grp, **v)
+                                           bf=bf, group=grp, uniform=args.uniform_operands,
+                                           **v)
                             print(json.dumps(r), flush=True)
     ctx.close()
     return 0
