@@ -696,16 +696,33 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
 //   16) holds keys 16t + 4fg + i. A query's 64 scores of a block sit in
 //   the four lanes fr, fr+16, fr+32, fr+48 (two shuffles per statistic).
 // * O^T += V^T·P^T per 32-key step kc: lane (fr, fg) feeds B element j with
-//   its own scores, key 32kc + 4fg + j (j < 4) or 32kc + 16 + 4fg + j - 4;
-//   V^T rows hold the keys in that order (chunk 4kc + fg of a 128-byte row
-//   is lane group fg's eight keys), so a V^T fragment is one 16-byte read.
+//   its own scores, key 32kc + 4fg + j (j < 4) or 32kc + 16 + 4fg + j - 4.
+//   V stays row-major in LDS (DMA-staged like K) and the V^T fragments come
+//   from ds_read_b64_tr_b16, which within each 16-lane group gives lane i
+//   element e = element i % 4 of what lane 4e + i / 4 addressed (checked on
+//   the GPU). Lane s of group fg addresses key row 32kc + 4fg + s / 4 (then
+//   16 rows further for elements 4..7), dims 16t + 4 (s % 4) .. +3, so lane
+//   (fr, fg) receives dim 16t + fr of exactly the keys its B element j
+//   holds. Rows go in pairs of 512 bytes (one 1 KiB DMA block) padded by 32
+//   bytes: the 16 rows of one read then land two per 32-byte bank slot.
 constexpr int kH256Waves = 8;
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v8bf attn_vt_frag(const uint8_t* lo, const uint8_t* hi) {
+  typedef __attribute__((address_space(3))) v4s* lds_v4s;
+  const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(lo));
+  const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(hi));
+  return __builtin_bit_cast(v8bf, (v8s)__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 __global__ __launch_bounds__(64 * kH256Waves) void attention_h256_kernel(AttnArgs p) {
   constexpr int DH = 256, KS = DH / 32, NDT = DH / 16;
-  constexpr int kRowB = DH * 2;               // bytes of one K row (512)
-  constexpr int kKB = kAttnKV * kRowB;        // K block bytes (32 KiB) = V^T block bytes
-  constexpr int kStage = 2 * kKB;             // K + V^T
+  constexpr int kRowB = DH * 2;               // bytes of one K or V row (512)
+  constexpr int kKB = kAttnKV * kRowB;        // K block bytes (32 KiB)
+  constexpr int kVPair = 2 * kRowB + 32;      // two V rows and their padding
+  constexpr int kVB = kAttnKV / 2 * kVPair;   // V block bytes (33 KiB)
+  constexpr int kStage = kKB + kVB;           // K + V
   constexpr int kKLoads = kKB / (kH256Waves * 1024);  // DMA instructions per wave (4)
   constexpr int kStride = DH + 4;             // output staging row (floats)
   constexpr int kOut = kH256Waves * 16 * kStride * 4;
@@ -751,38 +768,23 @@ __global__ __launch_bounds__(64 * kH256Waves) void attention_h256_kernel(AttnArg
                 sK + (wave * kKLoads + j) * 1024);
     }
   };
-  // V: thread (key group kgp = tid / 64: kc = kgp / 4, fg' = kgp % 4; d block
-  // db = tid % 64 of 4 dims) loads its 8 keys' 4 dims (8 bytes each) and
-  // writes 4 V^T rows, 16 bytes each, at chunk kgp.
-  const int kgp = tid >> 6, db = tid & 63;
-  int vkey[8];
-#pragma unroll
-  for (int x = 0; x < 8; x++)
-    vkey[x] = (kgp >> 2) * 32 + (x < 4 ? 4 * (kgp & 3) + x : 16 + 4 * (kgp & 3) + x - 4);
-  uint2 vx[8];
-  auto load_v = [&](int kb) {
-#pragma unroll
-    for (int x = 0; x < 8; x++) {
-      const int key = kb * kAttnKV + vkey[x];
-      vx[x] = *reinterpret_cast<const uint2*>(
-          vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 4);
-    }
-  };
-  auto write_vt = [&](int buf) {
+  // V DMA: 1 KiB block j holds rows 2j and 2j + 1 (lane l: row 2j + l / 32,
+  // bytes 16 (l % 32)), blocks kVPair apart
+  const int v_row = (wave * kKLoads) * 2 + (lane >> 5), v_col = (lane & 31) * 8;
+  auto issue_v = [&](int kb, int buf) {
     uint8_t* sV = lds + buf * kStage + kKB;
 #pragma unroll
-    for (int dd = 0; dd < 4; dd++) {
-      // byte selectors of v_perm_b32 for the low / high 16 bits of each source
-      v4i w;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t a = dd < 2 ? vx[2 * q].x : vx[2 * q].y;
-        const uint32_t c = dd < 2 ? vx[2 * q + 1].x : vx[2 * q + 1].y;
-        w[q] = (int)((dd & 1) ? ((a >> 16) | (c & 0xffff0000u)) : ((a & 0xffffu) | (c << 16)));
-      }
-      *reinterpret_cast<v4i*>(sV + lds_off(db * 4 + dd, kgp)) = w;
+    for (int j = 0; j < kKLoads; j++) {
+      const int kg = kb * kAttnKV + v_row + 2 * j;
+      lds_dma16(vbase + (size_t)(r0 + (kg < len ? kg : len - 1)) * p.ldqkv + v_col,
+                sV + (wave * kKLoads + j) * kVPair);
     }
   };
+  // this lane's transposed-read address in a V block (key row 4fg + fr / 4,
+  // dims 4 (fr % 4) .. +3); step kc adds 16 row pairs, elements 4..7 eight
+  // pairs, dim tile t 32 bytes
+  const int vt_row = 4 * fg + (fr >> 2);
+  const int vt_off = (vt_row >> 1) * kVPair + (vt_row & 1) * kRowB + 8 * (fr & 3);
 
   v4f o[NDT];
 #pragma unroll
@@ -800,8 +802,7 @@ __global__ __launch_bounds__(64 * kH256Waves) void attention_h256_kernel(AttnArg
   }
 
   issue_k(kb_lo, 0);
-  load_v(kb_lo);
-  write_vt(0);
+  issue_v(kb_lo, 0);
   __syncthreads();
 
   for (int kb = kb_lo; kb < kb_hi; kb++) {
@@ -809,10 +810,10 @@ __global__ __launch_bounds__(64 * kH256Waves) void attention_h256_kernel(AttnArg
     const bool next = kb + 1 < kb_hi;
     if (next) {
       issue_k(kb + 1, buf ^ 1);
-      load_v(kb + 1);
+      issue_v(kb + 1, buf ^ 1);
     }
     const uint8_t* sK = lds + buf * kStage;
-    const uint8_t* sV = sK + kKB;
+    const uint8_t* sV = sK + kKB + vt_off;
     const int key0 = kb * kAttnKV;
 
     if (qw0 < len) {  // a wave whose queries all lie past the text only stages
@@ -884,13 +885,13 @@ __global__ __launch_bounds__(64 * kH256Waves) void attention_h256_kernel(AttnArg
         }
 #pragma unroll
         for (int t = 0; t < NDT; t++) {
-          const v8bf vf = *reinterpret_cast<const v8bf*>(sV + lds_off(t * 16 + fr, 4 * kc + fg));
+          const uint8_t* v = sV + kc * 16 * kVPair + t * 32;
+          const v8bf vf = attn_vt_frag(v, v + 8 * kVPair);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, ph, o[t], 0, 0, 0);
         }
       }
     }
 
-    if (next) write_vt(buf ^ 1);
     __syncthreads();  // next block landed (vmcnt) and this block's reads are done
   }
 
