@@ -406,20 +406,41 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
 // ---- bf16 operands, pipelined --------------------------------------------------
 // The same algorithm and fragment layouts for bf16 q|k|v rows, with the key
 // blocks double-buffered: while a block is multiplied, the next block's K
-// rows stream into LDS by global_load_lds_dwordx4 and its V rows are loaded
-// into registers, transposed 8x8 there and written as V^T rows.
+// and V rows stream into LDS by global_load_lds_dwordx4.
 //
 // K block: [64 keys][DH] bf16, 16-byte chunk c of row r at slot c ^ kswz(r)
 // (16 consecutive rows of one fragment read land in 16 distinct bank
-// groups). V^T block: [DH][64] bf16, one 128-byte row per d, chunk cc at
-// lds_off(d, cc). Within each 16-key group the keys are stored in the order
-// the P^T registers hold them (see below), so a lane's V^T fragment is one
-// 16-byte read.
+// groups). V block: [64 keys][DH] bf16 as well, 64-byte pieces swizzled by
+// attn_vswz; the PV products read it transposed (ds_read_b64_tr_b16), so
+// each lane's V^T fragment holds the keys in the order its P^T registers
+// do (see below).
 template <int DH>
 __device__ __forceinline__ int attn_kswz(int r) {
   constexpr int C = DH / 8;                       // chunks per K row
   constexpr int W = DH * 2 < 256 ? 256 / (DH * 2) : 1;  // rows per 256-B bank window
   return (r / W) & ((C < 16 ? C : 16) - 1);
+}
+
+// Two ds_read_b64_tr_b16 (CDNA4's transposing LDS read) make one 8-element
+// bf16 A fragment of a PV product from row-major V: within each 16-lane
+// group, lane i element e is element i % 4 of the 8 bytes lane 4e + i / 4
+// addressed (checked on the GPU). `lo` gives elements 0..3, `hi` 4..7.
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v8bf attn_vt_frag(const uint8_t* lo, const uint8_t* hi) {
+  typedef __attribute__((address_space(3))) v4s* lds_v4s;
+  const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(lo));
+  const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(hi));
+  return __builtin_bit_cast(v8bf, (v8s)__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// V rows in LDS, row-major as DMA-staged: 64-byte piece q of row r sits at
+// piece q ^ attn_vswz<DH>(r). A transposed read of the 32x32 kernel covers 8
+// consecutive rows x 64 bytes; the swizzle spreads them two per 64-byte bank
+// window (head dim 32 needs none).
+template <int DH>
+__device__ __forceinline__ int attn_vswz(int r) {
+  return DH == 64 ? (r >> 1) & 1 : DH >= 128 ? r & 3 : 0;
 }
 
 template <int DH, int T>
@@ -429,7 +450,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   constexpr int KS = DH / 16, DT = DH / 32;
   constexpr int kRowB = DH * 2;               // bytes of one K row
   constexpr int kKB = kAttnKV * kRowB;        // K block bytes
-  constexpr int kStage = 2 * kKB * T;         // K + V^T (same size), per plane
+  constexpr int kStage = 2 * kKB * T;         // K + V (same size), per plane
   constexpr int kKLoads = kKB / (4 * 1024);   // DMA instructions per wave per block
   static_assert(kKLoads >= 1 && kKB % 4096 == 0, "K block must split into 4 waves x 1 KiB");
   constexpr int kOut = 4 * 32 * (DH + 4) * 4;  // output staging (attn_store_rows)
@@ -481,79 +502,38 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
       }
     }
   };
-  // V, two ways to the V^T block (same bytes):
-  // * DH < 256 (kPairs): work item w (of 32 key pairs x DH/8 d blocks,
-  //   spread over all threads) loads keys 2kp, 2kp+1 of d block db (two
-  //   16-byte row pieces) and writes them as 8 four-byte words of V^T, one
-  //   per d. In P^T order block-local key k sits in chunk 2(k/16) + (k/4)%2
-  //   at element ((k/8)%2)*4 + k%4, so the two keys of a pair share a word.
-  // * DH = 256: thread t owns key group kgp = t / (DH/8) (chunk kgp: 16-key
-  //   group kgp/2, lane half kgp%2) and d block db = t % (DH/8); its 8 keys,
-  //   in P^T order key(e) = (kgp/2)*16 + (e/4)*8 + (kgp%2)*4 + e%4, are
-  //   transposed 8x8 in registers and written as 16-byte V^T pieces (every
-  //   thread busy, a quarter of the LDS write instructions).
-  constexpr bool kPairs = DH < 256;
-  constexpr int kVItems = kPairs ? 32 * (DH / 8) : 256;
-  constexpr int kVPer = (kVItems + 255) / 256;
-  constexpr int kVRegs = kPairs ? 2 : 8;
-  v4i vx[T][kVPer][kVRegs];
-  auto load_v = [&](int kb) {
+  // V DMA: the K slots with the V swizzle on 64-byte pieces (4 chunks)
+  int v_chunk[kKLoads];
+#pragma unroll
+  for (int j = 0; j < kKLoads; j++) {
+    const int off = (wave * kKLoads + j) * 1024 + lane * 16;
+    v_chunk[j] = ((off % kRowB) >> 4) ^ (4 * attn_vswz<DH>(k_row[j]));
+  }
+  auto issue_v = [&](int kb, int buf) {
 #pragma unroll
     for (int t = 0; t < T; t++) {
+      uint8_t* sV = lds + buf * kStage + t * 2 * kKB + kKB;
       const __bf16* vbase = (t ? qkv_lo : qkv) + vvo;
 #pragma unroll
-      for (int u = 0; u < kVPer; u++) {
-        const int w = tid + u * 256;
-        if (kVItems % 256 != 0 && w >= kVItems) break;
-        const int kg = w / (DH / 8), db = w % (DH / 8);
-#pragma unroll
-        for (int x = 0; x < kVRegs; x++) {
-          const int key = kb * kAttnKV + (kPairs ? 2 * kg + x
-                                                 : (kg >> 1) * 16 + (x >> 2) * 8 + (kg & 1) * 4 + (x & 3));
-          vx[t][u][x] = *reinterpret_cast<const v4i*>(
-              vbase + (size_t)(r0 + (key < len ? key : len - 1)) * p.ldqkv + db * 8);
-        }
+      for (int j = 0; j < kKLoads; j++) {
+        const int kg = kb * kAttnKV + k_row[j];
+        lds_dma16(vbase + (size_t)(r0 + (kg < len ? kg : len - 1)) * p.ldqkv + v_chunk[j] * 8,
+                  sV + (wave * kKLoads + j) * 1024);
       }
     }
   };
-  auto write_vt = [&](int buf) {
+  // PV A fragments (lane (fr, g): dim 32t + fr of keys 16kc + 8(e/4) + 4g +
+  // e%4, the key order of P^T's B fragment): lane s of 16-lane group G
+  // addresses row 16kc + 4(G/2) + s/4 (+8 for elements 4..7), dims 32t +
+  // 16(G%2) + 4(s%4) .. +3. The swizzle of those rows depends on s only, and
+  // the per-t offset lands in bits 6.. of a row that the XOR owns alone.
+  int vt_off[DT];
+  {
+    const int s16 = lane & 15, vr = 4 * (lane >> 5) + (s16 >> 2);
+    const int base = vr * kRowB + 64 * attn_vswz<DH>(vr) + 32 * ((lane >> 4) & 1) + 8 * (s16 & 3);
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-    uint8_t* sV = lds + buf * kStage + t * 2 * kKB + kKB;
-#pragma unroll
-    for (int u = 0; u < kVPer; u++) {
-      const int w = tid + u * 256;
-      if (kVItems % 256 != 0 && w >= kVItems) break;
-      const int kg = w / (DH / 8), db = w % (DH / 8);
-      if constexpr (kPairs) {
-        const int k = 2 * kg;  // even key of the pair (block-local)
-        const int chunk = 2 * (k >> 4) + ((k >> 2) & 1);
-        const int word = ((k >> 3) & 1) * 2 + ((k & 3) >> 1);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const uint32_t a = (uint32_t)vx[t][u][0][e >> 1], c = (uint32_t)vx[t][u][1][e >> 1];
-          const uint32_t pair =
-              (e & 1) ? ((a >> 16) | (c & 0xffff0000u)) : ((a & 0xffffu) | (c << 16));
-          *reinterpret_cast<uint32_t*>(sV + lds_off(db * 8 + e, chunk) + word * 4) = pair;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {  // d = db*8 + 2j (low halves) and 2j + 1 (high halves)
-          v4i lo, hi;
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const uint32_t a = (uint32_t)vx[t][u][2 * i][j], c = (uint32_t)vx[t][u][2 * i + 1][j];
-            lo[i] = (int)((a & 0xffffu) | (c << 16));
-            hi[i] = (int)((a >> 16) | (c & 0xffff0000u));
-          }
-          const int d = db * 8 + 2 * j;
-          *reinterpret_cast<v4i*>(sV + lds_off(d, kg)) = lo;
-          *reinterpret_cast<v4i*>(sV + lds_off(d + 1, kg)) = hi;
-        }
-      }
-    }
-    }
-  };
+    for (int t = 0; t < DT; t++) vt_off[t] = base ^ (64 * t);
+  }
 
   v16f o[DT];
 #pragma unroll
@@ -576,16 +556,15 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   const bool text_mask = !p.causal && p.window <= 0;
 
   issue_k(kb_lo, 0);
-  load_v(kb_lo);
-  write_vt(0);
-  __syncthreads();  // waits for the DMA (vmcnt) and orders the V^T writes
+  issue_v(kb_lo, 0);
+  __syncthreads();  // waits for the DMA (vmcnt)
 
   for (int kb = kb_lo; kb < kb_hi; kb++) {
     const int buf = (kb - kb_lo) & 1;
     const bool next = kb + 1 < kb_hi;
     if (next) {
       issue_k(kb + 1, buf ^ 1);
-      load_v(kb + 1);
+      issue_v(kb + 1, buf ^ 1);
     }
     const uint8_t* sK = lds + buf * kStage;
     const uint8_t* sV = sK + kKB;
@@ -650,7 +629,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     }
 
     // O^T += V^T · P^T over 4 chunks of 16 keys; lane half g, element e of
-    // chunk kc is register sc[kc/2][(kc%2)*8 + e], V^T chunk 2kc + g.
+    // chunk kc is register sc[kc/2][(kc%2)*8 + e], key 16kc + 8(e/4) + 4g + e%4.
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) {
       v8bf ph, pl;
@@ -662,11 +641,11 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
       }
 #pragma unroll
       for (int t = 0; t < DT; t++) {
-        const int vo = lds_off(t * 32 + fr, 2 * kc + fg);
-        const v8bf vf = *reinterpret_cast<const v8bf*>(sV + vo);
+        const int vo = kc * 16 * kRowB + vt_off[t];
+        const v8bf vf = attn_vt_frag(sV + vo, sV + vo + 8 * kRowB);
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[t], 0, 0, 0);
         if constexpr (T == 2) {
-          const v8bf vl = *reinterpret_cast<const v8bf*>(sVl + vo);
+          const v8bf vl = attn_vt_frag(sVl + vo, sVl + vo + 8 * kRowB);
           o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[t], 0, 0, 0);
           o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, o[t], 0, 0, 0);
         }
@@ -674,7 +653,6 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
     }
     }
 
-    if (next) write_vt(buf ^ 1);
     __syncthreads();  // next block landed (vmcnt) and this block's reads are done
   }
 
@@ -707,14 +685,6 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
 //   bytes: the 16 rows of one read then land two per 32-byte bank slot.
 constexpr int kH256Waves = 8;
 
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef short v8s __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ v8bf attn_vt_frag(const uint8_t* lo, const uint8_t* hi) {
-  typedef __attribute__((address_space(3))) v4s* lds_v4s;
-  const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(lo));
-  const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(hi));
-  return __builtin_bit_cast(v8bf, (v8s)__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
-}
 
 __global__ __launch_bounds__(64 * kH256Waves) void attention_h256_kernel(AttnArgs p) {
   constexpr int DH = 256, KS = DH / 32, NDT = DH / 16;
