@@ -406,7 +406,7 @@ static hipError_t launch_pl(const GemmPlArgs& a, hipStream_t s) {
 // MI355X at M = 16384 over the Qwen3/BERT linears; 8 waves 2-15% faster than
 // 4 at the same tile): tile 6 for one-term W8 when the 256x256 grid gives
 // at least every other CU a workgroup, 4 for the other products when it
-// gives every CU one, else 5 down to half a round of its tiles, else 128x128
+// gives every CU one, else 5 down to 96 tiles, else 128x128
 // while its grid has at least 192 workgroups; below that (MiniLM's M ~ 2300,
 // or N = 384) 64x64, which keeps the CUs busy: at M = 2304 the weight-only
 // int8 linears take 9.8 / 5.6 / 11.6 µs (384x1152, 384x384, 1536x384)
@@ -425,9 +425,11 @@ int pick_planes_tile(int M, int N, int K, int a_terms, int b_terms) {
     return t6 > 256 && tail != 0 && tail <= 128 && K <= 1536 ? 10 : 6;
   }
   if (a_terms + b_terms < 4 && ceil_div(M, 256) * ceil_div(N, 256) >= 256) return 4;
-  // 256x128 down to half a round of tiles (fp32 at M = 10102, N = 768: 240
-  // tiles, 43.5 / 154 µs at K = 768 / 3072 against 53.6 / 190 on 128x128)
-  if (ceil_div(M, 256) * ceil_div(N, 128) >= 128) return 5;
+  // 256x128 down to 96 tiles (fp32 at M = 10102, N = 768: 240 tiles, 43.5 /
+  // 154 µs at K = 768 / 3072 against 53.6 / 190 on 128x128; the two-stream
+  // fp32 BERT-base forward's parts, ~5050 rows, give 120 tiles at N = 768:
+  // 1.49 against 1.41 M tokens/s end to end with 128x128 there)
+  if (ceil_div(M, 256) * ceil_div(N, 128) >= 96) return 5;
   return ceil_div(M, 128) * ceil_div(N, 128) >= 192 ? 3 : 8;
 }
 
