@@ -854,13 +854,15 @@ static hipError_t launch_epi(const GemmI8Args& a, int tile, hipStream_t s) {
 int pick_i8_tile(int M, int N, int K, int epi) {
   (void)epi;
   const int tiles = ceil_div(M, 128) * ceil_div(N, 256);
-  // deep K on a grid of at most one 128x256 workgroup per CU (the BERT-base
-  // FFN2 at M = 10102: 34.2 against 35.5 µs fp32 out, 31.9 against 33.2
-  // int32 out), down to a quarter of the CUs: the two-stream headline runs
-  // FFN2 on parts of ~5050 rows (120 such tiles), where this tile instead of
-  // 128x128 took the whole forward from 3.28 to 3.34 M tokens/s (interleaved
-  // runs); B fragments straight to registers halve the LDS reads
-  if (K >= 2048 && tiles <= 256 && tiles >= 64) return 13;
+  // The fragment-B 128x256 tile (B fragments straight to registers halve
+  // the LDS reads) for deep K on a grid of at most one such workgroup per CU
+  // (the BERT-base FFN2 at M = 10102: 34.2 against 35.5 µs fp32 out, 31.9
+  // against 33.2 int32 out), and for any K on 64..127 of them: the
+  // two-stream headline runs its parts of ~5050 rows, where O and FFN2 give
+  // 120 such tiles; against 128x128 there the whole forward went from 3.28
+  // to 3.34 M tokens/s with FFN2 on it and from 3.47 to 3.51 with O as well
+  // (interleaved runs)
+  if ((K >= 2048 || tiles < 128) && tiles <= 256 && tiles >= 64) return 13;
   if (tiles < 128) return 3;
   // deep K on a grid of at least one 256x256 tile per CU: the 128x128-wave
   // tile (4-12 % ahead of tiles 7 and 9 at M = 16384, K = 2048 and 3072)
