@@ -77,8 +77,10 @@ void *rh_context_stream(rh_context *ctx);
  *   RH_CTX_BF_TILE   tile of the bf16-planes GEMM: 0 = automatic, 1 = 256x256,
  *                    2 = 256x128, 3 = 128x128, 4 = 256x256, 5 = 256x128
  *                    (eight waves), 6 = 256x256, 7 = 256x128 (eight waves,
- *                    128-byte k stages; one-term weight-only int8 only, the
- *                    other products take 3)
+ *                    128-byte k stages), 8 = 64x64, 9 = 128x64 (four waves),
+ *                    10 = 128x256 (eight waves, three 64-byte k stages, two
+ *                    workgroups per CU); 6, 7 and 10 for the one-term
+ *                    weight-only int8 product only, the other products take 3
  *   RH_CTX_TILE_GROUP  GEMM tile order: consecutive workgroups walk this many
  *                    row blocks down a column block (1 = row-major; default 4) */
 #define RH_CTX_F32_ALGO 1
