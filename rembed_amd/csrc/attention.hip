@@ -525,8 +525,9 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(AttnArgs p) {
   // PV A fragments (lane (fr, g): dim 32t + fr of keys 16kc + 8(e/4) + 4g +
   // e%4, the key order of P^T's B fragment): lane s of 16-lane group G
   // addresses row 16kc + 4(G/2) + s/4 (+8 for elements 4..7), dims 32t +
-  // 16(G%2) + 4(s%4) .. +3. The swizzle of those rows depends on s only, and
-  // the per-t offset lands in bits 6.. of a row that the XOR owns alone.
+  // 16(G%2) + 4(s%4) .. +3. The swizzle of those rows depends on s only;
+  // 64t and the swizzled piece offset share bits 6 and up of a row's bytes,
+  // below its row index, so base ^ 64t addresses dim tile t.
   int vt_off[DT];
   {
     const int s16 = lane & 15, vr = 4 * (lane >> 5) + (s16 >> 2);
