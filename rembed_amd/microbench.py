@@ -23,17 +23,24 @@ PEAK = {"i8": 5000.0, "w8": 2500.0, "f32": 2500.0}  # TOP/s of the MFMA used
 
 
 def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u8=False, bf=0,
-               group=4, uniform=False):
+               group=4, uniform=False, copies=1, requantize=False):
     """Normal weights and activations (an encoder's distribution); uniform:
     values uniform in [-1, 1), whose int8 images are near-uniform bytes
-    (the matrix cores clock lower on high-entropy operands)."""
+    (the matrix cores clock lower on high-entropy operands). copies > 1:
+    that many packed weights, used in turn, as a forward's layers use theirs
+    (a launch then reads its weight past the L2 instead of from it).
+    requantize (int8): the activation rows are quantized again before every
+    launch, so each launch reads u8 rows just written, as in a forward."""
     rng = np.random.default_rng(k * 7 + n)
     draw = ((lambda shape: rng.uniform(-1.0, 1.0, shape).astype(np.float32)) if uniform
             else (lambda shape: rng.standard_normal(shape, dtype=np.float32)))
     bT = (draw((n, k)) * 0.02).astype(np.float32)
     bias = rng.standard_normal(n, dtype=np.float32) * 0.02
     pack = {"i8": T.PackB8VNNI, "w8": T.PackB8, "f32": T.PackB}[mode]
-    pb = pack(ctx, bT, k, n, bias=bias)
+    pbs = [pack(ctx, bT, k, n, bias=bias)]
+    for _ in range(copies - 1):
+        pbs.append(pack(ctx, (draw((n, k)) * 0.02).astype(np.float32), k, n, bias=bias))
+    turn = [0]
     a = ctx.upload(draw((m, k)))
     dst = ctx.alloc(m * n * 4)
     ldq = T.ldq_for(k)
@@ -52,6 +59,10 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
     absmax = ctx.alloc(m * 4) if fused_u8 else None
 
     def run():
+        pb = pbs[turn[0] % len(pbs)]
+        turn[0] += 1
+        if mode == "i8" and requantize:
+            T.QuantizeRowsU8(ctx, a, m, k, qa, ldq, rs)
         if mode == "i8":
             if fused_u8:  # linear + QuantizeRowU8 of the outputs (two passes)
                 T.LinearU8(ctx, qa, ldq, rs, pb, m, act, qout, ldo, rs_out, absmax)
@@ -82,6 +93,7 @@ def bench_case(ctx, mode, m, k, n, iters, act=0, tile=0, acc_only=False, fused_u
     split_us = sp["total_ms"] * 1e3 / sp["launches"] if sp["launches"] else 0.0
     return {"mode": mode, "m": m, "k": k, "n": n, "act": act, "tile": tile, "bf": bf,
             "group": group, "operands": "uniform" if uniform else "normal",
+            "weight_copies": copies, "requantize": requantize,
             "acc_only": acc_only, "fused_u8": fused_u8, "us": round(us, 2),
             "split_us": round(split_us, 2), "tops": round(tops, 1),
             "frac": round(tops / PEAK[mode], 4),
@@ -264,6 +276,12 @@ def main():
                     help="with --hipblaslt (int8): per-row quantized normal operand bytes, "
                          "as this benchmark feeds the library's GEMMs, instead of uniformly "
                          "random bytes")
+    ap.add_argument("--weight-copies", type=int, default=1,
+                    help="pack this many weights per shape and use them in turn, as a "
+                         "forward's layers do (default 1: one weight, L2-resident)")
+    ap.add_argument("--requantize", action="store_true",
+                    help="int8: quantize the activation rows again before every launch, so "
+                         "each launch reads freshly written u8 rows (as in a forward)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -313,7 +331,8 @@ def main():
                         for grp in [int(g) for g in args.groups.split(",")]:
                             r = bench_case(ctx, mode, args.m, k, n, args.iters, tile=tile,
                                            bf=bf, group=grp, uniform=args.uniform_operands,
-                                           **v)
+                                           copies=args.weight_copies,
+                                           requantize=args.requantize, **v)
                             print(json.dumps(r), flush=True)
     ctx.close()
     return 0
