@@ -266,9 +266,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="bert-base-int8",
                     help="default: the configuration the metric is quoted on")
-    ap.add_argument("--ffn1", choices=["fused", "split"], default="split",
+    ap.add_argument("--ffn1", choices=["fused", "onepass", "split"], default="onepass",
                     help="full-int8 FFN1: fused = GELU rows re-quantized inside the GEMM "
-                         "(two passes, no fp32 intermediate); split = fp32 rows + QuantizeRowU8")
+                         "(two passes, no fp32 intermediate); onepass = one GEMM pass whose "
+                         "workgroups meet per row block on the row |max|; split = fp32 rows + "
+                         "QuantizeRowU8")
     ap.add_argument("--no-u8-diff", action="store_true",
                     help="skip the per-layer u8 comparison with the oracle (full int8)")
     ap.add_argument("--forwards-only", action="store_true",
@@ -316,7 +318,7 @@ def main():
         model.set_graph(args.graph == "on")
     if quant == 2:
         assert model.quantized_activations(), "full-int8 path did not take"
-        model.set_fused_ffn1(args.ffn1 == "fused")
+        model.set_fused_ffn1({"split": 0, "fused": 1, "onepass": 2}[args.ffn1])
     elif quant == 1:
         assert model.quantized() and not model.quantized_activations()
     gkind = {2: 0, 1: 1, 0: 2}[quant]  # profile kind of the workload's GEMMs
@@ -384,7 +386,10 @@ def main():
     ctx.sync()
     profiled_ms_per_step = (time.perf_counter() - t1) * 1e3 / args.steps
     model.check()
-    gemm = ctx.profile_read(gkind)
+    gemm_plain = ctx.profile_read(gkind)
+    # the one-pass FFN1 launches (full int8): GEMM + GELU + QuantizeRowU8
+    fused = ctx.profile_read(5)
+    gemm = {k: gemm_plain[k] + fused[k] for k in gemm_plain}
     attn = ctx.profile_read(3)
     split = ctx.profile_read(4)  # bf16 split of the W8/fp32 GEMMs' activations
     ctx.profile(False)
@@ -393,6 +398,9 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     value = tokens * args.steps / elapsed
     per_launch_ms = gemm["total_ms"] / max(1, gemm["launches"])
+
+    def rate(st):  # TOP/s (TFLOP/s) of a profile tally
+        return st["total_ops"] / (st["total_ms"] * 1e-3) / 1e12 if st["total_ms"] else 0.0
     achieved = gemm["total_ops"] / (gemm["total_ms"] * 1e-3) / 1e12  # TOP/s
     gemm_ms_step = gemm["total_ms"] / args.steps
     attn_ms_step = attn["total_ms"] / args.steps
@@ -478,7 +486,10 @@ def main():
             "bound": "mfma",
             "kernel": ("gemm_i8_kernel / gemm_i8f_kernel" if quant == 2 else
                        "gemm_planes_kernel") +
-                      f" (all {gemm['launches'] // args.steps} GEMM launches per step)",
+                      f" (all {gemm['launches'] // args.steps} GEMM launches per step" +
+                      (f"; {fused['launches'] // args.steps} of them FFN1 with the GELU + "
+                       "QuantizeRowU8 row pass in the epilogue, counted at GEMM ops)"
+                       if fused["launches"] else ")"),
             "achieved": round(achieved, 2),
             "peak": peak,
             "unit": "TFLOP/s",
@@ -486,6 +497,17 @@ def main():
             "traffic": traffic,
             "ops_per_launch": gemm["total_ops"] / max(1, gemm["launches"]),
             "avg_launch_ms": round(per_launch_ms, 5),
+            **({"gemm_only": {
+                "launches_per_step": gemm_plain["launches"] // args.steps,
+                "achieved": round(rate(gemm_plain), 2),
+                "frac": round(rate(gemm_plain) / peak, 4),
+                "avg_launch_ms": round(gemm_plain["total_ms"] / max(1, gemm_plain["launches"]), 5)},
+               "fused_ffn1": {
+                "launches_per_step": fused["launches"] // args.steps,
+                "gemm_achieved": round(rate(fused), 2),
+                "gemm_frac": round(rate(fused) / peak, 4),
+                "avg_launch_ms": round(fused["total_ms"] / max(1, fused["launches"]), 5)}}
+               if fused["launches"] else {}),
         },
         "profiled_ms_per_step": round(profiled_ms_per_step, 4),
         "gemm_ms_per_step": round(gemm_ms_step, 4),

@@ -100,7 +100,9 @@ int rh_memcpy_d2h(rh_context *ctx, void *host_dst, const void *dev_src, size_t b
 /* Per-launch GEMM timing with HIP events on the context's stream.
  * kind: 0 = full-int8 GEMM, 1 = weight-only int8 GEMM, 2 = fp32 GEMM,
  * 3 = attention, 4 = bf16 split of GEMM activations (weight-only int8 and
- * fp32 GEMMs on bf16 planes). Reading syncs the stream. */
+ * fp32 GEMMs on bf16 planes), 5 = full-int8 GEMM with the GELU +
+ * QuantizeRowU8 row pass in its epilogue (the one-pass FFN1; ops count the
+ * GEMM only). Reading syncs the stream. */
 typedef struct {
   int64_t launches;
   double total_ms;    /* sum of per-launch event durations */
@@ -354,9 +356,13 @@ void rh_model_destroy(rh_model *m);
  * 3 = three-term bf16 split (fp32-grade; the default for RH_QUANT_NONE and,
  * in every mode, for the BERT family: RH_ARCH_BERT, RH_ARCH_DISTILBERT,
  * RH_ARCH_MPNET).
- * RH_OPT_FUSED_FFN1: 1 = full-int8 FFN1 writes u8 rows directly (two GEMM
- * passes, no fp32 intermediate), 0 = fp32 GELU rows then QuantizeRowU8
- * (default); both give identical bytes. RH_OPT_PRODUCER_PLANES: 1 = the
+ * RH_OPT_FUSED_FFN1: full-int8 FFN1 + GELU + QuantizeRowU8 (bert.go:910-916).
+ * 2 = one GEMM pass writes the u8 rows: its workgroups exchange each row's
+ * |max| per row block (default; a bounded wait, and a wait that timed out
+ * fails rh_model_embed / rh_model_embed_tokens and rh_model_check with
+ * RH_ERR_HIP); 1 = two GEMM passes (row |max|, then the bytes); 0 = fp32
+ * FFN1 rows, then GELU + QuantizeRowU8 as a separate pass. All give
+ * identical bytes. RH_OPT_PRODUCER_PLANES: 1 = the
  * kernels that produce a weight-only int8 / fp32 GEMM's input (norms,
  * attention, the previous GEMM) write its bf16 hi/lo planes directly
  * (default), 0 = they write fp32 rows and each GEMM splits them; both give

@@ -375,9 +375,12 @@ int pack_weight_gated(Context* ctx, int mode, const float* gate, const float* up
 int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                 const float* rs, int m, int epi, void* out, int ldo, int act,
                 const float* bias, float* row_absmax, float* rs_out, double ops,
-                void* out_lo) {
+                void* out_lo, unsigned* sync, unsigned* slots, int slot_ld,
+                unsigned* sync_err) {
   if (m <= 0) return RH_OK;
   if (epi == EPI_PLANES && !out_lo) return fail(RH_ERR_INVALID, "planes epilogue needs a lo plane");
+  if (epi == EPI_QSYNC && (!sync || !slots || !sync_err))
+    return fail(RH_ERR_INVALID, "single-pass quantizing epilogue needs its counters");
   GemmI8Args g{};
   g.A = qa;
   g.lda = ldq;
@@ -399,12 +402,17 @@ int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
   g.row_absmax = row_absmax;
   g.rs_out = rs_out;
   g.tile_group = ctx->tile_group;
+  g.sync = sync;
+  g.slots = slots;
+  g.slot_ld = slot_ld;
+  g.sync_err = sync_err;
   const double M = m, K = w->k, N = w->n;
-  static const double out_bytes[] = {4, 2, 0, 1, 4, 4};  // per output element
+  static const double out_bytes[] = {4, 2, 0, 1, 4, 4, 1};  // per output element
   const double bytes = M * K + K * N + M * N * out_bytes[epi] + 4 * M + 8 * N +
-                       (bias ? 4 * N : 0) + (epi == EPI_QUANT ? 4 * M : 0);
+                       (bias ? 4 * N : 0) +
+                       (epi == EPI_QUANT || epi == EPI_QSYNC ? 4 * M : 0);
   int slot = -1;
-  hipError_t e = ctx->prof_begin(0, ops, bytes, &slot);
+  hipError_t e = ctx->prof_begin(epi == EPI_QSYNC ? 5 : 0, ops, bytes, &slot);
   if (e == hipSuccess) e = launch_gemm_i8(g, ctx->i8_tile, ctx->stream);
   if (e == hipSuccess) e = ctx->prof_end(slot);
   if (e != hipSuccess) return hip_fail(e, "int8 gemm launch", __FILE__, __LINE__);

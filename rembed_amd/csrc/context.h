@@ -130,7 +130,8 @@ int run_linear_qk(Context* ctx, const rh_weight* w, const Planes& pin, int m,
 int run_gemm_i8(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                 const float* rs, int m, int epi, void* out, int ldo, int act,
                 const float* bias, float* row_absmax, float* rs_out, double ops,
-                void* out_lo = nullptr);
+                void* out_lo = nullptr, unsigned* sync = nullptr,
+                unsigned* slots = nullptr, int slot_ld = 0, unsigned* sync_err = nullptr);
 // run_gemm_i8 with the residual + LayerNorm finish (launch_gemm_i8_ln).
 int run_gemm_i8_ln(Context* ctx, const rh_weight* w, const uint8_t* qa, int ldq,
                    const float* rs, int m, const I8LnArgs& f, double ops);

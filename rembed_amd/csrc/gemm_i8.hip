@@ -209,6 +209,184 @@ __device__ __forceinline__ void i8_epilogue(const GemmI8Args& p, v16i (&acc)[TM]
   }
 }
 
+// Single-pass GELU + QuantizeRowU8 epilogue (EPI_QSYNC), for FFN1 feeding
+// FFN2's u8 rows (bert.go:910-916, pack_vnni.go:85-117) without the fp32
+// intermediate. Sweep 1 dequantizes the tile through the LDS transpose (the
+// same float32 operations as the other epilogues), keeps the values in
+// registers and publishes each row's |max| over the tile's columns in the
+// row's slot for this column tile. Each row's thread then reads the row's
+// tiles_n slots until none holds the empty mark: their max is the |max|
+// over the whole row, as QuantizeRowU8 takes it. Sweep 2 quantizes the held
+// values and stores the bytes. The last workgroup of a row block to leave
+// (a departure count per row block) empties the block's slots and zeroes
+// its count for the next launch.
+//
+// A row block's column tiles are consecutive workgroups of one XCD
+// (qsync_tile), which starts its workgroups in order: once a row block's
+// first tile runs, the tiles it waits for are the next ones queued on that
+// XCD, and at most tiles_n - 1 workgroups of one launch wait at a time (two
+// launches on two streams leave most of an XCD's 64 slots to workgroups
+// that finish), so every wait ends. It is bounded all the same: past
+// kSyncWaitTicks of the 100 MHz clock the row is taken as complete and
+// sync_err is set. Slots are written and read by device-scope atomic
+// stores and loads, coherent across the XCDs.
+constexpr uint64_t kSyncWaitTicks = 20000000;  // 200 ms
+constexpr unsigned kSlotEmpty = 0xFFFFFFFFu;   // never the bits of a |max|
+
+template <int BM, int WM, int WN, int TM, int TN, int NW, int NT>
+__device__ __forceinline__ void i8_epilogue_qsync(const GemmI8Args& p, v16i (&acc)[TM][TN],
+                                                  uint8_t* lds, int row0, int col0, int rb,
+                                                  int cb, int tiles_n, int wave, int wm, int wn,
+                                                  int tid) {
+  constexpr int WGN = NW / 2;
+  constexpr int kEpiStride = WN + 4;
+  constexpr int kEpiBytes = NW * 32 * kEpiStride * 4;
+  constexpr int kLanesPerRow = WN / 4;
+  constexpr int kRowsPerPass = 64 / kLanesPerRow;
+  constexpr int kPasses = 32 / kRowsPerPass;
+  static_assert(TM * kPasses * 4 <= 64, "values held per lane");
+  static_assert(BM <= NT, "one thread per row gathers the row's slots");
+  const int lane = tid & 63;
+  const int fr = lane & 31, fg = lane >> 5;
+  __syncthreads();
+  int* ep = reinterpret_cast<int*>(lds) + wave * 32 * kEpiStride;
+  float* rs_l = reinterpret_cast<float*>(lds + kEpiBytes);  // [BM] row scales
+  float* mx_l = rs_l + BM;                                   // [BM][WGN] per-wave row |max|
+  float* sc_l = mx_l + BM * WGN;                             // [BM] output row scales
+  float* inv_l = sc_l + BM;                                  // [BM] their reciprocals
+  unsigned* last_l = reinterpret_cast<unsigned*>(inv_l + BM);
+  for (int r = tid; r < BM; r += NT) rs_l[r] = row0 + r < p.M ? p.row_scales[row0 + r] : 0.0f;
+  __syncthreads();
+  const int c4 = (lane % kLanesPerRow) * 4;
+  const int gcol = col0 + wn * WN + c4;
+  const bool col_ok = gcol < p.N;
+  v4f cs = {1.0f, 1.0f, 1.0f, 1.0f}, bs = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (col_ok) {
+    cs = *reinterpret_cast<const v4f*>(p.col_scales + gcol);
+    if (p.bias) bs = *reinterpret_cast<const v4f*>(p.bias + gcol);
+  }
+  v4f val[TM][kPasses];
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        ep[((r >> 2) * 8 + fg * 4 + (r & 3)) * kEpiStride + j * 32 + fr] = acc[i][j][r];
+    wait_lgkmcnt0();
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int it = 0; it < kPasses; it++) {
+      const int rr = lane / kLanesPerRow + it * kRowsPerPass;
+      const int trow = wm * WM + i * 32 + rr;
+      const v4i a = *reinterpret_cast<const v4i*>(ep + rr * kEpiStride + c4);
+      v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (row0 + trow < p.M && col_ok) {
+        const float rs = rs_l[trow];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float x = (float)a[e] * rs;
+          x = x * cs[e];
+          if (p.bias) x = x + bs[e];
+          v[e] = apply_act(x, p.act);
+        }
+      }
+      val[i][it] = v;
+      // invalid lanes contribute 0; every lane takes part in the shuffles
+      float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+      for (int o = kLanesPerRow / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      if (lane % kLanesPerRow == 0) mx_l[trow * WGN + wn] = m;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  if (tid < BM && row0 + tid < p.M) {
+    // publish this tile's |max| of the row, then gather the row's slots
+    float m = mx_l[tid * WGN];
+#pragma unroll
+    for (int w = 1; w < WGN; w++) m = fmaxf(m, mx_l[tid * WGN + w]);
+    unsigned* slot = p.slots + (size_t)(row0 + tid) * p.slot_ld;
+    __hip_atomic_store(slot + cb, __float_as_uint(m), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    unsigned mx = 0;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      unsigned v[kQsyncMaxTiles];
+#pragma unroll
+      for (int c = 0; c < kQsyncMaxTiles; c++)
+        v[c] = c < tiles_n
+                   ? __hip_atomic_load(slot + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : 0u;
+      bool full = true;
+      mx = 0;
+#pragma unroll
+      for (int c = 0; c < kQsyncMaxTiles; c++) {
+        full = full && v[c] != kSlotEmpty;
+        mx = max(mx, v[c] == kSlotEmpty ? 0u : v[c]);
+      }
+      if (full) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncWaitTicks) {
+        atomicOr(p.sync_err, 1u);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    // QuantizeRowU8's scale (pack_vnni.go:94-101); |max| bits order as floats
+    float sc = __uint_as_float(mx) / 127.0f;
+    if (sc == 0.0f) sc = 1.0f;
+    sc_l[tid] = sc;
+    inv_l[tid] = 1.0f / sc;
+  }
+  __syncthreads();
+  // every read of the slots has returned: count this workgroup out
+  // (the count's value is needed only after the stores below)
+  unsigned dep = 0;
+  if (tid == 0) dep = atomicAdd(p.sync + rb, 1u);
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int it = 0; it < kPasses; it++) {
+      const int trow = wm * WM + i * 32 + lane / kLanesPerRow + it * kRowsPerPass;
+      const int grow = row0 + trow;
+      if (grow < p.M && col_ok) {
+        const float inv = inv_l[trow];
+        const v4f v = val[i][it];
+        const uint32_t w = quant_byte(v[0], inv) | (quant_byte(v[1], inv) << 8) |
+                           (quant_byte(v[2], inv) << 16) | (quant_byte(v[3], inv) << 24);
+        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p.out) + (size_t)grow * p.ldo + gcol) = w;
+        if (gcol == 0) p.rs_out[grow] = sc_l[trow];
+      }
+    }
+  if (tid == 0) last_l[0] = dep == (unsigned)tiles_n - 1;
+  __syncthreads();
+  if (last_l[0]) {
+    for (int i = tid; i < BM * tiles_n; i += NT) {
+      const int r = i / tiles_n, c = i - r * tiles_n;
+      if (row0 + r < p.M)
+        __hip_atomic_store(p.slots + (size_t)(row0 + r) * p.slot_ld + c, kSlotEmpty,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0) __hip_atomic_store(p.sync + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// EPI_QSYNC workgroup -> tile: workgroup b runs on XCD b % 8 (the dispatch
+// order) as that XCD's (b / 8)-th; each XCD owns ceil(tiles_m / 8)
+// consecutive row blocks and runs them one after another, a row block's
+// column tiles in a row. Workgroups past the last row block have no tile
+// (rb >= tiles_m). Pairs of row blocks down each column (the order of the
+// other tiles) took 101 against 86 µs at M = 10102, N = 3072: a row
+// block's tiles then spread over twice as many workgroups, which wait
+// longer for the last of them.
+__device__ __forceinline__ void qsync_tile(int b, int tiles_m, int tiles_n, int& rb, int& cb) {
+  constexpr int kXcd = 8;
+  const int per_xcd = (tiles_m + kXcd - 1) / kXcd;
+  const int k = b / kXcd;
+  rb = (b % kXcd) * per_xcd + k / tiles_n;
+  cb = k % tiles_n;
+}
+
 // WGN waves along N: 2 = a 2x2 grid of 4 waves, 4 = a 2x4 grid of 8 (two per
 // SIMD when one workgroup fills a CU).
 // BK: k bytes per stage and row, 64 (i8_slot rows) or 128 (lds_off rows;
@@ -226,6 +404,8 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
   constexpr int kEpiBytes = NW * 32 * kEpiStride * 4;
   static_assert(LA >= 1 && LB >= 1 && TN >= 1, "tile too small for the wave grid");
   static_assert(NS * kStage >= kEpiBytes + 3 * BM * 4, "epilogue LDS");
+  static_assert(EPI != EPI_QSYNC || NS * kStage >= kEpiBytes + (3 + WGN) * BM * 4 + 4,
+                "single-pass epilogue LDS");
   static_assert(NS * kStage <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
 
@@ -234,9 +414,14 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
   const int tiles_n = (p.N + BN - 1) / BN;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
   int rb, cb;
-  tile_origin(tile, (p.M + BM - 1) / BM, tiles_n, p.tile_group, rb, cb);
+  if constexpr (EPI == EPI_QSYNC) {
+    qsync_tile(blockIdx.x, (p.M + BM - 1) / BM, tiles_n, rb, cb);
+    if (rb >= (p.M + BM - 1) / BM) return;
+  } else {
+    tile_origin(xcd_remap(blockIdx.x, gridDim.x), (p.M + BM - 1) / BM, tiles_n, p.tile_group,
+                rb, cb);
+  }
   const int row0 = rb * BM;
   const int col0 = cb * BN;
   const int nk = (p.K + BK - 1) / BK;
@@ -358,7 +543,11 @@ __global__ __launch_bounds__(128 * WGN) void gemm_i8_kernel(GemmI8Args p) {
     }
   }
 
-  i8_epilogue<BM, WM, WN, TM, TN, NW, NT, EPI>(p, acc, lds, row0, col0, wave, wm, wn, tid);
+  if constexpr (EPI == EPI_QSYNC)
+    i8_epilogue_qsync<BM, WM, WN, TM, TN, NW, NT>(p, acc, lds, row0, col0, rb, cb, tiles_n,
+                                                  wave, wm, wn, tid);
+  else
+    i8_epilogue<BM, WM, WN, TM, TN, NW, NT, EPI>(p, acc, lds, row0, col0, wave, wm, wn, tid);
 }
 
 // ---- 128x128 wave tiles for the long-K problems ---------------------------------
@@ -872,8 +1061,31 @@ int pick_i8_tile(int M, int N, int K, int epi) {
   return (K >= 2048 || tiles <= 256) ? 9 : 7;
 }
 
+// EPI_QSYNC on the 128x256 tiles of gemm_i8_kernel (7, 9, 10; any other
+// choice takes 7), on the grid qsync_tile maps: 8 XCDs x ceil(tiles_m / 8)
+// row blocks x tiles_n.
+template <int BN, int NS, int WGN = 2, int BK = 64>
+static hipError_t launch_qsync_tile(const GemmI8Args& a, hipStream_t s) {
+  const int g = 8 * ceil_div(ceil_div(a.M, 128), 8) * ceil_div(a.N, BN);
+  timed_launch((gemm_i8_kernel<128, BN, NS, EPI_QSYNC, WGN, BK>), dim3(g), dim3(128 * WGN), 0,
+               s, a);
+  return hipGetLastError();
+}
+
+static hipError_t launch_qsync(const GemmI8Args& a, int tile, hipStream_t s) {
+  if (!a.sync || !a.sync_err || !a.slots || !a.rs_out || !a.out || !a.col_scales ||
+      is_glu(a.act) || ceil_div(a.N, 256) > kQsyncMaxTiles || a.slot_ld < ceil_div(a.N, 256))
+    return hipErrorInvalidValue;
+  switch (tile) {
+    case 9: return launch_qsync_tile<256, 2, 4, 128>(a, s);
+    case 10: return launch_qsync_tile<256, 3, 4, 128>(a, s);
+    default: return launch_qsync_tile<256, 3, 4>(a, s);
+  }
+}
+
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a.epi == EPI_QSYNC) return launch_qsync(a, tile > 0 && tile <= kI8TileConfigs ? tile : 7, s);
   if (tile <= 0 || tile > kI8TileConfigs) {
     tile = pick_i8_tile(a.M, a.N, a.K, a.epi);
     if (tile == 13 && !a.Bf) tile = 9;  // no fragment-ordered image of B

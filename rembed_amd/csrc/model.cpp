@@ -136,7 +136,10 @@ struct rh_model {
   float *normed = nullptr, *pooled = nullptr, *dense_hid = nullptr;
   int32_t* pos_d = nullptr;
   int attn_precision = 3;
-  bool fused_ffn1 = false;  // RH_OPT_FUSED_FFN1
+  // RH_OPT_FUSED_FFN1: 0 split, 1 two passes, 2 one pass (default: 3.58-3.59
+  // against 3.46-3.47 M tokens/s for split on the BERT-base int8 batch,
+  // interleaved runs on one box)
+  int fused_ffn1 = 2;
   // RH_OPT_EXACT (BERT family): LayerNorm's sums and attention in the
   // reference's own float32 order (fp32 q|k|v rows), so a full-int8 forward
   // is byte-identical to the reference's
@@ -179,6 +182,13 @@ struct rh_model {
   int ld0 = 0, ld1 = 0;
   uint8_t *qa = nullptr, *qa2 = nullptr;  // u8 activations: width H / width I
   float *rs = nullptr, *rs2 = nullptr, *absmax = nullptr;
+  // the one-pass FFN1 (RH_OPT_FUSED_FFN1 2): per row one slot per column
+  // tile [cap][kQsyncMaxTiles] (all ones when empty), and per part one
+  // departure count per 128-row block (qsync_stride words after word 0,
+  // the timeout flag); set when allocated and left so by every launch
+  unsigned* qslots = nullptr;
+  unsigned* qsync = nullptr;
+  int qsync_stride = 0;
   int32_t* cu_d = nullptr;
   int32_t* ids_d = nullptr;
   float* out_d = nullptr;
@@ -210,9 +220,10 @@ struct rh_model {
                     (void*)rs, (void*)cu_d, (void*)ids_d, (void*)out_d, (void*)qkvh,
                     (void*)qa2, (void*)rs2, (void*)absmax, (void*)normed, (void*)pooled,
                     (void*)dense_hid, (void*)p0h, (void*)p0l, (void*)p1h, (void*)p1l,
-                    (void*)pos_d, (void*)hid2})
+                    (void*)pos_d, (void*)hid2, (void*)qslots, (void*)qsync})
       if (p) (void)hipFree(p);
     x = qkv = ctxb = y = hid = rs = out_d = rs2 = absmax = normed = pooled = dense_hid = nullptr;
+    qslots = qsync = nullptr;
     hid2 = nullptr;
     pos_d = nullptr;
     qa = qa2 = nullptr;
@@ -333,9 +344,10 @@ struct rh_model {
       for (void* p : {(void*)x, (void*)qkv, (void*)ctxb, (void*)y, (void*)hid, (void*)qa,
                       (void*)rs, (void*)qkvh, (void*)qa2, (void*)rs2, (void*)absmax,
                       (void*)normed, (void*)pos_d, (void*)p0h, (void*)p0l, (void*)p1h,
-                      (void*)p1l, (void*)hid2})
+                      (void*)p1l, (void*)hid2, (void*)qslots, (void*)qsync})
         if (p) RH_HIP(hipFree(p));
       x = qkv = ctxb = y = hid = rs = rs2 = absmax = normed = hid2 = nullptr;
+      qslots = qsync = nullptr;
       qa = qa2 = nullptr;
       qkvh = p0h = p0l = p1h = p1l = nullptr;
       pos_d = nullptr;
@@ -356,6 +368,11 @@ struct rh_model {
       RH_HIP(dalloc(&rs, r));
       RH_HIP(dalloc(&rs2, r));
       RH_HIP(dalloc(&absmax, r));
+      RH_HIP(dalloc(&qslots, r * kQsyncMaxTiles));
+      RH_HIP(hipMemset(qslots, 0xFF, r * kQsyncMaxTiles * sizeof(unsigned)));
+      qsync_stride = (int)(r / 128) + 1;
+      RH_HIP(dalloc(&qsync, 1 + (size_t)kMaxParts * qsync_stride));
+      RH_HIP(hipMemset(qsync, 0, (1 + (size_t)kMaxParts * qsync_stride) * sizeof(unsigned)));
       if (quant != RH_QUANT_FULL) {
         ld0 = (int)round_up(std::max(H, ctx_width()), 64);
         ld1 = (int)round_up(I, 64);
@@ -456,6 +473,7 @@ struct rh_model {
   struct Part {
     int row0, rows, b0, nb, max_len;
     hipStream_t s;
+    int idx;  // 0..streams-1
   };
   bool uses_split_ws(const rh_weight* w, bool pin) const {
     return linear_on_planes(ctx, w) && !pin;
@@ -527,7 +545,7 @@ int rh_model::plan_parts(const std::vector<int32_t>& cu, bool allowed, hipStream
       ps = sx[k];
     }
     Part p{cu[bounds[k]], cu[bounds[k + 1]] - cu[bounds[k]], bounds[k],
-           bounds[k + 1] - bounds[k], 0, ps};
+           bounds[k + 1] - bounds[k], 0, ps, k};
     for (int b = bounds[k]; b < bounds[k + 1]; b++) p.max_len = std::max(p.max_len, cu[b + 1] - cu[b]);
     parts.push_back(p);
   }
@@ -785,9 +803,9 @@ int rh_model::forward_bert(const int32_t* ids_dev, int stride, const std::vector
     const Planes pnv = last ? Planes{} : at(plane(0, layers[li + 1].qkv));
     // FFN2 finishes the layer (residual + LayerNorm + next QKV's u8 rows) in
     // its epilogue on the split full-int8 path
-    const bool fused_ln2 = !(fused_ffn1 && qf1 && needs_q(L.f2)) && qf1 && needs_q(L.f2) &&
-                           fuse_ln(L.f2, xn_planes);
-    if (fused_ffn1 && qf1 && needs_q(L.f2)) {
+    const bool fused_ln2 = !(fused_ffn1 == 1 && qf1 && needs_q(L.f2)) && qf1 &&
+                           needs_q(L.f2) && fuse_ln(L.f2, xn_planes);
+    if (fused_ffn1 == 1 && qf1 && needs_q(L.f2)) {
       // FFN1 + GELU + QuantizeRowU8 without the fp32 intermediate: pass 1
       // finds each row's |max| of the GELU output, pass 2 recomputes the
       // identical values and writes the u8 bytes and row scales FFN2 reads.
@@ -810,10 +828,21 @@ int rh_model::forward_bert(const int32_t* ids_dev, int stride, const std::vector
       // FFN2's row quantizer, which has VALU to spare where the GEMM
       // epilogue does not. Same float32 operations in the same order as
       // GELU(dense(x)) then QuantizeRowU8 (bert.go:910-916).
-      st = run_linear(ctx, L.f1, xp, H, Mp, hidp, I, ACT_NONE, L.f1->d_bias, qap, ldq_for(H),
-                      rsp, false);
-      if (st) return st;
-      RH_HIP(launch_quantize_rows_u8(hidp, I, Mp, I, qa2p, ldq_for(I), rs2p, ps, ACT_GELU));
+      if (fused_ffn1 == 2 && I <= 256 * kQsyncMaxTiles) {
+        // one pass: FFN1's workgroups exchange the GELU rows' |max| per row
+        // block and write the u8 bytes and row scales (EPI_QSYNC), the same
+        // bytes as the two kernels below
+        st = run_gemm_i8(ctx, L.f1, qap, ldq_for(H), rsp, Mp, EPI_QSYNC, qa2p, ldq_for(I),
+                         ACT_GELU, L.f1->d_bias, nullptr, rs2p, 2.0 * MH * H * I, nullptr,
+                         qsync + 1 + (size_t)P.idx * qsync_stride,
+                         qslots + r0 * kQsyncMaxTiles, kQsyncMaxTiles, qsync);
+        if (st) return st;
+      } else {
+        st = run_linear(ctx, L.f1, xp, H, Mp, hidp, I, ACT_NONE, L.f1->d_bias, qap,
+                        ldq_for(H), rsp, false);
+        if (st) return st;
+        RH_HIP(launch_quantize_rows_u8(hidp, I, Mp, I, qa2p, ldq_for(I), rs2p, ps, ACT_GELU));
+      }
       if (fused_ln2) {
         st = run_gemm_i8_ln(ctx, L.f2, qa2p, ldq_for(I), rs2p, Mp,
                             ln_args(xp, L.ln2_g, L.ln2_b, qn ? qap : nullptr, ldq_for(H),
@@ -1676,8 +1705,8 @@ int rh_model_set_option(rh_model* m, int option, int value) {
       return RH_OK;
     }
     if (option == RH_OPT_FUSED_FFN1) {
-      if (value != 0 && value != 1) return fail(RH_ERR_INVALID, "fused FFN1 must be 0 or 1");
-      m->fused_ffn1 = value != 0;
+      if (value < 0 || value > 2) return fail(RH_ERR_INVALID, "fused FFN1 must be 0, 1 or 2");
+      m->fused_ffn1 = value;
       return RH_OK;
     }
     if (option == RH_OPT_EXACT) {
@@ -1898,7 +1927,15 @@ static int embed_common(rh_model* m, const int64_t* ids, const int32_t* lens, in
   else
     RH_HIP(hipMemcpyAsync(out, m->x, (size_t)M * H * sizeof(float), hipMemcpyDeviceToHost,
                           s));
+  // a one-pass FFN1 row wait that timed out left bytes that may be wrong
+  unsigned late = 0;
+  const bool onepass = m->qsync && m->fused_ffn1 == 2;
+  if (onepass) RH_HIP(hipMemcpyAsync(&late, m->qsync, sizeof(unsigned), hipMemcpyDeviceToHost, s));
   RH_HIP(hipStreamSynchronize(s));
+  if (late) {
+    RH_HIP(hipMemset(m->qsync, 0, sizeof(unsigned)));
+    return fail(RH_ERR_HIP, "one-pass FFN1: a row's wait for its row maxima timed out");
+  }
   return RH_OK;
 }
 
@@ -1941,6 +1978,14 @@ int rh_model_check(rh_model* m) {
   return api_call([&]() -> int {
     MODEL_GUARD(m);
     RH_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (m->qsync) {
+      unsigned late = 0;
+      RH_HIP(hipMemcpy(&late, m->qsync, sizeof(unsigned), hipMemcpyDeviceToHost));
+      if (late) {
+        RH_HIP(hipMemset(m->qsync, 0, sizeof(unsigned)));
+        return fail(RH_ERR_HIP, "one-pass FFN1: a row's wait for its row maxima timed out");
+      }
+    }
     if (!m->err_d) return RH_OK;
     int flag = 0;
     RH_HIP(hipMemcpy(&flag, m->err_d, sizeof(int), hipMemcpyDeviceToHost));

@@ -122,8 +122,10 @@ enum I8Epi : int {
   EPI_QUANT = 3,   // out u8 [M][ldo] = QuantizeRowU8(value row) using
                    // row_absmax from a preceding EPI_ABSMAX pass; rs_out[M]
   EPI_ACC = 4,     // out int32 [M][ldo] = reference-form accumulators
-  EPI_PLANES = 5   // out / out_lo bf16 [M][ldo]: hi = bf16(value), lo =
+  EPI_PLANES = 5,  // out / out_lo bf16 [M][ldo]: hi = bf16(value), lo =
                    // bf16(value - hi), both rounded to nearest even
+  EPI_QSYNC = 6    // EPI_QUANT in one pass: the workgroups of a row block
+                   // exchange their row maxima through `slots`
 };
 
 struct GemmI8Args {
@@ -145,6 +147,13 @@ struct GemmI8Args {
   float* row_absmax;        // EPI_ABSMAX target / EPI_QUANT input
   float* rs_out;            // EPI_QUANT row scales
   int tile_group;           // row blocks per group of the tile order (tile_origin)
+  // EPI_QSYNC: departures per 128-row block (zero on entry and on exit),
+  // row maxima slots [M][slot_ld] per column tile (kSlotEmpty on entry and
+  // on exit), bit 0 of sync_err set if a row's wait timed out
+  unsigned* sync;
+  unsigned* slots;
+  int slot_ld;
+  unsigned* sync_err;
 };
 
 // B formats of the bf16-MFMA GEMM family.
@@ -240,6 +249,8 @@ enum F32Algo : int { F32_SPLIT3 = 0, F32_NATIVE = 1 };
 // Launchers (gemm_i8.hip, gemm_bf16.hip). Return hipError_t of the launch.
 // tile: 0 = automatic, else one of the configurations RH_CTX_I8_TILE lists.
 constexpr int kI8TileConfigs = 15;
+// EPI_QSYNC: column tiles per row at most (N <= 16 x 256)
+constexpr int kQsyncMaxTiles = 16;
 hipError_t launch_gemm_i8(const GemmI8Args& a, int tile, hipStream_t s);
 // The residual + LayerNorm finish of a full-int8 linear whose N is the
 // hidden width (the attention output and FFN2 projections of the BERT

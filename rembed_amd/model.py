@@ -141,8 +141,13 @@ class Model:
         residual add + LayerNorm in their epilogue (identical results)."""
         check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSED_LN, 1 if on else 0))
 
-    def set_fused_ffn1(self, on):
-        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSED_FFN1, 1 if on else 0))
+    def set_fused_ffn1(self, mode):
+        """RH_OPT_FUSED_FFN1 (full int8): 0 / False = fp32 FFN1 rows, then
+        GELU + QuantizeRowU8 as a separate pass; 1 / True = two GEMM passes
+        (row |max|, then the u8 bytes); 2 = one pass whose workgroups meet
+        per row block on the row |max|. Identical bytes in every mode."""
+        mode = int(mode)
+        check(lib.rh_model_set_option(self.h, _lib.RH_OPT_FUSED_FFN1, mode))
 
     def set_producer_planes(self, on=True):
         """Weight-only int8 / fp32 GEMM inputs written as bf16 planes by their
@@ -219,4 +224,6 @@ class Model:
                                         stride, out_dev.ptr))
 
     def check(self):
+        """rh_model_check: waits for the model's work and reports a device-side
+        error (an out-of-range token id, a one-pass FFN1 wait that timed out)."""
         check(lib.rh_model_check(self.h))

@@ -116,10 +116,36 @@ def test_fused_ffn1_identical(gpu_ctx, minilm):
     shape, t, ids, lens = minilm
     from rembed_amd.model import Model
     m = Model(gpu_ctx, shape, t, 2)
+    m.set_fused_ffn1(0)
     plain = m.embed(ids, lens)
-    m.set_fused_ffn1(True)
+    m.set_fused_ffn1(1)
     fused = m.embed(ids, lens)
     assert np.array_equal(plain, fused)
+
+
+@pytest.mark.parametrize("model", ["minilm", "bertbase"])
+@pytest.mark.parametrize("streams", [1, 2])
+def test_onepass_ffn1_identical(gpu_ctx, request, model, streams):
+    """The one-pass full-int8 FFN1 (RH_OPT_FUSED_FFN1 2: the GEMM's
+    workgroups meet per row block on the GELU rows' |max| and write
+    QuantizeRowU8's bytes, bert.go:910-916) gives the same embeddings, bit
+    for bit, as fp32 rows followed by the separate GELU + quantize pass.
+    Repeated calls and a smaller batch after the full one check that every
+    launch leaves its departure counts zero and its row slots empty for the
+    next; no wait timed out (rh_model_check)."""
+    from rembed_amd.model import Model
+    shape, t, ids, lens = request.getfixturevalue(model)
+    say(f"{shape.name}: {len(lens)} texts, {int(lens.sum())} rows, {streams} stream(s)")
+    m = Model(gpu_ctx, shape, t, 2)
+    m.set_streams(streams)
+    m.set_fused_ffn1(0)
+    plain = m.embed(ids, lens)
+    few = m.embed(ids[:5], lens[:5])
+    m.set_fused_ffn1(2)
+    for rep in range(3):
+        assert np.array_equal(m.embed(ids, lens), plain), rep
+        assert np.array_equal(m.embed(ids[:5], lens[:5]), few), rep
+    m.check()
 
 
 @pytest.mark.parametrize("model", ["minilm", "bertbase"])
