@@ -56,9 +56,10 @@ def stats(path, steps, title, command):
 
 # The int8 GEMMs of one BERT-base layer in launch order: name, K, N, bytes
 # per output element (QKV rows go to fp32-grade attention as bf16 hi/lo
-# planes, 2 + 2 bytes).
-BERT_BASE_I8_LAYER = [("QKV", 768, 2304, 4), ("O", 768, 768, 4), ("FFN1", 768, 3072, 4),
-                      ("FFN2", 3072, 768, 4)]
+# planes, 2 + 2 bytes; the one-pass FFN1 writes FFN2's u8 rows, its launch
+# also runs GELU + QuantizeRowU8 over them).
+BERT_BASE_I8_LAYER = [("QKV", 768, 2304, 4), ("O", 768, 768, 4),
+                      ("FFN1 + GELU + QuantizeRowU8", 768, 3072, 1), ("FFN2", 3072, 768, 4)]
 INT8_PEAK_TOPS, HBM_PEAK_GBS = 5000.0, 8000.0
 
 
