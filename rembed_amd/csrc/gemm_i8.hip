@@ -24,9 +24,11 @@
 //
 // Epilogue (shared by both): per 32-row band a wave parks its accumulators
 // in LDS and reads rows back 4 columns per lane, so every output is a
-// 4-wide vector store. Variants (EPI): fp32 or bf16 values, the raw
-// accumulators, or the two passes of a fused row quantization (row |max| by
-// atomics, then u8 bytes).
+// 4-wide vector store. Variants (EPI): fp32 or bf16 values, bf16 hi/lo
+// planes, the raw accumulators, the two passes of a fused row quantization
+// (row |max| by atomics, then u8 bytes), or that quantization in one pass
+// (i8_epilogue_qsync: the workgroups of a row block exchange the row
+// maxima).
 #include "gemm_common.h"
 #include "rows_common.h"
 
